@@ -1,0 +1,233 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X batched token sampler (one decode step = one
+mlxf_sample call over a [B, V] logits matrix already resident in HBM).
+
+Default workload: config C3 (B=32, V=151936, fp32, T=1, top-k 50, top-p 0.95),
+the configuration the headline metric is quoted on.  Prints ONE JSON line.
+
+Timing: hipEvents (torch.cuda.Event on the stream the library launches on)
+around K back-to-back steps after W warm-up steps; the input is rotated over
+enough copies to exceed 512 MB so neither L2 nor the 256 MB MALL holds it when
+a step starts ("cold" HBM).  Per-kernel durations come from a second pass
+through mlxf_sample_profiled (HIP events around each kernel on the same
+stream).  cpu_baseline times the CPU restatement of the reference sampler
+(oracle/, "port") on the same workload with a bounded number of repetitions.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = ("µs/decode-step and sampled rows/sec at B=32,V=151936; achieved HBM GB/s")
+HBM_PEAK_GBPS = 8000.0
+ROTATE_BYTES = 512 << 20
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Step:
+    """Pre-allocated device state for one workload; run() issues one mlxf_sample."""
+
+    def __init__(self, wl, torch, lib, rotate=True):
+        import numpy as np
+        self.wl, self.torch, self.lib = wl, torch, lib
+        dev = torch.device("cuda:0")
+        host = wl.logits
+        nbytes = host.nbytes
+        self.R = max(3, -(-ROTATE_BYTES // nbytes) + 1) if rotate else 1
+        t = torch.from_numpy(host.view(np.int16)).view(torch.bfloat16) if wl.dtype == "bf16" \
+            else torch.from_numpy(host)
+        one = t.to(dev)
+        self.buf = one.unsqueeze(0).repeat(self.R, 1, 1).contiguous()
+        del one
+        d = lambda a, ty: torch.as_tensor(a, dtype=ty).to(dev)
+        self.T, self.k, self.p = d(wl.T, torch.float32), d(wl.k, torch.int32), d(wl.p, torch.float32)
+        self.tlp, self.u = d(wl.tlp, torch.int32), d(wl.u, torch.float32)
+        B = wl.B
+        self.ids = torch.empty(B, dtype=torch.int32, device=dev)
+        self.lp = torch.empty(B, dtype=torch.float32, device=dev)
+        self.K = wl.K_max
+        self.tids = torch.empty((B, max(self.K, 1)), dtype=torch.int32, device=dev)
+        self.tlpo = torch.empty((B, max(self.K, 1)), dtype=torch.float32, device=dev)
+        self.code = {"f32": 0, "bf16": 1, "f16": 2}[wl.dtype]
+        from mlxforge_amd import _lib
+        self.ws_bytes = _lib.workspace_size(B, wl.V, self.K, self.code)
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
+        self.stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        P = ctypes.c_void_p
+        self.args_tail = [P(self.T.data_ptr()), P(self.k.data_ptr()), P(self.p.data_ptr()),
+                          P(self.tlp.data_ptr()), P(self.u.data_ptr()), P(self.ids.data_ptr()),
+                          P(self.lp.data_ptr()),
+                          P(self.tids.data_ptr()) if self.K else None,
+                          P(self.tlpo.data_ptr()) if self.K else None, self.K,
+                          P(self.ws.data_ptr()), self.ws_bytes, self.stream]
+        self.row_bytes = wl.V * wl.elem_size
+        self.i = 0
+
+    def _logits(self):
+        p = self.buf[self.i % self.R].data_ptr()
+        self.i += 1
+        return ctypes.c_void_p(p)
+
+    def run(self):
+        err = ctypes.c_void_p()
+        rc = self.lib.mlxf_sample(self._logits(), self.code, self.wl.B, self.wl.V, self.wl.V,
+                                  *self.args_tail, ctypes.byref(err))
+        if rc:
+            from mlxforge_amd import _lib
+            _lib.check(rc, err)
+
+    def run_profiled(self, out):
+        err = ctypes.c_void_p()
+        rc = self.lib.mlxf_sample_profiled(self._logits(), self.code, self.wl.B, self.wl.V,
+                                           self.wl.V, *self.args_tail, out, ctypes.byref(err))
+        if rc:
+            from mlxforge_amd import _lib
+            _lib.check(rc, err)
+
+
+def time_steps(step, torch, warmup, steps):
+    for _ in range(warmup):
+        step.run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step.run()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def stage_times(step, steps):
+    from mlxforge_amd import _lib
+    arr = (ctypes.c_float * _lib.NUM_STAGES)()
+    acc = [0.0] * _lib.NUM_STAGES
+    for _ in range(steps):
+        step.run_profiled(arr)
+        for j in range(_lib.NUM_STAGES):
+            acc[j] += arr[j]
+    return {n: acc[j] / steps for j, n in enumerate(_lib.STAGE_NAMES)}
+
+
+def cpu_baseline(wl, seconds):
+    """The CPU restatement of the reference sampler (oracle, reference-shaped:
+    full-vocab sorts for top-p and top_logprobs) on the same decode step."""
+    from oracle import oracle as orc
+    code = {"f32": orc.F32, "bf16": orc.BF16, "f16": orc.F16}[wl.dtype]
+    threads = min(os.cpu_count() or 1, 16)
+    orc.sample(wl.logits[:1], T=wl.T[:1], k=wl.k[:1], p=wl.p[:1], tlp=wl.tlp[:1], u=wl.u[:1],
+               K_max=wl.K_max, dtype=code, nthreads=1)  # load + warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        orc.sample(wl.logits, T=wl.T, k=wl.k, p=wl.p, tlp=wl.tlp, u=wl.u, K_max=wl.K_max,
+                   dtype=code, nthreads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 200:
+            break
+    rows_per_s = reps * wl.B / el
+    return {"value": round(rows_per_s, 2), "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} full decode steps of {wl.name} ({reps * wl.B} rows, "
+                      f"{el:.1f} s wall), oracle/sampler_oracle.c -O2, {threads} threads",
+            "us_per_step": round(el / reps * 1e6, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other configs' lines")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); rows are independent, so N GPUs would each run this "
+              f"same step on B/N rows with no communication.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from mlxforge_amd import _lib, workloads
+    lib = _lib.load()
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+
+    def measure(cfg, steps, warmup):
+        wl = workloads.make(cfg)
+        st = Step(wl, torch, lib)
+        ms = time_steps(st, torch, warmup, steps)
+        stages = stage_times(st, max(20, steps // 4))
+        st_hot = Step(wl, torch, lib, rotate=False)
+        ms_hot = time_steps(st_hot, torch, warmup, steps)
+        del st, st_hot
+        torch.cuda.empty_cache()
+        return wl, ms, ms_hot, stages
+
+    log(f"[bench] config C{args.config}: warmup {args.warmup}, steps {args.steps}")
+    wl, ms, ms_hot, stages = measure(args.config, args.steps, args.warmup)
+    alg = wl.algorithmic_bytes()
+    dom = max(stages, key=stages.get)
+    dom_ms = stages[dom]
+    # the dominant kernel's algorithmic bytes: the compulsory read of the logits
+    dom_bytes = wl.B * wl.V * wl.elem_size
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(wl.B / (ms * 1e-3), 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"f32": "f32", "bf16": "bf16", "f16": "f16"}[wl.dtype],
+        "data": "synthetic (seeded numpy PCG64 logits and uniforms, mlxforge_amd/workloads.py)",
+        "config": {"workload": wl.name, "B": wl.B, "V": wl.V,
+                   "logits_dtype": wl.dtype, "input_rotation": "cold (>512 MB of copies)"},
+        "us_per_step": round(ms * 1e3, 2),
+        "us_per_step_hot": round(ms_hot * 1e3, 2),
+        "achieved_GBps_step": round(alg / (ms * 1e-3) / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": dom_bytes,
+                     "kernel_us": round(dom_ms * 1e3, 2)},
+        "stage_us": {k: round(v * 1e3, 2) for k, v in stages.items()},
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    if not args.no_extra:
+        extra = {}
+        for cfg in (1, 2, 3, 4, 5):
+            if cfg == args.config:
+                continue
+            log(f"[bench] extra config C{cfg}")
+            w2, m2, mh2, s2 = measure(cfg, min(args.steps, 100), min(args.warmup, 10))
+            extra[f"C{cfg}"] = {"workload": w2.name, "us_per_step": round(m2 * 1e3, 2),
+                                "us_per_step_hot": round(mh2 * 1e3, 2),
+                                "rows_per_s": round(w2.B / (m2 * 1e-3), 1),
+                                "achieved_GBps_step": round(w2.algorithmic_bytes() / (m2 * 1e-3) / 1e9, 1),
+                                "stage_us": {k: round(v * 1e3, 2) for k, v in s2.items()}}
+        out["other_configs"] = extra
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

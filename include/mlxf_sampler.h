@@ -1,0 +1,118 @@
+/*
+ * mlxf_sampler.h -- C ABI of the MI355X (gfx950) batched token sampler.
+ *
+ * Drop-in for the decode step's sampler boundary of hvasconcelos/mlxforge:
+ *   Sampler::sample(logits, params, key[, history])  src/sample/sampler.h:51-58
+ *   Sampler::greedy(logits)                           src/sample/sampler.h:61
+ * as driven row by row by Worker::sample_rows / finalize_sample
+ * (src/runtime/worker.cpp:448-514).  One call samples every row of a [B, V]
+ * logits matrix with per-row parameters, asynchronously on the caller's HIP
+ * stream (the analogue of the reference's single mx::async_eval per step,
+ * src/runtime/worker.cpp:498).
+ *
+ * Conventions (mirroring the reference's product C ABI, src/capi/mlxforge.h:10-23):
+ *   - no C++ types cross this boundary; every pointer named d_* is device memory;
+ *   - every fallible call returns 0 on success or a negative MLXF_E* code, and if
+ *     `err` is non-NULL sets *err to a malloc'd message the caller releases with
+ *     mlxf_string_free();
+ *   - no exception ever crosses the boundary;
+ *   - the library allocates nothing in mlxf_sample / mlxf_greedy: scratch is the
+ *     caller-provided workspace (size from mlxf_sampler_workspace_size);
+ *   - calls are reentrant per stream; two calls that share a workspace must be
+ *     ordered on one stream.
+ */
+#ifndef MLXF_SAMPLER_H
+#define MLXF_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLXF_SAMPLER_ABI_VERSION 1
+
+/* Logits element types.  Production logits are fp16 (src/model/decoder_model.cpp:368). */
+#define MLXF_DTYPE_F32 0
+#define MLXF_DTYPE_BF16 1
+#define MLXF_DTYPE_F16 2
+
+/* Return codes. */
+#define MLXF_OK 0
+#define MLXF_EINVAL (-1)     /* bad argument (shape, dtype, NULL pointer, alignment) */
+#define MLXF_EWORKSPACE (-2) /* workspace NULL or smaller than mlxf_sampler_workspace_size */
+#define MLXF_EHIP (-3)       /* a HIP runtime call or kernel launch failed */
+
+/* Largest top_logprobs column count supported per call.  The reference's HTTP
+ * layer admits top_logprobs in [0, 20] (src/server/openai.cpp:150-152). */
+#define MLXF_MAX_TOP_LOGPROBS 64
+/* Largest vocabulary accepted (the nucleus mass is summed in 64-bit fixed point
+ * with 2^-42 resolution; V * 2^42 must fit in 64 bits). */
+#define MLXF_MAX_VOCAB 4194304
+
+/* ABI version of the loaded library (MLXF_SAMPLER_ABI_VERSION it was built with).
+ * No reference counterpart for the sampler itself; mirrors mlxforge_abi_version
+ * (src/capi/mlxforge.h:56). */
+int mlxf_sampler_abi_version(void);
+
+/* Bytes of device workspace mlxf_sample / mlxf_greedy need for this shape.
+ * Replaces the lazily allocated MLX temporaries of Sampler::sample
+ * (src/sample/sampler.cpp:141-166); the caller owns and reuses the buffer. */
+int mlxf_sampler_workspace_size(int B, int V, int K_max, int dtype, size_t* bytes, char** err);
+
+/* Sample one token per row.  Replaces the per-row loop of Worker::sample_rows
+ * (src/runtime/worker.cpp:453-483) calling Sampler::sample
+ * (src/sample/sampler.cpp:141-166), with the MLX random::categorical draw
+ * (src/sample/sampler.cpp:165) replaced by an inverse-CDF draw from a
+ * caller-supplied uniform per row.
+ *
+ *   d_logits        [B, row_stride] elements of `dtype`; row r is
+ *                   d_logits + r * row_stride, only its first V entries are read
+ *                   (row_stride > V covers the bucket-padded (bucket, 1, V) view,
+ *                   src/runtime/worker.cpp:533).
+ *   d_temperature   [B] fp32 or NULL (NULL: every row greedy).  A row is greedy
+ *                   when T <= 0 or T is not finite (src/sample/sampler.h:16,
+ *                   src/capi/mlxforge.cpp:55).  T is rounded to `dtype` before
+ *                   dividing (src/sample/sampler.cpp:158).
+ *   d_top_k         [B] int32 or NULL.  <= 0 disables; clamped to V
+ *                   (src/sample/sampler.cpp:159-161).  Ties at the k-th value are kept.
+ *   d_top_p         [B] fp32 or NULL.  Active when 0 < p < 1, else disabled
+ *                   (src/capi/mlxforge.cpp:57); applied after top-k.
+ *   d_top_logprobs  [B] int32 or NULL (NULL: all -1).  -1: no logprob work for the
+ *                   row (out_logprobs[r] = NaN); 0: chosen-token logprob only;
+ *                   N > 0: also the min(N, K_max, V) most likely alternatives
+ *                   (src/sample/sampler.h:24-29, src/runtime/worker.cpp:477).
+ *   d_uniforms      [B] fp32 in [0, 1), one per row; may be NULL only when
+ *                   d_temperature is NULL.  Values outside [0, 1) are clamped.
+ *   d_out_ids       [B] int32 sampled token ids.
+ *   d_out_logprobs  [B] fp32 or NULL: log_softmax of the unscaled logits at the
+ *                   chosen id (src/sample/sampler.cpp:146-154).
+ *   d_out_top_ids, d_out_top_logprobs
+ *                   [B, K_max] (NULL allowed when K_max == 0): alternatives in
+ *                   descending logprob order, ties by ascending id; unused
+ *                   columns hold id -1 and logprob -inf.
+ *   d_workspace     >= mlxf_sampler_workspace_size(B, V, K_max, dtype) bytes,
+ *                   256-byte aligned.
+ *   stream          hipStream_t (NULL = the default stream).
+ */
+int mlxf_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                const int32_t* d_top_logprobs, const float* d_uniforms, int32_t* d_out_ids,
+                float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
+                int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err);
+
+/* argmax over each row, lowest index on ties: Sampler::greedy
+ * (src/sample/sampler.h:61, src/sample/sampler.cpp:59-61). */
+int mlxf_greedy(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                int32_t* d_out_ids, void* d_workspace, size_t workspace_bytes, void* stream,
+                char** err);
+
+/* Release a message returned through `err` (mirrors mlxforge_string_free). */
+void mlxf_string_free(char* s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLXF_SAMPLER_H */

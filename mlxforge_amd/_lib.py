@@ -1,0 +1,87 @@
+"""ctypes binding of libmlxf_sampler.so (the C ABI in include/mlxf_sampler.h).
+
+The library is loaded from this package directory only.  There is no fallback:
+if the HIP library is missing or fails to load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmlxf_sampler.so")
+
+DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
+OK, EINVAL, EWORKSPACE, EHIP = 0, -1, -2, -3
+MAX_TOP_LOGPROBS = 64
+MAX_VOCAB = 4194304
+
+# Every function include/*.h declares.
+SYMBOLS = (
+    "mlxf_sampler_abi_version",
+    "mlxf_sampler_workspace_size",
+    "mlxf_sample",
+    "mlxf_greedy",
+    "mlxf_string_free",
+    "mlxf_sample_profiled",
+)
+NUM_STAGES = 5
+STAGE_NAMES = ("k_scan", "k_plan", "k_extract", "k_select", "k_draw")
+
+_lib = None
+
+
+class SamplerError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{msg} (code {code})")
+        self.code = code
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I, I64, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+    PP = ctypes.POINTER(ctypes.c_void_p)
+    L.mlxf_sampler_abi_version.argtypes = []
+    L.mlxf_sampler_abi_version.restype = I
+    L.mlxf_sampler_workspace_size.argtypes = [I, I, I, I, ctypes.POINTER(SZ), PP]
+    L.mlxf_sampler_workspace_size.restype = I
+    L.mlxf_sample.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, I, P, SZ, P, PP]
+    L.mlxf_sample.restype = I
+    L.mlxf_greedy.argtypes = [P, I, I, I, I64, P, P, SZ, P, PP]
+    L.mlxf_greedy.restype = I
+    L.mlxf_sample_profiled.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, I, P, SZ, P,
+                                       ctypes.POINTER(ctypes.c_float), PP]
+    L.mlxf_sample_profiled.restype = I
+    L.mlxf_string_free.argtypes = [P]
+    L.mlxf_string_free.restype = None
+    _lib = L
+    return L
+
+
+def check(rc: int, err: ctypes.c_void_p) -> None:
+    """Raise SamplerError for a negative return code, freeing the message."""
+    if rc == OK:
+        return
+    msg = "mlxf: error"
+    if err.value:
+        msg = ctypes.string_at(err.value).decode("utf-8", "replace")
+        load().mlxf_string_free(err)
+    raise SamplerError(rc, msg)
+
+
+def abi_version() -> int:
+    return load().mlxf_sampler_abi_version()
+
+
+def workspace_size(B: int, V: int, K_max: int, dtype: int) -> int:
+    n = ctypes.c_size_t(0)
+    err = ctypes.c_void_p()
+    rc = load().mlxf_sampler_workspace_size(B, V, K_max, dtype, ctypes.byref(n), ctypes.byref(err))
+    check(rc, err)
+    return n.value

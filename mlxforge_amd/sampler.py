@@ -1,0 +1,160 @@
+"""Host-side mirror of mlxforge's sampler interface over the HIP C ABI.
+
+* ``SamplingParams`` / ``SampleResult`` mirror src/sample/sampler.h:15-45.
+* ``sample_rows`` is the decode-step boundary: what Worker::sample_rows +
+  finalize_sample (src/runtime/worker.cpp:448-514) compute, as one launch
+  sequence over all rows with per-row parameter arrays.
+* ``Sampler.sample`` / ``Sampler.greedy`` mirror the per-call static API
+  (src/sample/sampler.h:51-61) with one parameter set for every row.
+
+PyTorch provides device memory and the current stream only; every result is
+computed by libmlxf_sampler.so.  The MLX PRNG key of the reference is replaced
+by one caller-supplied uniform per row (the inverse-CDF draw of the C ABI).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16,
+           torch.float16: _lib.DTYPE_F16}
+
+
+@dataclass
+class SamplingParams:
+    """Per-request knobs with the reference's sentinels (src/sample/sampler.h:15-36)."""
+    temperature: float = 1.0   # <= 0 => greedy
+    top_k: int = 0             # <= 0 => disabled
+    top_p: float = 1.0         # >= 1 => disabled
+    min_p: float = 0.0         # <= 0 => disabled (not on the GPU path yet)
+    repetition_penalty: float = 1.0
+    frequency_penalty: float = 0.0
+    presence_penalty: float = 0.0
+    seed: int = 0
+    top_logprobs: int = -1     # -1 off, 0 chosen only, N > 0 alternatives
+
+    def has_penalties(self) -> bool:
+        return (self.repetition_penalty != 1.0 or self.frequency_penalty != 0.0
+                or self.presence_penalty != 0.0)
+
+
+@dataclass
+class SampleResult:
+    """src/sample/sampler.h:38-45 (logprobs are fp32 for every input dtype)."""
+    tokens: torch.Tensor         # (B,) int32
+    logprobs: torch.Tensor       # (B,) fp32
+    top_tokens: torch.Tensor     # (B, K) int32
+    top_logprobs: torch.Tensor   # (B, K) fp32
+
+
+class Workspace:
+    """Caller-owned device scratch, grown on demand and reused across steps."""
+
+    def __init__(self, device=None):
+        self.device = torch.device(device) if device is not None else torch.device("cuda")
+        self.buf = None
+
+    def get(self, B: int, V: int, K_max: int, dtype: int) -> torch.Tensor:
+        need = _lib.workspace_size(B, V, K_max, dtype)
+        if self.buf is None or self.buf.numel() < need:
+            # 256-byte alignment: torch's caching allocator returns >= 512-byte aligned blocks.
+            self.buf = torch.empty(max(need, 256), dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+_default_ws: dict = {}
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _param(x, B, dtype, device):
+    if x is None:
+        return None
+    if not torch.is_tensor(x):
+        return torch.full((B,), x, dtype=dtype, device=device)
+    if x.dtype != dtype or x.device != device or not x.is_contiguous() or x.numel() != B:
+        raise ValueError(f"per-row parameter must be a contiguous {dtype} tensor of {B} on {device}")
+    return x
+
+
+def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
+                top_logprobs=None, uniforms=None, K_max: int = 0, V: int | None = None,
+                workspace: Workspace | None = None) -> SampleResult:
+    """Sample one token per row of a [B, row_stride] logits view.
+
+    Per-row parameters are device tensors of length B (or Python scalars, which
+    are broadcast); None disables the knob (temperature None = all greedy).
+    """
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be a [B, V] view with unit stride along V")
+    if logits.dtype not in _DTYPES:
+        raise ValueError(f"unsupported logits dtype {logits.dtype}")
+    dev = logits.device
+    B = logits.shape[0]
+    V = logits.shape[1] if V is None else V
+    T = _param(temperature, B, torch.float32, dev)
+    k = _param(top_k, B, torch.int32, dev)
+    p = _param(top_p, B, torch.float32, dev)
+    tlp = _param(top_logprobs, B, torch.int32, dev)
+    u = _param(uniforms, B, torch.float32, dev)
+    ids = torch.empty(B, dtype=torch.int32, device=dev)
+    lp = torch.empty(B, dtype=torch.float32, device=dev)
+    top_ids = torch.empty((B, K_max), dtype=torch.int32, device=dev)
+    top_lp = torch.empty((B, K_max), dtype=torch.float32, device=dev)
+    code = _DTYPES[logits.dtype]
+    if workspace is None:
+        workspace = _default_ws.setdefault(dev, Workspace(dev))
+    ws = workspace.get(B, V, K_max, code)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    err = ctypes.c_void_p()
+    rc = _lib.load().mlxf_sample(
+        _ptr(logits), code, B, V, logits.stride(0), _ptr(T), _ptr(k), _ptr(p), _ptr(tlp), _ptr(u),
+        _ptr(ids), _ptr(lp), _ptr(top_ids) if K_max else None, _ptr(top_lp) if K_max else None,
+        K_max, _ptr(ws), ws.numel(), ctypes.c_void_p(stream), ctypes.byref(err))
+    _lib.check(rc, err)
+    return SampleResult(ids, lp, top_ids, top_lp)
+
+
+def greedy(logits: torch.Tensor, workspace: Workspace | None = None) -> torch.Tensor:
+    """argmax per row, lowest index on ties (src/sample/sampler.cpp:59-61)."""
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be a [B, V] view with unit stride along V")
+    dev = logits.device
+    B, V = logits.shape
+    code = _DTYPES[logits.dtype]
+    ids = torch.empty(B, dtype=torch.int32, device=dev)
+    if workspace is None:
+        workspace = _default_ws.setdefault(dev, Workspace(dev))
+    ws = workspace.get(B, V, 0, code)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    err = ctypes.c_void_p()
+    rc = _lib.load().mlxf_greedy(_ptr(logits), code, B, V, logits.stride(0), _ptr(ids), _ptr(ws),
+                                 ws.numel(), ctypes.c_void_p(stream), ctypes.byref(err))
+    _lib.check(rc, err)
+    return ids
+
+
+class Sampler:
+    """Per-call API of src/sample/sampler.h:47-79, one parameter set for all rows."""
+
+    @staticmethod
+    def sample(logits: torch.Tensor, params: SamplingParams, uniforms) -> SampleResult:
+        if params.min_p > 0.0 or params.has_penalties():
+            raise NotImplementedError("min_p and penalties are not on the GPU path yet")
+        B, V = logits.shape
+        K = min(max(params.top_logprobs, 0), V)
+        # Sampler::sample always returns the chosen-token logprob (sampler.cpp:151-154).
+        res = sample_rows(logits, temperature=params.temperature, top_k=params.top_k,
+                          top_p=params.top_p, top_logprobs=max(params.top_logprobs, 0),
+                          uniforms=uniforms, K_max=K)
+        return res
+
+    @staticmethod
+    def greedy(logits: torch.Tensor) -> torch.Tensor:
+        return greedy(logits)

@@ -1,0 +1,137 @@
+"""ctypes binding of the CPU oracle (oracle/sampler_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
+bench.py's cpu_baseline leg, always as the checker.  The product package
+(mlxforge_amd) never imports this module.
+
+Arguments mirror the product's C ABI ``mlxf_sample`` (include/mlxf_sampler.h)
+with host numpy arrays in place of device pointers.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, BF16, F16 = 0, 1, 2
+FLAG_GREEDY, FLAG_TOPP_AMBIG, FLAG_DRAW_AMBIG = 1, 2, 4
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE] + (["-B"] if force else []), check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        L.orc_sample.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_long,
+                                 P, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, ctypes.c_int]
+        L.orc_sample.restype = ctypes.c_int
+        L.orc_filter_row.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                     ctypes.c_int, ctypes.c_float, ctypes.c_float, P]
+        L.orc_filter_row.restype = ctypes.c_int
+        L.orc_round_bf16.argtypes = [ctypes.c_float]
+        L.orc_round_bf16.restype = ctypes.c_float
+        L.orc_round_f16.argtypes = [ctypes.c_float]
+        L.orc_round_f16.restype = ctypes.c_float
+        L.orc_greedy_row.argtypes = [P, ctypes.c_int]
+        L.orc_greedy_row.restype = ctypes.c_int
+        L.orc_lse_row.argtypes = [P, ctypes.c_int]
+        L.orc_lse_row.restype = ctypes.c_double
+        L.orc_draw_row.argtypes = [P, ctypes.c_int, ctypes.c_float, P]
+        L.orc_draw_row.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def dtype_code(arr: np.ndarray, dtype: int | None = None) -> int:
+    if dtype is not None:
+        return dtype
+    if arr.dtype == np.float32:
+        return F32
+    if arr.dtype == np.float16:
+        return F16
+    raise ValueError("pass dtype=BF16 explicitly for uint16 bf16 bit patterns")
+
+
+def sample(logits: np.ndarray, T=None, k=None, p=None, tlp=None, u=None, K_max: int = 0,
+           dtype: int | None = None, V: int | None = None, nthreads: int | None = None):
+    """Run the oracle over a [B, row_stride] host array.
+
+    For bf16, pass the raw uint16 bit patterns with dtype=BF16.
+    Returns dict(ids, lp, top_ids, top_lp, flags, margins).
+    """
+    logits = np.ascontiguousarray(logits)
+    B, stride = logits.shape
+    V = stride if V is None else V
+    code = dtype_code(logits, dtype)
+    f = lambda a, t: None if a is None else np.ascontiguousarray(np.asarray(a, dtype=t).reshape(B))
+    T, p, u = f(T, np.float32), f(p, np.float32), f(u, np.float32)
+    k, tlp = f(k, np.int32), f(tlp, np.int32)
+    ids = np.zeros(B, np.int32)
+    lp = np.zeros(B, np.float32)
+    top_ids = np.zeros((B, max(K_max, 1)), np.int32)
+    top_lp = np.zeros((B, max(K_max, 1)), np.float32)
+    flags = np.zeros(B, np.int32)
+    margins = np.zeros((B, 2), np.float64)
+    if nthreads is None:
+        nthreads = min(os.cpu_count() or 1, 16)
+    rc = lib().orc_sample(_ptr(logits), code, B, V, stride, _ptr(T), _ptr(k), _ptr(p), _ptr(tlp),
+                          _ptr(u), _ptr(ids), _ptr(lp), _ptr(top_ids), _ptr(top_lp), K_max,
+                          _ptr(flags), _ptr(margins), nthreads)
+    if rc != 0:
+        raise ValueError("orc_sample rejected its arguments")
+    return dict(ids=ids, lp=lp, top_ids=top_ids[:, :K_max], top_lp=top_lp[:, :K_max],
+                flags=flags, margins=margins)
+
+
+def filter_row(z, T=0.0, k=0, p=1.0, min_p=0.0, dtype: int = F32) -> np.ndarray:
+    """z' after temperature / top-k / top-p / min-p (dropped entries are -inf)."""
+    z = np.ascontiguousarray(np.asarray(z, np.float32))
+    out = np.zeros_like(z)
+    rc = lib().orc_filter_row(_ptr(z), z.size, dtype, T, k, p, min_p, _ptr(out))
+    assert rc == 0
+    return out
+
+
+def greedy_row(z) -> int:
+    z = np.ascontiguousarray(np.asarray(z, np.float32))
+    return lib().orc_greedy_row(_ptr(z), z.size)
+
+
+def lse_row(z) -> float:
+    z = np.ascontiguousarray(np.asarray(z, np.float32))
+    return lib().orc_lse_row(_ptr(z), z.size)
+
+
+def draw_row(zs, u: float):
+    zs = np.ascontiguousarray(np.asarray(zs, np.float32))
+    m = np.zeros(1, np.float64)
+    i = lib().orc_draw_row(_ptr(zs), zs.size, u, _ptr(m))
+    return i, float(m[0])
+
+
+def round_bf16(x: float) -> float:
+    return lib().orc_round_bf16(x)
+
+
+def round_f16(x: float) -> float:
+    return lib().orc_round_f16(x)

@@ -1,0 +1,84 @@
+"""The C-ABI library loads and exports every symbol include/mlxf_sampler.h
+declares; host-side argument checks answer without touching a GPU."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from mlxforge_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mlxf_sampler.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
+
+
+def declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(mlxf_\w+)\s*\(", text))
+    return sorted(names)
+
+
+def test_header_matches_binding_list():
+    assert declared_functions() == sorted(_lib.SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+
+
+def test_abi_version():
+    text = open(HEADER).read()
+    want = int(re.search(r"#define MLXF_SAMPLER_ABI_VERSION (\d+)", text).group(1))
+    assert _lib.abi_version() == want
+
+
+def test_workspace_size_is_positive_and_monotone():
+    a = _lib.workspace_size(8, 151936, 0, _lib.DTYPE_BF16)
+    b = _lib.workspace_size(64, 151936, 20, _lib.DTYPE_F32)
+    assert 0 < a < b
+
+
+@pytest.mark.parametrize("args", [
+    (-1, 10, 0, 0), (1, 0, 0, 0), (1, 10, 65, 0), (1, 10, 0, 7), (1, _lib.MAX_VOCAB + 1, 0, 0)])
+def test_workspace_size_rejects_bad_shapes(args):
+    with pytest.raises(_lib.SamplerError) as ei:
+        _lib.workspace_size(*args)
+    assert ei.value.code == _lib.EINVAL and "mlxf" in str(ei.value)
+
+
+def test_sample_argument_errors_need_no_gpu():
+    L = _lib.load()
+    err = ctypes.c_void_p()
+    fake = ctypes.c_void_p(0x1000)
+    # NULL logits
+    rc = L.mlxf_sample(None, 0, 1, 10, 10, None, None, None, None, None, fake, None, None, None,
+                       0, fake, 1 << 20, None, ctypes.byref(err))
+    assert rc == _lib.EINVAL and err.value
+    L.mlxf_string_free(err)
+    # row_stride < V
+    err = ctypes.c_void_p()
+    rc = L.mlxf_sample(fake, 0, 1, 10, 9, None, None, None, None, None, fake, None, None, None,
+                       0, fake, 1 << 20, None, ctypes.byref(err))
+    assert rc == _lib.EINVAL
+    L.mlxf_string_free(err)
+    # temperature without uniforms
+    err = ctypes.c_void_p()
+    rc = L.mlxf_sample(fake, 0, 1, 10, 10, fake, None, None, None, None, fake, None, None, None,
+                       0, fake, 1 << 20, None, ctypes.byref(err))
+    assert rc == _lib.EINVAL
+    L.mlxf_string_free(err)
+    # workspace too small
+    err = ctypes.c_void_p()
+    rc = L.mlxf_sample(fake, 0, 1, 10, 10, None, None, None, None, None, fake, None, None, None,
+                       0, fake, 16, None, ctypes.byref(err))
+    assert rc == _lib.EWORKSPACE
+    L.mlxf_string_free(err)
+    # B == 0 is a no-op success; a NULL err pointer is allowed
+    assert L.mlxf_sample(None, 0, 0, 10, 10, None, None, None, None, None, None, None, None, None,
+                         0, None, 0, None, None) == 0

@@ -1,0 +1,228 @@
+"""GPU parity: the HIP sampler (through the C ABI) against the CPU oracle.
+
+Covers the five benchmark configurations at full size, the reference's own
+known answers and real-logit fixtures, and the edge cases the reference's
+tests and C ABI sanitisation imply (ties, k > V, degenerate rows, NaN / inf,
+padded and unaligned rows, out-of-range parameters).
+"""
+import glob
+import os
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():  # pragma: no cover - collected on CPU-only hosts too
+    pytest.skip("no GPU", allow_module_level=True)
+
+from mlxforge_amd import sampler, workloads  # noqa: E402
+from tests import gpu_util as gu  # noqa: E402
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_config_parity(cfg):
+    wl = workloads.make(cfg)
+    say(f"[parity] config {cfg}: {wl.name}")
+    dev = gu.to_device(wl.logits, wl.dtype)
+    g = gu.gpu_sample(dev, T=wl.T, k=wl.k, p=wl.p, tlp=wl.tlp, u=wl.u, K_max=wl.K_max)
+    o = gu.oracle_sample(wl.logits, wl.dtype, T=wl.T, k=wl.k, p=wl.p, tlp=wl.tlp, u=wl.u,
+                         K_max=wl.K_max)
+    rep = gu.compare(g, o, wl.dtype, tlp=wl.tlp, label=f"C{cfg}")
+    say(f"[parity] config {cfg}: {rep}")
+    # determinism: a second run is bit-identical
+    g2 = gu.gpu_sample(dev, T=wl.T, k=wl.k, p=wl.p, tlp=wl.tlp, u=wl.u, K_max=wl.K_max)
+    assert np.array_equal(g["ids"], g2["ids"])
+    assert np.array_equal(g["lp"].view(np.uint32), g2["lp"].view(np.uint32))
+
+
+FIXTURES = sorted(glob.glob(os.path.join(HERE, "golden", "fixtures", "*")))
+
+
+@pytest.mark.parametrize("fx", FIXTURES, ids=[os.path.basename(f) for f in FIXTURES])
+def test_real_logit_fixture_greedy(fx):
+    logits = np.load(os.path.join(fx, "logits_last.npy"), allow_pickle=False)
+    want = np.load(os.path.join(fx, "argmax.npy"), allow_pickle=False)
+    dev = gu.to_device(logits, "f16")
+    assert sampler.greedy(dev).cpu().numpy().tolist() == want.tolist()
+    g = gu.gpu_sample(dev, tlp=[5], K_max=5)
+    o = gu.oracle_sample(logits, "f16", tlp=[5], K_max=5)
+    assert g["ids"].tolist() == want.tolist()
+    gu.compare(g, o, "f16", tlp=[5], label=os.path.basename(fx))
+
+
+def _rows(z):
+    return torch.tensor(np.asarray(z, np.float32), device="cuda:0")
+
+
+def test_known_answers():  # tests/sample/sampler_test.cpp
+    # greedy (:41-44)
+    assert sampler.greedy(_rows([[1, 3, 2], [5, 0, -1]])).tolist() == [1, 0]
+    # T=0 is greedy (:46-52)
+    P = sampler.SamplingParams
+    r = sampler.Sampler.sample(_rows([[0.2, 0.9, 0.1, 0.4]]), P(temperature=0.0), [0.7])
+    assert r.tokens.tolist() == [1]
+    # ranked alternatives (:163-181)
+    r = sampler.Sampler.sample(_rows([[1, 4, 2, 3, 0]]), P(temperature=0.0, top_logprobs=3), [0.0])
+    assert r.top_tokens.tolist() == [[1, 3, 2]]
+    assert r.tokens.tolist() == [1] and abs(r.logprobs.item() - r.top_logprobs[0, 0].item()) < 1e-6
+    # full top-k normalised (:183-192)
+    r = sampler.Sampler.sample(_rows([[0.5, 1.5, -0.5, 2.0]]), P(temperature=0.0, top_logprobs=4),
+                               [0.0])
+    assert abs(torch.exp(r.top_logprobs.double()).sum().item() - 1.0) < 1e-6
+    # pre-temperature ordering (:194-203)
+    r = sampler.Sampler.sample(_rows([[1, 4, 2, 3]]), P(temperature=0.8, top_logprobs=2), [0.5])
+    assert r.top_tokens.tolist() == [[1, 3]]
+    # top-p keeps {0,1} of probs (.5,.3,.15,.05) at p=.7 (:63-74): every u lands in them
+    lg = np.log(np.array([0.5, 0.3, 0.15, 0.05], np.float32))
+    for u in np.linspace(0.0, 0.999, 37):
+        r = sampler.Sampler.sample(_rows([lg]), P(temperature=1.0, top_p=0.7), [float(u)])
+        assert r.tokens.item() in (0, 1)
+    # top-k=2 of distinct (5,1,4,2,3) keeps {0,2} (:54-61)
+    for u in np.linspace(0.0, 0.999, 37):
+        r = sampler.Sampler.sample(_rows([[5, 1, 4, 2, 3]]), P(temperature=1.0, top_k=2), [float(u)])
+        assert r.tokens.item() in (0, 2)
+    # same uniforms reproduce, different diverge (:126-134)
+    z = torch.zeros(64, 16, device="cuda:0")
+    u1 = torch.rand(64, generator=torch.Generator().manual_seed(42)).cuda()
+    u2 = torch.rand(64, generator=torch.Generator().manual_seed(7)).cuda()
+    a1 = sampler.Sampler.sample(z, P(), u1).tokens
+    a2 = sampler.Sampler.sample(z, P(), u1).tokens
+    b = sampler.Sampler.sample(z, P(), u2).tokens
+    assert torch.equal(a1, a2) and not torch.equal(a1, b)
+    assert torch.equal(a1.long(), (u1.double() * 16).floor().long())
+
+
+def _random_case(rng, B, V, dtype):
+    kind = rng.integers(0, 4)
+    if kind == 0:
+        z = rng.standard_normal((B, V)).astype(np.float32) * rng.uniform(0.05, 6)
+    elif kind == 1:
+        z = rng.integers(-3, 4, (B, V)).astype(np.float32)  # heavy ties
+    elif kind == 2:
+        z = (rng.gumbel(size=(B, V)) * 2).astype(np.float32)
+    else:
+        z = rng.standard_normal((B, V)).astype(np.float32) * 0.01
+    if dtype == "bf16":
+        host = workloads.to_bf16_bits(z)
+    elif dtype == "f16":
+        host = z.astype(np.float16)
+    else:
+        host = z
+    T = np.where(rng.random(B) < 0.2, 0.0, rng.uniform(0.2, 2.0, B)).astype(np.float32)
+    k = np.where(rng.random(B) < 0.5, rng.integers(1, V + 5, B), 0).astype(np.int32)
+    p = np.where(rng.random(B) < 0.5, rng.uniform(0.05, 0.999, B), 1.0).astype(np.float32)
+    tlp = rng.integers(-1, 6, B).astype(np.int32)
+    u = rng.random(B).astype(np.float32)
+    return host, T, k, p, tlp, u
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("V", [1, 3, 7, 8, 9, 100, 2047, 2048, 2049, 5000, 33000])
+def test_random_shapes(dtype, V):
+    rng = np.random.default_rng(1000 + V + 7 * len(dtype))
+    B = 1 if V > 20000 else 5
+    host, T, k, p, tlp, u = _random_case(rng, B, V, dtype)
+    K_max = min(5, V)
+    say(f"[parity] random dtype={dtype} V={V} B={B}")
+    g = gu.gpu_sample(gu.to_device(host, dtype), T=T, k=k, p=p, tlp=tlp, u=u, K_max=K_max)
+    o = gu.oracle_sample(host, dtype, T=T, k=k, p=p, tlp=tlp, u=u, K_max=K_max)
+    gu.compare(g, o, dtype, tlp=tlp, label=f"random {dtype} V={V}")
+
+
+def test_padded_and_unaligned_rows():
+    rng = np.random.default_rng(5)
+    B, V = 6, 3001
+    full = rng.standard_normal((B, V + 5)).astype(np.float32) * 3
+    dev_full = torch.from_numpy(full).cuda()
+    T = np.full(B, 0.9, np.float32)
+    p = np.full(B, 0.8, np.float32)
+    u = rng.random(B).astype(np.float32)
+    tlp = np.full(B, 3, np.int32)
+    # row_stride > V (bucket padding) and a 4-byte-offset view (scalar load path)
+    for off in (0, 1):
+        view = dev_full[:, off:off + V]
+        host = np.ascontiguousarray(full[:, off:off + V])
+        g = gu.gpu_sample(view, T=T, p=p, tlp=tlp, u=u, K_max=3)
+        o = gu.oracle_sample(host, "f32", T=T, p=p, tlp=tlp, u=u, K_max=3)
+        gu.compare(g, o, "f32", tlp=tlp, label=f"stride off={off}")
+
+
+def test_degenerate_rows():
+    V = 3000
+    z = np.zeros((6, V), np.float32)
+    z[0] = -np.inf                       # all masked
+    z[1, ::7] = np.nan                   # NaN reads as -inf
+    z[2, 5] = np.inf
+    z[2, 2000] = np.inf                  # two +inf entries share the mass
+    z[3] = 1.0                           # constant row: every entry ties
+    z[4, 1234] = 7.0
+    z[4, 2345] = 7.0                     # duplicate maximum
+    z[5] = np.linspace(-5, 5, V, dtype=np.float32)
+    host = z
+    T = np.array([1.0, 1.0, 1.0, 1.0, 0.0, 1.0], np.float32)
+    k = np.array([0, 3, 0, 10, 0, 1], np.int32)
+    p = np.array([0.5, 0.9, 1.0, 0.3, 1.0, 1.0], np.float32)
+    tlp = np.array([0, 2, 2, 4, 3, 1], np.int32)
+    for u in (0.0, 0.37, 0.999999):
+        uu = np.full(6, u, np.float32)
+        g = gu.gpu_sample(gu.to_device(host, "f32"), T=T, k=k, p=p, tlp=tlp, u=uu, K_max=4)
+        o = gu.oracle_sample(host, "f32", T=T, k=k, p=p, tlp=tlp, u=uu, K_max=4)
+        gu.compare(g, o, "f32", tlp=tlp, label=f"degenerate u={u}")
+    assert g["ids"][4] == 1234
+
+
+def test_parameter_sanitisation():
+    rng = np.random.default_rng(9)
+    V = 4000
+    z = (rng.standard_normal((8, V)) * 2).astype(np.float32)
+    T = np.array([np.nan, np.inf, -1.0, 0.0, 1e-30, 1.0, 1.0, 1.0], np.float32)
+    k = np.array([0, 0, 0, 0, 0, 10 ** 6, -5, 1], np.int32)
+    p = np.array([1.0, 1.0, 1.0, 1.0, 1.0, 1e-7, 1.5, np.nan], np.float32)
+    u = np.array([0.5, 0.5, 0.5, 0.5, 0.5, -3.0, 7.0, np.nan], np.float32)
+    tlp = np.zeros(8, np.int32)
+    g = gu.gpu_sample(gu.to_device(z, "f32"), T=T, k=k, p=p, tlp=tlp, u=u)
+    o = gu.oracle_sample(z, "f32", T=T, k=k, p=p, tlp=tlp, u=u)
+    gu.compare(g, o, "f32", tlp=tlp, label="sanitisation")
+
+
+def test_large_candidate_sets():
+    # top-p over a flat row: the boundary bin holds far more candidates than LDS
+    rng = np.random.default_rng(11)
+    V = 60000
+    z = np.zeros((3, V), np.float32)
+    z[1] = rng.integers(0, 2, V).astype(np.float32) * 1e-3
+    z[2] = (rng.standard_normal(V) * 1e-4).astype(np.float32)
+    T = np.ones(3, np.float32)
+    p = np.array([0.5, 0.7, 0.95], np.float32)
+    k = np.array([0, 40000, 0], np.int32)
+    u = np.array([0.3, 0.6, 0.9], np.float32)
+    for dtype in ("f32", "bf16"):
+        host = z if dtype == "f32" else workloads.to_bf16_bits(z)
+        g = gu.gpu_sample(gu.to_device(host, dtype), T=T, k=k, p=p, u=u)
+        o = gu.oracle_sample(host, dtype, T=T, k=k, p=p, u=u)
+        gu.compare(g, o, dtype, label=f"large candidates {dtype}")
+
+
+def test_workspace_errors():
+    from mlxforge_amd import _lib
+    z = torch.zeros(2, 100, device="cuda:0")
+    ws = sampler.Workspace("cuda:0")
+    ws.buf = torch.empty(16, dtype=torch.uint8, device="cuda:0")
+    ids = torch.empty(2, dtype=torch.int32, device="cuda:0")
+    import ctypes
+    err = ctypes.c_void_p()
+    rc = _lib.load().mlxf_greedy(ctypes.c_void_p(z.data_ptr()), 0, 2, 100, 100,
+                                 ctypes.c_void_p(ids.data_ptr()), ctypes.c_void_p(ws.buf.data_ptr()),
+                                 16, None, ctypes.byref(err))
+    assert rc == _lib.EWORKSPACE
+    _lib.load().mlxf_string_free(err)

@@ -1,0 +1,290 @@
+"""Pins the CPU oracle (oracle/sampler_oracle.c) before it is trusted as the checker.
+
+Every case either comes from the reference's own tests / fixtures
+(tests/sample/sampler_test.cpp, reference/fixtures*/), or checks the oracle
+against an independent formulation (numpy/scipy/torch, brute force, closed
+forms) chosen so that a plausible slip (strict vs non-strict cutoff, wrong tie
+order, dropped normalisation, off-by-one k) fails.
+"""
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+from scipy.special import logsumexp
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+F32, BF16, F16 = 0, 1, 2
+
+
+def log(x):
+    return np.log(np.asarray(x, np.float32)).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Known answers ported from tests/sample/sampler_test.cpp
+# ---------------------------------------------------------------------------
+
+def test_greedy_returns_argmax(orc):  # sampler_test.cpp:41-44
+    z = np.array([[1.0, 3.0, 2.0], [5.0, 0.0, -1.0]], np.float32)
+    r = orc.sample(z)
+    assert r["ids"].tolist() == [1, 0]
+
+
+def test_temperature_zero_is_greedy(orc):  # :46-52
+    z = np.array([[0.2, 0.9, 0.1, 0.4]], np.float32)
+    r = orc.sample(z, T=[0.0], u=[0.7])
+    assert r["ids"].tolist() == [orc.greedy_row(z[0])]
+
+
+def test_top_k_keeps_exactly_k(orc):  # :54-61
+    f = orc.filter_row([5.0, 1.0, 4.0, 2.0, 3.0], k=2)
+    assert np.isfinite(f).sum() == 2
+    assert np.isfinite(f[0]) and np.isfinite(f[2]) and not np.isfinite(f[1])
+
+
+def test_top_p_smallest_prefix(orc):  # :63-74
+    f = orc.filter_row(log([0.5, 0.3, 0.15, 0.05]), p=0.7)
+    assert np.isfinite(f).tolist() == [True, True, False, False]
+
+
+def test_top_p_is_strict_on_prior_mass(orc):
+    # prior mass of the 3rd token is exactly 0.8 (in float64 of the float32 logs,
+    # up to rounding); p just above keeps it, p at 0.79 does not.
+    lg = log([0.5, 0.3, 0.15, 0.05])
+    assert np.isfinite(orc.filter_row(lg, p=0.79)).sum() == 2
+    assert np.isfinite(orc.filter_row(lg, p=0.81)).sum() == 3
+    assert np.isfinite(orc.filter_row(lg, p=0.96)).sum() == 4
+
+
+def test_min_p(orc):  # :76-87
+    f = orc.filter_row(log([0.5, 0.3, 0.15, 0.05]), min_p=0.4)
+    assert np.isfinite(f).tolist() == [True, True, False, False]
+
+
+def test_same_uniforms_reproduce_different_diverge(orc):  # :126-134 (key -> uniforms)
+    z = np.zeros((64, 16), np.float32)
+    rng = np.random.default_rng(42)
+    u1 = rng.random(64, dtype=np.float32)
+    u2 = np.random.default_rng(7).random(64, dtype=np.float32)
+    a1 = orc.sample(z, T=np.ones(64), u=u1)["ids"]
+    a2 = orc.sample(z, T=np.ones(64), u=u1)["ids"]
+    b = orc.sample(z, T=np.ones(64), u=u2)["ids"]
+    assert (a1 == a2).all() and (a1 != b).any()
+    # uniform row: inverse CDF picks floor(u * 16)
+    assert (a1 == np.floor(u1.astype(np.float64) * 16).astype(int)).all()
+
+
+def test_batched_shapes_and_logprob_nonpositive(orc):  # :136-142
+    z = np.array([[1.0, 2.0, 3.0], [3.0, 2.0, 1.0]], np.float32)
+    r = orc.sample(z, T=[1.0, 1.0], u=[0.3, 0.9], tlp=[0, 0])
+    assert r["ids"].shape == (2,) and r["lp"].shape == (2,)
+    assert (r["lp"] <= 0).all()
+
+
+def test_top_logprobs_off_and_zero(orc):  # :144-161
+    z = np.array([[1.0, 2.0, 3.0]], np.float32)
+    r = orc.sample(z, T=[0.0], tlp=[-1], K_max=0)
+    assert r["top_ids"].shape == (1, 0) and np.isnan(r["lp"][0])
+    r = orc.sample(z, T=[0.0], tlp=[0], K_max=0)
+    assert r["ids"].tolist() == [2] and r["lp"][0] <= 0
+
+
+def test_top_logprobs_ranked(orc):  # :163-181
+    z = np.array([[1.0, 4.0, 2.0, 3.0, 0.0]], np.float32)
+    r = orc.sample(z, T=[0.0], tlp=[3], K_max=3)
+    assert r["top_ids"][0].tolist() == [1, 3, 2]
+    lp = r["top_lp"][0]
+    assert lp[0] >= lp[1] >= lp[2] and (lp <= 0).all()
+    assert r["ids"].tolist() == [1] and r["lp"][0] == pytest.approx(lp[0])
+
+
+def test_full_top_k_is_normalised(orc):  # :183-192
+    z = np.array([[0.5, 1.5, -0.5, 2.0]], np.float32)
+    r = orc.sample(z, T=[0.0], tlp=[4], K_max=4)
+    assert np.exp(r["top_lp"][0].astype(np.float64)).sum() == pytest.approx(1.0, abs=1e-6)
+
+
+def test_top_logprobs_pre_temperature(orc):  # :194-203
+    z = np.array([[1.0, 4.0, 2.0, 3.0]], np.float32)
+    r = orc.sample(z, T=[0.8], tlp=[2], K_max=2, u=[0.5])
+    assert r["top_ids"][0].tolist() == [1, 3]
+
+
+# ---------------------------------------------------------------------------
+# Real-logit known answers (reference/fixtures*/argmax.npy, fp16 logits)
+# ---------------------------------------------------------------------------
+
+FIXTURES = sorted(glob.glob(os.path.join(HERE, "golden", "fixtures", "*")))
+
+
+@pytest.mark.parametrize("fx", FIXTURES, ids=[os.path.basename(f) for f in FIXTURES])
+def test_real_logit_greedy_fixture(orc, fx):
+    logits = np.load(os.path.join(fx, "logits_last.npy"), allow_pickle=False)
+    want = np.load(os.path.join(fx, "argmax.npy"), allow_pickle=False)
+    assert logits.dtype == np.float16
+    r = orc.sample(logits, T=np.zeros(1), tlp=[0])
+    assert r["ids"].tolist() == want.tolist()
+    z64 = logits.astype(np.float64)[0]
+    assert r["lp"][0] == pytest.approx(z64[want[0]] - logsumexp(z64), abs=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Independent formulations
+# ---------------------------------------------------------------------------
+
+def test_lse_closed_form(orc):
+    rng = np.random.default_rng(1)
+    for scale in (0.1, 2.0, 30.0):
+        z = (rng.standard_normal(5000) * scale).astype(np.float32)
+        assert orc.lse_row(z) == pytest.approx(logsumexp(z.astype(np.float64)), abs=1e-9)
+    # single finite entry among -inf: LSE equals it
+    z = np.full(7, -np.inf, np.float32)
+    z[3] = 1.25
+    assert orc.lse_row(z) == 1.25
+
+
+def test_top_k_against_sorted_threshold_with_ties(orc):
+    rng = np.random.default_rng(2)
+    for trial in range(200):
+        V = int(rng.integers(1, 60))
+        z = rng.integers(-4, 5, V).astype(np.float32)  # heavy ties
+        k = int(rng.integers(1, V + 3))
+        f = orc.filter_row(z, k=k)
+        kk = min(k, V)
+        tau = np.sort(z)[::-1][kk - 1]
+        assert (np.isfinite(f) == (z >= tau)).all()
+        assert np.isfinite(f).sum() >= kk
+
+
+def _brute_top_p(zs, p):
+    """Smallest n such that the first n entries of the (z desc, idx asc) order carry
+    mass >= p; an independent statement of 'keep j iff prior mass < p'."""
+    V = zs.size
+    order = sorted(range(V), key=lambda i: (-zs[i], i))
+    m = max(zs)
+    w = [math.exp(float(zs[i]) - float(m)) if np.isfinite(zs[i]) else 0.0 for i in order]
+    W = math.fsum(w)
+    for n in range(1, V + 1):
+        if math.fsum(w[:n]) >= p * W:
+            return set(order[:n])
+    return set(order)
+
+
+def test_top_p_against_brute_force(orc):
+    rng = np.random.default_rng(3)
+    checked = 0
+    for trial in range(400):
+        V = int(rng.integers(1, 9))
+        z = (rng.integers(-6, 7, V) * 0.5).astype(np.float32)  # ties included
+        p = float(np.float32(rng.uniform(0.05, 0.999)))
+        f = orc.filter_row(z, p=p)
+        got = set(np.nonzero(np.isfinite(f))[0].tolist())
+        # skip exact-boundary cases where float64 summation order could matter
+        order = sorted(range(V), key=lambda i: (-z[i], i))
+        w = np.exp(z[order].astype(np.float64) - z.max())
+        cs = np.cumsum(w) / w.sum()
+        if np.min(np.abs(cs - p)) < 1e-12:
+            continue
+        assert got == _brute_top_p(z, p), (z, p)
+        checked += 1
+    assert checked > 300
+
+
+def test_draw_is_inverse_cdf(orc):
+    z = np.array([0.0, 1.0, -1.0, 2.0, 0.5], np.float32)
+    q = np.exp(z.astype(np.float64) - z.max())
+    q /= q.sum()
+    N = 20000
+    counts = np.zeros(5, int)
+    for j in range(N):
+        i, _ = orc.draw_row(z, float(np.float32((j + 0.5) / N)))
+        counts[i] += 1
+    assert np.abs(counts - q * N).max() <= 2
+
+
+def test_draw_ascending_vocab_order(orc):
+    # equal weights: u in [j/4, (j+1)/4) picks the j-th kept entry in index order
+    zs = np.array([-np.inf, 0.0, -np.inf, 0.0, 0.0, -np.inf, 0.0], np.float32)
+    kept = [1, 3, 4, 6]
+    for j in range(4):
+        i, _ = orc.draw_row(zs, (j + 0.5) / 4)
+        assert i == kept[j]
+
+
+def test_bf16_rounding_matches_torch(orc):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(4)
+    base = (rng.standard_normal(1000).astype(np.float32).view(np.uint32) & np.uint32(0xFFFF0000))
+    halfway = (base | np.uint32(0x8000)).view(np.float32)  # exactly between two bf16 values
+    x = np.concatenate([rng.standard_normal(2000).astype(np.float32) * 10, halfway])
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    got = np.array([orc.round_bf16(float(v)) for v in x], np.float32)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    for v in (0.7, 0.9, 0.95, 0.8, 1.2):  # values the configs use
+        assert orc.round_bf16(v) == float(torch.tensor(v).to(torch.bfloat16))
+
+
+def test_f16_rounding_matches_numpy(orc):
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.standard_normal(3000).astype(np.float32) * 100,
+                        rng.standard_normal(1000).astype(np.float32) * 1e-6,  # subnormal halves
+                        np.array([65504, 65519, 65520, 1e6, -7e-8, 3e-8], np.float32)])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).astype(np.float32)
+    got = np.array([orc.round_f16(float(v)) for v in x], np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_bf16_temperature_and_division(orc):
+    # D1: z' = bf16(z / bf16(T)); T = 0.7 becomes 0.69921875
+    bits = np.array([[0x4000, 0x3f80, 0xbf80]], np.uint16)  # 2, 1, -1
+    out = orc.filter_row(np.array([2.0, 1.0, -1.0], np.float32), T=0.7, dtype=BF16)
+    Tb = np.float32(0.69921875)
+    want = [orc.round_bf16(float(np.float32(v) / Tb)) for v in (2.0, 1.0, -1.0)]
+    assert out.tolist() == want
+    assert bits.shape == (1, 3)
+
+
+def test_nan_reads_as_neg_inf_and_degenerate_rows(orc):
+    z = np.array([[np.nan, 1.0, np.nan, 1.0]], np.float32)
+    assert orc.sample(z)["ids"].tolist() == [1]
+    allneg = np.full((1, 5), -np.inf, np.float32)
+    r = orc.sample(allneg, T=[1.0], u=[0.99], tlp=[0])
+    assert r["ids"].tolist() == [4] and np.isnan(r["lp"][0])  # uniform over the row
+    assert orc.sample(allneg)["ids"].tolist() == [0]
+    inf = np.array([[1.0, np.inf, 3.0, np.inf]], np.float32)
+    r = orc.sample(inf, T=[1.0], u=[0.75])
+    assert r["ids"].tolist() == [3]  # mass split evenly between the two +inf entries
+
+
+def test_parameter_sanitisation(orc):
+    z = np.array([[0.0, 3.0, 1.0, 2.0]], np.float32)
+    for T in (np.nan, np.inf, -1.0, 0.0):
+        assert orc.sample(z, T=[T], u=[0.1])["ids"].tolist() == [1]
+    # k > V clamps, k <= 0 and p outside (0, 1) disable
+    a = orc.sample(z, T=[1.0], k=[100], u=[0.2])["ids"]
+    b = orc.sample(z, T=[1.0], k=[0], p=[1.5], u=[0.2])["ids"]
+    c = orc.sample(z, T=[1.0], p=[-0.2], u=[0.2])["ids"]
+    assert a.tolist() == b.tolist() == c.tolist()
+
+
+def test_ambiguity_flags(orc):
+    # two tokens, probs (0.5, 0.5): the cutoff prior mass 0.5 sits exactly at p=0.5
+    z = np.array([[0.0, 0.0, -30.0]], np.float32)
+    r = orc.sample(z, T=[1.0], p=[0.5], u=[0.3])
+    assert r["flags"][0] & orc.FLAG_TOPP_AMBIG
+    r = orc.sample(z, T=[1.0], p=[0.7], u=[0.3])
+    assert not (r["flags"][0] & orc.FLAG_TOPP_AMBIG)
+    # draw boundary: u at the cumulative mass of the first kept token
+    r = orc.sample(z, T=[1.0], u=[0.5])
+    assert r["flags"][0] & orc.FLAG_DRAW_AMBIG
+
+
+def test_workloads_are_deterministic(orc):
+    from mlxforge_amd import workloads
+    a, b = workloads.make(1), workloads.make(1)
+    assert np.array_equal(a.logits, b.logits) and a.B == 1 and a.V == 128256
+    assert a.algorithmic_bytes() == 513048
+    assert workloads.make(3).algorithmic_bytes() == 19448576
