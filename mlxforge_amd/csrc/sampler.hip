@@ -986,13 +986,18 @@ __global__ __launch_bounds__(ROW_THREADS) void k_select(Args a) {
       tau = prefix;
     }
 
-    // (2) mass of the top-k set
+    // (2) mass of the top-k set: the candidates >= tau plus everything above R
+    // (bins below R are below tau).  Without top-k it is the whole row.
     unsigned long long wk = 0;
-    for (int c = tid; c < n; c += ROW_THREADS) {
-      const unsigned int key = cv.get(c).x;
-      if (key >= tau) wk += quant(wexp(key2f(key), st.Mp));
+    if (md.kk > 0) {
+      for (int c = tid; c < n; c += ROW_THREADS) {
+        const unsigned int key = cv.get(c).x;
+        if (key >= tau) wk += quant(wexp(key2f(key), st.Mp));
+      }
+      wk = block_sum<unsigned long long, ROW_WAVES>(wk, s_u64) + mass_above;
+    } else {
+      for (int t = 0; t < S; ++t) wk += s_total[t];
     }
-    wk = block_sum<unsigned long long, ROW_WAVES>(wk, s_u64) + mass_above;
 
     if (!md.topp) {
       vkey = tau;

@@ -77,7 +77,9 @@ def _param(x, B, dtype, device):
     if x is None:
         return None
     if not torch.is_tensor(x):
-        return torch.full((B,), x, dtype=dtype, device=device)
+        if isinstance(x, (int, float)):
+            return torch.full((B,), x, dtype=dtype, device=device)
+        x = torch.as_tensor(x, dtype=dtype).reshape(-1).to(device)
     if x.dtype != dtype or x.device != device or not x.is_contiguous() or x.numel() != B:
         raise ValueError(f"per-row parameter must be a contiguous {dtype} tensor of {B} on {device}")
     return x
