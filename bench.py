@@ -8,10 +8,10 @@ the configuration the headline metric is quoted on.  Prints ONE JSON line.
 Timing: hipEvents (torch.cuda.Event on the stream the library launches on)
 around K back-to-back steps after W warm-up steps; the input is rotated over
 enough copies to exceed 512 MB so neither L2 nor the 256 MB MALL holds it when
-a step starts ("cold" HBM).  Per-kernel durations come from a second pass
-through mlxf_sample_profiled (HIP events around each kernel on the same
-stream).  cpu_baseline times the CPU restatement of the reference sampler
-(oracle/, "port") on the same workload with a bounded number of repetitions.
+a step starts ("cold" HBM).  A step is one launch of the single kernel
+k_sample, so the per-step time is that kernel's average launch duration.
+cpu_baseline times the CPU restatement of the reference sampler (oracle/,
+"port") on the same workload with a bounded number of repetitions.
 """
 from __future__ import annotations
 
@@ -62,7 +62,7 @@ class Step:
         self.code = {"f32": 0, "bf16": 1, "f16": 2}[wl.dtype]
         from mlxforge_amd import _lib
         self.ws_bytes = _lib.workspace_size(B, wl.V, self.K, self.code)
-        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
+        self.ws = torch.zeros(self.ws_bytes, dtype=torch.uint8, device=dev)
         self.stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         P = ctypes.c_void_p
         self.args_tail = [P(self.T.data_ptr()), P(self.k.data_ptr()), P(self.p.data_ptr()),
@@ -87,14 +87,6 @@ class Step:
             from mlxforge_amd import _lib
             _lib.check(rc, err)
 
-    def run_profiled(self, out):
-        err = ctypes.c_void_p()
-        rc = self.lib.mlxf_sample_profiled(self._logits(), self.code, self.wl.B, self.wl.V,
-                                           self.wl.V, *self.args_tail, out, ctypes.byref(err))
-        if rc:
-            from mlxforge_amd import _lib
-            _lib.check(rc, err)
-
 
 def time_steps(step, torch, warmup, steps):
     for _ in range(warmup):
@@ -107,17 +99,6 @@ def time_steps(step, torch, warmup, steps):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
-
-
-def stage_times(step, steps):
-    from mlxforge_amd import _lib
-    arr = (ctypes.c_float * _lib.NUM_STAGES)()
-    acc = [0.0] * _lib.NUM_STAGES
-    for _ in range(steps):
-        step.run_profiled(arr)
-        for j in range(_lib.NUM_STAGES):
-            acc[j] += arr[j]
-    return {n: acc[j] / steps for j, n in enumerate(_lib.STAGE_NAMES)}
 
 
 def cpu_baseline(wl, seconds):
@@ -170,21 +151,18 @@ def main():
         wl = workloads.make(cfg)
         st = Step(wl, torch, lib)
         ms = time_steps(st, torch, warmup, steps)
-        stages = stage_times(st, max(20, steps // 4))
         st_hot = Step(wl, torch, lib, rotate=False)
         ms_hot = time_steps(st_hot, torch, warmup, steps)
         del st, st_hot
         torch.cuda.empty_cache()
-        return wl, ms, ms_hot, stages
+        return wl, ms, ms_hot
 
     log(f"[bench] config C{args.config}: warmup {args.warmup}, steps {args.steps}")
-    wl, ms, ms_hot, stages = measure(args.config, args.steps, args.warmup)
+    wl, ms, ms_hot = measure(args.config, args.steps, args.warmup)
     alg = wl.algorithmic_bytes()
-    dom = max(stages, key=stages.get)
-    dom_ms = stages[dom]
-    # the dominant kernel's algorithmic bytes: the compulsory read of the logits
-    dom_bytes = wl.B * wl.V * wl.elem_size
-    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    # one kernel per step: its algorithmic bytes are the step's (logits read
+    # once, ids / logprobs / top-K written, per-row parameters read)
+    achieved = alg / (ms * 1e-3) / 1e9
     out = {
         "metric": METRIC,
         "value": round(wl.B / (ms * 1e-3), 1),
@@ -203,12 +181,11 @@ def main():
         "us_per_step": round(ms * 1e3, 2),
         "us_per_step_hot": round(ms_hot * 1e3, 2),
         "achieved_GBps_step": round(alg / (ms * 1e-3) / 1e9, 1),
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": "k_sample", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": dom_bytes,
-                     "kernel_us": round(dom_ms * 1e3, 2)},
-        "stage_us": {k: round(v * 1e3, 2) for k, v in stages.items()},
+                     "algorithmic_bytes_per_launch": alg,
+                     "kernel_us": round(ms * 1e3, 2)},
     }
     if not args.no_cpu:
         log("[bench] cpu baseline")
@@ -219,12 +196,13 @@ def main():
             if cfg == args.config:
                 continue
             log(f"[bench] extra config C{cfg}")
-            w2, m2, mh2, s2 = measure(cfg, min(args.steps, 100), min(args.warmup, 10))
+            w2, m2, mh2 = measure(cfg, min(args.steps, 100), min(args.warmup, 10))
             extra[f"C{cfg}"] = {"workload": w2.name, "us_per_step": round(m2 * 1e3, 2),
                                 "us_per_step_hot": round(mh2 * 1e3, 2),
                                 "rows_per_s": round(w2.B / (m2 * 1e-3), 1),
                                 "achieved_GBps_step": round(w2.algorithmic_bytes() / (m2 * 1e-3) / 1e9, 1),
-                                "stage_us": {k: round(v * 1e3, 2) for k, v in s2.items()}}
+                                "hbm_frac": round(w2.algorithmic_bytes() / (m2 * 1e-3) / 1e9
+                                                  / HBM_PEAK_GBPS, 4)}
         out["other_configs"] = extra
     print(json.dumps(out), flush=True)
 

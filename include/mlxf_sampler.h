@@ -17,7 +17,9 @@
  *     mlxf_string_free();
  *   - no exception ever crosses the boundary;
  *   - the library allocates nothing in mlxf_sample / mlxf_greedy: scratch is the
- *     caller-provided workspace (size from mlxf_sampler_workspace_size);
+ *     caller-provided workspace (size from mlxf_sampler_workspace_size), zeroed
+ *     once before first use (mlxf_sampler_workspace_init, or any zero fill);
+ *     every call leaves it ready for the next;
  *   - calls are reentrant per stream; two calls that share a workspace must be
  *     ordered on one stream.
  */
@@ -47,9 +49,8 @@ extern "C" {
 /* Largest top_logprobs column count supported per call.  The reference's HTTP
  * layer admits top_logprobs in [0, 20] (src/server/openai.cpp:150-152). */
 #define MLXF_MAX_TOP_LOGPROBS 64
-/* Largest vocabulary accepted (the nucleus mass is summed in 64-bit fixed point
- * with 2^-42 resolution; V * 2^42 must fit in 64 bits). */
-#define MLXF_MAX_VOCAB 4194304
+/* Largest vocabulary accepted: at most 64 slices of 16384 logits per row. */
+#define MLXF_MAX_VOCAB 1048576
 
 /* ABI version of the loaded library (MLXF_SAMPLER_ABI_VERSION it was built with).
  * No reference counterpart for the sampler itself; mirrors mlxforge_abi_version
@@ -60,6 +61,13 @@ int mlxf_sampler_abi_version(void);
  * Replaces the lazily allocated MLX temporaries of Sampler::sample
  * (src/sample/sampler.cpp:141-166); the caller owns and reuses the buffer. */
 int mlxf_sampler_workspace_size(int B, int V, int K_max, int dtype, size_t* bytes, char** err);
+
+/* Prepare a freshly allocated workspace for its first call (zeroes the per-row
+ * counters at its start with a fill kernel on `stream`; no hipMemset, so it may
+ * be captured in a graph).  A workspace that came from a zero fill needs no
+ * call.  No reference counterpart: the reference's MLX temporaries need none. */
+int mlxf_sampler_workspace_init(void* d_workspace, size_t workspace_bytes, void* stream,
+                                char** err);
 
 /* Sample one token per row.  Replaces the per-row loop of Worker::sample_rows
  * (src/runtime/worker.cpp:453-483) calling Sampler::sample

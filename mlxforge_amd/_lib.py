@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "libmlxf_sampler.so")
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 OK, EINVAL, EWORKSPACE, EHIP = 0, -1, -2, -3
 MAX_TOP_LOGPROBS = 64
-MAX_VOCAB = 4194304
+MAX_VOCAB = 1048576
 
 # Every function include/*.h declares.
 SYMBOLS = (
@@ -23,10 +23,8 @@ SYMBOLS = (
     "mlxf_sample",
     "mlxf_greedy",
     "mlxf_string_free",
-    "mlxf_sample_profiled",
+    "mlxf_sampler_workspace_init",
 )
-NUM_STAGES = 5
-STAGE_NAMES = ("k_scan", "k_plan", "k_extract", "k_select", "k_draw")
 
 _lib = None
 
@@ -55,9 +53,8 @@ def load() -> ctypes.CDLL:
     L.mlxf_sample.restype = I
     L.mlxf_greedy.argtypes = [P, I, I, I, I64, P, P, SZ, P, PP]
     L.mlxf_greedy.restype = I
-    L.mlxf_sample_profiled.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, I, P, SZ, P,
-                                       ctypes.POINTER(ctypes.c_float), PP]
-    L.mlxf_sample_profiled.restype = I
+    L.mlxf_sampler_workspace_init.argtypes = [P, SZ, P, PP]
+    L.mlxf_sampler_workspace_init.restype = I
     L.mlxf_string_free.argtypes = [P]
     L.mlxf_string_free.restype = None
     _lib = L

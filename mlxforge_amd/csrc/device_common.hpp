@@ -1,0 +1,349 @@
+// device_common.hpp -- device helpers of the gfx950 sampler: monotone float
+// keys, dtype rounding, raw vector loads, the weight function, device-coherent
+// accesses, wave/block scans and the best-64 list sort / merge.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <climits>
+
+#include "mlxf_sampler.h"
+
+namespace mlxf {
+
+constexpr int THREADS = 1024;  // one workgroup per row slice; 16 waves
+constexpr int WAVES = THREADS / 64;
+constexpr int VEC = 8;                  // elements per 16-byte (bf16/f16) or 32-byte (f32) load
+constexpr int CHUNK = THREADS * VEC;    // elements one load instruction covers across the block
+constexpr int MAX_S = 64;               // slices per row (<= 64: one wave combines them)
+constexpr int NBIN = 2048;              // digit / histogram width (11 bits)
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr unsigned int KEY_NEG_INF = 0x007fffffu;  // key of -inf; smaller keys are NaNs
+constexpr unsigned int KEY_POS_INF = 0xff800000u;
+
+// Monotone unsigned key of a float: a < b  <=>  key(a) < key(b) (no NaNs).
+__device__ __forceinline__ unsigned int f2key(float f) {
+  const unsigned int u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key2f(unsigned int k) {
+  const unsigned int u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+// Round-to-nearest-even into the logits dtype (the temperature division of
+// src/sample/sampler.cpp:158 is carried out in the logits dtype).
+template <int DT>
+__device__ __forceinline__ float round_dt(float x) {
+  if constexpr (DT == MLXF_DTYPE_BF16) {
+    unsigned int u = __float_as_uint(x);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return __uint_as_float(u & 0xffff0000u);
+  } else if constexpr (DT == MLXF_DTYPE_F16) {
+    return __half2float(__float2half_rn(x));
+  } else {
+    return x;
+  }
+}
+
+// z' = round_dtype(z / T), IEEE division.  Monotone non-decreasing in z.
+template <int DT>
+__device__ __forceinline__ float fz(float z, float Tr) {
+  return round_dt<DT>(z / Tr);
+}
+
+// Smallest key k (over non-NaN floats) with fz(key2f(k)) >= y.
+template <int DT>
+__device__ __forceinline__ unsigned int gkey(float y, float Tr) {
+  unsigned int lo = KEY_NEG_INF, hi = KEY_POS_INF;
+  if (!(fz<DT>(INFINITY, Tr) >= y)) return KEY_POS_INF;
+  while (lo < hi) {
+    const unsigned int mid = lo + ((hi - lo) >> 1);
+    if (fz<DT>(key2f(mid), Tr) >= y)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  return lo;
+}
+
+template <int DT>
+constexpr int elem_size() {
+  return DT == MLXF_DTYPE_F32 ? 4 : 2;
+}
+
+template <int DT>
+__device__ __forceinline__ float ld1(const void* row, int i) {
+  float v;
+  if constexpr (DT == MLXF_DTYPE_F32) {
+    v = static_cast<const float*>(row)[i];
+  } else if constexpr (DT == MLXF_DTYPE_BF16) {
+    v = __uint_as_float(static_cast<unsigned int>(static_cast<const unsigned short*>(row)[i]) << 16);
+  } else {
+    v = __half2float(static_cast<const __half*>(row)[i]);
+  }
+  return v != v ? -INFINITY : v;  // NaN reads as -inf
+}
+
+// Raw storage of 8 consecutive elements: two 16-byte words for fp32, one for
+// the 16-bit types.  Loading raw and decoding later keeps several slices'
+// loads in flight in few registers.
+template <int DT>
+struct Raw8 {
+  static constexpr int NQ = DT == MLXF_DTYPE_F32 ? 2 : 1;
+  uint4 q[NQ];
+};
+
+template <int DT>
+__device__ __forceinline__ unsigned int neg_inf_bits() {
+  return DT == MLXF_DTYPE_F32 ? 0xff800000u : (DT == MLXF_DTYPE_BF16 ? 0xff80u : 0xfc00u);
+}
+
+template <int DT>
+__device__ __forceinline__ unsigned int ld_bits(const void* row, int i) {
+  if constexpr (DT == MLXF_DTYPE_F32)
+    return static_cast<const unsigned int*>(row)[i];
+  else
+    return static_cast<const unsigned short*>(row)[i];
+}
+
+// 8 consecutive elements from i0 (i0 % 8 == 0); entries at or past `end` read
+// as -inf.
+template <int DT, bool VECOK>
+__device__ __forceinline__ void load_raw(const void* row, int i0, int end, Raw8<DT>& r) {
+  const int nv = end - i0;
+  if (VECOK && nv >= VEC) {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const char*>(row) +
+                                                    static_cast<size_t>(i0) * elem_size<DT>());
+#pragma unroll
+    for (int q = 0; q < Raw8<DT>::NQ; ++q) r.q[q] = p[q];
+  } else {
+    unsigned int b[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) b[j] = j < nv ? ld_bits<DT>(row, i0 + j) : neg_inf_bits<DT>();
+    if constexpr (DT == MLXF_DTYPE_F32) {
+      r.q[0] = make_uint4(b[0], b[1], b[2], b[3]);
+      r.q[1] = make_uint4(b[4], b[5], b[6], b[7]);
+    } else {
+      r.q[0] = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16),
+                          b[6] | (b[7] << 16));
+    }
+  }
+}
+
+// Raw -> fp32 values; NaN reads as -inf.
+template <int DT>
+__device__ __forceinline__ void decode8(const Raw8<DT>& r, float* v) {
+  if constexpr (DT == MLXF_DTYPE_F32) {
+    const unsigned int w[8] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[0].w,
+                               r.q[1].x, r.q[1].y, r.q[1].z, r.q[1].w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(w[j]);
+  } else {
+    const unsigned int w[4] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[0].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == MLXF_DTYPE_BF16) {
+        v[2 * j] = __uint_as_float(w[j] << 16);
+        v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      } else {
+        __half_raw lo, hi;
+        lo.x = static_cast<unsigned short>(w[j] & 0xffffu);
+        hi.x = static_cast<unsigned short>(w[j] >> 16);
+        v[2 * j] = __half2float(__half(lo));
+        v[2 * j + 1] = __half2float(__half(hi));
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) v[j] = v[j] != v[j] ? -INFINITY : v[j];
+}
+
+template <int DT, bool VECOK>
+__device__ __forceinline__ void load8(const void* row, int i0, int end, float* v) {
+  Raw8<DT> r;
+  load_raw<DT, VECOK>(row, i0, end, r);
+  decode8<DT>(r, v);
+}
+
+// exp(x - m) with exp(m - m) = 1 also for infinite m.
+__device__ __forceinline__ float wexp(float x, float m) {
+  const float e = __builtin_amdgcn_exp2f((x - m) * LOG2E);
+  return x == m ? 1.0f : e;
+}
+__device__ __forceinline__ double wexp_d(float x, float m) {
+  return x == m ? 1.0 : exp(static_cast<double>(x) - static_cast<double>(m));
+}
+
+// floor(w * 2^42) for w in [0, 1]: fixed-point mass, exact and order-free to sum.
+__device__ __forceinline__ unsigned long long quant(float w) {
+  const float t = w * 1024.0f;
+  const float h = floorf(t);
+  const float fr = t - h;
+  const unsigned int lo = static_cast<unsigned int>(fr * 4294967296.0f);
+  const unsigned int hi = static_cast<unsigned int>(h);
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+constexpr double QUNIT = 1.0 / 4398046511104.0;  // 2^-42
+
+// Device-coherent 64-bit accesses (relaxed, agent scope).  Data one workgroup
+// hands to another goes through these: they compile to sc1 loads / stores that
+// are coherent across the XCDs' L2 caches without an L2-wide write-back or
+// invalidate, which a release/acquire fence would cost per workgroup.
+__device__ __forceinline__ void st_dev(void* p, unsigned long long v) {
+  __hip_atomic_store(static_cast<unsigned long long*>(p), v, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_dev(const void* p) {
+  return __hip_atomic_load(static_cast<unsigned long long*>(const_cast<void*>(p)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long pack2(unsigned int lo, unsigned int hi) {
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+__device__ __forceinline__ void st_dev(uint2* p, uint2 v) { st_dev(static_cast<void*>(p), pack2(v.x, v.y)); }
+__device__ __forceinline__ uint2 ld_dev2(const uint2* p) {
+  const unsigned long long w = ld_dev(static_cast<const void*>(p));
+  return make_uint2(static_cast<unsigned int>(w), static_cast<unsigned int>(w >> 32));
+}
+
+__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) {
+  return av > bv || (av == bv && ai < bi);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const T y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Scan over the block (WAVES waves): *excl / *incl are this thread's exclusive
+// and inclusive prefix, *total the block sum.  incl is defined as the next
+// thread's excl, so for floating T the ranges [excl, incl) of consecutive
+// threads meet bit for bit.  lds: WAVES entries.  Contains barriers: call from
+// uniform control flow.
+template <typename T>
+__device__ __forceinline__ void block_scan(T x, T* lds, T* excl, T* incl, T* total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const T inc = wave_incl_scan(x);
+  __syncthreads();  // lds may still be read by a previous call
+  if (lane == 63) lds[wid] = inc;
+  __syncthreads();
+  const T wt = lane < WAVES ? lds[lane] : T(0);
+  const T wsc = wave_incl_scan(wt);  // every wave derives the same wave offsets
+  const T off = wid == 0 ? T(0) : __shfl(wsc, wid - 1, 64);
+  const T off_next = __shfl(wsc, wid, 64);
+  T exw = __shfl_up(inc, 1, 64);
+  if (lane == 0) exw = T(0);
+  const T ex = exw + off;
+  const T nx = __shfl_down(ex, 1, 64);
+  *excl = ex;
+  *incl = lane == 63 ? off_next : nx;
+  *total = __shfl(wsc, WAVES - 1, 64);
+}
+
+template <typename T>
+__device__ __forceinline__ T block_excl_scan(T x, T* lds, T* total) {
+  T ex, in;
+  block_scan<T>(x, lds, &ex, &in, total);
+  return ex;
+}
+
+// Block sum in a fixed order (deterministic for floating T).  lds: WAVES entries.
+template <typename T>
+__device__ __forceinline__ T block_sum(T x, T* lds) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  x = wave_sum(x);
+  __syncthreads();  // lds may still be read by a previous call
+  if (lane == 0) lds[wid] = x;
+  __syncthreads();
+  T t = lds[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) t += lds[w];
+  return t;
+}
+
+// Bitonic sort of one entry per lane, best (v desc, i asc) in lane 0.
+__device__ __forceinline__ void wave_sort(float& v, int& i) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const float ov = __shfl_xor(v, j, 64);
+      const int oi = __shfl_xor(i, j, 64);
+      const bool first = (lane & j) == 0;
+      const bool asc = (lane & k) == 0;
+      const bool ob = better(ov, oi, v, i);
+      if ((first == asc) ? ob : !ob) {
+        v = ov;
+        i = oi;
+      }
+    }
+  }
+}
+
+// Merge the sorted lane list (lv, li) with another sorted list (nv, ni),
+// keeping the best 64.
+__device__ __forceinline__ void wave_list_merge(float& lv, int& li, float nv, int ni) {
+  const int lane = threadIdx.x & 63;
+  const float rv = __shfl(nv, 63 - lane, 64);
+  const int ri = __shfl(ni, 63 - lane, 64);
+  if (better(rv, ri, lv, li)) {
+    lv = rv;
+    li = ri;
+  }
+#pragma unroll
+  for (int j = 32; j > 0; j >>= 1) {
+    const float ov = __shfl_xor(lv, j, 64);
+    const int oi = __shfl_xor(li, j, 64);
+    const bool first = (lane & j) == 0;
+    const bool ob = better(ov, oi, lv, li);
+    if (first ? ob : !ob) {
+      lv = ov;
+      li = oi;
+    }
+  }
+}
+
+struct TopEnt {
+  float v;
+  int i;
+};
+
+// Waves [0, nw) each hold a sorted list (lv, li); on return wave 0 holds the
+// best 64 of their union.  Pairwise rounds through `lists` (WAVES * 64 LDS
+// entries).  Whole workgroup, nw uniform; ends with a barrier.
+__device__ __forceinline__ void tree_merge(float& lv, int& li, TopEnt* lists, int nw) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (int n = nw; n > 1;) {
+    const int h = (n + 1) >> 1;
+    if (wid >= h && wid < n) {
+      lists[wid * 64 + lane].v = lv;
+      lists[wid * 64 + lane].i = li;
+    }
+    __syncthreads();
+    if (wid < n - h) {
+      const TopEnt o = lists[(wid + h) * 64 + lane];
+      wave_list_merge(lv, li, o.v, o.i);
+    }
+    n = h;
+  }
+  __syncthreads();
+}
+
+}  // namespace mlxf

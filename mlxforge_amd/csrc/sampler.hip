@@ -2,100 +2,80 @@
 // include/mlxf_sampler.h.
 //
 // Replaces the per-row MLX graph of Sampler::sample (src/sample/sampler.cpp:
-// 141-166) with one launch sequence over all rows of a [B, V] logits matrix.
-// Each row is cut into S slices of L elements; a slice is one 256-thread
-// workgroup that streams its part of the row with 16-byte loads.
+// 141-166), run once per row by Worker::sample_rows (src/runtime/worker.cpp:
+// 448-486), with ONE kernel launch over all rows of a [B, V] logits matrix.
 //
-//   k_scan    (S x B)  one HBM pass: row max / lowest-index argmax, the log-sum-
-//                      exp partial, the slice's top-K by (z desc, idx asc) for
-//                      top_logprobs, and -- for rows with top-k / top-p -- a
-//                      2048-bin histogram (count, mass) of z' = z / T over the
-//                      top 11 bits of its monotone key.
-//   k_plan    (B)      combines the slices: greedy id + logprob, merged top-K,
-//                      max z', and the range R of histogram bins that can hold
-//                      the top-k / top-p boundary.
-//   k_extract (S x B)  re-reads the slice (L2/MALL), sums the exact fixed-point
-//                      mass above R and of the whole slice, and compacts the
-//                      elements inside R in index order.
-//   k_select  (B)      exact radix selection over the candidates: the k-th
-//                      largest z' (ties kept), the nucleus cutoff (value v* and
-//                      the last kept index among ties at v*), the kept mass per
-//                      slice and the slice holding the draw.
-//   k_draw    (B)      inverse-CDF walk of that one slice in vocabulary order.
-//
-// Every mass is exp(z' - max z') rounded down to a multiple of 2^-42 and summed
-// as uint64, so the sums are exact, independent of summation order, and the
-// draw walk sees exactly the per-slice masses k_select chose the slice with.
+// Grid (S, B): row r is cut into S slices of L = 1024 * EPT elements; slice s
+// is one 1024-thread workgroup that loads its whole slice into registers with
+// 16-byte loads (one HBM read of the logits) and reduces it there:
+//   * max and lowest-index argmax of z, and sum exp(z - max) when a logprob is
+//     wanted;
+//   * when top_logprobs or a top-k <= 63 is asked for: the slice's best 64
+//     entries by (z desc, index asc).  The 64th best of the 1024 per-thread
+//     maxima bounds the slice's 64th best from below; the at most 64 * EPT
+//     elements at or above it are sorted in 64-entry chunks and merged;
+//   * top-k > 63: a 4096-bin count histogram of z keys gives the bin of the
+//     slice's k-th largest z; everything from the (temperature-mapped) lower
+//     edge of that bin up is written out as a candidate;
+//   * temperature-only and top-p rows: the sum of w = exp(z' - max z') over the
+//     slice (z' = z / T in the logits dtype), and for top-p a 2048-bin
+//     histogram of z' keys with (count, truncated w) packed in one 64-bit word.
+// The slice then takes a ticket on the row's counter; the workgroup that draws
+// the row's last ticket finishes the row.  No workgroup ever waits for another.
+//   * greedy: argmax, logprob and top_logprobs from the slice summaries;
+//   * top-k <= 63: the merged best-64 list of the row decides everything in one
+//     wave (the k-th largest z', the nucleus prefix, the draw), after checking
+//     that the list holds every element at or above the k-th value of z';
+//   * top-k > 63: 8-bit radix selections over the candidates;
+//   * temperature-only: the slice that holds u * sum(w), then a walk of that
+//     slice in vocabulary order;
+//   * top-p: the combined histogram, with the bound of its truncation error,
+//     brackets the nucleus boundary in a range R of bins; a compare-only pass
+//     over the row collects R's elements and the exact mass of the smaller
+//     side of R; radix selections over R's elements give the cutoff value and
+//     the last kept index among its ties; then the walk of the one slice that
+//     holds the draw.
+// Masses that decide a cutoff are exact 64-bit fixed-point sums (2^-42 units)
+// or fp64 sums in a fixed order, so every result is reproducible bit for bit.
+// Data one workgroup leaves for another travels through device-coherent (sc1)
+// loads and stores, so no L2-wide write-back is ever needed.
 // There is no MFMA anywhere: nothing here is a dense contraction.
-#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <climits>
 #include <cmath>
-#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <string>
 
+#include "device_common.hpp"
 #include "mlxf_sampler.h"
-#include "mlxf_sampler_diag.h"
 
+namespace mlxf {
 namespace {
 
-constexpr int NB = 2048;          // histogram bins: key >> 21
-constexpr int BIN_SHIFT = 21;
-constexpr int SLICE_THREADS = 256;
-constexpr int VEC = 8;            // elements per thread per iteration (16 B of bf16)
-constexpr int ITER_ELEMS = SLICE_THREADS * VEC;
-constexpr int ROW_THREADS = 1024;
-constexpr int ROW_WAVES = ROW_THREADS / 64;
-constexpr int TARGET_BLOCKS = 1024;  // ~4 workgroups per CU on 256 CUs
-constexpr int MAX_S = 32;
-constexpr int CAND_LDS = 6144;       // candidates staged in LDS by k_select
-constexpr float LOG2E = 1.4426950408889634f;
+enum { KIND_GREEDY = 0, KIND_TEMP = 1, KIND_KLIST = 2, KIND_KHIST = 3, KIND_TOPP = 4 };
+constexpr int LIST = 64;
+constexpr int KLIST_MAX = LIST - 1;  // top-k resolved from the best-64 lists
+constexpr int CAND_LDS = 4096;
+constexpr int CNT_BINS = 4096;  // z-key >> 20: the per-slice top-k threshold bins
+constexpr int RBINS = 256;      // radix digit
+constexpr unsigned long long MASK40 = (1ull << 40) - 1;
+constexpr double HUNIT = 1.0 / 16777216.0;  // 2^-24: histogram mass unit
 
-enum { KIND_GREEDY = 0, KIND_TEMP = 1, KIND_HIST = 2 };
-
-struct TopEnt {
-  float v;
-  int i;
-};
-
-struct SliceRec {
+struct SliceRec {  // four 64-bit words
   float zmax;
   int zarg;
-  float lse_s;  // sum exp(z - zmax) over the slice
-  float pad;
-};
-
-struct SliceMass {
-  unsigned long long above;  // mass of bins above R
-  unsigned long long total;  // mass of the whole slice
+  float mps;  // max z' over the slice
   unsigned int ncand;
-  unsigned int pad0;
-  unsigned long long pad1;
-};
-
-struct RowState {
-  int kind;
-  int zarg;
-  float zmax;
-  float Mp;  // max z'
-  double lse;
-  int b_lo, b_hi;
-  unsigned int cnt_above;
-  unsigned int vkey;
-  int idx_cut;
-  int s_star;
-  unsigned long long target_rem;
+  double lse_s;  // sum exp(z - zmax) over the slice
+  double msum;   // sum w(z', mps) over the slice
 };
 
 struct Args {
   const void* logits;
   long long row_stride;
-  int B, V, K_max;
-  int S, L;
+  int B, V, K_max, S, L;
   const float* T;
   const int* k;
   const float* p;
@@ -105,131 +85,16 @@ struct Args {
   float* out_lp;
   int* out_top_ids;
   float* out_top_lp;
-  // workspace views
-  RowState* rs;
+  unsigned int* ctr;
   SliceRec* rec;
-  TopEnt* top;
-  unsigned int* hcnt;
-  unsigned long long* hmass;
-  SliceMass* sm;
-  uint2* cand;
+  unsigned long long* list;  // [B*S][64] packed (z bits, index)
+  unsigned long long* hist;  // [B*S][NBIN]
+  uint2* cand;               // [B*S][L]
 };
 
-// ---------------------------------------------------------------- helpers --
-
-__device__ __forceinline__ unsigned int f2key(float f) {
-  unsigned int u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float key2f(unsigned int k) {
-  unsigned int u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
-  return __uint_as_float(u);
-}
-
-// Round-to-nearest-even into the logits dtype (the dtype-faithful temperature
-// division of src/sample/sampler.cpp:158).
-template <int DT>
-__device__ __forceinline__ float round_dt(float x) {
-  if constexpr (DT == MLXF_DTYPE_BF16) {
-    unsigned int u = __float_as_uint(x);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return __uint_as_float(u & 0xffff0000u);
-  } else if constexpr (DT == MLXF_DTYPE_F16) {
-    return __half2float(__float2half_rn(x));
-  } else {
-    return x;
-  }
-}
-
-template <int DT>
-constexpr int elem_size() {
-  return DT == MLXF_DTYPE_F32 ? 4 : 2;
-}
-
-template <int DT>
-__device__ __forceinline__ float ld1(const void* row, int i) {
-  float v;
-  if constexpr (DT == MLXF_DTYPE_F32) {
-    v = static_cast<const float*>(row)[i];
-  } else if constexpr (DT == MLXF_DTYPE_BF16) {
-    v = __uint_as_float(static_cast<unsigned int>(static_cast<const unsigned short*>(row)[i]) << 16);
-  } else {
-    v = __half2float(static_cast<const __half*>(row)[i]);
-  }
-  return v != v ? -INFINITY : v;  // NaN reads as -inf
-}
-
-// 8 consecutive elements starting at i0 (i0 % 8 == 0); entries past `end` are
-// -inf and *nv counts the valid ones.
-template <int DT, bool VECOK>
-__device__ __forceinline__ void load8(const void* row, int i0, int end, float (&v)[VEC], int& nv) {
-  nv = end - i0;
-  nv = nv < 0 ? 0 : (nv > VEC ? VEC : nv);
-  if (VECOK && nv == VEC) {
-    if constexpr (DT == MLXF_DTYPE_F32) {
-      const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(row) + i0);
-      float4 a = p[0], b = p[1];
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
-      uint4 q = *reinterpret_cast<const uint4*>(static_cast<const unsigned short*>(row) + i0);
-      unsigned int w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if constexpr (DT == MLXF_DTYPE_BF16) {
-          v[2 * j] = __uint_as_float(w[j] << 16);
-          v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-        } else {
-          __half_raw lo, hi;
-          lo.x = static_cast<unsigned short>(w[j] & 0xffffu);
-          hi.x = static_cast<unsigned short>(w[j] >> 16);
-          v[2 * j] = __half2float(__half(lo));
-          v[2 * j + 1] = __half2float(__half(hi));
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) v[j] = v[j] != v[j] ? -INFINITY : v[j];
-  } else {
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) v[j] = j < nv ? ld1<DT>(row, i0 + j) : -INFINITY;
-  }
-}
-
-// exp(x - m), with exp(m - m) = 1 also for infinite m.
-__device__ __forceinline__ float wexp(float x, float m) {
-  float e = __builtin_amdgcn_exp2f((x - m) * LOG2E);
-  return x == m ? 1.0f : e;
-}
-__device__ __forceinline__ double wexp_d(float x, float m) {
-  return x == m ? 1.0 : exp(static_cast<double>(x) - static_cast<double>(m));
-}
-
-// floor(w * 2^42) for w in [0, 1]: the fixed-point mass unit.
-__device__ __forceinline__ unsigned long long quant(float w) {
-  float t = w * 1024.0f;
-  float h = floorf(t);
-  float fr = t - h;
-  unsigned int lo = static_cast<unsigned int>(fr * 4294967296.0f);
-  unsigned int hi = static_cast<unsigned int>(h);
-  return (static_cast<unsigned long long>(hi) << 32) | lo;
-}
-
-__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) {
-  return av > bv || (av == bv && ai < bi);
-}
-
 struct Mode {
-  int sampling;
-  float Tr;
-  int kk;
-  int topp;
-  float pr;
-  int K;
-  int need_lse;
-  int want_lp;
-  float u;
-  int kind;
+  int sampling, kk, topp, K, need_lse, want_lp, kind, need_list;
+  float Tr, pr, u;
 };
 
 // Per-row parameters with the reference's sentinels and the C ABI's
@@ -256,7 +121,13 @@ __device__ __forceinline__ Mode decode(const Args& a, int r) {
   if (!(u >= 0.0f)) u = 0.0f;
   if (u >= 1.0f) u = 0x1.fffffep-1f;
   m.u = u;
-  m.kind = !m.sampling ? KIND_GREEDY : ((m.kk > 0 || m.topp) ? KIND_HIST : KIND_TEMP);
+  if (!m.sampling)
+    m.kind = KIND_GREEDY;
+  else if (m.kk > 0)
+    m.kind = m.kk <= KLIST_MAX ? KIND_KLIST : KIND_KHIST;
+  else
+    m.kind = m.topp ? KIND_TOPP : KIND_TEMP;
+  m.need_list = (K > 0 || m.kind == KIND_KLIST) ? 1 : 0;
   return m;
 }
 
@@ -266,560 +137,102 @@ __device__ __forceinline__ const void* row_ptr(const Args& a, int r) {
          static_cast<size_t>(r) * static_cast<size_t>(a.row_stride) * elem_size<DT>();
 }
 
-// Bitonic sort of one entry per lane, best (v desc, i asc) in lane 0.
-__device__ __forceinline__ void wave_sort(float& v, int& i) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int k = 2; k <= 64; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      float ov = __shfl_xor(v, j, 64);
-      int oi = __shfl_xor(i, j, 64);
-      const bool first = (lane & j) == 0;
-      const bool asc = (lane & k) == 0;
-      const bool ob = better(ov, oi, v, i);
-      const bool take = (first == asc) ? ob : !ob;
-      if (take) {
-        v = ov;
-        i = oi;
-      }
-    }
+__device__ __forceinline__ unsigned long long pack_ent(float v, int i) {
+  return pack2(__float_as_uint(v), static_cast<unsigned int>(i));
+}
+
+// 64-bit mass added to an LDS counter; one atomic per wave when every active
+// lane adds to the same counter (the common case: candidates come in slice
+// order, and ties share digits).
+__device__ __forceinline__ void lds_add_agg(unsigned long long* base, int idx, unsigned long long q,
+                                            bool act) {
+  const unsigned long long bal = __ballot(act);
+  if (!bal) return;
+  const int first = __ffsll(static_cast<long long>(bal)) - 1;
+  const int i0 = __shfl(idx, first, 64);
+  if (__ballot(act && idx != i0) == 0) {
+    const unsigned long long s = wave_sum(act ? q : 0ull);
+    if ((threadIdx.x & 63) == first && s) atomicAdd(base + i0, s);
+  } else if (act && q) {
+    atomicAdd(base + idx, q);
+  }
+}
+__device__ __forceinline__ void lds_cnt_agg(unsigned int* base, int idx, bool act) {
+  const unsigned long long bal = __ballot(act);
+  if (!bal) return;
+  const int first = __ffsll(static_cast<long long>(bal)) - 1;
+  const int i0 = __shfl(idx, first, 64);
+  if (__ballot(act && idx != i0) == 0) {
+    if ((threadIdx.x & 63) == first) atomicAdd(base + i0, static_cast<unsigned int>(__popcll(bal)));
+  } else if (act) {
+    atomicAdd(base + idx, 1u);
   }
 }
 
-// Final bitonic merge stage (k = 64) of a bitonic lane sequence.
-__device__ __forceinline__ void wave_merge(float& v, int& i) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int j = 32; j > 0; j >>= 1) {
-    float ov = __shfl_xor(v, j, 64);
-    int oi = __shfl_xor(i, j, 64);
-    const bool first = (lane & j) == 0;
-    const bool ob = better(ov, oi, v, i);
-    const bool take = first ? ob : !ob;
-    if (take) {
-      v = ov;
-      i = oi;
-    }
-  }
-}
+// ------------------------------------------------------------ shared memory --
 
-// (lv, li): sorted top-64 list of the wave.  Merge a sorted list (nv, ni).
-__device__ __forceinline__ void wave_list_merge(float& lv, int& li, float nv, int ni) {
-  const int lane = threadIdx.x & 63;
-  float rv = __shfl(nv, 63 - lane, 64);
-  int ri = __shfl(ni, 63 - lane, 64);
-  if (better(rv, ri, lv, li)) {
-    lv = rv;
-    li = ri;
-  }
-  wave_merge(lv, li);
-}
+union Region0 {  // 32 KB
+  TopEnt lists[WAVES * LIST];
+  uint2 cand[CAND_LDS];
+};
+union Region1 {  // 24 KB
+  unsigned int cnt[CNT_BINS];
+  unsigned long long hist[NBIN];
+  TopEnt surv[WAVES * LIST];
+  struct {
+    double sp[MAX_S * WAVES];
+    unsigned long long sq[MAX_S * WAVES];
+  } pass;
+};
+struct Small {
+  Args args;
+  Mode md;
+  float rf[WAVES];
+  int ri[WAVES];
+  double rd[WAVES + 1];
+  unsigned long long ru[WAVES + 1];
+  int rint[WAVES + 1];
+  unsigned int ticket;
+  float thv;
+  int thi;
+  float zmax;
+  int zarg;
+  double lse;
+  float Mp;
+  float szmax[MAX_S];
+  int szarg[MAX_S];
+  double slse[MAX_S];
+  unsigned int ncnd[MAX_S];
+  float mps[MAX_S];
+  double scale[MAX_S];
+  double msum[MAX_S];
+  int off[MAX_S + 1];
+  double side[MAX_S];
+  unsigned long long inR[MAX_S];
+  unsigned long long keepq[MAX_S];
+  double keep[MAX_S];
+  TopEnt mlist[LIST];  // the row's merged best-64
+  unsigned int rc[RBINS];
+  unsigned long long rm[RBINS];
+  int sel[16];
+  unsigned long long selu[4];
+  double seld[4];
+  unsigned int ncand;
+  unsigned int kmin, kmax;
+  int found;
+  int pos_hi, pos_lo, pos_last;
+};
 
-template <typename T>
-__device__ __forceinline__ T wave_sum(T x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-  return x;
-}
-
-// Inclusive scan within a wave.
-template <typename T>
-__device__ __forceinline__ T wave_incl_scan(T x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    T y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
-
-// Exclusive block scan (NW waves); *total gets the block sum.  Uses lds[NW+1].
-template <typename T, int NW>
-__device__ __forceinline__ T block_excl_scan(T x, T* lds, T* total) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  T inc = wave_incl_scan(x);
-  __syncthreads();
-  if (lane == 63) lds[wid] = inc;
-  __syncthreads();
-  if (wid == 0) {
-    T t = lane < NW ? lds[lane] : T(0);
-    T s = wave_incl_scan(t);
-    if (lane < NW) lds[lane] = s - t;
-    if (lane == NW - 1) lds[NW] = s;
-  }
-  __syncthreads();
-  T res = inc - x + lds[wid];
-  *total = lds[NW];
-  return res;
-}
-
-template <typename T, int NW>
-__device__ __forceinline__ T block_sum(T x, T* lds) {
-  T tot;
-  (void)block_excl_scan<T, NW>(x, lds, &tot);
-  return tot;
-}
-
-// =================================================================== k_scan ==
-
-template <int DT, bool VECOK>
-__global__ __launch_bounds__(SLICE_THREADS) void k_scan(Args a) {
-  __shared__ unsigned int s_cnt[NB];
-  __shared__ unsigned long long s_mass[NB];
-  __shared__ TopEnt s_top[4][64];
-  __shared__ float s_f[8];
-  __shared__ int s_i[8];
-  __shared__ double s_d[8];
-
-  const int s = blockIdx.x, r = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const Mode md = decode<DT>(a, r);
-  const void* row = row_ptr<DT>(a, r);
-  const int beg = s * a.L;
-  const int end = min(a.V, beg + a.L);
-
-  float bm = -INFINITY;
-  int bi = INT_MAX;
-  float tm = -INFINITY, ts = 0.0f;
-  float lv = -INFINITY;
-  int li = INT_MAX;
-  float thr_v = -INFINITY;
-  int thr_i = INT_MAX;
-
-  for (int base = beg; base < end; base += ITER_ELEMS) {
-    const int i0 = base + tid * VEC;
-    float v[VEC];
-    int nv;
-    load8<DT, VECOK>(row, i0, end, v, nv);
-#pragma unroll
-    for (int j = 0; j < VEC; ++j)
-      if (j < nv && v[j] > bm) {
-        bm = v[j];
-        bi = i0 + j;
-      }
-    if (md.need_lse) {
-      float m8 = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) m8 = fmaxf(m8, v[j]);
-      if (m8 > tm) {
-        ts *= wexp(tm, m8);
-        tm = m8;
-      }
-#pragma unroll
-      for (int j = 0; j < VEC; ++j)
-        if (j < nv) ts += wexp(v[j], tm);
-    }
-    if (md.K > 0) {
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        float ev = j < nv ? v[j] : -INFINITY;
-        int ei = j < nv ? i0 + j : INT_MAX;
-        const bool c = better(ev, ei, thr_v, thr_i);
-        if (__ballot(c)) {
-          if (!c) {
-            ev = -INFINITY;
-            ei = INT_MAX;
-          }
-          wave_sort(ev, ei);
-          wave_list_merge(lv, li, ev, ei);
-          thr_v = __shfl(lv, md.K - 1, 64);
-          thr_i = __shfl(li, md.K - 1, 64);
-        }
-      }
-    }
-  }
-
-  // ---- block argmax (v desc, i asc)
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float ov = __shfl_xor(bm, o, 64);
-    int oi = __shfl_xor(bi, o, 64);
-    if (better(ov, oi, bm, bi)) {
-      bm = ov;
-      bi = oi;
-    }
-  }
-  if (lane == 0) {
-    s_f[wid] = bm;
-    s_i[wid] = bi;
-  }
-  // ---- LSE partial
-  if (md.need_lse) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      float om = __shfl_xor(tm, o, 64);
-      float os = __shfl_xor(ts, o, 64);
-      float nm = fmaxf(tm, om);
-      ts = ts * wexp(tm, nm) + os * wexp(om, nm);
-      tm = nm;
-    }
-    if (lane == 0) {
-      s_f[4 + wid] = tm;
-      s_d[wid] = ts;
-    }
-  }
-  __syncthreads();
-  float zmax = s_f[0];
-  int zarg = s_i[0];
-  for (int w = 1; w < 4; ++w)
-    if (better(s_f[w], s_i[w], zmax, zarg)) {
-      zmax = s_f[w];
-      zarg = s_i[w];
-    }
-  if (tid == 0) {
-    SliceRec rc;
-    rc.zmax = zmax;
-    rc.zarg = zarg;
-    rc.lse_s = 0.0f;
-    rc.pad = 0.0f;
-    if (md.need_lse) {
-      double acc = 0.0;
-      for (int w = 0; w < 4; ++w) acc += s_d[w] * wexp_d(s_f[4 + w], zmax);
-      rc.lse_s = static_cast<float>(acc);
-    }
-    a.rec[r * a.S + s] = rc;
-  }
-
-  // ---- top-K: merge the four wave lists
-  if (md.K > 0) {
-    s_top[wid][lane].v = lv;
-    s_top[wid][lane].i = li;
-    __syncthreads();
-    if (wid == 0) {
-      for (int w = 1; w < 4; ++w) wave_list_merge(lv, li, s_top[w][lane].v, s_top[w][lane].i);
-      if (lane < md.K) {
-        TopEnt e;
-        e.v = lv;
-        e.i = li;
-        a.top[(static_cast<size_t>(r) * a.S + s) * a.K_max + lane] = e;
-      }
-    }
-  }
-
-  // ---- histogram of z' (count, fixed-point mass relative to the slice max z')
-  if (md.kind == KIND_HIST) {
-    for (int b = tid; b < NB; b += SLICE_THREADS) {
-      s_cnt[b] = 0u;
-      s_mass[b] = 0ull;
-    }
-    __syncthreads();
-    const float mps = round_dt<DT>(zmax / md.Tr);
-    for (int base = beg; base < end; base += ITER_ELEMS) {
-      const int i0 = base + tid * VEC;
-      float v[VEC];
-      int nv;
-      load8<DT, VECOK>(row, i0, end, v, nv);
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        if (j < nv) {
-          const float zp = round_dt<DT>(v[j] / md.Tr);
-          const unsigned int b = f2key(zp) >> BIN_SHIFT;
-          atomicAdd(&s_cnt[b], 1u);
-          const unsigned long long q = quant(wexp(zp, mps));
-          if (q) atomicAdd(&s_mass[b], q);
-        }
-      }
-    }
-    __syncthreads();
-    const size_t off = (static_cast<size_t>(r) * a.S + s) * NB;
-    for (int b = tid; b < NB; b += SLICE_THREADS) {
-      a.hcnt[off + b] = s_cnt[b];
-      a.hmass[off + b] = s_mass[b];
-    }
-  }
-}
-
-// =================================================================== k_plan ==
-
-template <int DT>
-__global__ __launch_bounds__(ROW_THREADS) void k_plan(Args a) {
-  __shared__ float s_mps[MAX_S];
-  __shared__ double s_scale[MAX_S];
-  __shared__ TopEnt s_top[MAX_S * 64];
-  __shared__ unsigned int s_scan_u[ROW_WAVES + 1];
-  __shared__ double s_scan_d[ROW_WAVES + 1];
-  __shared__ int s_res[4];
-  __shared__ float s_zmax;
-  __shared__ int s_zarg;
-  __shared__ double s_lse;
-
-  const int r = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const Mode md = decode<DT>(a, r);
-  const int S = a.S;
-
-  // ---- combine slice records (wave 0; S <= 64)
-  if (wid == 0) {
-    float zm = -INFINITY;
-    int za = INT_MAX;
-    float ls = 0.0f;
-    if (lane < S) {
-      const SliceRec rc = a.rec[r * S + lane];
-      zm = rc.zmax;
-      za = rc.zarg;
-      ls = rc.lse_s;
-    }
-    float bm = zm;
-    int bi = za;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      float ov = __shfl_xor(bm, o, 64);
-      int oi = __shfl_xor(bi, o, 64);
-      if (better(ov, oi, bm, bi)) {
-        bm = ov;
-        bi = oi;
-      }
-    }
-    double part = (lane < S && md.need_lse) ? static_cast<double>(ls) * wexp_d(zm, bm) : 0.0;
-    part = wave_sum(part);
-    if (md.sampling && lane < S) {
-      const float mps = round_dt<DT>(zm / md.Tr);
-      const float Mp = round_dt<DT>(bm / md.Tr);
-      s_mps[lane] = mps;
-      s_scale[lane] = wexp_d(mps, Mp);
-    }
-    if (lane == 0) {
-      s_zmax = bm;
-      s_zarg = bi;
-      s_lse = md.need_lse ? static_cast<double>(bm) + log(part) : static_cast<double>(NAN);
-    }
-  }
-  __syncthreads();
-  const float zmax = s_zmax;
-  const int zarg = s_zarg;
-  const double lse = s_lse;
-
-  if (tid == 0) {
-    RowState st;
-    st.kind = md.kind;
-    st.zarg = zarg;
-    st.zmax = zmax;
-    st.Mp = md.sampling ? round_dt<DT>(zmax / md.Tr) : 0.0f;
-    st.lse = lse;
-    st.b_lo = NB;
-    st.b_hi = -1;
-    st.cnt_above = 0;
-    st.vkey = 0;
-    st.idx_cut = INT_MAX;
-    st.s_star = 0;
-    st.target_rem = 0;
-    a.rs[r] = st;
-    if (md.kind == KIND_GREEDY) {
-      a.out_ids[r] = zarg;
-      if (a.out_lp)
-        a.out_lp[r] = md.want_lp ? static_cast<float>(static_cast<double>(zmax) - lse) : NAN;
-    }
-  }
-
-  // ---- top_logprobs: merge the S sorted slice lists
-  if (a.K_max > 0) {
-    const int K = md.K;
-    const int n = S * K;
-    for (int e = tid; e < n; e += ROW_THREADS) s_top[e] = a.top[(static_cast<size_t>(r) * S + e / K) * a.K_max + e % K];
-    __syncthreads();
-    for (int e = tid; e < n; e += ROW_THREADS) {
-      const TopEnt me = s_top[e];
-      const int own = e / K;
-      int rank = e % K;
-      for (int t = 0; t < S; ++t) {
-        if (t == own) continue;
-        int lo = 0, hi = K;  // count entries of list t better than me
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          const TopEnt o = s_top[t * K + mid];
-          if (better(o.v, o.i, me.v, me.i))
-            lo = mid + 1;
-          else
-            hi = mid;
-        }
-        rank += lo;
-      }
-      if (rank < K && me.i < a.V) {
-        a.out_top_ids[static_cast<size_t>(r) * a.K_max + rank] = me.i;
-        a.out_top_lp[static_cast<size_t>(r) * a.K_max + rank] =
-            static_cast<float>(static_cast<double>(me.v) - lse);
-      }
-    }
-    for (int c = K + tid; c < a.K_max; c += ROW_THREADS) {
-      a.out_top_ids[static_cast<size_t>(r) * a.K_max + c] = -1;
-      a.out_top_lp[static_cast<size_t>(r) * a.K_max + c] = -INFINITY;
-    }
-  }
-
-  if (md.kind != KIND_HIST) return;
-
-  // ---- combined histogram, scanned from the top bin down
-  // Thread t owns descending positions q = 2t, 2t+1 (bins NB-1-2t, NB-2-2t).
-  const size_t hbase = static_cast<size_t>(r) * S * NB;
-  unsigned int c[2] = {0u, 0u};
-  double m[2] = {0.0, 0.0};
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int b = NB - 1 - (2 * tid + h);
-    for (int t = 0; t < S; ++t) {
-      c[h] += a.hcnt[hbase + static_cast<size_t>(t) * NB + b];
-      m[h] += static_cast<double>(a.hmass[hbase + static_cast<size_t>(t) * NB + b]) * s_scale[t];
-    }
-  }
-  unsigned int ctot;
-  double mtot;
-  const unsigned int cex = block_excl_scan<unsigned int, ROW_WAVES>(c[0] + c[1], s_scan_u, &ctot);
-  const double mex = block_excl_scan<double, ROW_WAVES>(m[0] + m[1], s_scan_d, &mtot);
-  const unsigned int cin[2] = {cex + c[0], cex + c[0] + c[1]};
-  const double min_[2] = {mex + m[0], mex + m[0] + m[1]};
-  const unsigned int cprev[2] = {cex, cin[0]};
-  const double mprev[2] = {mex, min_[0]};
-
-  if (tid == 0) {
-    s_res[0] = -1;
-    s_res[1] = -1;
-    s_res[2] = -1;
-    s_res[3] = NB;
-  }
-  __syncthreads();
-  // top-k boundary bin: first position whose inclusive count reaches k.
-  if (md.kk > 0) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      if (cin[h] >= static_cast<unsigned int>(md.kk) && cprev[h] < static_cast<unsigned int>(md.kk))
-        s_res[0] = NB - 1 - (2 * tid + h);
-  }
-  // lowest non-empty bin
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-    if (c[h]) atomicMin(&s_res[3], NB - 1 - (2 * tid + h));
-  __syncthreads();
-  const int b_k = s_res[0];
-  double W_lo = mtot, W_hi = mtot;
-  if (md.kk > 0) {
-    // masses strictly above and including b_k
-    const int q = NB - 1 - b_k;
-    if ((q >> 1) == tid) {
-      const int h = q & 1;
-      s_scan_d[0] = mprev[h];
-      s_scan_d[1] = min_[h];
-    }
-    __syncthreads();
-    W_lo = s_scan_d[0];
-    W_hi = s_scan_d[1];
-    __syncthreads();
-  }
-  int lo_bin, hi_bin;
-  if (md.topp) {
-    const double eps = 1e-5;
-    const double t_hi = static_cast<double>(md.pr) * W_lo * (1.0 - eps);  // highest crossing
-    const double t_lo = static_cast<double>(md.pr) * W_hi * (1.0 + eps);  // lowest crossing
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int b = NB - 1 - (2 * tid + h);
-      if (min_[h] >= t_hi && (2 * tid + h == 0 || mprev[h] < t_hi)) s_res[1] = b;
-      if (min_[h] >= t_lo && (2 * tid + h == 0 || mprev[h] < t_lo)) s_res[2] = b;
-    }
-    __syncthreads();
-    int bp_hi = s_res[1] < 0 ? s_res[3] : s_res[1];
-    int bp_lo = s_res[2] < 0 ? s_res[3] : s_res[2];
-    if (md.kk > 0) {
-      lo_bin = b_k;
-      hi_bin = bp_hi > b_k ? bp_hi : b_k;
-    } else {
-      lo_bin = bp_lo;
-      hi_bin = bp_hi;
-    }
-  } else {
-    lo_bin = b_k;
-    hi_bin = b_k;
-  }
-  // count strictly above hi_bin
-  if (tid == 0) s_res[0] = 0;
-  __syncthreads();
-  {
-    const int q = NB - 1 - hi_bin;
-    if ((q >> 1) == tid) s_res[0] = static_cast<int>(cprev[q & 1]);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    a.rs[r].b_lo = lo_bin;
-    a.rs[r].b_hi = hi_bin;
-    a.rs[r].cnt_above = static_cast<unsigned int>(s_res[0]);
-  }
-}
-
-// ================================================================ k_extract ==
-
-template <int DT, bool VECOK>
-__global__ __launch_bounds__(SLICE_THREADS) void k_extract(Args a) {
-  __shared__ int s_scan[5];
-  __shared__ unsigned long long s_u64[5];
-
-  const int s = blockIdx.x, r = blockIdx.y;
-  const int tid = threadIdx.x;
-  const RowState st = a.rs[r];
-  if (st.kind == KIND_GREEDY) return;
-  const Mode md = decode<DT>(a, r);
-  const void* row = row_ptr<DT>(a, r);
-  const int beg = s * a.L;
-  const int end = min(a.V, beg + a.L);
-  const float Mp = st.Mp;
-  const unsigned int blo = static_cast<unsigned int>(st.b_lo);
-  const int bhi = st.b_hi;
-  uint2* cand = a.cand + (static_cast<size_t>(r) * a.S + s) * a.L;
-
-  unsigned long long tot = 0, above = 0;
-  int ncand = 0;
-  for (int base = beg; base < end; base += ITER_ELEMS) {
-    const int i0 = base + tid * VEC;
-    float v[VEC];
-    int nv;
-    load8<DT, VECOK>(row, i0, end, v, nv);
-    unsigned int keys[VEC];
-    unsigned int cm = 0;
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const float zp = round_dt<DT>(v[j] / md.Tr);
-      keys[j] = f2key(zp);
-      const int b = static_cast<int>(keys[j] >> BIN_SHIFT);
-      const unsigned long long q = j < nv ? quant(wexp(zp, Mp)) : 0ull;
-      tot += q;
-      if (b > bhi) above += q;
-      if (j < nv && b >= static_cast<int>(blo) && b <= bhi) cm |= 1u << j;
-    }
-    if (st.kind == KIND_HIST) {
-      int total;
-      const int cnt = __popc(cm);
-      const int ex = block_excl_scan<int, 4>(cnt, s_scan, &total);
-      int pos = ncand + ex;
-#pragma unroll
-      for (int j = 0; j < VEC; ++j)
-        if (cm & (1u << j)) cand[pos++] = make_uint2(keys[j], static_cast<unsigned int>(i0 + j));
-      ncand += total;
-    }
-  }
-  tot = block_sum<unsigned long long, 4>(tot, s_u64);
-  above = block_sum<unsigned long long, 4>(above, s_u64);
-  if (tid == 0) {
-    SliceMass m;
-    m.above = above;
-    m.total = tot;
-    m.ncand = static_cast<unsigned int>(ncand);
-    m.pad0 = 0;
-    m.pad1 = 0;
-    a.sm[r * a.S + s] = m;
-  }
-}
-
-// ================================================================= k_select ==
-
-// Candidate list of one row: per-slice regions concatenated in slice order.
+// A row's candidate list: in LDS, in global memory contiguous, or in global
+// memory as the per-slice regions of the first pass (located through off[]).
 struct CandView {
-  const uint2* g;   // global base of the row's regions
-  const uint2* l;   // LDS copy, or nullptr
-  const int* off;   // [S+1] prefix of per-slice counts (LDS)
+  uint2* l;
+  uint2* g;
+  const int* off;  // nullptr: g is contiguous
   int S, L;
-  __device__ __forceinline__ uint2 get(int c) const {
-    if (l) return l[c];
-    int lo = 0, hi = S;  // slice s with off[s] <= c < off[s+1]
+  __device__ __forceinline__ uint2* at(int c) const {
+    if (!off) return g + c;
+    int lo = 0, hi = S;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
       if (off[mid] <= c)
@@ -827,396 +240,1139 @@ struct CandView {
       else
         hi = mid;
     }
-    return g[static_cast<size_t>(lo) * L + (c - off[lo])];
+    return g + static_cast<size_t>(lo) * L + (c - off[lo]);
   }
+  // candidate c (global entries may come from other workgroups)
+  __device__ __forceinline__ uint2 get(int c) const { return l ? l[c] : ld_dev2(at(c)); }
 };
 
-// Digit (descending) at which the running total crosses `target`, over a
-// 256-bin histogram held in LDS; wave 0 only.  Returns the digit and, through
-// *before, the sum of the digits above it.  `mode_count`: crossing is
-// before < target <= before + h[d]; mass mode: first d with before + h[d] >=
-// target (falls back to the lowest non-empty digit via cnt).
-template <typename T>
-__device__ __forceinline__ int find_digit(const T* h, const unsigned int* cnt, T target, T* before,
-                                          bool* none) {
-  const int lane = threadIdx.x & 63;
-  T loc[4];
-  T sum = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    loc[j] = h[255 - (4 * lane + j)];
-    sum += loc[j];
-  }
-  T inc = wave_incl_scan(sum);
-  T ex = inc - sum;
-  int found = 256;
-  T bef = 0;
-  T run = ex;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (found == 256 && run + loc[j] >= target && loc[j] > 0) {
-      found = 4 * lane + j;
-      bef = run;
+// --------------------------------------------------- radix selection (block) --
+//
+// One selection over the candidates that satisfy `part(e)`, on the field
+// F(e) = e.x (key) or e.y (index), scanning values in descending or ascending
+// order, measuring either counts or fixed-point masses wq(e).  It returns the
+// first value v in scan order at which  before + measure(v) >= target
+// (> target when strict) with measure(v) > 0, where `before` is the measure of
+// the values that precede v; *before_out gets `before`, *gcount the number of
+// participants equal to v.  In mass mode, when no value qualifies (the target
+// exceeds the total), the last value in scan order is returned and *none is
+// set.  Rounds of 8-bit digits; the leading digits the participants all share
+// are skipped.  Must be called by the whole workgroup.
+template <bool BY_KEY, bool DESC, bool MASS, typename PART, typename WQ>
+__device__ unsigned int radix_select(const CandView& cv, int n, PART part, WQ wq,
+                                     unsigned long long target, bool strict, Small& sh,
+                                     unsigned long long* before_out, unsigned int* gcount,
+                                     bool* none) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  // ---- range of the field over participants, and their count and measure
+  unsigned int lo = 0xffffffffu, hi = 0u;
+  unsigned long long cnt_all = 0, mass_all = 0;
+  for (int c = tid; c < n; c += THREADS) {
+    const uint2 e = cv.get(c);
+    if (part(e)) {
+      const unsigned int f = BY_KEY ? e.x : e.y;
+      lo = min(lo, f);
+      hi = max(hi, f);
+      cnt_all += 1;
+      if (MASS) mass_all += wq(e);
     }
-    run += loc[j];
   }
-  // lowest descending position with a hit
-  int best = found;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) best = min(best, __shfl_xor(best, o, 64));
-  T bsel = 0;
-  const unsigned long long who = __ballot(found == best && best < 256);
-  if (who) {
-    const int src = __ffsll(static_cast<long long>(who)) - 1;
-    bsel = __shfl(bef, src, 64);
+  for (int o = 32; o > 0; o >>= 1) {
+    lo = min(lo, __shfl_xor(lo, o, 64));
+    hi = max(hi, __shfl_xor(hi, o, 64));
   }
-  if (best < 256) {
-    *none = false;
-    *before = bsel;
-    return 255 - best;
+  if (tid == 0) {
+    sh.kmin = 0xffffffffu;
+    sh.kmax = 0u;
   }
-  // no crossing: lowest non-empty digit, everything above it counted
-  int low = -1;
+  __syncthreads();
+  if (lane == 0) {
+    atomicMin(&sh.kmin, lo);
+    atomicMax(&sh.kmax, hi);
+  }
+  cnt_all = block_sum<unsigned long long>(cnt_all, sh.ru);
+  if (MASS) mass_all = block_sum<unsigned long long>(mass_all, sh.ru);
+  lo = sh.kmin;
+  hi = sh.kmax;
+  __syncthreads();
+  if (cnt_all == 0) {
+    *before_out = 0;
+    *gcount = 0;
+    *none = true;
+    return 0;
+  }
+  const unsigned long long tot = MASS ? mass_all : cnt_all;
+  const bool reach = strict ? tot > target : tot >= target;
+  if (lo == hi) {  // a single value
+    *before_out = 0;
+    *gcount = static_cast<unsigned int>(cnt_all);
+    *none = MASS && !reach;
+    return lo;
+  }
+  if (MASS && !reach) {
+    // nothing qualifies: the last value in scan order, everything before it
+    const unsigned int v = DESC ? lo : hi;
+    unsigned long long cv_cnt = 0, cv_mass = 0;
+    for (int c = tid; c < n; c += THREADS) {
+      const uint2 e = cv.get(c);
+      if (part(e) && (BY_KEY ? e.x : e.y) == v) {
+        cv_cnt += 1;
+        cv_mass += wq(e);
+      }
+    }
+    cv_cnt = block_sum<unsigned long long>(cv_cnt, sh.ru);
+    cv_mass = block_sum<unsigned long long>(cv_mass, sh.ru);
+    *before_out = mass_all - cv_mass;
+    *gcount = static_cast<unsigned int>(cv_cnt);
+    *none = true;
+    return v;
+  }
+  const unsigned int diff = lo ^ hi;
+  const int top = 31 - __clz(static_cast<int>(diff));
+  int shift = (top >> 3) << 3;
+  unsigned int mask = shift + 8 >= 32 ? 0u : ~((1u << (shift + 8)) - 1u);
+  unsigned int prefix = lo & mask;
+  unsigned long long before = 0;
+  unsigned int g = 0;
+  for (; shift >= 0; shift -= 8) {
+    for (int d = tid; d < RBINS; d += THREADS) {
+      sh.rc[d] = 0u;
+      if (MASS) sh.rm[d] = 0ull;
+    }
+    __syncthreads();
+    for (int base = 0; base < n; base += THREADS) {
+      const int c = base + tid;
+      uint2 e = make_uint2(0u, 0u);
+      bool act = false;
+      if (c < n) {
+        e = cv.get(c);
+        const unsigned int f = BY_KEY ? e.x : e.y;
+        act = part(e) && (f & mask) == prefix;
+      }
+      const unsigned int f = BY_KEY ? e.x : e.y;
+      const int d = static_cast<int>((f >> shift) & 255u);
+      lds_cnt_agg(sh.rc, d, act);
+      if (MASS) lds_add_agg(sh.rm, d, act ? wq(e) : 0ull, act);
+    }
+    __syncthreads();
+    if (wid == 0) {
+      // lane l owns scan positions 4l..4l+3
+      unsigned long long val[4];
+      unsigned int cnt[4];
+      unsigned long long sum = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (cnt[255 - (4 * lane + j)]) low = max(low, 4 * lane + j);
+      for (int q = 0; q < 4; ++q) {
+        const int pos = 4 * lane + q;
+        const int d = DESC ? RBINS - 1 - pos : pos;
+        cnt[q] = sh.rc[d];
+        val[q] = MASS ? sh.rm[d] : static_cast<unsigned long long>(cnt[q]);
+        sum += val[q];
+      }
+      const unsigned long long inc = wave_incl_scan(sum);
+      unsigned long long run = inc - sum;
+      const unsigned long long tg = target > before ? target - before : 0ull;
+      int found = 4 * 64, lastne = -1;
+      unsigned long long bef = 0, bef_last = 0;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) low = max(low, __shfl_xor(low, o, 64));
-  T bsum = 0;
+      for (int q = 0; q < 4; ++q) {
+        const int pos = 4 * lane + q;
+        if (found == 4 * 64 && val[q] > 0 && (strict ? run + val[q] > tg : run + val[q] >= tg)) {
+          found = pos;
+          bef = run;
+        }
+        if (cnt[q] > 0) {
+          lastne = pos;
+          bef_last = run;
+        }
+        run += val[q];
+      }
+      int best = found;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (4 * lane + j < low) bsum += loc[j];
-  bsum = wave_sum(bsum);
-  *none = true;
-  *before = bsum;
-  return low < 0 ? 0 : 255 - low;
+      for (int o = 32; o > 0; o >>= 1) best = min(best, __shfl_xor(best, o, 64));
+      int lbest = lastne;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) lbest = max(lbest, __shfl_xor(lbest, o, 64));
+      // the total reaches the target, so some digit qualifies; the last
+      // non-empty digit only guards against a total that rounding made short
+      unsigned long long b;
+      if (best < 4 * 64) {
+        b = __shfl(bef, best >> 2, 64);
+      } else {
+        best = lbest < 0 ? 0 : lbest;
+        b = __shfl(bef_last, best >> 2, 64);
+      }
+      if (lane == 0) {
+        const int d = DESC ? RBINS - 1 - best : best;
+        sh.sel[0] = d;
+        sh.sel[2] = static_cast<int>(sh.rc[d]);
+        sh.selu[0] = b;
+      }
+    }
+    __syncthreads();
+    prefix |= static_cast<unsigned int>(sh.sel[0]) << shift;
+    mask |= 255u << shift;
+    before += sh.selu[0];
+    g = static_cast<unsigned int>(sh.sel[2]);
+    __syncthreads();
+  }
+  *before_out = before;
+  *gcount = g;
+  *none = false;
+  return prefix;
+}
+
+// -------------------------------------------------- candidate-set finishing --
+
+// Top-k (then optionally top-p) and the draw, all on a candidate set that holds
+// every element whose z' reaches the row's k-th largest z' (keys are z' keys).
+// Returns the drawn index.
+__device__ int resolve_topk(const Mode& md, const CandView& cv, int n, float Mp, Small& sh) {
+  auto wq = [Mp](uint2 e) { return quant(wexp(key2f(e.x), Mp)); };
+  auto all = [](uint2) { return true; };
+  unsigned long long bef;
+  unsigned int g;
+  bool none;
+  // (1) k-th largest key, with multiplicity
+  const unsigned int tau = radix_select<true, true, false>(
+      cv, n, all, wq, static_cast<unsigned long long>(md.kk), false, sh, &bef, &g, &none);
+  // (2) mass of the top-k set
+  unsigned long long wk = 0;
+  for (int c = threadIdx.x; c < n; c += THREADS) {
+    const uint2 e = cv.get(c);
+    if (e.x >= tau) wk += wq(e);
+  }
+  wk = block_sum<unsigned long long>(wk, sh.ru);
+  unsigned int vkey = tau;
+  int idx_cut = INT_MAX;
+  unsigned long long Wf = wk;
+  if (md.topp) {
+    // (3) nucleus cutoff: keep while the mass before an element is < p * W_k
+    const unsigned long long PW =
+        static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(wk)));
+    auto ge_tau = [tau](uint2 e) { return e.x >= tau; };
+    unsigned long long pgt;
+    vkey = radix_select<true, true, true>(cv, n, ge_tau, wq, PW, false, sh, &pgt, &g, &none);
+    const unsigned long long wstar = wq(make_uint2(vkey, 0u));
+    unsigned long long t = g;
+    if (!none && wstar > 0) {
+      const unsigned long long need = PW > pgt ? (PW - pgt + wstar - 1) / wstar : 0ull;
+      t = need < t ? need : t;
+    }
+    if (t == 0) t = 1;
+    if (t < g) {  // (4) the t-th smallest index among the ties at the cutoff
+      auto eq_v = [vkey](uint2 e) { return e.x == vkey; };
+      idx_cut = static_cast<int>(
+          radix_select<false, false, false>(cv, n, eq_v, wq, t, false, sh, &bef, &g, &none));
+    }
+    Wf = pgt + t * wstar;
+  }
+  // (5) inverse-CDF draw in vocabulary order over the kept set
+  unsigned long long T = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(Wf));
+  if (Wf == 0)
+    T = 0;
+  else if (T >= Wf)
+    T = Wf - 1;
+  auto kept = [vkey, idx_cut](uint2 e) {
+    return e.x > vkey || (e.x == vkey && static_cast<int>(e.y) <= idx_cut);
+  };
+  if (Wf == 0) {  // every kept weight underflowed: the lowest kept index
+    return static_cast<int>(radix_select<false, false, false>(cv, n, kept, wq, 1ull, false, sh, &bef,
+                                                              &g, &none));
+  }
+  return static_cast<int>(radix_select<false, false, true>(cv, n, kept, wq, T, true, sh, &bef, &g, &none));
+}
+
+// ------------------------------------------------------- last-block stages --
+
+// Walk slice s in vocabulary order; the first kept element at which the
+// running mass w(z', mps_s) exceeds rem is the draw.  Kept: key(z') > vkey, or
+// equal with index <= idx_cut.  Thread t owns EPT consecutive elements.
+template <int DT, int EPT, bool VECOK>
+__device__ int final_scan(const Args& a, const Mode& md, const void* row, int s, double rem,
+                          unsigned int vkey, int idx_cut, Small& sh) {
+  const int tid = threadIdx.x;
+  const int b0 = s * a.L;
+  const int e0 = min(a.V, b0 + a.L);
+  const float mps = sh.mps[s];
+  const int my0 = b0 + tid * EPT;
+  auto weight = [&](float z, int i) {
+    const float zp = fz<DT>(z, md.Tr);
+    const unsigned int key = f2key(zp);
+    const bool kept = i < e0 && (key > vkey || (key == vkey && i <= idx_cut));
+    return kept ? wexp(zp, mps) : 0.0f;
+  };
+  float z[EPT];
+#pragma unroll
+  for (int it = 0; it < EPT / VEC; ++it) load8<DT, VECOK>(row, my0 + it * VEC, e0, z + it * VEC);
+  double sum = 0.0;
+  int last_pos = -1;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const float ww = weight(z[e], my0 + e);
+    sum += static_cast<double>(ww);
+    if (ww > 0.0f) last_pos = my0 + e;
+  }
+  double ex, in, tot;
+  block_scan<double>(sum, sh.rd, &ex, &in, &tot);
+  if (tid == 0) sh.found = -1;
+  __syncthreads();
+  if (ex <= rem && rem < in) {
+    double c = ex;
+    int pick = -1;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const float ww = weight(z[e], my0 + e);
+      c += static_cast<double>(ww);
+      if (pick < 0 && c > rem && ww > 0.0f) pick = my0 + e;
+    }
+    sh.found = pick < 0 ? last_pos : pick;  // rounding inside the thread: its last positive element
+  }
+  __syncthreads();
+  int id = sh.found;
+  if (id < 0) {  // rem at or past the slice total (fp64 rounding): last kept element
+    int lp = last_pos;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lp = max(lp, __shfl_xor(lp, o, 64));
+    if ((tid & 63) == 0) sh.rint[tid >> 6] = lp;
+    __syncthreads();
+    if (tid == 0) {
+      int m = -1;
+      for (int w2 = 0; w2 < WAVES; ++w2) m = max(m, sh.rint[w2]);
+      sh.found = m < 0 ? b0 : m;
+    }
+    __syncthreads();
+    id = sh.found;
+  }
+  return id;
 }
 
 template <int DT>
-__global__ __launch_bounds__(ROW_THREADS) void k_select(Args a) {
-  __shared__ uint2 s_cand[CAND_LDS];
-  __shared__ unsigned int s_hc[256];
-  __shared__ unsigned long long s_hm[256];
-  __shared__ int s_off[MAX_S + 1];
-  __shared__ unsigned long long s_above[MAX_S];
-  __shared__ unsigned long long s_total[MAX_S];
-  __shared__ unsigned long long s_keep[MAX_S];
-  __shared__ unsigned long long s_u64[ROW_WAVES + 1];
-  __shared__ int s_int[ROW_WAVES + 1];
-  __shared__ unsigned int s_sel[4];
-  __shared__ unsigned long long s_selm[2];
-  __shared__ int s_cut;
+__device__ void write_sampled(const Args& a, const Mode& md, const void* row, int r, int id,
+                              const Small& sh) {
+  if (threadIdx.x != 0) return;
+  a.out_ids[r] = id;
+  if (a.out_lp)
+    a.out_lp[r] = md.want_lp ? static_cast<float>(static_cast<double>(ld1<DT>(row, id)) - sh.lse)
+                             : NAN;
+}
 
-  const int r = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  RowState st = a.rs[r];
-  if (st.kind == KIND_GREEDY) return;
-  const Mode md = decode<DT>(a, r);
-  const int S = a.S;
-
-  if (tid < S) {
-    const SliceMass m = a.sm[r * S + tid];
-    s_above[tid] = m.above;
-    s_total[tid] = m.total;
-    s_keep[tid] = m.above;
-    s_off[tid + 1] = static_cast<int>(m.ncand);
+// Index of the slice holding u * (total kept mass) and the remaining target in
+// that slice's own units.  keep[t] are slice-unit masses, scale[t] converts them
+// to row units.
+__device__ void pick_slice(const double* keep, const double* scale, int S, float u, int* sst_out,
+                           double* rem_out) {
+  double W = 0.0;
+  for (int t = 0; t < S; ++t) W += keep[t] * scale[t];
+  const double T = static_cast<double>(u) * W;
+  double cum = 0.0, before = 0.0;
+  int sst = -1;
+  for (int t = 0; t < S; ++t) {
+    const double m = keep[t] * scale[t];
+    if (m > 0.0) {
+      sst = t;
+      before = cum;
+      if (cum + m > T) break;
+    }
+    cum += m;
   }
-  if (tid == 0) s_off[0] = 0;
+  if (sst < 0) {
+    sst = 0;
+    before = 0.0;
+  }
+  *sst_out = sst;
+  *rem_out = scale[sst] > 0.0 ? (T - before) / scale[sst] : 0.0;
+}
+
+// Temperature only: all elements kept.
+template <int DT, int EPT, bool VECOK>
+__device__ void finish_temp(const Args& a, const Mode& md, const void* row, int r, Small& sh) {
+  if (threadIdx.x == 0) {
+    int sst;
+    double rem;
+    pick_slice(sh.msum, sh.scale, a.S, md.u, &sst, &rem);
+    sh.sel[0] = sst;
+    sh.seld[0] = rem;
+  }
   __syncthreads();
-  if (tid == 0)
-    for (int t = 0; t < S; ++t) s_off[t + 1] += s_off[t];
-  __syncthreads();
+  const int id = final_scan<DT, EPT, VECOK>(a, md, row, sh.sel[0], sh.seld[0], 0u, INT_MAX, sh);
+  write_sampled<DT>(a, md, row, r, id, sh);
+}
 
-  unsigned int vkey = 0;
-  int idx_cut = INT_MAX;
-  unsigned long long W = 0;
+// Top-k <= 63 from the row's merged best-64 list, by one wave.  Returns false
+// when the list may miss elements tied at the k-th value of z' (then the caller
+// extracts the candidates from the row).
+template <int DT>
+__device__ bool klist_resolve(const Mode& md, float Mp, const Small& sh, int* id_out) {
+  const int lane = threadIdx.x & 63;
+  const float lv = sh.mlist[lane].v;
+  const int li = sh.mlist[lane].i;
+  const bool real = li != INT_MAX;
+  const float zp = real ? fz<DT>(lv, md.Tr) : -INFINITY;
+  const float tau = __shfl(zp, md.kk - 1, 64);
+  const int last_i = __shfl(li, LIST - 1, 64);
+  const float last_zp = __shfl(zp, LIST - 1, 64);
+  // every element with z' >= tau is in the list unless the list's last entry reaches tau
+  if (last_i != INT_MAX && !(last_zp < tau)) return false;
+  const bool in_k = real && zp >= tau;
+  float sv = in_k ? zp : -INFINITY;
+  int si = in_k ? li : INT_MAX;
+  wave_sort(sv, si);  // (z' desc, index asc)
+  const bool k1 = si != INT_MAX;
+  const unsigned long long w = k1 ? quant(wexp(sv, Mp)) : 0ull;
+  const unsigned long long incl = wave_incl_scan(w);
+  const unsigned long long Wk = __shfl(incl, 63, 64);
+  bool keep = k1;
+  if (md.topp) {
+    const unsigned long long PW =
+        static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
+    keep = k1 && (incl - w) < PW;
+  }
+  const unsigned long long wf = keep ? w : 0ull;
+  const unsigned long long Wf = wave_sum(wf);
+  unsigned long long T = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(Wf));
+  if (Wf == 0)
+    T = 0;
+  else if (T >= Wf)
+    T = Wf - 1;
+  // mass of kept entries with index <= mine, in vocabulary order
+  unsigned long long cum = 0;
+  for (int q = 0; q < 64; ++q) {
+    const unsigned int wlo = __builtin_amdgcn_readlane(static_cast<unsigned int>(wf), q);
+    const unsigned int whi = __builtin_amdgcn_readlane(static_cast<unsigned int>(wf >> 32), q);
+    const int iq = __builtin_amdgcn_readlane(si, q);
+    if (iq <= si) cum += pack2(wlo, whi);
+  }
+  int cand = (keep && (Wf == 0 || (wf > 0 && cum > T))) ? si : INT_MAX;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) cand = min(cand, __shfl_xor(cand, o, 64));
+  *id_out = cand == INT_MAX ? __shfl(si, 0, 64) : cand;
+  return true;
+}
 
-  if (st.kind == KIND_TEMP) {
-    for (int t = 0; t < S; ++t) W += s_total[t];
-    if (tid < S) s_keep[tid] = s_total[tid];
-  } else {
-    const int n = s_off[S];
-    const uint2* g = a.cand + static_cast<size_t>(r) * S * a.L;
-    const bool in_lds = n <= CAND_LDS;
-    if (in_lds) {
-      for (int t = 0; t < S; ++t) {
-        const int o = s_off[t], cnt = s_off[t + 1] - o;
-        for (int j = tid; j < cnt; j += ROW_THREADS) s_cand[o + j] = g[static_cast<size_t>(t) * a.L + j];
+// Compare-only pass over the row (the finishing workgroup alone): elements with
+// z key in [klo, khi) become candidates (z' key, index), and the in-range mass
+// of slice t (2^-42 units of w(z', mps_t)) goes to r1.pass.sq[t * WAVES + wave];
+// when `sum_side` is 1 (above: z key >= khi) or 2 (below: z key < klo) the mass
+// of that side goes to r1.pass.sp.  has_hi false: no upper bound.  G slices'
+// loads are in flight at once.
+template <int DT, int EPT, bool VECOK>
+__device__ void row_pass(const Args& a, const Mode& md, const void* row, int r, unsigned int klo,
+                         bool has_hi, unsigned int khi, int sum_side, Region0& r0, Region1& r1,
+                         Small& sh) {
+  constexpr int NIT = EPT / VEC;
+  constexpr int G = (DT == MLXF_DTYPE_F32 ? 32 : 64) / EPT;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int S = a.S;
+  uint2* g = a.cand + static_cast<size_t>(r) * S * a.L;
+#pragma unroll 1
+  for (int t0 = 0; t0 < S; t0 += G) {
+    Raw8<DT> q[G][NIT];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      const int t = t0 + gi;
+      if (t < S) {
+        const int b0 = t * a.L, e0 = min(a.V, b0 + a.L);
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) load_raw<DT, VECOK>(row, b0 + it * CHUNK + tid * VEC, e0, q[gi][it]);
       }
     }
-    __syncthreads();
-    CandView cv;
-    cv.g = g;
-    cv.l = in_lds ? s_cand : nullptr;
-    cv.off = s_off;
-    cv.S = S;
-    cv.L = a.L;
-
-    unsigned long long mass_above = 0;
-    for (int t = 0; t < S; ++t) mass_above += s_above[t];
-
-    // (1) top-k: k_rel-th largest key among candidates (ties kept)
-    unsigned int tau = 0;
-    if (md.kk > 0) {
-      unsigned int prefix = 0, mask = 0;
-      unsigned int krel = static_cast<unsigned int>(md.kk) - st.cnt_above;
-      for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int d = tid; d < 256; d += ROW_THREADS) s_hc[d] = 0u;
-        __syncthreads();
-        for (int c = tid; c < n; c += ROW_THREADS) {
-          const unsigned int key = cv.get(c).x;
-          if ((key & mask) == prefix) atomicAdd(&s_hc[(key >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        if (wid == 0) {
-          unsigned int bef;
-          bool none;
-          const int d = find_digit<unsigned int>(s_hc, s_hc, krel, &bef, &none);
-          if (lane == 0) {
-            s_sel[0] = static_cast<unsigned int>(d);
-            s_sel[1] = bef;
-          }
-        }
-        __syncthreads();
-        prefix |= s_sel[0] << shift;
-        mask |= 255u << shift;
-        krel -= s_sel[1];
-        __syncthreads();
-      }
-      tau = prefix;
-    }
-
-    // (2) mass of the top-k set: the candidates >= tau plus everything above R
-    // (bins below R are below tau).  Without top-k it is the whole row.
-    unsigned long long wk = 0;
-    if (md.kk > 0) {
-      for (int c = tid; c < n; c += ROW_THREADS) {
-        const unsigned int key = cv.get(c).x;
-        if (key >= tau) wk += quant(wexp(key2f(key), st.Mp));
-      }
-      wk = block_sum<unsigned long long, ROW_WAVES>(wk, s_u64) + mass_above;
-    } else {
-      for (int t = 0; t < S; ++t) wk += s_total[t];
-    }
-
-    if (!md.topp) {
-      vkey = tau;
-      idx_cut = INT_MAX;
-      W = wk;
-    } else {
-      // (3) nucleus: smallest v with (mass strictly above v) < p * W_k
-      const double x = static_cast<double>(md.pr) * static_cast<double>(wk);
-      const unsigned long long PW = static_cast<unsigned long long>(ceil(x));
-      unsigned long long P = mass_above;
-      unsigned int prefix = 0, mask = 0;
-      bool all_kept = false;
-      unsigned int gcount = 0;
-      for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int d = tid; d < 256; d += ROW_THREADS) {
-          s_hc[d] = 0u;
-          s_hm[d] = 0ull;
-        }
-        __syncthreads();
-        for (int c = tid; c < n; c += ROW_THREADS) {
-          const unsigned int key = cv.get(c).x;
-          if (key >= tau && (key & mask) == prefix) {
-            const unsigned int d = (key >> shift) & 255u;
-            atomicAdd(&s_hc[d], 1u);
-            const unsigned long long q = quant(wexp(key2f(key), st.Mp));
-            if (q) atomicAdd(&s_hm[d], q);
-          }
-        }
-        __syncthreads();
-        if (wid == 0) {
-          unsigned long long bef;
-          bool none;
-          // all_kept rounds keep picking the lowest non-empty digit
-          const unsigned long long tgt = all_kept ? ~0ull : (PW > P ? PW - P : 0ull);
-          const int d = find_digit<unsigned long long>(s_hm, s_hc, tgt, &bef, &none);
-          if (lane == 0) {
-            s_sel[0] = static_cast<unsigned int>(d);
-            s_sel[1] = none ? 1u : 0u;
-            s_sel[2] = s_hc[d];
-            s_selm[0] = bef;
-          }
-        }
-        __syncthreads();
-        prefix |= s_sel[0] << shift;
-        mask |= 255u << shift;
-        P += s_selm[0];
-        all_kept = all_kept || (s_sel[1] != 0u);
-        gcount = s_sel[2];
-        __syncthreads();
-      }
-      vkey = prefix;
-      const unsigned long long wstar = quant(wexp(key2f(vkey), st.Mp));
-      unsigned long long t = gcount;
-      if (!all_kept && wstar > 0) {
-        const unsigned long long need = (PW - P + wstar - 1) / wstar;
-        t = need < t ? need : t;
-      }
-      W = P + t * wstar;
-      // (4) index cut: the t-th candidate (buffer = index order) with key == v*
-      if (t >= gcount) {
-        idx_cut = INT_MAX;
-      } else {
-        const int per = (n + ROW_THREADS - 1) / ROW_THREADS;
-        const int c0 = tid * per, c1 = min(n, c0 + per);
-        int cnt = 0;
-        for (int c = c0; c < c1; ++c) cnt += cv.get(c).x == vkey ? 1 : 0;
-        int tot;
-        const int ex = block_excl_scan<int, ROW_WAVES>(cnt, s_int, &tot);
-        if (tid == 0) s_cut = INT_MAX;
-        __syncthreads();
-        const int want = static_cast<int>(t);  // 1-based rank
-        if (ex < want && ex + cnt >= want) {
-          int seen = ex;
-          for (int c = c0; c < c1; ++c) {
-            const uint2 e = cv.get(c);
-            if (e.x == vkey && ++seen == want) {
-              s_cut = static_cast<int>(e.y);
-              break;
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      const int t = t0 + gi;
+      if (t < S) {
+        const int b0 = t * a.L, e0 = min(a.V, b0 + a.L);
+        const float mps = sh.mps[t];
+        float part = 0.0f;
+        unsigned long long pq = 0;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          float z[VEC];
+          decode8<DT>(q[gi][it], z);
+          const int i0 = b0 + it * CHUNK + tid * VEC;
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            const int i = i0 + j;
+            const bool valid = i < e0;
+            const unsigned int zk = f2key(z[j]);
+            const bool above = valid && has_hi && zk >= khi;
+            const bool inr = valid && !above && zk >= klo;
+            const bool side = sum_side == 1 ? above : (sum_side == 2 && valid && !above && !inr);
+            unsigned int zpk = 0;
+            if (side || inr) {  // most elements need neither the division nor the exp
+              const float zp = fz<DT>(z[j], md.Tr);
+              const float w = wexp(zp, mps);
+              if (side) part += w;
+              if (inr) pq += quant(w);
+              zpk = f2key(zp);
+            }
+            const unsigned long long bal = __ballot(inr);
+            if (bal) {
+              unsigned int basepos = 0;
+              if (lane == 0) basepos = atomicAdd(&sh.ncand, static_cast<unsigned int>(__popcll(bal)));
+              basepos = __shfl(basepos, 0, 64);
+              if (inr) {
+                const unsigned int pos =
+                    basepos + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(bal >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(bal), 0u));
+                const uint2 ent = make_uint2(zpk, static_cast<unsigned int>(i));
+                st_dev(g + pos, ent);
+                if (pos < CAND_LDS) r0.cand[pos] = ent;
+              }
             }
           }
         }
-        __syncthreads();
-        idx_cut = s_cut;
-      }
-    }
-    // (5) kept mass per slice
-    for (int c = tid; c < n; c += ROW_THREADS) {
-      const uint2 e = cv.get(c);
-      const int idx = static_cast<int>(e.y);
-      if (e.x > vkey || (e.x == vkey && idx <= idx_cut)) {
-        const unsigned long long q = quant(wexp(key2f(e.x), st.Mp));
-        if (q) atomicAdd(&s_keep[idx / a.L], q);
-      }
-    }
-    __syncthreads();
-  }
-
-  if (tid == 0) {
-    unsigned long long tot = 0;
-    for (int t = 0; t < S; ++t) tot += s_keep[t];
-    W = tot;
-    const double x = static_cast<double>(md.u) * static_cast<double>(W);
-    unsigned long long tg = static_cast<unsigned long long>(x);
-    if (W == 0)
-      tg = 0;
-    else if (tg >= W)
-      tg = W - 1;
-    unsigned long long cum = 0;
-    int sst = S - 1;
-    for (int t = 0; t < S; ++t) {
-      if (cum + s_keep[t] > tg) {
-        sst = t;
-        break;
-      }
-      cum += s_keep[t];
-    }
-    a.rs[r].vkey = vkey;
-    a.rs[r].idx_cut = idx_cut;
-    a.rs[r].s_star = sst;
-    a.rs[r].target_rem = tg - cum;
-  }
-}
-
-// =================================================================== k_draw ==
-
-template <int DT, bool VECOK>
-__global__ __launch_bounds__(ROW_THREADS) void k_draw(Args a) {
-  __shared__ unsigned long long s_u64[ROW_WAVES + 1];
-  __shared__ int s_found;
-
-  const int r = blockIdx.x;
-  const int tid = threadIdx.x;
-  const RowState st = a.rs[r];
-  if (st.kind == KIND_GREEDY) return;
-  const Mode md = decode<DT>(a, r);
-  const void* row = row_ptr<DT>(a, r);
-  const int beg = st.s_star * a.L;
-  const int end = min(a.V, beg + a.L);
-  unsigned long long rem = st.target_rem;
-  if (tid == 0) s_found = -1;
-  __syncthreads();
-  for (int base = beg; base < end; base += ROW_THREADS * VEC) {
-    const int i0 = base + tid * VEC;
-    float v[VEC];
-    int nv;
-    load8<DT, VECOK>(row, i0, end, v, nv);
-    unsigned long long q[VEC];
-    unsigned long long sum = 0;
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const float zp = round_dt<DT>(v[j] / md.Tr);
-      const unsigned int key = f2key(zp);
-      const bool kept = j < nv && (key > st.vkey || (key == st.vkey && i0 + j <= st.idx_cut));
-      q[j] = kept ? quant(wexp(zp, st.Mp)) : 0ull;
-      sum += q[j];
-    }
-    unsigned long long total;
-    const unsigned long long ex = block_excl_scan<unsigned long long, ROW_WAVES>(sum, s_u64, &total);
-    if (ex <= rem && rem < ex + sum) {
-      unsigned long long c = ex;
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        c += q[j];
-        if (c > rem) {
-          s_found = i0 + j;
-          break;
+        const double pd = wave_sum(static_cast<double>(part));
+        pq = wave_sum(pq);
+        if (lane == 0) {
+          r1.pass.sp[t * WAVES + wid] = pd;
+          r1.pass.sq[t * WAVES + wid] = pq;
         }
       }
     }
-    __syncthreads();
-    if (s_found >= 0) break;
-    rem -= total;
   }
-  if (tid == 0) {
-    int id = s_found;
-    if (id < 0) id = beg;  // unreachable: the slice's kept mass exceeds rem
-    a.out_ids[r] = id;
-    if (a.out_lp) {
-      if (md.want_lp) {
-        const float z = ld1<DT>(row, id);
-        a.out_lp[r] = static_cast<float>(static_cast<double>(z) - st.lse);
-      } else {
-        a.out_lp[r] = NAN;
+  __builtin_amdgcn_s_waitcnt(0);  // candidate stores complete before other waves read them
+  __syncthreads();
+}
+
+// Top-k from candidates of the first pass (k > 63), or -- when the best-64 list
+// cannot decide a k <= 63 row -- from candidates extracted from the row now.
+template <int DT, int EPT, bool VECOK>
+__device__ void finish_topk(const Args& a, const Mode& md, const void* row, int r, bool from_row,
+                            Region0& r0, Region1& r1, Small& sh) {
+  const int tid = threadIdx.x;
+  const int S = a.S;
+  CandView cv;
+  int n;
+  if (from_row) {
+    // every element with z' >= z'(list entry k-1) -- i.e. z key >= g(that z')
+    if (tid == 0) {
+      const float tau_z = sh.mlist[md.kk - 1].v;
+      sh.sel[4] = static_cast<int>(gkey<DT>(fz<DT>(tau_z, md.Tr), md.Tr));
+      sh.ncand = 0;
+    }
+    __syncthreads();
+    row_pass<DT, EPT, VECOK>(a, md, row, r, static_cast<unsigned int>(sh.sel[4]), false, 0u, 0, r0,
+                             r1, sh);
+    n = static_cast<int>(sh.ncand);
+    cv.l = n <= CAND_LDS ? r0.cand : nullptr;
+    cv.g = a.cand + static_cast<size_t>(r) * S * a.L;
+    cv.off = nullptr;
+  } else {
+    if (tid == 0) {
+      int o = 0;
+      for (int t = 0; t < S; ++t) {
+        sh.off[t] = o;
+        o += static_cast<int>(sh.ncnd[t]);
+      }
+      sh.off[S] = o;
+    }
+    __syncthreads();
+    n = sh.off[S];
+    uint2* g = a.cand + static_cast<size_t>(r) * S * a.L;
+    const bool in_lds = n <= CAND_LDS;
+    for (int t = 0; t < S; ++t) {  // z key -> z' key
+      const int o = sh.off[t], cnt = sh.off[t + 1] - o;
+      uint2* src = g + static_cast<size_t>(t) * a.L;
+      for (int j = tid; j < cnt; j += THREADS) {
+        uint2 e = ld_dev2(src + j);
+        e.x = f2key(fz<DT>(key2f(e.x), md.Tr));
+        if (in_lds)
+          r0.cand[o + j] = e;
+        else
+          st_dev(src + j, e);
       }
     }
+    __builtin_amdgcn_s_waitcnt(0);  // global rewrites complete before other waves read them
+    __syncthreads();
+    cv.l = in_lds ? r0.cand : nullptr;
+    cv.g = g;
+    cv.off = sh.off;
   }
+  cv.S = S;
+  cv.L = a.L;
+  const int id = resolve_topk(md, cv, n, sh.Mp, sh);
+  write_sampled<DT>(a, md, row, r, id, sh);
+}
+
+// Top-p without top-k, in phases that hand their results on through LDS so
+// that little stays live in registers across phases:
+//   A: combined histogram (row units) with the bound of its truncation error;
+//      the bracket R = [blo, bhi] of bins that must hold the nucleus boundary;
+//      the side of R with fewer elements.
+//   B: R's edges as z-key thresholds (no division in the comparisons).
+//   C: compare-only pass over the row.
+//   D: mass above R per slice; check that R brackets the boundary (else redo
+//      with R = the whole row).
+//   E: exact cutoff and tie cut among R's elements, kept mass per slice, the
+//      slice that holds the draw, and the walk of that slice.
+template <int DT, int EPT, bool VECOK>
+__device__ void finish_topp(const Args& a, const Mode& md, const void* row, int r, Region0& r0,
+                            Region1& r1, Small& sh) {
+  const int tid = threadIdx.x;
+  const int S = a.S;
+
+  // ---- A: thread t owns descending positions 2t, 2t+1 (bins NBIN-1-2t, NBIN-2-2t)
+  {
+    const size_t hb = static_cast<size_t>(r) * S * NBIN;
+    unsigned int c[2] = {0u, 0u};
+    double m[2] = {0.0, 0.0}, e[2] = {0.0, 0.0};
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int b = NBIN - 1 - (2 * tid + q);
+#pragma unroll 8
+      for (int t = 0; t < S; ++t) {
+        const unsigned long long h = ld_dev(a.hist + hb + static_cast<size_t>(t) * NBIN + b);
+        const unsigned int ct = static_cast<unsigned int>(h >> 40);
+        c[q] += ct;
+        m[q] += static_cast<double>(h & MASK40) * HUNIT * sh.scale[t];
+        e[q] += static_cast<double>(ct) * HUNIT * sh.scale[t];
+      }
+    }
+    if (tid == 0) {
+      double W = 0.0;
+      for (int t = 0; t < S; ++t) W += sh.msum[t] * sh.scale[t];
+      sh.seld[2] = static_cast<double>(md.pr) * W;  // p * W, row units
+      sh.pos_hi = NBIN;
+      sh.pos_lo = NBIN;
+      sh.pos_last = -1;
+    }
+    double exA, inA, totA, exU, inU, totU;
+    block_scan<double>(m[0] + m[1], sh.rd, &exA, &inA, &totA);
+    block_scan<double>(m[0] + m[1] + e[0] + e[1], sh.rd, &exU, &inU, &totU);
+    const double PW = sh.seld[2];
+    // first position whose cumulative upper bound reaches p*W: the boundary is
+    // not above it; first position whose cumulative lower bound reaches it:
+    // the boundary is not below it
+    const double t_hi = PW * (1.0 - 1e-9), t_lo = PW * (1.0 + 1e-9);
+    int ph = NBIN, pl = NBIN, last = -1;
+    double runA = exA, runU = exU;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      runA += m[q];
+      runU += m[q] + e[q];
+      if (c[q] > 0) {
+        if (ph == NBIN && runU >= t_hi) ph = 2 * tid + q;
+        if (pl == NBIN && runA >= t_lo) pl = 2 * tid + q;
+        last = 2 * tid + q;
+      }
+    }
+    if (ph < NBIN) atomicMin(&sh.pos_hi, ph);
+    if (pl < NBIN) atomicMin(&sh.pos_lo, pl);
+    if (last >= 0) atomicMax(&sh.pos_last, last);
+    __syncthreads();
+    int p_hi = sh.pos_hi, p_lo = sh.pos_lo;
+    const int p_last = sh.pos_last < 0 ? NBIN - 1 : sh.pos_last;
+    if (p_hi > p_last) p_hi = p_last;
+    if (p_lo > p_last) p_lo = p_last;
+    // positions count down from the top bin: bhi = NBIN-1-p_hi >= blo = NBIN-1-p_lo
+    int ca = 0, cb = 0;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pos = 2 * tid + q;
+      if (pos < p_hi) ca += static_cast<int>(c[q]);
+      if (pos > p_lo) cb += static_cast<int>(c[q]);
+    }
+    ca = block_sum<int>(ca, sh.rint);
+    cb = block_sum<int>(cb, sh.rint);
+    if (tid == 0) {
+      sh.sel[2] = NBIN - 1 - p_lo;  // blo
+      sh.sel[3] = NBIN - 1 - p_hi;  // bhi
+      sh.sel[7] = ca <= cb ? 1 : 2;  // sum the side with fewer elements
+    }
+    __syncthreads();
+  }
+
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    // ---- B
+    if (tid == 0) {
+      const int blo = sh.sel[2], bhi = sh.sel[3];
+      const unsigned int klo_edge = max(static_cast<unsigned int>(blo) << 21, KEY_NEG_INF);
+      sh.sel[4] = static_cast<int>(attempt == 0 ? gkey<DT>(key2f(klo_edge), md.Tr) : 0u);
+      const unsigned int hi_edge = static_cast<unsigned int>(bhi + 1) << 21;
+      const bool has_hi = attempt == 0 && bhi < NBIN - 1 && hi_edge <= KEY_POS_INF;
+      sh.sel[5] = has_hi ? 1 : 0;
+      sh.sel[6] = static_cast<int>(has_hi ? gkey<DT>(key2f(hi_edge), md.Tr) : 0u);
+      sh.sel[8] = attempt == 0 ? sh.sel[7] : 0;  // R = whole row: no side to sum
+      sh.ncand = 0;
+    }
+    __syncthreads();
+    // ---- C
+    row_pass<DT, EPT, VECOK>(a, md, row, r, static_cast<unsigned int>(sh.sel[4]), sh.sel[5] != 0,
+                             static_cast<unsigned int>(sh.sel[6]), sh.sel[8], r0, r1, sh);
+    // ---- D
+    if (tid < S) {
+      double sd = 0.0;
+      unsigned long long sq = 0;
+      for (int w2 = 0; w2 < WAVES; ++w2) {
+        sd += r1.pass.sp[tid * WAVES + w2];
+        sq += r1.pass.sq[tid * WAVES + w2];
+      }
+      sh.side[tid] = sd;
+      sh.inR[tid] = sq;
+      sh.keepq[tid] = 0ull;
+    }
+    __syncthreads();
+    const int n = static_cast<int>(sh.ncand);
+    CandView cv;
+    cv.l = n <= CAND_LDS ? r0.cand : nullptr;
+    cv.g = a.cand + static_cast<size_t>(r) * S * a.L;
+    cv.off = nullptr;
+    cv.S = S;
+    cv.L = a.L;
+    const float Mp = sh.Mp;
+    auto wq = [Mp](uint2 e) { return quant(wexp(key2f(e.x), Mp)); };
+    if (tid == 0) {
+      const int side = sh.sel[8];
+      double pa = 0.0, inr_tot = 0.0;
+      for (int t = 0; t < S; ++t) {
+        const double inr = static_cast<double>(sh.inR[t]) * QUNIT;
+        const double ab = side == 1 ? sh.side[t] : (side == 2 ? sh.msum[t] - sh.side[t] - inr : 0.0);
+        sh.keep[t] = ab < 0.0 ? 0.0 : ab;  // above-R mass, slice units
+        pa += sh.keep[t] * sh.scale[t];
+        inr_tot += inr * sh.scale[t];
+      }
+      const double need = sh.seld[2] - pa;  // nucleus mass still to cover inside R, row units
+      const bool bracketed = need > 0.0 && need <= inr_tot * (1.0 + 1e-9) + 1e-12;
+      sh.sel[9] = bracketed ? 1 : 0;
+      const double nq = need / QUNIT;
+      sh.selu[1] = nq <= 1.0 ? 1ull : static_cast<unsigned long long>(ceil(nq));
+    }
+    __syncthreads();
+    if (sh.sel[9] == 0 && attempt == 0) {  // R missed the boundary: R = whole row
+      if (tid == 0) {
+        sh.sel[2] = 0;
+        sh.sel[3] = NBIN - 1;
+      }
+      __syncthreads();
+      continue;
+    }
+    // ---- E
+    const unsigned long long target = sh.selu[1];
+    unsigned long long pgt, bef;
+    unsigned int g_cnt;
+    bool all_kept;
+    auto any = [](uint2) { return true; };
+    const unsigned int vkey =
+        radix_select<true, true, true>(cv, n, any, wq, target, false, sh, &pgt, &g_cnt, &all_kept);
+    const unsigned long long wstar = wq(make_uint2(vkey, 0u));
+    unsigned long long tk = g_cnt;
+    if (!all_kept && wstar > 0) {
+      const unsigned long long nd = target > pgt ? (target - pgt + wstar - 1) / wstar : 0ull;
+      tk = nd < tk ? nd : tk;
+    }
+    if (tk == 0) tk = 1;
+    int idx_cut = INT_MAX;
+    if (tk < g_cnt) {
+      auto eq_v = [vkey](uint2 e) { return e.x == vkey; };
+      unsigned int g2;
+      bool none2;
+      idx_cut = static_cast<int>(
+          radix_select<false, false, false>(cv, n, eq_v, wq, tk, false, sh, &bef, &g2, &none2));
+    }
+    for (int base = 0; base < n; base += THREADS) {
+      const int c = base + tid;
+      bool kept = false;
+      int st = 0;
+      unsigned long long q = 0;
+      if (c < n) {
+        const uint2 e = cv.get(c);
+        kept = e.x > vkey || (e.x == vkey && static_cast<int>(e.y) <= idx_cut);
+        st = static_cast<int>(e.y) / a.L;
+        q = kept ? quant(wexp(key2f(e.x), sh.mps[st])) : 0ull;
+      }
+      lds_add_agg(sh.keepq, st, q, kept);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int t = 0; t < S; ++t) sh.keep[t] += static_cast<double>(sh.keepq[t]) * QUNIT;
+      int sst;
+      double rem;
+      pick_slice(sh.keep, sh.scale, S, md.u, &sst, &rem);
+      sh.sel[0] = sst;
+      sh.seld[1] = rem;
+    }
+    __syncthreads();
+    const int id = final_scan<DT, EPT, VECOK>(a, md, row, sh.sel[0], sh.seld[1], vkey, idx_cut, sh);
+    write_sampled<DT>(a, md, row, r, id, sh);
+    return;
+  }
+}
+
+// Everything the last slice of a row does.
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ void finish_row(int r, Region0& r0, Region1& r1, Small& sh) {
+  const Args& a = sh.args;
+  const Mode& md = sh.md;  // in LDS: callees that are not inlined take it by reference
+  const void* row = row_ptr<DT>(a, r);
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int S = a.S;
+
+  if (tid < S) {
+    const unsigned long long* rp = reinterpret_cast<const unsigned long long*>(a.rec + (r * S + tid));
+    const unsigned long long w0 = ld_dev(rp + 0), w1 = ld_dev(rp + 1);
+    sh.szmax[tid] = __uint_as_float(static_cast<unsigned int>(w0));
+    sh.szarg[tid] = static_cast<int>(w0 >> 32);
+    sh.mps[tid] = __uint_as_float(static_cast<unsigned int>(w1));
+    sh.ncnd[tid] = static_cast<unsigned int>(w1 >> 32);
+    sh.slse[tid] = __longlong_as_double(static_cast<long long>(ld_dev(rp + 2)));
+    sh.msum[tid] = __longlong_as_double(static_cast<long long>(ld_dev(rp + 3)));
+  }
+  // the row's best 64: wave w merges the lists of slices w, w + 16, ...; then a tree
+  if (md.need_list) {
+    float lv = -INFINITY;
+    int li = INT_MAX;
+    for (int t = wid; t < S; t += WAVES) {
+      const unsigned long long w = ld_dev(a.list + (static_cast<size_t>(r) * S + t) * LIST + lane);
+      wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
+    }
+    tree_merge(lv, li, r0.lists, S < WAVES ? S : WAVES);
+    if (wid == 0) {
+      sh.mlist[lane].v = lv;
+      sh.mlist[lane].i = li;
+    }
+  }
+  __syncthreads();
+  if (wid == 0) {
+    const float zm = lane < S ? sh.szmax[lane] : -INFINITY;
+    const int za = lane < S ? sh.szarg[lane] : INT_MAX;
+    float rm = zm;
+    int ra = za;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(rm, o, 64);
+      const int oi = __shfl_xor(ra, o, 64);
+      if (better(ov, oi, rm, ra)) {
+        rm = ov;
+        ra = oi;
+      }
+    }
+    double part = (lane < S && md.need_lse) ? sh.slse[lane] * wexp_d(zm, rm) : 0.0;
+    part = wave_sum(part);
+    const float Mp = md.sampling ? fz<DT>(rm, md.Tr) : 0.0f;
+    if (lane < S && md.sampling) sh.scale[lane] = wexp_d(sh.mps[lane], Mp);
+    if (lane == 0) {
+      sh.zmax = rm;
+      sh.zarg = ra;
+      sh.lse = md.need_lse ? static_cast<double>(rm) + log(part) : static_cast<double>(NAN);
+      sh.Mp = Mp;
+    }
+  }
+  __syncthreads();
+
+  if (tid == 0 && md.kind == KIND_GREEDY) {
+    a.out_ids[r] = sh.zarg;
+    if (a.out_lp)
+      a.out_lp[r] = md.want_lp ? static_cast<float>(static_cast<double>(sh.zmax) - sh.lse) : NAN;
+  }
+  if (a.K_max > 0 && tid < a.K_max) {  // top_logprobs: the first K of the best-64
+    const size_t o = static_cast<size_t>(r) * a.K_max + tid;
+    if (tid < md.K) {
+      a.out_top_ids[o] = sh.mlist[tid].i;
+      a.out_top_lp[o] = static_cast<float>(static_cast<double>(sh.mlist[tid].v) - sh.lse);
+    } else {
+      a.out_top_ids[o] = -1;
+      a.out_top_lp[o] = -INFINITY;
+    }
+  }
+
+  if (md.topp && !(md.pr > 0.0f)) {
+    // p rounds to 0 in the logits dtype: the nucleus keeps nothing, every
+    // logit is masked, and the draw is uniform over the vocabulary
+    if (tid == 0) {
+      const double x = floor(static_cast<double>(md.u) * static_cast<double>(a.V));
+      write_sampled<DT>(a, md, row, r, x < a.V - 1 ? static_cast<int>(x) : a.V - 1, sh);
+    }
+  } else if (md.kind == KIND_TEMP) {
+    finish_temp<DT, EPT, VECOK>(a, md, row, r, sh);
+  } else if (md.kind == KIND_KLIST) {
+    if (wid == 0) {
+      int id = -1;
+      const bool ok = klist_resolve<DT>(md, sh.Mp, sh, &id);
+      if (lane == 0) {
+        sh.sel[10] = ok ? 1 : 0;
+        sh.sel[11] = id;
+      }
+    }
+    __syncthreads();
+    if (sh.sel[10])
+      write_sampled<DT>(a, md, row, r, sh.sel[11], sh);
+    else
+      finish_topk<DT, EPT, VECOK>(a, md, row, r, true, r0, r1, sh);
+  } else if (md.kind == KIND_KHIST) {
+    finish_topk<DT, EPT, VECOK>(a, md, row, r, false, r0, r1, sh);
+  } else if (md.kind == KIND_TOPP) {
+    finish_topp<DT, EPT, VECOK>(a, md, row, r, r0, r1, sh);
+  }
+}
+
+// =================================================================== kernel ==
+
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS) void k_sample(Args a) {
+  __shared__ Region0 r0;
+  __shared__ Region1 r1;
+  __shared__ Small sh;
+
+  const int s = blockIdx.x, r = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int S = a.S;
+  const Mode md = decode<DT>(a, r);
+  const void* row = row_ptr<DT>(a, r);
+  const int beg = s * a.L;
+  const int end = min(a.V, beg + a.L);
+  constexpr int NIT = EPT / VEC;
+
+  float v[EPT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
+#define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
+
+  // ---- max and lowest-index argmax: per thread, then per wave, then the slice
+  float tbv = -INFINITY;
+  int tbi = INT_MAX;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int i = MLXF_IDX(e);
+    if (i < end && better(v[e], i, tbv, tbi)) {
+      tbv = v[e];
+      tbi = i;
+    }
+  }
+  float bm = tbv;
+  int bi = tbi;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bm, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (better(ov, oi, bm, bi)) {
+      bm = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    sh.rf[wid] = bm;
+    sh.ri[wid] = bi;
+  }
+  __syncthreads();
+  float zmax = sh.rf[0];
+  int zarg = sh.ri[0];
+  for (int w2 = 1; w2 < WAVES; ++w2)
+    if (better(sh.rf[w2], sh.ri[w2], zmax, zarg)) {
+      zmax = sh.rf[w2];
+      zarg = sh.ri[w2];
+    }
+
+  // ---- log-sum-exp partial
+  double lse_s = 0.0;
+  if (md.need_lse) {
+    float t = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      if (MLXF_IDX(e) < end) t += wexp(v[e], zmax);
+    lse_s = block_sum<double>(static_cast<double>(t), sh.rd);
+  }
+
+  // ---- best 64 of the slice.  theta = the 64th best thread maximum: at least
+  // 64 elements reach it, so the slice's best 64 all do; at most 64 threads
+  // hold elements that reach it, so at most 64 * EPT elements survive.
+  if (md.need_list) {
+    float lv = tbv;
+    int li = tbi;
+    wave_sort(lv, li);
+    tree_merge(lv, li, r0.lists, WAVES);
+    if (tid == LIST - 1) {
+      sh.thv = lv;
+      sh.thi = li;
+    }
+    __syncthreads();
+    const float thv = sh.thv;
+    const int thi = sh.thi;
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && !better(thv, thi, v[e], MLXF_IDX(e))) ? 1 : 0;
+    int ntot;
+    int pos = block_excl_scan<int>(mine, sh.rint, &ntot);
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int i = MLXF_IDX(e);
+      if (i < end && !better(thv, thi, v[e], i)) {
+        r1.surv[pos].v = v[e];
+        r1.surv[pos].i = i;
+        ++pos;
+      }
+    }
+    __syncthreads();
+    const int nch = (ntot + LIST - 1) / LIST;  // <= EPT <= WAVES
+    float sv = -INFINITY;
+    int si = INT_MAX;
+    if (wid < nch) {
+      const int c = wid * LIST + lane;
+      if (c < ntot) {
+        sv = r1.surv[c].v;
+        si = r1.surv[c].i;
+      }
+    }
+    __syncthreads();
+    if (wid < nch) wave_sort(sv, si);
+    tree_merge(sv, si, r0.lists, nch);
+    if (wid == 0) st_dev(a.list + (static_cast<size_t>(r) * S + s) * LIST + lane, pack_ent(sv, si));
+  }
+
+  // ---- per-kind slice work
+  float mps = 0.0f;
+  double msum = 0.0;
+  unsigned int ncand = 0;
+  if (md.kind == KIND_TEMP || md.kind == KIND_TOPP) {
+    mps = fz<DT>(zmax, md.Tr);
+    const bool hist = md.kind == KIND_TOPP;
+    if (hist) {
+      for (int b = tid; b < NBIN; b += THREADS) r1.hist[b] = 0ull;
+      __syncthreads();
+    }
+    double t = 0.0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      if (MLXF_IDX(e) < end) {
+        const float zp = fz<DT>(v[e], md.Tr);
+        const float w = wexp(zp, mps);
+        t += static_cast<double>(w);
+        if (hist)
+          atomicAdd(&r1.hist[f2key(zp) >> 21],
+                    (1ull << 40) +
+                        static_cast<unsigned long long>(static_cast<unsigned int>(w * 16777216.0f)));
+      }
+    }
+    msum = block_sum<double>(t, sh.rd);
+    if (hist) {
+      __syncthreads();
+      const size_t off = (static_cast<size_t>(r) * S + s) * NBIN;
+      for (int b = tid; b < NBIN; b += THREADS) st_dev(a.hist + off + b, r1.hist[b]);
+    }
+  } else if (md.kind == KIND_KHIST) {
+    for (int b = tid; b < CNT_BINS; b += THREADS) r1.cnt[b] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      if (MLXF_IDX(e) < end) atomicAdd(&r1.cnt[f2key(v[e]) >> 20], 1u);
+    __syncthreads();
+    // thread t owns descending positions 4t..4t+3 (bins 4095-4t .. 4092-4t)
+    int c4[4], sum4 = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c4[q] = static_cast<int>(r1.cnt[CNT_BINS - 1 - (4 * tid + q)]);
+      sum4 += c4[q];
+    }
+    int total;
+    const int ex = block_excl_scan<int>(sum4, sh.rint, &total);
+    const int kk_s = md.kk < (end - beg) ? md.kk : (end - beg);
+    int run = ex;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (run < kk_s && run + c4[q] >= kk_s) sh.sel[0] = CNT_BINS - 1 - (4 * tid + q);
+      run += c4[q];
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned int edge = max(static_cast<unsigned int>(sh.sel[0]) << 20, KEY_NEG_INF);
+      sh.sel[1] = static_cast<int>(gkey<DT>(fz<DT>(key2f(edge), md.Tr), md.Tr));
+    }
+    __syncthreads();
+    const unsigned int thr = static_cast<unsigned int>(sh.sel[1]);
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && f2key(v[e]) >= thr) ? 1 : 0;
+    int ctot;
+    int pos = block_excl_scan<int>(mine, sh.rint, &ctot);
+    uint2* dst = a.cand + (static_cast<size_t>(r) * S + s) * a.L;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int i = MLXF_IDX(e);
+      const unsigned int key = f2key(v[e]);
+      if (i < end && key >= thr) st_dev(dst + pos++, make_uint2(key, static_cast<unsigned int>(i)));
+    }
+    ncand = static_cast<unsigned int>(ctot);
+  }
+#undef MLXF_IDX
+
+  if (tid == 0) {
+    unsigned long long* rp = reinterpret_cast<unsigned long long*>(a.rec + (r * S + s));
+    st_dev(rp + 0, pack2(__float_as_uint(zmax), static_cast<unsigned int>(zarg)));
+    st_dev(rp + 1, pack2(__float_as_uint(mps), ncand));
+    st_dev(rp + 2, static_cast<unsigned long long>(__double_as_longlong(lse_s)));
+    st_dev(rp + 3, static_cast<unsigned long long>(__double_as_longlong(msum)));
+  }
+
+  // ---- ticket: the last slice of the row finishes it.  Every wave waits for
+  // its device-coherent stores to complete before the ticket is drawn.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    sh.ticket = __hip_atomic_fetch_add(a.ctr + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (sh.ticket != static_cast<unsigned int>(S - 1)) return;
+  if (tid == 0) {
+    __hip_atomic_store(a.ctr + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+    sh.args = a;
+    sh.md = md;
+  }
+  __syncthreads();
+  finish_row<DT, EPT, VECOK>(r, r0, r1, sh);
+}
+
+// Zero the per-row counters of a fresh workspace.
+__global__ void k_zero(unsigned int* p, size_t n) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
 }
 
 // ================================================================ host side ==
 
 struct Layout {
-  int S, L;
-  size_t off_rs, off_rec, off_top, off_hcnt, off_hmass, off_sm, off_cand, total;
+  int S, L, EPT;
+  size_t off_ctr, off_rec, off_list, off_hist, off_cand, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
+constexpr size_t CTR_BYTES_MAX = 65536 * sizeof(unsigned int);
+
+// EPT: the largest of {16, 8} that still gives >= 512 workgroups with at most
+// MAX_S slices per row; otherwise the smallest EPT with S <= MAX_S.
 Layout make_layout(int B, int V, int K_max) {
+  (void)K_max;
   Layout l;
-  int S0 = (TARGET_BLOCKS + B - 1) / (B > 0 ? B : 1);
-  S0 = S0 < 1 ? 1 : (S0 > MAX_S ? MAX_S : S0);
-  int L = (V + S0 - 1) / S0;
-  L = (L + ITER_ELEMS - 1) / ITER_ELEMS * ITER_ELEMS;
-  l.S = (V + L - 1) / L;
-  l.L = L;
+  int ept = 0;
+  for (int e : {16, 8}) {
+    const int L = THREADS * e;
+    const int S = (V + L - 1) / L;
+    if (S <= MAX_S && static_cast<long long>(B) * S >= 512) {
+      ept = e;
+      break;
+    }
+  }
+  if (!ept) {
+    for (int e : {8, 16}) {
+      const int L = THREADS * e;
+      if ((V + L - 1) / L <= MAX_S) {
+        ept = e;
+        break;
+      }
+    }
+  }
+  l.EPT = ept;
+  l.L = THREADS * ept;
+  l.S = (V + l.L - 1) / l.L;
   const size_t BS = static_cast<size_t>(B) * l.S;
   size_t o = 0;
-  l.off_rs = o;
-  o = align256(o + sizeof(RowState) * B);
+  l.off_ctr = o;  // first: mlxf_sampler_workspace_init zeroes the start of the buffer
+  o = align256(o + sizeof(unsigned int) * (B > 0 ? B : 1));
   l.off_rec = o;
   o = align256(o + sizeof(SliceRec) * BS);
-  l.off_top = o;
-  o = align256(o + sizeof(TopEnt) * BS * (K_max > 0 ? K_max : 1));
-  l.off_hcnt = o;
-  o = align256(o + sizeof(unsigned int) * BS * NB);
-  l.off_hmass = o;
-  o = align256(o + sizeof(unsigned long long) * BS * NB);
-  l.off_sm = o;
-  o = align256(o + sizeof(SliceMass) * BS);
+  l.off_list = o;
+  o = align256(o + sizeof(unsigned long long) * BS * LIST);
+  l.off_hist = o;
+  o = align256(o + sizeof(unsigned long long) * BS * NBIN);
   l.off_cand = o;
   o = align256(o + sizeof(uint2) * BS * l.L);
   l.total = o;
@@ -1250,74 +1406,26 @@ int check_shape(int B, int V, int K_max, int dtype, char** err) {
   return MLXF_OK;
 }
 
-constexpr int NUM_STAGES = 5;
-
-// ev (optional): NUM_STAGES + 1 events recorded around the kernels.
-template <int DT, bool VECOK>
-hipError_t launch_all(const Args& a, hipStream_t st, hipEvent_t* ev) {
-  const dim3 slices(a.S, a.B);
-  auto mark = [&](int i) {
-    if (ev) (void)hipEventRecord(ev[i], st);
-  };
-  mark(0);
-  hipLaunchKernelGGL((k_scan<DT, VECOK>), slices, dim3(SLICE_THREADS), 0, st, a);
-  mark(1);
-  hipLaunchKernelGGL((k_plan<DT>), dim3(a.B), dim3(ROW_THREADS), 0, st, a);
-  mark(2);
-  if (a.T) {
-    hipLaunchKernelGGL((k_extract<DT, VECOK>), slices, dim3(SLICE_THREADS), 0, st, a);
-    mark(3);
-    hipLaunchKernelGGL((k_select<DT>), dim3(a.B), dim3(ROW_THREADS), 0, st, a);
-    mark(4);
-    hipLaunchKernelGGL((k_draw<DT, VECOK>), dim3(a.B), dim3(ROW_THREADS), 0, st, a);
-    mark(5);
-  } else {
-    mark(3);
-    mark(4);
-    mark(5);
-  }
+template <int DT, int EPT>
+hipError_t launch_ept(const Args& a, bool vecok, hipStream_t st) {
+  const dim3 grid(a.S, a.B);
+  if (vecok)
+    hipLaunchKernelGGL((k_sample<DT, EPT, true>), grid, dim3(THREADS), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_sample<DT, EPT, false>), grid, dim3(THREADS), 0, st, a);
   return hipGetLastError();
 }
 
 template <int DT>
-hipError_t dispatch_vec(const Args& a, bool vecok, hipStream_t st, hipEvent_t* ev) {
-  return vecok ? launch_all<DT, true>(a, st, ev) : launch_all<DT, false>(a, st, ev);
+hipError_t launch_dt(const Args& a, int ept, bool vecok, hipStream_t st) {
+  return ept == 8 ? launch_ept<DT, 8>(a, vecok, st) : launch_ept<DT, 16>(a, vecok, st);
 }
-
-}  // namespace
-
-extern "C" {
-
-int mlxf_sampler_abi_version(void) { return MLXF_SAMPLER_ABI_VERSION; }
-
-void mlxf_string_free(char* s) { std::free(s); }
-
-int mlxf_sampler_workspace_size(int B, int V, int K_max, int dtype, size_t* bytes, char** err) {
-  try {
-    const int rc = check_shape(B, V, K_max, dtype, err);
-    if (rc) return rc;
-    if (!bytes) {
-      set_err(err, "mlxf: bytes must not be NULL");
-      return MLXF_EINVAL;
-    }
-    *bytes = make_layout(B, V, K_max).total;
-    return MLXF_OK;
-  } catch (...) {
-    set_err(err, "mlxf: unexpected exception");
-    return MLXF_EINVAL;
-  }
-}
-
-}  // extern "C"
-
-namespace {
 
 int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
                const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
                const int32_t* d_top_logprobs, const float* d_uniforms, int32_t* d_out_ids,
                float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
-               int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err,
-               hipEvent_t* ev) {
+               int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err) {
   try {
     int rc = check_shape(B, V, K_max, dtype, err);
     if (rc) return rc;
@@ -1372,21 +1480,19 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
     a.out_lp = d_out_logprobs;
     a.out_top_ids = d_out_top_ids;
     a.out_top_lp = d_out_top_logprobs;
-    a.rs = reinterpret_cast<RowState*>(ws + l.off_rs);
+    a.ctr = reinterpret_cast<unsigned int*>(ws + l.off_ctr);
     a.rec = reinterpret_cast<SliceRec*>(ws + l.off_rec);
-    a.top = reinterpret_cast<TopEnt*>(ws + l.off_top);
-    a.hcnt = reinterpret_cast<unsigned int*>(ws + l.off_hcnt);
-    a.hmass = reinterpret_cast<unsigned long long*>(ws + l.off_hmass);
-    a.sm = reinterpret_cast<SliceMass*>(ws + l.off_sm);
+    a.list = reinterpret_cast<unsigned long long*>(ws + l.off_list);
+    a.hist = reinterpret_cast<unsigned long long*>(ws + l.off_hist);
     a.cand = reinterpret_cast<uint2*>(ws + l.off_cand);
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e;
     if (dtype == MLXF_DTYPE_F32)
-      e = dispatch_vec<MLXF_DTYPE_F32>(a, vecok, st, ev);
+      e = launch_dt<MLXF_DTYPE_F32>(a, l.EPT, vecok, st);
     else if (dtype == MLXF_DTYPE_BF16)
-      e = dispatch_vec<MLXF_DTYPE_BF16>(a, vecok, st, ev);
+      e = launch_dt<MLXF_DTYPE_BF16>(a, l.EPT, vecok, st);
     else
-      e = dispatch_vec<MLXF_DTYPE_F16>(a, vecok, st, ev);
+      e = launch_dt<MLXF_DTYPE_F16>(a, l.EPT, vecok, st);
     if (e != hipSuccess) {
       set_err(err, std::string("mlxf: kernel launch failed: ") + hipGetErrorString(e));
       return MLXF_EHIP;
@@ -1399,8 +1505,53 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
 }
 
 }  // namespace
+}  // namespace mlxf
+
+using mlxf::check_shape;
+using mlxf::make_layout;
+using mlxf::run_sample;
+using mlxf::set_err;
 
 extern "C" {
+
+int mlxf_sampler_abi_version(void) { return MLXF_SAMPLER_ABI_VERSION; }
+
+void mlxf_string_free(char* s) { std::free(s); }
+
+int mlxf_sampler_workspace_size(int B, int V, int K_max, int dtype, size_t* bytes, char** err) {
+  try {
+    const int rc = check_shape(B, V, K_max, dtype, err);
+    if (rc) return rc;
+    if (!bytes) {
+      set_err(err, "mlxf: bytes must not be NULL");
+      return MLXF_EINVAL;
+    }
+    *bytes = make_layout(B, V, K_max).total;
+    return MLXF_OK;
+  } catch (...) {
+    set_err(err, "mlxf: unexpected exception");
+    return MLXF_EINVAL;
+  }
+}
+
+int mlxf_sampler_workspace_init(void* d_workspace, size_t workspace_bytes, void* stream,
+                                char** err) {
+  if (!d_workspace || (reinterpret_cast<uintptr_t>(d_workspace) & 255u)) {
+    set_err(err, "mlxf: workspace must be non-NULL and 256-byte aligned");
+    return MLXF_EINVAL;
+  }
+  const size_t bytes = workspace_bytes < mlxf::CTR_BYTES_MAX ? workspace_bytes : mlxf::CTR_BYTES_MAX;
+  const size_t n = bytes / sizeof(unsigned int);
+  if (n == 0) return MLXF_OK;
+  hipLaunchKernelGGL(mlxf::k_zero, dim3(static_cast<unsigned int>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<unsigned int*>(d_workspace), n);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_err(err, std::string("mlxf: kernel launch failed: ") + hipGetErrorString(e));
+    return MLXF_EHIP;
+  }
+  return MLXF_OK;
+}
 
 int mlxf_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
                 const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
@@ -1409,53 +1560,15 @@ int mlxf_sample(const void* d_logits, int dtype, int B, int V, int64_t row_strid
                 int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err) {
   return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p,
                     d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
-                    d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, err, nullptr);
-}
-
-int mlxf_sample_profiled(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
-                         const float* d_temperature, const int32_t* d_top_k,
-                         const float* d_top_p, const int32_t* d_top_logprobs,
-                         const float* d_uniforms, int32_t* d_out_ids, float* d_out_logprobs,
-                         int32_t* d_out_top_ids, float* d_out_top_logprobs, int K_max,
-                         void* d_workspace, size_t workspace_bytes, void* stream,
-                         float* stage_ms, char** err) {
-  if (!stage_ms) {
-    set_err(err, "mlxf: stage_ms must not be NULL");
-    return MLXF_EINVAL;
-  }
-  hipEvent_t ev[NUM_STAGES + 1] = {};
-  for (int i = 0; i <= NUM_STAGES; ++i) {
-    if (hipEventCreate(&ev[i]) != hipSuccess) {
-      for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
-      set_err(err, "mlxf: hipEventCreate failed");
-      return MLXF_EHIP;
-    }
-  }
-  int rc = run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p,
-                      d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
-                      d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, err, ev);
-  if (rc == MLXF_OK && B > 0) {
-    if (hipEventSynchronize(ev[NUM_STAGES]) != hipSuccess) {
-      set_err(err, "mlxf: hipEventSynchronize failed");
-      rc = MLXF_EHIP;
-    } else {
-      for (int i = 0; i < NUM_STAGES; ++i) {
-        float ms = 0.0f;
-        (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
-        stage_ms[i] = ms;
-      }
-    }
-  }
-  for (int i = 0; i <= NUM_STAGES; ++i) (void)hipEventDestroy(ev[i]);
-  return rc;
+                    d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, err);
 }
 
 int mlxf_greedy(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
                 int32_t* d_out_ids, void* d_workspace, size_t workspace_bytes, void* stream,
                 char** err) {
-  return mlxf_sample(d_logits, dtype, B, V, row_stride, nullptr, nullptr, nullptr, nullptr,
-                     nullptr, d_out_ids, nullptr, nullptr, nullptr, 0, d_workspace,
-                     workspace_bytes, stream, err);
+  return run_sample(d_logits, dtype, B, V, row_stride, nullptr, nullptr, nullptr, nullptr, nullptr,
+                    d_out_ids, nullptr, nullptr, nullptr, 0, d_workspace, workspace_bytes, stream,
+                    err);
 }
 
 }  // extern "C"

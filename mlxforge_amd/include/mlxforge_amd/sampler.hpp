@@ -1,0 +1,242 @@
+// sampler.hpp -- C++ host wrapper over the C ABI of libmlxf_sampler
+// (include/mlxf_sampler.h), mirroring the reference's sampler interface
+// (src/sample/sampler.h:15-79) for C++ callers such as a decode-step worker.
+//
+//   mlxforge::SamplingParams / SampleResult / Sampler  (src/sample/sampler.h)
+//   ->  mlxforge_amd::SamplingParams / SampleResult / Sampler
+//
+// Differences the boundary forces, each stated where it appears:
+//   * logits are a device view (DeviceLogits) instead of an mx::array;
+//   * the MLX PRNG key is replaced by one caller-supplied uniform per row
+//     (inverse-CDF draw; the reference's random::categorical,
+//     src/sample/sampler.cpp:165);
+//   * results are copied back to host vectors (what the reference's worker
+//     does right after its async_eval, src/runtime/worker.cpp:498-512);
+//   * min_p and the penalties are not on the GPU path: sample() reports them
+//     as an error instead of ignoring them.
+// Header-only; needs the HIP runtime for device buffers and copies.  The
+// sampler library itself never allocates: this wrapper owns the workspace.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "mlxf_sampler.h"
+
+namespace mlxforge_amd {
+
+// src/sample/sampler.h:15-36, same fields, defaults and sentinels.
+struct SamplingParams {
+  float temperature = 1.0f;  // <= 0 => greedy (argmax)
+  int top_k = 0;             // <= 0 => disabled
+  float top_p = 1.0f;        // >= 1 => disabled
+  float min_p = 0.0f;        // <= 0 => disabled (not on the GPU path)
+  float repetition_penalty = 1.0f;
+  float frequency_penalty = 0.0f;
+  float presence_penalty = 0.0f;
+  uint64_t seed = 0;
+  int top_logprobs = -1;  // -1 off, 0 chosen only, N > 0 alternatives
+
+  bool has_penalties() const {
+    return repetition_penalty != 1.0f || frequency_penalty != 0.0f || presence_penalty != 0.0f;
+  }
+};
+
+// src/sample/sampler.h:38-45 as host vectors; top_* are row-major (B, K).
+struct SampleResult {
+  std::vector<int32_t> tokens;
+  std::vector<float> logprobs;
+  int K = 0;
+  std::vector<int32_t> top_tokens;
+  std::vector<float> top_logprobs;
+};
+
+// A [B, V] logits matrix in device memory; row r starts at data + r * row_stride.
+struct DeviceLogits {
+  const void* data = nullptr;
+  int dtype = MLXF_DTYPE_F32;
+  int B = 0;
+  int V = 0;
+  int64_t row_stride = 0;  // 0: V
+};
+
+class SamplerError : public std::runtime_error {
+ public:
+  SamplerError(int code, const std::string& msg) : std::runtime_error(msg), code_(code) {}
+  int code() const { return code_; }
+
+ private:
+  int code_;
+};
+
+namespace detail {
+inline void check(int rc, char* err) {
+  if (rc == MLXF_OK) return;
+  std::string msg = err ? err : "mlxf: error";
+  mlxf_string_free(err);
+  throw SamplerError(rc, msg);
+}
+inline void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw SamplerError(MLXF_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+template <typename T>
+struct DeviceBuf {
+  T* p = nullptr;
+  size_t n = 0;
+  void reserve(size_t want) {
+    if (want <= n) return;
+    if (p) hipFree(p);
+    p = nullptr;
+    n = 0;
+    hip_check(hipMalloc(reinterpret_cast<void**>(&p), want * sizeof(T) + 256), "hipMalloc");
+    n = want;
+  }
+  ~DeviceBuf() {
+    if (p) hipFree(p);
+  }
+};
+}  // namespace detail
+
+// Batched sampler on one HIP stream.  Reuses its device buffers across calls;
+// not thread-safe (one instance per worker thread / stream, as the reference
+// confines MLX to its worker thread, src/runtime/worker.h:1-4).
+class Sampler {
+ public:
+  explicit Sampler(hipStream_t stream = nullptr) : stream_(stream) {}
+  Sampler(const Sampler&) = delete;
+  Sampler& operator=(const Sampler&) = delete;
+
+  // One token per row with per-row parameters: what Worker::sample_rows +
+  // finalize_sample compute (src/runtime/worker.cpp:448-514), in one launch.
+  SampleResult sample_rows(const DeviceLogits& logits, const std::vector<SamplingParams>& params,
+                           const std::vector<float>& uniforms) {
+    const int B = logits.B;
+    if (static_cast<int>(params.size()) != B || static_cast<int>(uniforms.size()) != B)
+      throw SamplerError(MLXF_EINVAL, "mlxf: params and uniforms need one entry per row");
+    std::vector<float> T(B), p(B);
+    std::vector<int32_t> k(B), tlp(B);
+    int K_max = 0;
+    for (int r = 0; r < B; ++r) {
+      const SamplingParams& sp = params[r];
+      if (sp.min_p > 0.0f || sp.has_penalties())
+        throw SamplerError(MLXF_EINVAL, "mlxf: min_p and penalties are not on the GPU path");
+      T[r] = sp.temperature;
+      k[r] = sp.top_k;
+      p[r] = sp.top_p;
+      tlp[r] = sp.top_logprobs;
+      if (sp.top_logprobs > K_max) K_max = sp.top_logprobs;
+    }
+    if (K_max > logits.V) K_max = logits.V;
+    if (K_max > MLXF_MAX_TOP_LOGPROBS)
+      throw SamplerError(MLXF_EINVAL, "mlxf: top_logprobs above MLXF_MAX_TOP_LOGPROBS");
+    return run(logits, T.data(), k.data(), p.data(), tlp.data(), uniforms.data(), K_max);
+  }
+
+  // Sampler::sample(logits, params, key) (src/sample/sampler.h:51-52) with one
+  // parameter set for every row.  As in the reference, the chosen-token
+  // logprob is always computed (src/sample/sampler.cpp:151-154).
+  SampleResult sample(const DeviceLogits& logits, const SamplingParams& params,
+                      const std::vector<float>& uniforms) {
+    std::vector<SamplingParams> rows(logits.B, params);
+    for (auto& r : rows) r.top_logprobs = params.top_logprobs < 0 ? 0 : params.top_logprobs;
+    return sample_rows(logits, rows, uniforms);
+  }
+
+  // Sampler::greedy (src/sample/sampler.h:61): argmax, lowest index on ties.
+  std::vector<int32_t> greedy(const DeviceLogits& logits) {
+    const int B = logits.B, V = logits.V;
+    const int64_t stride = logits.row_stride ? logits.row_stride : V;
+    char* err = nullptr;
+    size_t ws = 0;
+    detail::check(mlxf_sampler_workspace_size(B, V, 0, logits.dtype, &ws, &err), err);
+    ensure_workspace(ws);
+    ids_.reserve(B > 0 ? B : 1);
+    err = nullptr;
+    detail::check(mlxf_greedy(logits.data, logits.dtype, B, V, stride, ids_.p, ws_.p, ws_bytes_,
+                              stream_, &err),
+                  err);
+    std::vector<int32_t> out(B);
+    if (B) {
+      detail::hip_check(hipMemcpyAsync(out.data(), ids_.p, B * sizeof(int32_t), hipMemcpyDeviceToHost, stream_),
+                        "hipMemcpyAsync");
+    }
+    detail::hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    return out;
+  }
+
+ private:
+  void ensure_workspace(size_t bytes) {
+    if (bytes <= ws_bytes_) return;
+    ws_.reserve(bytes);
+    ws_bytes_ = bytes;
+    char* err = nullptr;
+    detail::check(mlxf_sampler_workspace_init(ws_.p, ws_bytes_, stream_, &err), err);
+  }
+
+  template <typename T>
+  void upload(detail::DeviceBuf<T>& d, const T* h, int n) {
+    d.reserve(n > 0 ? n : 1);
+    if (n)
+      detail::hip_check(hipMemcpyAsync(d.p, h, n * sizeof(T), hipMemcpyHostToDevice, stream_),
+                        "hipMemcpyAsync");
+  }
+
+  SampleResult run(const DeviceLogits& logits, const float* T, const int32_t* k, const float* p,
+                   const int32_t* tlp, const float* u, int K_max) {
+    const int B = logits.B, V = logits.V;
+    const int64_t stride = logits.row_stride ? logits.row_stride : V;
+    char* err = nullptr;
+    size_t ws = 0;
+    detail::check(mlxf_sampler_workspace_size(B, V, K_max, logits.dtype, &ws, &err), err);
+    ensure_workspace(ws);
+    upload(T_, T, B);
+    upload(k_, k, B);
+    upload(p_, p, B);
+    upload(tlp_, tlp, B);
+    upload(u_, u, B);
+    ids_.reserve(B > 0 ? B : 1);
+    lp_.reserve(B > 0 ? B : 1);
+    const size_t BK = static_cast<size_t>(B) * (K_max > 0 ? K_max : 1);
+    top_ids_.reserve(BK);
+    top_lp_.reserve(BK);
+    err = nullptr;
+    detail::check(mlxf_sample(logits.data, logits.dtype, B, V, stride, T_.p, k_.p, p_.p, tlp_.p, u_.p,
+                              ids_.p, lp_.p, K_max ? top_ids_.p : nullptr, K_max ? top_lp_.p : nullptr,
+                              K_max, ws_.p, ws_bytes_, stream_, &err),
+                  err);
+    SampleResult res;
+    res.K = K_max;
+    res.tokens.resize(B);
+    res.logprobs.resize(B);
+    res.top_tokens.resize(static_cast<size_t>(B) * K_max);
+    res.top_logprobs.resize(static_cast<size_t>(B) * K_max);
+    if (B) {
+      detail::hip_check(hipMemcpyAsync(res.tokens.data(), ids_.p, B * sizeof(int32_t),
+                                       hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
+      detail::hip_check(hipMemcpyAsync(res.logprobs.data(), lp_.p, B * sizeof(float),
+                                       hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
+      if (K_max) {
+        detail::hip_check(hipMemcpyAsync(res.top_tokens.data(), top_ids_.p,
+                                         res.top_tokens.size() * sizeof(int32_t),
+                                         hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
+        detail::hip_check(hipMemcpyAsync(res.top_logprobs.data(), top_lp_.p,
+                                         res.top_logprobs.size() * sizeof(float),
+                                         hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
+      }
+    }
+    detail::hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    return res;
+  }
+
+  hipStream_t stream_;
+  detail::DeviceBuf<unsigned char> ws_;
+  size_t ws_bytes_ = 0;
+  detail::DeviceBuf<float> T_, p_, u_, lp_, top_lp_;
+  detail::DeviceBuf<int32_t> k_, tlp_, ids_, top_ids_;
+};
+
+}  // namespace mlxforge_amd

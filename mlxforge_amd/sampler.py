@@ -61,8 +61,9 @@ class Workspace:
     def get(self, B: int, V: int, K_max: int, dtype: int) -> torch.Tensor:
         need = _lib.workspace_size(B, V, K_max, dtype)
         if self.buf is None or self.buf.numel() < need:
-            # 256-byte alignment: torch's caching allocator returns >= 512-byte aligned blocks.
-            self.buf = torch.empty(max(need, 256), dtype=torch.uint8, device=self.device)
+            # Zero-filled once (the per-row counters start at 0; every call leaves
+            # them at 0).  torch's caching allocator returns >= 512-byte aligned blocks.
+            self.buf = torch.zeros(max(need, 256), dtype=torch.uint8, device=self.device)
         return self.buf
 
 
