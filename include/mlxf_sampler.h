@@ -49,8 +49,8 @@ extern "C" {
 /* Largest top_logprobs column count supported per call.  The reference's HTTP
  * layer admits top_logprobs in [0, 20] (src/server/openai.cpp:150-152). */
 #define MLXF_MAX_TOP_LOGPROBS 64
-/* Largest vocabulary accepted: at most 64 slices of 16384 logits per row. */
-#define MLXF_MAX_VOCAB 1048576
+/* Largest vocabulary accepted: at most 64 slices of 8192 logits per row. */
+#define MLXF_MAX_VOCAB 524288
 
 /* ABI version of the loaded library (MLXF_SAMPLER_ABI_VERSION it was built with).
  * No reference counterpart for the sampler itself; mirrors mlxforge_abi_version

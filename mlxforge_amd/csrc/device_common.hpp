@@ -13,7 +13,7 @@
 
 namespace mlxf {
 
-constexpr int THREADS = 1024;  // one workgroup per row slice; 16 waves
+constexpr int THREADS = 256;  // one workgroup per row slice; 4 waves, one per SIMD
 constexpr int WAVES = THREADS / 64;
 constexpr int VEC = 8;                  // elements per 16-byte (bf16/f16) or 32-byte (f32) load
 constexpr int CHUNK = THREADS * VEC;    // elements one load instruction covers across the block
@@ -209,14 +209,104 @@ __device__ __forceinline__ uint2 ld_dev2(const uint2* p) {
   return make_uint2(static_cast<unsigned int>(w), static_cast<unsigned int>(w >> 32));
 }
 
+// (av, ai) before (bv, bi) in (value desc, index asc) order.  Bitwise, not
+// short-circuit: the short-circuit form compiles to exec-mask branches.
 __device__ __forceinline__ bool better(float av, int ai, float bv, int bi) {
-  return av > bv || (av == bv && ai < bi);
+  return (av > bv) | ((av == bv) & (ai < bi));
 }
 
+// ---- cross-lane exchange on the VALU (DPP and gfx950 permlane swaps; no
+// LDS round trip as ds_bpermute would take).  xshf<M>(x) is lane (lane ^ M)'s
+// value.  Call only with the whole wave active.
+template <int M>
+__device__ __forceinline__ int xshf_i(int v) {
+  const int lane = threadIdx.x & 63;
+  if constexpr (M == 1) {
+    return __builtin_amdgcn_mov_dpp(v, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return __builtin_amdgcn_mov_dpp(v, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (M == 4) {
+    const int dn = __builtin_amdgcn_mov_dpp(v, 0x124, 0xf, 0xf, false);  // row_ror:4  (i - 4)
+    const int up = __builtin_amdgcn_mov_dpp(v, 0x12c, 0xf, 0xf, false);  // row_ror:12 (i + 4)
+    return (lane & 4) ? dn : up;
+  } else if constexpr (M == 8) {
+    return __builtin_amdgcn_mov_dpp(v, 0x128, 0xf, 0xf, false);  // row_ror:8
+  } else if constexpr (M == 15) {
+    return __builtin_amdgcn_mov_dpp(v, 0x140, 0xf, 0xf, false);  // row_mirror
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return static_cast<int>((lane & 16) ? r[0] : r[1]);
+  } else {
+    static_assert(M == 32, "xor distance");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return static_cast<int>((lane & 32) ? r[0] : r[1]);
+  }
+}
+template <int M>
+__device__ __forceinline__ int xshf(int v) { return xshf_i<M>(v); }
+template <int M>
+__device__ __forceinline__ unsigned int xshf(unsigned int v) {
+  return static_cast<unsigned int>(xshf_i<M>(static_cast<int>(v)));
+}
+template <int M>
+__device__ __forceinline__ float xshf(float v) { return __int_as_float(xshf_i<M>(__float_as_int(v))); }
+template <int M>
+__device__ __forceinline__ unsigned long long xshf(unsigned long long v) {
+  const unsigned int lo = xshf<M>(static_cast<unsigned int>(v));
+  const unsigned int hi = xshf<M>(static_cast<unsigned int>(v >> 32));
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+template <int M>
+__device__ __forceinline__ long long xshf(long long v) {
+  return static_cast<long long>(xshf<M>(static_cast<unsigned long long>(v)));
+}
+template <int M>
+__device__ __forceinline__ double xshf(double v) { return __longlong_as_double(xshf<M>(__double_as_longlong(v))); }
+
+// Value of a wave-uniform lane `src` (v_readlane: scalar, no LDS).
+__device__ __forceinline__ int rdl(int v, int src) { return __builtin_amdgcn_readlane(v, src); }
+__device__ __forceinline__ unsigned int rdl(unsigned int v, int src) {
+  return static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(v), src));
+}
+__device__ __forceinline__ float rdl(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+__device__ __forceinline__ unsigned long long rdl(unsigned long long v, int src) {
+  const unsigned int lo = rdl(static_cast<unsigned int>(v), src);
+  const unsigned int hi = rdl(static_cast<unsigned int>(v >> 32), src);
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+// Butterfly sum: every lane ends with the same value (each step adds the same
+// two operands in either order).
 template <typename T>
 __device__ __forceinline__ T wave_sum(T x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  x += xshf<32>(x);
+  x += xshf<16>(x);
+  x += xshf<8>(x);
+  x += xshf<4>(x);
+  x += xshf<2>(x);
+  x += xshf<1>(x);
+  return x;
+}
+template <typename T>
+__device__ __forceinline__ T wave_max(T x) {
+  x = max(x, xshf<32>(x));
+  x = max(x, xshf<16>(x));
+  x = max(x, xshf<8>(x));
+  x = max(x, xshf<4>(x));
+  x = max(x, xshf<2>(x));
+  x = max(x, xshf<1>(x));
+  return x;
+}
+template <typename T>
+__device__ __forceinline__ T wave_min(T x) {
+  x = min(x, xshf<32>(x));
+  x = min(x, xshf<16>(x));
+  x = min(x, xshf<8>(x));
+  x = min(x, xshf<4>(x));
+  x = min(x, xshf<2>(x));
+  x = min(x, xshf<1>(x));
   return x;
 }
 
@@ -277,47 +367,77 @@ __device__ __forceinline__ T block_sum(T x, T* lds) {
   return t;
 }
 
+// One compare-exchange stage at xor distance J: in `asc` runs the better
+// entry moves to the lower lane.
+template <int J>
+__device__ __forceinline__ void cx(float& v, int& i, bool asc) {
+  const int lane = threadIdx.x & 63;
+  const float ov = xshf<J>(v);
+  const int oi = xshf<J>(i);
+  const bool first = (lane & J) == 0;
+  const bool ob = better(ov, oi, v, i);
+  if ((first == asc) ? ob : !ob) {
+    v = ov;
+    i = oi;
+  }
+}
+template <int K>
+__device__ __forceinline__ void bitonic_stage(float& v, int& i) {
+  const bool asc = ((threadIdx.x & 63) & K) == 0;
+  if constexpr (K >= 64) cx<32>(v, i, asc);
+  if constexpr (K >= 32) cx<16>(v, i, asc);
+  if constexpr (K >= 16) cx<8>(v, i, asc);
+  if constexpr (K >= 8) cx<4>(v, i, asc);
+  if constexpr (K >= 4) cx<2>(v, i, asc);
+  cx<1>(v, i, asc);
+}
+
 // Bitonic sort of one entry per lane, best (v desc, i asc) in lane 0.
 __device__ __forceinline__ void wave_sort(float& v, int& i) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int k = 2; k <= 64; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      const float ov = __shfl_xor(v, j, 64);
-      const int oi = __shfl_xor(i, j, 64);
-      const bool first = (lane & j) == 0;
-      const bool asc = (lane & k) == 0;
-      const bool ob = better(ov, oi, v, i);
-      if ((first == asc) ? ob : !ob) {
-        v = ov;
-        i = oi;
-      }
-    }
-  }
+  bitonic_stage<2>(v, i);
+  bitonic_stage<4>(v, i);
+  bitonic_stage<8>(v, i);
+  bitonic_stage<16>(v, i);
+  bitonic_stage<32>(v, i);
+  bitonic_stage<64>(v, i);
 }
 
 // Merge the sorted lane list (lv, li) with another sorted list (nv, ni),
-// keeping the best 64.
+// keeping the best 64: reverse the incoming list (lane ^ 63), keep the better
+// of each pair, then one bitonic half-cleaning pass.
 __device__ __forceinline__ void wave_list_merge(float& lv, int& li, float nv, int ni) {
-  const int lane = threadIdx.x & 63;
-  const float rv = __shfl(nv, 63 - lane, 64);
-  const int ri = __shfl(ni, 63 - lane, 64);
+  const float rv = xshf<32>(xshf<16>(xshf<15>(nv)));
+  const int ri = xshf<32>(xshf<16>(xshf<15>(ni)));
   if (better(rv, ri, lv, li)) {
     lv = rv;
     li = ri;
   }
-#pragma unroll
-  for (int j = 32; j > 0; j >>= 1) {
-    const float ov = __shfl_xor(lv, j, 64);
-    const int oi = __shfl_xor(li, j, 64);
-    const bool first = (lane & j) == 0;
-    const bool ob = better(ov, oi, lv, li);
-    if (first ? ob : !ob) {
-      lv = ov;
-      li = oi;
-    }
+  cx<32>(lv, li, true);
+  cx<16>(lv, li, true);
+  cx<8>(lv, li, true);
+  cx<4>(lv, li, true);
+  cx<2>(lv, li, true);
+  cx<1>(lv, li, true);
+}
+
+// Best (v desc, i asc) over the wave, in every lane.
+__device__ __forceinline__ void wave_best(float& v, int& i) {
+#define MLXF_BEST_STEP(M)                  \
+  {                                        \
+    const float ov = xshf<M>(v);           \
+    const int oi = xshf<M>(i);             \
+    if (better(ov, oi, v, i)) {            \
+      v = ov;                              \
+      i = oi;                              \
+    }                                      \
   }
+  MLXF_BEST_STEP(32)
+  MLXF_BEST_STEP(16)
+  MLXF_BEST_STEP(8)
+  MLXF_BEST_STEP(4)
+  MLXF_BEST_STEP(2)
+  MLXF_BEST_STEP(1)
+#undef MLXF_BEST_STEP
 }
 
 struct TopEnt {

@@ -5,13 +5,14 @@
 // 141-166), run once per row by Worker::sample_rows (src/runtime/worker.cpp:
 // 448-486), with ONE kernel launch over all rows of a [B, V] logits matrix.
 //
-// Grid (S, B): row r is cut into S slices of L = 1024 * EPT elements; slice s
-// is one 1024-thread workgroup that loads its whole slice into registers with
-// 16-byte loads (one HBM read of the logits) and reduces it there:
+// Grid (S, B): row r is cut into S slices of L = 256 * EPT elements (EPT up to
+// 32); slice s is one 256-thread workgroup (4 waves, up to 256 VGPRs each, two
+// workgroups per CU) that loads its whole slice into registers with 16-byte
+// loads (one HBM read of the logits) and reduces it there:
 //   * max and lowest-index argmax of z, and sum exp(z - max) when a logprob is
 //     wanted;
 //   * when top_logprobs or a top-k <= 63 is asked for: the slice's best 64
-//     entries by (z desc, index asc).  The 64th best of the 1024 per-thread
+//     entries by (z desc, index asc).  The 64th best of the 256 per-thread
 //     maxima bounds the slice's 64th best from below; the at most 64 * EPT
 //     elements at or above it are sorted in 64-entry chunks and merged;
 //   * top-k > 63: a 4096-bin count histogram of z keys gives the bin of the
@@ -149,7 +150,7 @@ __device__ __forceinline__ void lds_add_agg(unsigned long long* base, int idx, u
   const unsigned long long bal = __ballot(act);
   if (!bal) return;
   const int first = __ffsll(static_cast<long long>(bal)) - 1;
-  const int i0 = __shfl(idx, first, 64);
+  const int i0 = rdl(idx, first);
   if (__ballot(act && idx != i0) == 0) {
     const unsigned long long s = wave_sum(act ? q : 0ull);
     if ((threadIdx.x & 63) == first && s) atomicAdd(base + i0, s);
@@ -161,7 +162,7 @@ __device__ __forceinline__ void lds_cnt_agg(unsigned int* base, int idx, bool ac
   const unsigned long long bal = __ballot(act);
   if (!bal) return;
   const int first = __ffsll(static_cast<long long>(bal)) - 1;
-  const int i0 = __shfl(idx, first, 64);
+  const int i0 = rdl(idx, first);
   if (__ballot(act && idx != i0) == 0) {
     if ((threadIdx.x & 63) == first) atomicAdd(base + i0, static_cast<unsigned int>(__popcll(bal)));
   } else if (act) {
@@ -172,13 +173,12 @@ __device__ __forceinline__ void lds_cnt_agg(unsigned int* base, int idx, bool ac
 // ------------------------------------------------------------ shared memory --
 
 union Region0 {  // 32 KB
-  TopEnt lists[WAVES * LIST];
   uint2 cand[CAND_LDS];
+  TopEnt surv[CAND_LDS];  // >= 64 * EPT: the most elements that can reach theta
 };
-union Region1 {  // 24 KB
+union Region1 {  // 16 KB
   unsigned int cnt[CNT_BINS];
   unsigned long long hist[NBIN];
-  TopEnt surv[WAVES * LIST];
   struct {
     double sp[MAX_S * WAVES];
     unsigned long long sq[MAX_S * WAVES];
@@ -187,9 +187,11 @@ union Region1 {  // 24 KB
 struct Small {
   Args args;
   Mode md;
+  TopEnt lists[WAVES * LIST];  // tree merges
   float rf[WAVES];
   int ri[WAVES];
   double rd[WAVES + 1];
+  double rd2[WAVES];
   unsigned long long ru[WAVES + 1];
   int rint[WAVES + 1];
   unsigned int ticket;
@@ -277,11 +279,8 @@ __device__ unsigned int radix_select(const CandView& cv, int n, PART part, WQ wq
       if (MASS) mass_all += wq(e);
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    lo = min(lo, __shfl_xor(lo, o, 64));
-    hi = max(hi, __shfl_xor(hi, o, 64));
-  }
+  lo = wave_min(lo);
+  hi = wave_max(hi);
   if (tid == 0) {
     sh.kmin = 0xffffffffu;
     sh.kmax = 0u;
@@ -387,20 +386,16 @@ __device__ unsigned int radix_select(const CandView& cv, int n, PART part, WQ wq
         }
         run += val[q];
       }
-      int best = found;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) best = min(best, __shfl_xor(best, o, 64));
-      int lbest = lastne;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) lbest = max(lbest, __shfl_xor(lbest, o, 64));
+      int best = wave_min(found);
+      const int lbest = wave_max(lastne);
       // the total reaches the target, so some digit qualifies; the last
       // non-empty digit only guards against a total that rounding made short
       unsigned long long b;
       if (best < 4 * 64) {
-        b = __shfl(bef, best >> 2, 64);
+        b = rdl(bef, best >> 2);
       } else {
         best = lbest < 0 ? 0 : lbest;
-        b = __shfl(bef_last, best >> 2, 64);
+        b = rdl(bef_last, best >> 2);
       }
       if (lane == 0) {
         const int d = DESC ? RBINS - 1 - best : best;
@@ -487,7 +482,9 @@ __device__ int resolve_topk(const Mode& md, const CandView& cv, int n, float Mp,
 
 // Walk slice s in vocabulary order; the first kept element at which the
 // running mass w(z', mps_s) exceeds rem is the draw.  Kept: key(z') > vkey, or
-// equal with index <= idx_cut.  Thread t owns EPT consecutive elements.
+// equal with index <= idx_cut.  Thread t owns EPT consecutive elements, read 8
+// at a time (the thread that holds the crossing reads its elements again; they
+// are in L2 by then).
 template <int DT, int EPT, bool VECOK>
 __device__ int final_scan(const Args& a, const Mode& md, const void* row, int s, double rem,
                           unsigned int vkey, int idx_cut, Small& sh) {
@@ -502,16 +499,18 @@ __device__ int final_scan(const Args& a, const Mode& md, const void* row, int s,
     const bool kept = i < e0 && (key > vkey || (key == vkey && i <= idx_cut));
     return kept ? wexp(zp, mps) : 0.0f;
   };
-  float z[EPT];
-#pragma unroll
-  for (int it = 0; it < EPT / VEC; ++it) load8<DT, VECOK>(row, my0 + it * VEC, e0, z + it * VEC);
   double sum = 0.0;
   int last_pos = -1;
+#pragma unroll 2
+  for (int it = 0; it < EPT / VEC; ++it) {
+    float z[VEC];
+    load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    const float ww = weight(z[e], my0 + e);
-    sum += static_cast<double>(ww);
-    if (ww > 0.0f) last_pos = my0 + e;
+    for (int j = 0; j < VEC; ++j) {
+      const float ww = weight(z[j], my0 + it * VEC + j);
+      sum += static_cast<double>(ww);
+      if (ww > 0.0f) last_pos = my0 + it * VEC + j;
+    }
   }
   double ex, in, tot;
   block_scan<double>(sum, sh.rd, &ex, &in, &tot);
@@ -520,20 +519,22 @@ __device__ int final_scan(const Args& a, const Mode& md, const void* row, int s,
   if (ex <= rem && rem < in) {
     double c = ex;
     int pick = -1;
+    for (int it = 0; it < EPT / VEC && pick < 0; ++it) {
+      float z[VEC];
+      load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const float ww = weight(z[e], my0 + e);
-      c += static_cast<double>(ww);
-      if (pick < 0 && c > rem && ww > 0.0f) pick = my0 + e;
+      for (int j = 0; j < VEC; ++j) {
+        const float ww = weight(z[j], my0 + it * VEC + j);
+        c += static_cast<double>(ww);
+        if (pick < 0 && c > rem && ww > 0.0f) pick = my0 + it * VEC + j;
+      }
     }
     sh.found = pick < 0 ? last_pos : pick;  // rounding inside the thread: its last positive element
   }
   __syncthreads();
   int id = sh.found;
   if (id < 0) {  // rem at or past the slice total (fp64 rounding): last kept element
-    int lp = last_pos;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) lp = max(lp, __shfl_xor(lp, o, 64));
+    const int lp = wave_max(last_pos);
     if ((tid & 63) == 0) sh.rint[tid >> 6] = lp;
     __syncthreads();
     if (tid == 0) {
@@ -609,9 +610,9 @@ __device__ bool klist_resolve(const Mode& md, float Mp, const Small& sh, int* id
   const int li = sh.mlist[lane].i;
   const bool real = li != INT_MAX;
   const float zp = real ? fz<DT>(lv, md.Tr) : -INFINITY;
-  const float tau = __shfl(zp, md.kk - 1, 64);
-  const int last_i = __shfl(li, LIST - 1, 64);
-  const float last_zp = __shfl(zp, LIST - 1, 64);
+  const float tau = rdl(zp, md.kk - 1);
+  const int last_i = rdl(li, LIST - 1);
+  const float last_zp = rdl(zp, LIST - 1);
   // every element with z' >= tau is in the list unless the list's last entry reaches tau
   if (last_i != INT_MAX && !(last_zp < tau)) return false;
   const bool in_k = real && zp >= tau;
@@ -621,7 +622,7 @@ __device__ bool klist_resolve(const Mode& md, float Mp, const Small& sh, int* id
   const bool k1 = si != INT_MAX;
   const unsigned long long w = k1 ? quant(wexp(sv, Mp)) : 0ull;
   const unsigned long long incl = wave_incl_scan(w);
-  const unsigned long long Wk = __shfl(incl, 63, 64);
+  const unsigned long long Wk = rdl(incl, 63);
   bool keep = k1;
   if (md.topp) {
     const unsigned long long PW =
@@ -643,10 +644,8 @@ __device__ bool klist_resolve(const Mode& md, float Mp, const Small& sh, int* id
     const int iq = __builtin_amdgcn_readlane(si, q);
     if (iq <= si) cum += pack2(wlo, whi);
   }
-  int cand = (keep && (Wf == 0 || (wf > 0 && cum > T))) ? si : INT_MAX;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) cand = min(cand, __shfl_xor(cand, o, 64));
-  *id_out = cand == INT_MAX ? __shfl(si, 0, 64) : cand;
+  const int cand = wave_min((keep && (Wf == 0 || (wf > 0 && cum > T))) ? si : INT_MAX);
+  *id_out = cand == INT_MAX ? rdl(si, 0) : cand;
   return true;
 }
 
@@ -661,7 +660,9 @@ __device__ void row_pass(const Args& a, const Mode& md, const void* row, int r, 
                          bool has_hi, unsigned int khi, int sum_side, Region0& r0, Region1& r1,
                          Small& sh) {
   constexpr int NIT = EPT / VEC;
-  constexpr int G = (DT == MLXF_DTYPE_F32 ? 32 : 64) / EPT;
+  // slices whose raw loads are in flight together: about 64 VGPRs of raw data
+  constexpr int G0 = (DT == MLXF_DTYPE_F32 ? 64 : 128) / EPT;
+  constexpr int G = G0 > 8 ? 8 : G0;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int S = a.S;
   uint2* g = a.cand + static_cast<size_t>(r) * S * a.L;
@@ -710,7 +711,7 @@ __device__ void row_pass(const Args& a, const Mode& md, const void* row, int r, 
             if (bal) {
               unsigned int basepos = 0;
               if (lane == 0) basepos = atomicAdd(&sh.ncand, static_cast<unsigned int>(__popcll(bal)));
-              basepos = __shfl(basepos, 0, 64);
+              basepos = rdl(basepos, 0);
               if (inr) {
                 const unsigned int pos =
                     basepos + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(bal >> 32),
@@ -812,14 +813,18 @@ __device__ void finish_topp(const Args& a, const Mode& md, const void* row, int 
   const int tid = threadIdx.x;
   const int S = a.S;
 
-  // ---- A: thread t owns descending positions 2t, 2t+1 (bins NBIN-1-2t, NBIN-2-2t)
+  // ---- A: thread t owns descending positions PB*t .. PB*t+PB-1 (bins NBIN-1-PB*t ...)
+  constexpr int PB = NBIN / THREADS;
   {
     const size_t hb = static_cast<size_t>(r) * S * NBIN;
-    unsigned int c[2] = {0u, 0u};
-    double m[2] = {0.0, 0.0}, e[2] = {0.0, 0.0};
+    unsigned int c[PB];
+    double m[PB], e[PB];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int b = NBIN - 1 - (2 * tid + q);
+    for (int q = 0; q < PB; ++q) {
+      c[q] = 0u;
+      m[q] = 0.0;
+      e[q] = 0.0;
+      const int b = NBIN - 1 - (PB * tid + q);
 #pragma unroll 8
       for (int t = 0; t < S; ++t) {
         const unsigned long long h = ld_dev(a.hist + hb + static_cast<size_t>(t) * NBIN + b);
@@ -837,9 +842,15 @@ __device__ void finish_topp(const Args& a, const Mode& md, const void* row, int 
       sh.pos_lo = NBIN;
       sh.pos_last = -1;
     }
+    double sA = 0.0, sU = 0.0;
+#pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      sA += m[q];
+      sU += m[q] + e[q];
+    }
     double exA, inA, totA, exU, inU, totU;
-    block_scan<double>(m[0] + m[1], sh.rd, &exA, &inA, &totA);
-    block_scan<double>(m[0] + m[1] + e[0] + e[1], sh.rd, &exU, &inU, &totU);
+    block_scan<double>(sA, sh.rd, &exA, &inA, &totA);
+    block_scan<double>(sU, sh.rd, &exU, &inU, &totU);
     const double PW = sh.seld[2];
     // first position whose cumulative upper bound reaches p*W: the boundary is
     // not above it; first position whose cumulative lower bound reaches it:
@@ -848,13 +859,13 @@ __device__ void finish_topp(const Args& a, const Mode& md, const void* row, int 
     int ph = NBIN, pl = NBIN, last = -1;
     double runA = exA, runU = exU;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < PB; ++q) {
       runA += m[q];
       runU += m[q] + e[q];
       if (c[q] > 0) {
-        if (ph == NBIN && runU >= t_hi) ph = 2 * tid + q;
-        if (pl == NBIN && runA >= t_lo) pl = 2 * tid + q;
-        last = 2 * tid + q;
+        if (ph == NBIN && runU >= t_hi) ph = PB * tid + q;
+        if (pl == NBIN && runA >= t_lo) pl = PB * tid + q;
+        last = PB * tid + q;
       }
     }
     if (ph < NBIN) atomicMin(&sh.pos_hi, ph);
@@ -868,8 +879,8 @@ __device__ void finish_topp(const Args& a, const Mode& md, const void* row, int 
     // positions count down from the top bin: bhi = NBIN-1-p_hi >= blo = NBIN-1-p_lo
     int ca = 0, cb = 0;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int pos = 2 * tid + q;
+    for (int q = 0; q < PB; ++q) {
+      const int pos = PB * tid + q;
       if (pos < p_hi) ca += static_cast<int>(c[q]);
       if (pos > p_lo) cb += static_cast<int>(c[q]);
     }
@@ -1026,7 +1037,7 @@ __device__ __forceinline__ void finish_row(int r, Region0& r0, Region1& r1, Smal
       const unsigned long long w = ld_dev(a.list + (static_cast<size_t>(r) * S + t) * LIST + lane);
       wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
     }
-    tree_merge(lv, li, r0.lists, S < WAVES ? S : WAVES);
+    tree_merge(lv, li, sh.lists, S < WAVES ? S : WAVES);
     if (wid == 0) {
       sh.mlist[lane].v = lv;
       sh.mlist[lane].i = li;
@@ -1038,15 +1049,7 @@ __device__ __forceinline__ void finish_row(int r, Region0& r0, Region1& r1, Smal
     const int za = lane < S ? sh.szarg[lane] : INT_MAX;
     float rm = zm;
     int ra = za;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(rm, o, 64);
-      const int oi = __shfl_xor(ra, o, 64);
-      if (better(ov, oi, rm, ra)) {
-        rm = ov;
-        ra = oi;
-      }
-    }
+    wave_best(rm, ra);
     double part = (lane < S && md.need_lse) ? sh.slse[lane] * wexp_d(zm, rm) : 0.0;
     part = wave_sum(part);
     const float Mp = md.sampling ? fz<DT>(rm, md.Tr) : 0.0f;
@@ -1109,7 +1112,7 @@ __device__ __forceinline__ void finish_row(int r, Region0& r0, Region1& r1, Smal
 // =================================================================== kernel ==
 
 template <int DT, int EPT, bool VECOK>
-__global__ __launch_bounds__(THREADS) void k_sample(Args a) {
+__global__ __launch_bounds__(THREADS, 2) void k_sample(Args a) {
   __shared__ Region0 r0;
   __shared__ Region1 r1;
   __shared__ Small sh;
@@ -1128,108 +1131,96 @@ __global__ __launch_bounds__(THREADS) void k_sample(Args a) {
   for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
 #define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
 
-  // ---- max and lowest-index argmax: per thread, then per wave, then the slice
-  float tbv = -INFINITY;
-  int tbi = INT_MAX;
+  // Histograms are cleared while the loads are in flight.  The pass has two
+  // barriers: B1 publishes the wave maxima (and list thresholds), B2 the
+  // argmax, the sums and the survivors.
+  if (md.kind == KIND_TOPP) {
+    for (int b = tid; b < NBIN; b += THREADS) r1.hist[b] = 0ull;
+  } else if (md.kind == KIND_KHIST) {
+    for (int b = tid; b < CNT_BINS; b += THREADS) r1.cnt[b] = 0u;
+  }
+  if (tid == 0) sh.ncand = 0u;
+
+  // ---- thread max; each wave's max and, for the best-64 list, the wave's 16th
+  // largest thread maximum (a bisection on the key with ballots)
+  float tmax = v[0];
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    const int i = MLXF_IDX(e);
-    if (i < end && better(v[e], i, tbv, tbi)) {
-      tbv = v[e];
-      tbi = i;
+  for (int e = 1; e < EPT; ++e) tmax = fmaxf(tmax, v[e]);
+  unsigned int tw = 0u;
+  if (md.need_list) {
+    const unsigned int k = f2key(tmax);
+#pragma unroll 4
+    for (int b = 31; b >= 0; --b) {
+      const unsigned int c = tw | (1u << b);
+      if (__popcll(__ballot(k >= c)) >= LIST / WAVES) tw = c;
     }
   }
-  float bm = tbv;
-  int bi = tbi;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bm, o, 64);
-    const int oi = __shfl_xor(bi, o, 64);
-    if (better(ov, oi, bm, bi)) {
-      bm = ov;
-      bi = oi;
+  {
+    const float wm = wave_max(tmax);
+    if (lane == 0) {
+      sh.rf[wid] = wm;
+      sh.rint[wid] = static_cast<int>(tw);
     }
   }
-  if (lane == 0) {
-    sh.rf[wid] = bm;
-    sh.ri[wid] = bi;
-  }
-  __syncthreads();
+  __syncthreads();  // B1
   float zmax = sh.rf[0];
-  int zarg = sh.ri[0];
-  for (int w2 = 1; w2 < WAVES; ++w2)
-    if (better(sh.rf[w2], sh.ri[w2], zmax, zarg)) {
-      zmax = sh.rf[w2];
-      zarg = sh.ri[w2];
-    }
+#pragma unroll
+  for (int w2 = 1; w2 < WAVES; ++w2) zmax = fmaxf(zmax, sh.rf[w2]);
+
+  // ---- lowest index holding the max: only threads that hold it look.  Entries
+  // at or past `end` read as -inf and come after the thread's valid entries.
+  int targ = INT_MAX;
+  if (tmax == zmax) {
+#pragma unroll
+    for (int e = EPT - 1; e >= 0; --e)
+      if (v[e] == zmax && MLXF_IDX(e) < end) targ = MLXF_IDX(e);
+  }
 
   // ---- log-sum-exp partial
-  double lse_s = 0.0;
   if (md.need_lse) {
     float t = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPT; ++e)
       if (MLXF_IDX(e) < end) t += wexp(v[e], zmax);
-    lse_s = block_sum<double>(static_cast<double>(t), sh.rd);
+    const double ws = wave_sum(static_cast<double>(t));
+    if (lane == 0) sh.rd[wid] = ws;
   }
 
-  // ---- best 64 of the slice.  theta = the 64th best thread maximum: at least
-  // 64 elements reach it, so the slice's best 64 all do; at most 64 threads
-  // hold elements that reach it, so at most 64 * EPT elements survive.
+  // ---- best-64 survivors.  theta, the smallest wave threshold, is reached by
+  // at least 64 elements (16 thread maxima per wave), so the slice's best 64
+  // all reach it.  Survivors are appended in LDS with one atomic per thread.
   if (md.need_list) {
-    float lv = tbv;
-    int li = tbi;
-    wave_sort(lv, li);
-    tree_merge(lv, li, r0.lists, WAVES);
-    if (tid == LIST - 1) {
-      sh.thv = lv;
-      sh.thi = li;
-    }
-    __syncthreads();
-    const float thv = sh.thv;
-    const int thi = sh.thi;
-    int mine = 0;
+    unsigned int tk = static_cast<unsigned int>(sh.rint[0]);
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && !better(thv, thi, v[e], MLXF_IDX(e))) ? 1 : 0;
-    int ntot;
-    int pos = block_excl_scan<int>(mine, sh.rint, &ntot);
+    for (int w2 = 1; w2 < WAVES; ++w2) tk = min(tk, static_cast<unsigned int>(sh.rint[w2]));
+    const float thv = key2f(tk < KEY_NEG_INF ? KEY_NEG_INF : tk);
+    if (tmax >= thv) {
+      int mine = 0;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const int i = MLXF_IDX(e);
-      if (i < end && !better(thv, thi, v[e], i)) {
-        r1.surv[pos].v = v[e];
-        r1.surv[pos].i = i;
-        ++pos;
+      for (int e = 0; e < EPT; ++e) mine += (v[e] >= thv && MLXF_IDX(e) < end) ? 1 : 0;
+      if (mine > 0) {
+        int pos = static_cast<int>(atomicAdd(&sh.ncand, static_cast<unsigned int>(mine)));
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          const int i = MLXF_IDX(e);
+          if (v[e] >= thv && i < end) {
+            if (pos < CAND_LDS) {
+              r0.surv[pos].v = v[e];
+              r0.surv[pos].i = i;
+            }
+            ++pos;
+          }
+        }
       }
     }
-    __syncthreads();
-    const int nch = (ntot + LIST - 1) / LIST;  // <= EPT <= WAVES
-    float sv = -INFINITY;
-    int si = INT_MAX;
-    if (wid < nch) {
-      const int c = wid * LIST + lane;
-      if (c < ntot) {
-        sv = r1.surv[c].v;
-        si = r1.surv[c].i;
-      }
-    }
-    __syncthreads();
-    if (wid < nch) wave_sort(sv, si);
-    tree_merge(sv, si, r0.lists, nch);
-    if (wid == 0) st_dev(a.list + (static_cast<size_t>(r) * S + s) * LIST + lane, pack_ent(sv, si));
   }
 
-  // ---- per-kind slice work
+  // ---- temperature-only / top-p: slice mass w = exp(z' - max z') and, for
+  // top-p, the (count, truncated w) histogram of z' keys
   float mps = 0.0f;
-  double msum = 0.0;
-  unsigned int ncand = 0;
   if (md.kind == KIND_TEMP || md.kind == KIND_TOPP) {
     mps = fz<DT>(zmax, md.Tr);
     const bool hist = md.kind == KIND_TOPP;
-    if (hist) {
-      for (int b = tid; b < NBIN; b += THREADS) r1.hist[b] = 0ull;
-      __syncthreads();
-    }
     double t = 0.0;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
@@ -1243,34 +1234,110 @@ __global__ __launch_bounds__(THREADS) void k_sample(Args a) {
                         static_cast<unsigned long long>(static_cast<unsigned int>(w * 16777216.0f)));
       }
     }
-    msum = block_sum<double>(t, sh.rd);
-    if (hist) {
-      __syncthreads();
-      const size_t off = (static_cast<size_t>(r) * S + s) * NBIN;
-      for (int b = tid; b < NBIN; b += THREADS) st_dev(a.hist + off + b, r1.hist[b]);
-    }
+    const double ws = wave_sum(t);
+    if (lane == 0) sh.rd2[wid] = ws;
   } else if (md.kind == KIND_KHIST) {
-    for (int b = tid; b < CNT_BINS; b += THREADS) r1.cnt[b] = 0u;
-    __syncthreads();
 #pragma unroll
     for (int e = 0; e < EPT; ++e)
       if (MLXF_IDX(e) < end) atomicAdd(&r1.cnt[f2key(v[e]) >> 20], 1u);
-    __syncthreads();
-    // thread t owns descending positions 4t..4t+3 (bins 4095-4t .. 4092-4t)
-    int c4[4], sum4 = 0;
+  }
+  {
+    const int wa = wave_min(targ);
+    if (lane == 0) sh.ri[wid] = wa;
+  }
+  __syncthreads();  // B2
+  int zarg = sh.ri[0];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      c4[q] = static_cast<int>(r1.cnt[CNT_BINS - 1 - (4 * tid + q)]);
-      sum4 += c4[q];
+  for (int w2 = 1; w2 < WAVES; ++w2) zarg = min(zarg, sh.ri[w2]);
+  double lse_s = 0.0, msum = 0.0;
+  if (md.need_lse) {
+    lse_s = sh.rd[0];
+#pragma unroll
+    for (int w2 = 1; w2 < WAVES; ++w2) lse_s += sh.rd[w2];
+  }
+  if (md.kind == KIND_TEMP || md.kind == KIND_TOPP) {
+    msum = sh.rd2[0];
+#pragma unroll
+    for (int w2 = 1; w2 < WAVES; ++w2) msum += sh.rd2[w2];
+  }
+
+  // ---- best 64 of the slice from the survivors
+  if (md.need_list) {
+    int ntot = static_cast<int>(sh.ncand);
+    if (ntot > CAND_LDS) {
+      // Heavy ties at theta: the exact (value desc, index asc) 64th best thread
+      // maximum instead, which at most 64 * EPT elements reach.
+      int tbi = INT_MAX;
+#pragma unroll
+      for (int e = EPT - 1; e >= 0; --e)
+        if (v[e] == tmax && MLXF_IDX(e) < end) tbi = MLXF_IDX(e);
+      float lv = tmax;
+      int li = tbi;
+      wave_sort(lv, li);
+      tree_merge(lv, li, sh.lists, WAVES);
+      if (tid == LIST - 1) {
+        sh.thv = lv;
+        sh.thi = li;
+      }
+      __syncthreads();
+      const float tv = sh.thv;
+      const int ti = sh.thi;
+      int mine = 0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && !better(tv, ti, v[e], MLXF_IDX(e))) ? 1 : 0;
+      int pos = block_excl_scan<int>(mine, sh.rint, &ntot);
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int i = MLXF_IDX(e);
+        if (i < end && !better(tv, ti, v[e], i)) {
+          r0.surv[pos].v = v[e];
+          r0.surv[pos].i = i;
+          ++pos;
+        }
+      }
+      __syncthreads();
+    }
+    // 64-entry chunks: wave w sorts chunks w, w + WAVES, ... into its own list
+    const int nch = (ntot + LIST - 1) / LIST;
+    float sv = -INFINITY;
+    int si = INT_MAX;
+    for (int ch = wid; ch < nch; ch += WAVES) {
+      const int c = ch * LIST + lane;
+      float cv = -INFINITY;
+      int ci = INT_MAX;
+      if (c < ntot) {
+        cv = r0.surv[c].v;
+        ci = r0.surv[c].i;
+      }
+      wave_sort(cv, ci);
+      wave_list_merge(sv, si, cv, ci);
+    }
+    tree_merge(sv, si, sh.lists, nch < WAVES ? nch : WAVES);
+    if (wid == 0) st_dev(a.list + (static_cast<size_t>(r) * S + s) * LIST + lane, pack_ent(sv, si));
+  }
+
+  unsigned int ncand = 0;
+  if (md.kind == KIND_TOPP) {
+    const size_t off = (static_cast<size_t>(r) * S + s) * NBIN;
+    for (int b = tid; b < NBIN; b += THREADS) st_dev(a.hist + off + b, r1.hist[b]);
+  } else if (md.kind == KIND_KHIST) {
+    // the bin of the slice's k-th largest z; thread t owns descending
+    // positions PC*t .. PC*t+PC-1
+    constexpr int PC = CNT_BINS / THREADS;
+    int cq[PC], sumq = 0;
+#pragma unroll
+    for (int q = 0; q < PC; ++q) {
+      cq[q] = static_cast<int>(r1.cnt[CNT_BINS - 1 - (PC * tid + q)]);
+      sumq += cq[q];
     }
     int total;
-    const int ex = block_excl_scan<int>(sum4, sh.rint, &total);
+    const int ex = block_excl_scan<int>(sumq, sh.rint, &total);
     const int kk_s = md.kk < (end - beg) ? md.kk : (end - beg);
     int run = ex;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (run < kk_s && run + c4[q] >= kk_s) sh.sel[0] = CNT_BINS - 1 - (4 * tid + q);
-      run += c4[q];
+    for (int q = 0; q < PC; ++q) {
+      if (run < kk_s && run + cq[q] >= kk_s) sh.sel[0] = CNT_BINS - 1 - (PC * tid + q);
+      run += cq[q];
     }
     __syncthreads();
     if (tid == 0) {
@@ -1337,22 +1404,23 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 
 constexpr size_t CTR_BYTES_MAX = 65536 * sizeof(unsigned int);
 
-// EPT: the largest of {16, 8} that still gives >= 512 workgroups with at most
-// MAX_S slices per row; otherwise the smallest EPT with S <= MAX_S.
+// EPT: the largest of {32, 16, 8} that still gives at least one workgroup
+// per CU (256) with at most MAX_S slices per row; otherwise the smallest EPT
+// with S <= MAX_S (short batches: as many slices as allowed).
 Layout make_layout(int B, int V, int K_max) {
   (void)K_max;
   Layout l;
   int ept = 0;
-  for (int e : {16, 8}) {
+  for (int e : {32, 16, 8}) {
     const int L = THREADS * e;
     const int S = (V + L - 1) / L;
-    if (S <= MAX_S && static_cast<long long>(B) * S >= 512) {
+    if (S <= MAX_S && static_cast<long long>(B) * S >= 256) {
       ept = e;
       break;
     }
   }
   if (!ept) {
-    for (int e : {8, 16}) {
+    for (int e : {8, 16, 32}) {
       const int L = THREADS * e;
       if ((V + L - 1) / L <= MAX_S) {
         ept = e;
@@ -1418,7 +1486,14 @@ hipError_t launch_ept(const Args& a, bool vecok, hipStream_t st) {
 
 template <int DT>
 hipError_t launch_dt(const Args& a, int ept, bool vecok, hipStream_t st) {
-  return ept == 8 ? launch_ept<DT, 8>(a, vecok, st) : launch_ept<DT, 16>(a, vecok, st);
+  switch (ept) {
+    case 8:
+      return launch_ept<DT, 8>(a, vecok, st);
+    case 16:
+      return launch_ept<DT, 16>(a, vecok, st);
+    default:
+      return launch_ept<DT, 32>(a, vecok, st);
+  }
 }
 
 int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
