@@ -44,6 +44,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -61,8 +62,6 @@ constexpr int KLIST_MAX = LIST - 1;  // top-k resolved from the best-64 lists
 constexpr int CAND_LDS = 4096;
 constexpr int CNT_BINS = 4096;  // z-key >> 20: the per-slice top-k threshold bins
 constexpr int RBINS = 256;      // radix digit
-constexpr unsigned long long MASK40 = (1ull << 40) - 1;
-constexpr double HUNIT = 1.0 / 16777216.0;  // 2^-24: histogram mass unit
 
 struct SliceRec {  // four 64-bit words
   float zmax;
@@ -86,12 +85,60 @@ struct Args {
   float* out_lp;
   int* out_top_ids;
   float* out_top_lp;
-  unsigned int* ctr;
+  unsigned int* ctr;          // [B] first-pass tickets
+  unsigned int* done2;        // [B] second-pass tickets
+  unsigned long long* next2;  // [B] second-pass items taken (epoch-stamped)
+  unsigned long long* gl;     // call-wide counters (GL_*, epoch-stamped)
+  unsigned long long* queue;  // [B] rows with second-pass items: (epoch, row + 1)
+  unsigned int epoch;         // this call's stamp (never 0)
+  int helpers;                // workgroups after the first B*S
   SliceRec* rec;
-  unsigned long long* list;  // [B*S][64] packed (z bits, index)
-  unsigned long long* hist;  // [B*S][NBIN]
-  uint2* cand;               // [B*S][L]
+  unsigned long long* list;   // [B*S][64] packed (z bits, index)
+  unsigned long long* hist;   // [B*S][NBIN]
+  uint2* cand;                // [B*S][L]
+  unsigned long long* plan;   // [B][PLAN_WORDS]
+  double* above;              // [B*S] mass above the bracket, slice units
+  unsigned int* ncand2;       // [B*S] second-pass candidates per slice
 };
+
+// Call-wide counters: queue slots reserved, rows finished, whether any row of
+// the call has a second pass, and the first queue slot whose row may still have
+// items left.  These, the per-row item counters and the
+// queue slots are 64-bit words (epoch << 32 | value): a word stamped by another
+// call reads as zero, so nothing needs resetting between calls.  (The per-row
+// tickets ctr / done2 are plain counters, reset by their last user.)
+enum { GL_QRES = 0, GL_ROWS = 1, GL_NEED = 2, GL_HEAD = 3, GL_WORDS = 8 };
+constexpr int IDLE_LIMIT = 1 << 16;  // bound on a helper's idle polls (each sleeps up to ~2 us)
+
+__device__ __forceinline__ unsigned int stamped(unsigned long long w, unsigned int epoch) {
+  return static_cast<unsigned int>(w >> 32) == epoch ? static_cast<unsigned int>(w) : 0u;
+}
+__device__ __forceinline__ unsigned int stamped_get(const unsigned long long* p, unsigned int epoch) {
+  return stamped(ld_dev(p), epoch);
+}
+// Take the next value of a stamped counter: the first taker in a call claims
+// the word (compare-exchange from the stale stamp to (epoch, 1)), everyone
+// else adds 1.  Returns the value taken, or `limit` once it has reached limit
+// (the low half never reaches the stamp: there are far fewer takers than 2^32).
+__device__ __forceinline__ unsigned int stamped_take(unsigned long long* p, unsigned int epoch,
+                                                     unsigned int limit) {
+  unsigned long long w = ld_dev(p);
+  if (static_cast<unsigned int>(w >> 32) != epoch) {
+    const unsigned long long claim = (static_cast<unsigned long long>(epoch) << 32) | 1u;
+    if (__hip_atomic_compare_exchange_strong(p, &w, claim, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT))
+      return 0u < limit ? 0u : limit;
+    if (static_cast<unsigned int>(w >> 32) != epoch) return limit;  // (another call's stamp: not ours)
+  }
+  const unsigned long long old = __hip_atomic_fetch_add(p, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned int v = static_cast<unsigned int>(old);
+  return v < limit ? v : limit;
+}
+
+// The plan a row's first pass leaves for its second pass (64-bit words): bracket z-key range [klo, khi), has_hi, value
+// mode (nv > 0: nv z' values from value index vbase), the nucleus mass still to
+// cover inside the bracket (2^-42 row units), the row's LSE and max z'.
+enum { PL_KEYS = 0, PL_MODE = 1, PL_TARGET = 2, PL_LSE = 3, PL_MP = 4, PLAN_WORDS = 5 };
 
 struct Mode {
   int sampling, kk, topp, K, need_lse, want_lp, kind, need_list;
@@ -174,11 +221,13 @@ __device__ __forceinline__ void lds_cnt_agg(unsigned int* base, int idx, bool ac
 
 union Region0 {  // 32 KB
   uint2 cand[CAND_LDS];
+  unsigned int vcnt[2 * CAND_LDS];     // 16-bit counters, two per word
+  unsigned short vc16[4 * CAND_LDS];   // per (slice, z' value) counts
   TopEnt surv[CAND_LDS];  // >= 64 * EPT: the most elements that can reach theta
 };
 union Region1 {  // 16 KB
   unsigned int cnt[CNT_BINS];
-  unsigned long long hist[NBIN];
+  unsigned long long hist[NBIN];  // exact 2^-42 masses of w(z', mps) per z'-key bin
   struct {
     double sp[MAX_S * WAVES];
     unsigned long long sq[MAX_S * WAVES];
@@ -223,6 +272,11 @@ struct Small {
   unsigned int kmin, kmax;
   int found;
   int pos_hi, pos_lo, pos_last;
+  int bmin[WAVES], bmax[WAVES];
+  int rlo[MAX_S], rhi[MAX_S];  // occupied histogram bins per slice
+  unsigned long long plan[PLAN_WORDS];
+  int qrow, qitem;
+  unsigned int qn, rdone;
 };
 
 // A row's candidate list: in LDS, in global memory contiguous, or in global
@@ -649,88 +703,101 @@ __device__ bool klist_resolve(const Mode& md, float Mp, const Small& sh, int* id
   return true;
 }
 
-// Compare-only pass over the row (the finishing workgroup alone): elements with
-// z key in [klo, khi) become candidates (z' key, index), and the in-range mass
-// of slice t (2^-42 units of w(z', mps_t)) goes to r1.pass.sq[t * WAVES + wave];
-// when `sum_side` is 1 (above: z key >= khi) or 2 (below: z key < klo) the mass
-// of that side goes to r1.pass.sp.  has_hi false: no upper bound.  G slices'
-// loads are in flight at once.
+// z' value index shift for the 16-bit types: z' is a bf16 / f16 value held in
+// fp32, so its key's low VSHIFT bits carry no information.
+template <int DT>
+constexpr int vshift() {
+  return DT == MLXF_DTYPE_BF16 ? 16 : 13;
+}
+
+// Compare-only pass over the row (the finishing workgroup alone).  Elements
+// with z key in [klo, khi) are "in range"; their mass (2^-42 units of
+// w(z', mps_t)) goes to r1.pass.sq[t * WAVES + wave].  In candidate mode
+// (nv == 0) they become candidates (z' key, index); in value mode (nv > 0, the
+// 16-bit types) they are counted per (slice, z' value) in 16-bit counters
+// r0.vcnt (value index (z' key >> vshift) - vbase).  When `sum_side` is 1
+// (above: z key >= khi) or 2 (below: z key < klo) the mass of that side goes to
+// r1.pass.sp (fp64).  has_hi false: no upper bound.  The next slice's loads
+// are in flight while a slice is processed.
 template <int DT, int EPT, bool VECOK>
 __device__ void row_pass(const Args& a, const Mode& md, const void* row, int r, unsigned int klo,
-                         bool has_hi, unsigned int khi, int sum_side, Region0& r0, Region1& r1,
-                         Small& sh) {
+                         bool has_hi, unsigned int khi, int sum_side, int nv, unsigned int vbase,
+                         Region0& r0, Region1& r1, Small& sh) {
   constexpr int NIT = EPT / VEC;
-  // slices whose raw loads are in flight together: about 64 VGPRs of raw data
-  constexpr int G0 = (DT == MLXF_DTYPE_F32 ? 64 : 128) / EPT;
-  constexpr int G = G0 > 8 ? 8 : G0;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int S = a.S;
   uint2* g = a.cand + static_cast<size_t>(r) * S * a.L;
+  if (nv > 0) {
+    for (int w = tid; w < (S * nv + 1) / 2; w += THREADS) r0.vcnt[w] = 0u;
+    __syncthreads();
+  }
+  // double buffer: slice t+1's loads are in flight while slice t is processed
+  Raw8<DT> cur[NIT], nxt[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) load_raw<DT, VECOK>(row, it * CHUNK + tid * VEC, min(a.V, a.L), cur[it]);
 #pragma unroll 1
-  for (int t0 = 0; t0 < S; t0 += G) {
-    Raw8<DT> q[G][NIT];
+  for (int t = 0; t < S; ++t) {
+    const int b0 = t * a.L, e0 = min(a.V, b0 + a.L);
+    if (t + 1 < S) {
+      const int nb0 = b0 + a.L, ne0 = min(a.V, nb0 + a.L);
 #pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-      const int t = t0 + gi;
-      if (t < S) {
-        const int b0 = t * a.L, e0 = min(a.V, b0 + a.L);
-#pragma unroll
-        for (int it = 0; it < NIT; ++it) load_raw<DT, VECOK>(row, b0 + it * CHUNK + tid * VEC, e0, q[gi][it]);
-      }
+      for (int it = 0; it < NIT; ++it) load_raw<DT, VECOK>(row, nb0 + it * CHUNK + tid * VEC, ne0, nxt[it]);
     }
+    const float mps = sh.mps[t];
+    double part = 0.0;
+    unsigned long long pq = 0;
 #pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-      const int t = t0 + gi;
-      if (t < S) {
-        const int b0 = t * a.L, e0 = min(a.V, b0 + a.L);
-        const float mps = sh.mps[t];
-        float part = 0.0f;
-        unsigned long long pq = 0;
+    for (int it = 0; it < NIT; ++it) {
+      float z[VEC];
+      decode8<DT>(cur[it], z);
+      const int i0 = b0 + it * CHUNK + tid * VEC;
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-          float z[VEC];
-          decode8<DT>(q[gi][it], z);
-          const int i0 = b0 + it * CHUNK + tid * VEC;
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) {
-            const int i = i0 + j;
-            const bool valid = i < e0;
-            const unsigned int zk = f2key(z[j]);
-            const bool above = valid && has_hi && zk >= khi;
-            const bool inr = valid && !above && zk >= klo;
-            const bool side = sum_side == 1 ? above : (sum_side == 2 && valid && !above && !inr);
-            unsigned int zpk = 0;
-            if (side || inr) {  // most elements need neither the division nor the exp
-              const float zp = fz<DT>(z[j], md.Tr);
-              const float w = wexp(zp, mps);
-              if (side) part += w;
-              if (inr) pq += quant(w);
-              zpk = f2key(zp);
-            }
-            const unsigned long long bal = __ballot(inr);
-            if (bal) {
-              unsigned int basepos = 0;
-              if (lane == 0) basepos = atomicAdd(&sh.ncand, static_cast<unsigned int>(__popcll(bal)));
-              basepos = rdl(basepos, 0);
-              if (inr) {
-                const unsigned int pos =
-                    basepos + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(bal >> 32),
-                                                        __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(bal), 0u));
-                const uint2 ent = make_uint2(zpk, static_cast<unsigned int>(i));
-                st_dev(g + pos, ent);
-                if (pos < CAND_LDS) r0.cand[pos] = ent;
-              }
+      for (int j = 0; j < VEC; ++j) {
+        const int i = i0 + j;
+        const bool valid = i < e0;
+        const unsigned int zk = f2key(z[j]);
+        const bool above = valid && has_hi && zk >= khi;
+        const bool inr = valid && !above && zk >= klo;
+        const bool side = sum_side == 1 ? above : (sum_side == 2 && valid && !above && !inr);
+        unsigned int zpk = 0;
+        if (side || inr) {  // most elements need neither the division nor the exp
+          const float zp = fz<DT>(z[j], md.Tr);
+          const float w = wexp(zp, mps);
+          if (side) part += static_cast<double>(w);
+          if (inr) pq += quant(w);
+          zpk = f2key(zp);
+        }
+        if (nv > 0) {
+          if (inr) {
+            const unsigned int c = static_cast<unsigned int>(t * nv) + ((zpk >> vshift<DT>()) - vbase);
+            atomicAdd(&r0.vcnt[c >> 1], 1u << (16 * (c & 1u)));
+          }
+        } else {
+          const unsigned long long bal = __ballot(inr);
+          if (bal) {
+            unsigned int basepos = 0;
+            if (lane == 0) basepos = atomicAdd(&sh.ncand, static_cast<unsigned int>(__popcll(bal)));
+            basepos = rdl(basepos, 0);
+            if (inr) {
+              const unsigned int pos =
+                  basepos + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(bal >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(bal), 0u));
+              const uint2 ent = make_uint2(zpk, static_cast<unsigned int>(i));
+              st_dev(g + pos, ent);
+              if (pos < CAND_LDS) r0.cand[pos] = ent;
             }
           }
         }
-        const double pd = wave_sum(static_cast<double>(part));
-        pq = wave_sum(pq);
-        if (lane == 0) {
-          r1.pass.sp[t * WAVES + wid] = pd;
-          r1.pass.sq[t * WAVES + wid] = pq;
-        }
       }
     }
+    const double pd = wave_sum(part);
+    pq = wave_sum(pq);
+    if (lane == 0) {
+      r1.pass.sp[t * WAVES + wid] = pd;
+      r1.pass.sq[t * WAVES + wid] = pq;
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) cur[it] = nxt[it];
   }
   __builtin_amdgcn_s_waitcnt(0);  // candidate stores complete before other waves read them
   __syncthreads();
@@ -753,8 +820,8 @@ __device__ void finish_topk(const Args& a, const Mode& md, const void* row, int 
       sh.ncand = 0;
     }
     __syncthreads();
-    row_pass<DT, EPT, VECOK>(a, md, row, r, static_cast<unsigned int>(sh.sel[4]), false, 0u, 0, r0,
-                             r1, sh);
+    row_pass<DT, EPT, VECOK>(a, md, row, r, static_cast<unsigned int>(sh.sel[4]), false, 0u, 0, 0, 0u,
+                             r0, r1, sh);
     n = static_cast<int>(sh.ncand);
     cv.l = n <= CAND_LDS ? r0.cand : nullptr;
     cv.g = a.cand + static_cast<size_t>(r) * S * a.L;
@@ -796,176 +863,445 @@ __device__ void finish_topk(const Args& a, const Mode& md, const void* row, int 
   write_sampled<DT>(a, md, row, r, id, sh);
 }
 
-// Top-p without top-k, in phases that hand their results on through LDS so
-// that little stays live in registers across phases:
-//   A: combined histogram (row units) with the bound of its truncation error;
-//      the bracket R = [blo, bhi] of bins that must hold the nucleus boundary;
-//      the side of R with fewer elements.
-//   B: R's edges as z-key thresholds (no division in the comparisons).
-//   C: compare-only pass over the row.
-//   D: mass above R per slice; check that R brackets the boundary (else redo
-//      with R = the whole row).
-//   E: exact cutoff and tie cut among R's elements, kept mass per slice, the
-//      slice that holds the draw, and the walk of that slice.
-template <int DT, int EPT, bool VECOK>
-__device__ void finish_topp(const Args& a, const Mode& md, const void* row, int r, Region0& r0,
-                            Region1& r1, Small& sh) {
+// Top-p without top-k, end of the first pass (the row's last slice): combine the
+// slices' exact mass histograms (occupied bins only) in row units, bracket the
+// nucleus boundary -- the bins [blo, bhi] whose cumulative mass from the top
+// reaches p * W within a relative 1e-12 -- and leave the plan for the second
+// pass: the bracket as z-key thresholds (no division in the comparisons),
+// value mode when the logits are 16-bit and the bracket holds few z' values,
+// p * W, the LSE and max z'; then queue the row for its second pass, whose S
+// items (one per slice) any workgroup may take.  Thread t owns descending
+// positions PB*t ..
+// PB*t+PB-1, i.e. the consecutive bins hb0 .. hb0+PB-1 (position PB*t+q is bin
+// hb0+PB-1-q); four slices' histograms are read per round.
+template <int DT>
+__device__ void plan_topp(const Args& a, const Mode& md, int r, Small& sh) {
   const int tid = threadIdx.x;
   const int S = a.S;
-
-  // ---- A: thread t owns descending positions PB*t .. PB*t+PB-1 (bins NBIN-1-PB*t ...)
   constexpr int PB = NBIN / THREADS;
-  {
-    const size_t hb = static_cast<size_t>(r) * S * NBIN;
-    unsigned int c[PB];
-    double m[PB], e[PB];
+  if (tid < S) {
+    const unsigned int rg = sh.ncnd[tid];
+    sh.rlo[tid] = static_cast<int>(rg & 0xffffu);
+    sh.rhi[tid] = static_cast<int>(rg >> 16);
+  }
+  if (tid == 0) {
+    sh.pos_hi = NBIN;
+    sh.pos_lo = NBIN;
+    sh.pos_last = -1;
+  }
+  __syncthreads();
+  const unsigned long long* hrow = a.hist + static_cast<size_t>(r) * S * NBIN;
+  const int hb0 = NBIN - PB * (tid + 1);
+  double m[PB];
 #pragma unroll
-    for (int q = 0; q < PB; ++q) {
-      c[q] = 0u;
-      m[q] = 0.0;
-      e[q] = 0.0;
-      const int b = NBIN - 1 - (PB * tid + q);
-#pragma unroll 8
-      for (int t = 0; t < S; ++t) {
-        const unsigned long long h = ld_dev(a.hist + hb + static_cast<size_t>(t) * NBIN + b);
-        const unsigned int ct = static_cast<unsigned int>(h >> 40);
-        c[q] += ct;
-        m[q] += static_cast<double>(h & MASK40) * HUNIT * sh.scale[t];
-        e[q] += static_cast<double>(ct) * HUNIT * sh.scale[t];
+  for (int q = 0; q < PB; ++q) m[q] = 0.0;
+#pragma unroll 1
+  for (int t0 = 0; t0 < S; t0 += 4) {
+    unsigned long long h[4][PB];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + u;
+      const int lo = t < S ? sh.rlo[t] : NBIN, hi = t < S ? sh.rhi[t] : -1;
+#pragma unroll
+      for (int j = 0; j < PB; ++j) {
+        const int b = hb0 + j;
+        h[u][j] = (b >= lo && b <= hi) ? ld_dev(hrow + static_cast<size_t>(t) * NBIN + b) : 0ull;
       }
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const double sc = t0 + u < S ? sh.scale[t0 + u] * QUNIT : 0.0;
+#pragma unroll
+      for (int j = 0; j < PB; ++j) m[PB - 1 - j] += static_cast<double>(h[u][j]) * sc;
+    }
+  }
+  double sA = 0.0;
+#pragma unroll
+  for (int q = 0; q < PB; ++q) sA += m[q];
+  double exA, inA, W;
+  block_scan<double>(sA, sh.rd, &exA, &inA, &W);
+  const double PW = static_cast<double>(md.pr) * W;
+  const double t_hi = PW * (1.0 - 1e-12), t_lo = PW * (1.0 + 1e-12);
+  int ph = NBIN, pl = NBIN, last = -1;
+  double run = exA;
+#pragma unroll
+  for (int q = 0; q < PB; ++q) {
+    run += m[q];
+    if (m[q] > 0.0) {
+      if (ph == NBIN && run >= t_hi) ph = PB * tid + q;
+      if (pl == NBIN && run >= t_lo) pl = PB * tid + q;
+      last = PB * tid + q;
+    }
+  }
+  if (ph < NBIN) atomicMin(&sh.pos_hi, ph);
+  if (pl < NBIN) atomicMin(&sh.pos_lo, pl);
+  if (last >= 0) atomicMax(&sh.pos_last, last);
+  __syncthreads();
+  if (tid == 0) {
+    const int p_last = sh.pos_last < 0 ? NBIN - 1 : sh.pos_last;
+    const int p_hi = min(sh.pos_hi, p_last), p_lo = min(sh.pos_lo, p_last);
+    const int bhi = NBIN - 1 - p_hi, blo = NBIN - 1 - p_lo;
+    const unsigned int klo_edge = max(static_cast<unsigned int>(blo) << 21, KEY_NEG_INF);
+    const unsigned int klo = gkey<DT>(key2f(klo_edge), md.Tr);
+    const unsigned int hi_edge = static_cast<unsigned int>(bhi + 1) << 21;
+    const bool has_hi = bhi < NBIN - 1 && hi_edge <= KEY_POS_INF;
+    const unsigned int khi = has_hi ? gkey<DT>(key2f(hi_edge), md.Tr) : 0u;
+    // value mode: every z' in the bracket is one of nv 16-bit values, counted
+    // per (slice, value) in 16-bit LDS counters by the resolving workgroup
+    int nv = 0;
+    if (DT != MLXF_DTYPE_F32) {
+      const int vpb = 1 << (21 - vshift<DT>());
+      const int want = (bhi - blo + 1) * vpb;
+      if (want <= 1024 && want * S <= 4 * CAND_LDS) nv = want;
+    }
+    const unsigned int vbase = static_cast<unsigned int>(blo) << (21 - vshift<DT>());
+    unsigned long long* pl_ = a.plan + static_cast<size_t>(r) * PLAN_WORDS;
+    st_dev(pl_ + PL_KEYS, pack2(klo, khi));
+    st_dev(pl_ + PL_MODE, pack2(static_cast<unsigned int>(has_hi ? 1 : 0) | (static_cast<unsigned int>(bhi) << 1),
+                                static_cast<unsigned int>(nv) | (vbase << 11)));  // kind bit 12 clear: top-p
+    st_dev(pl_ + PL_TARGET, static_cast<unsigned long long>(__double_as_longlong(PW)));
+    st_dev(pl_ + PL_LSE, static_cast<unsigned long long>(__double_as_longlong(sh.lse)));
+    st_dev(pl_ + PL_MP, static_cast<unsigned long long>(__float_as_uint(sh.Mp)));
+    __builtin_amdgcn_s_waitcnt(0);  // the plan is complete before the row is queued
+    const unsigned int qp = stamped_take(a.gl + GL_QRES, a.epoch, 0xffffffffu);
+    st_dev(a.queue + qp, (static_cast<unsigned long long>(a.epoch) << 32) | (static_cast<unsigned int>(r) + 1u));
+  }
+}
+
+// Top-k with k > 63, end of the first pass: the z-key bin that holds the
+// row's k-th largest z, from the slices' count histograms (occupied bins only);
+// the plan's bracket is every element whose z' reaches the z' of that bin's
+// lower edge (z key >= klo, no upper bound).  Value mode when the logits are
+// 16-bit and few z' values lie between that edge and the row's max z'.  Then
+// queue the row for its second pass.  Thread t owns descending positions
+// PC*t .. PC*t+PC-1 (bins cb0 .. cb0+PC-1).
+template <int DT>
+__device__ void plan_topk(const Args& a, const Mode& md, int r, Small& sh) {
+  const int tid = threadIdx.x;
+  const int S = a.S;
+  constexpr int PC = CNT_BINS / THREADS;
+  if (tid < S) {
+    const unsigned int rg = sh.ncnd[tid];
+    sh.rlo[tid] = static_cast<int>(rg & 0xffffu);
+    sh.rhi[tid] = static_cast<int>(rg >> 16);
+  }
+  if (tid == 0) sh.pos_hi = CNT_BINS;
+  __syncthreads();
+  const unsigned int* hrow = reinterpret_cast<const unsigned int*>(a.hist + static_cast<size_t>(r) * S * NBIN);
+  const int cb0 = CNT_BINS - PC * (tid + 1);
+  unsigned int c[PC];
+#pragma unroll
+  for (int q = 0; q < PC; ++q) c[q] = 0u;
+#pragma unroll 1
+  for (int t0 = 0; t0 < S; t0 += 2) {
+    unsigned int h[2][PC];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = t0 + u;
+      const int lo = t < S ? sh.rlo[t] : CNT_BINS, hi = t < S ? sh.rhi[t] : -1;
+#pragma unroll
+      for (int j = 0; j < PC; ++j) {
+        const int b = cb0 + j;
+        h[u][j] = (b >= lo && b <= hi)
+                      ? __hip_atomic_load(hrow + static_cast<size_t>(t) * CNT_BINS + b, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT)
+                      : 0u;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int j = 0; j < PC; ++j) c[PC - 1 - j] += h[u][j];
+  }
+  unsigned int sum = 0;
+#pragma unroll
+  for (int q = 0; q < PC; ++q) sum += c[q];
+  unsigned int ex, in, tot;
+  block_scan<unsigned int>(sum, reinterpret_cast<unsigned int*>(sh.rint), &ex, &in, &tot);
+  const unsigned int kk = static_cast<unsigned int>(md.kk);
+  unsigned int run = ex;
+  int found = CNT_BINS;
+#pragma unroll
+  for (int q = 0; q < PC; ++q) {
+    if (found == CNT_BINS && c[q] > 0 && run + c[q] >= kk) found = PC * tid + q;
+    run += c[q];
+  }
+  if (found < CNT_BINS) atomicMin(&sh.pos_hi, found);
+  __syncthreads();
+  if (tid == 0) {
+    const int pos = sh.pos_hi < CNT_BINS ? sh.pos_hi : CNT_BINS - 1;  // (k <= V: always found)
+    const int bstar = CNT_BINS - 1 - pos;
+    const unsigned int edge = max(static_cast<unsigned int>(bstar) << 20, KEY_NEG_INF);
+    const unsigned int klo = gkey<DT>(fz<DT>(key2f(edge), md.Tr), md.Tr);
+    int nv = 0;
+    unsigned int vbase = 0;
+    if (DT != MLXF_DTYPE_F32) {
+      const unsigned int vlo = f2key(fz<DT>(key2f(klo), md.Tr)) >> vshift<DT>();
+      const unsigned int vhi = f2key(sh.Mp) >> vshift<DT>();
+      const int want = static_cast<int>(vhi - vlo + 2) & ~1;  // whole pairs of counters
+      if (vhi >= vlo && want <= 1024 && want * S <= 4 * CAND_LDS) {
+        nv = want;
+        vbase = vlo;
+      }
+    }
+    unsigned long long* pl_ = a.plan + static_cast<size_t>(r) * PLAN_WORDS;
+    st_dev(pl_ + PL_KEYS, pack2(klo, 0u));
+    st_dev(pl_ + PL_MODE, pack2(static_cast<unsigned int>(NBIN - 1) << 1 | (1u << 12),  // kind bit: top-k
+                                static_cast<unsigned int>(nv) | (vbase << 11)));
+    st_dev(pl_ + PL_TARGET, static_cast<unsigned long long>(kk));
+    st_dev(pl_ + PL_LSE, static_cast<unsigned long long>(__double_as_longlong(sh.lse)));
+    st_dev(pl_ + PL_MP, static_cast<unsigned long long>(__float_as_uint(sh.Mp)));
+    __builtin_amdgcn_s_waitcnt(0);  // the plan is complete before the row is queued
+    const unsigned int qp = stamped_take(a.gl + GL_QRES, a.epoch, 0xffffffffu);
+    st_dev(a.queue + qp, (static_cast<unsigned long long>(a.epoch) << 32) | (static_cast<unsigned int>(r) + 1u));
+  }
+}
+
+// Second pass, the row's last item: the exact nucleus cutoff inside the
+// bracket and the draw.  Value mode (16-bit logits): per (slice, z' value)
+// counts give the cutoff value v*, the number t of its ties that are kept
+// (lowest indices first), the slice holding the t-th tie (scanned for its
+// index) and every slice's kept mass.  Candidate mode: radix selections over
+// the bracket's elements.  Then the slice that holds the draw is walked.
+template <int DT, int EPT, bool VECOK>
+__device__ void resolve_row(int r, Region0& r0, Region1& r1, Small& sh) {
+  const Args& a = sh.args;
+  const Mode& md = sh.md;
+  const void* row = row_ptr<DT>(a, r);
+  const int tid = threadIdx.x;
+  const int S = a.S;
+  const unsigned long long wmode = sh.plan[PL_MODE];
+  const bool khist = ((wmode >> 12) & 1ull) != 0;  // top-k (k > 63) row, else top-p
+  const int nv = static_cast<int>((wmode >> 32) & 0x7ffu);
+  const unsigned int vbase = static_cast<unsigned int>(wmode >> 43);
+  const double PW = khist ? 0.0 : __longlong_as_double(static_cast<long long>(sh.plan[PL_TARGET]));
+  const unsigned int kk = khist ? static_cast<unsigned int>(sh.plan[PL_TARGET]) : 0u;
+  const float Mp = __uint_as_float(static_cast<unsigned int>(sh.plan[PL_MP]));
+  if (tid == 0) {
+    sh.lse = __longlong_as_double(static_cast<long long>(sh.plan[PL_LSE]));
+    sh.Mp = Mp;
+  }
+  if (tid < S) {
+    const unsigned long long* rp = reinterpret_cast<const unsigned long long*>(a.rec + (r * S + tid));
+    const float mps = __uint_as_float(static_cast<unsigned int>(ld_dev(rp + 1)));
+    sh.mps[tid] = mps;
+    sh.scale[tid] = wexp_d(mps, Mp);
+    sh.keep[tid] = __longlong_as_double(static_cast<long long>(ld_dev(a.above + (r * S + tid))));
+    sh.keepq[tid] = 0ull;
+    sh.ncnd[tid] = nv > 0 ? 0u : __hip_atomic_load(a.ncand2 + (r * S + tid), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double pa = 0.0;
+    for (int t = 0; t < S; ++t) pa += sh.keep[t] * sh.scale[t];
+    const double nq = (PW - pa) / QUNIT;  // nucleus mass still to cover inside the bracket
+    sh.selu[1] = nq <= 1.0 ? 1ull : static_cast<unsigned long long>(ceil(nq));
+    int o = 0;
+    for (int t = 0; t < S; ++t) {
+      sh.off[t] = o;
+      o += static_cast<int>(sh.ncnd[t]);
+    }
+    sh.off[S] = o;
+  }
+  __syncthreads();
+  unsigned long long target = sh.selu[1];
+  unsigned int vkey;
+  int idx_cut = INT_MAX;
+  if (nv > 0) {
+    // per (slice, value) counts: slice t left nv/2 words of two 32-bit counts
+    const int words = nv / 2;
+#pragma unroll 4
+    for (int idx = tid; idx < S * words; idx += THREADS) {
+      const int t = idx / words, w = idx - t * words;
+      const unsigned long long x =
+          ld_dev(reinterpret_cast<const unsigned long long*>(a.cand + (static_cast<size_t>(r) * S + t) * a.L) + w);
+      r0.vc16[t * nv + 2 * w] = static_cast<unsigned short>(x);
+      r0.vc16[t * nv + 2 * w + 1] = static_cast<unsigned short>(x >> 32);
+    }
+    __syncthreads();
+    // Values are scanned from the top (value index nv-1) down; thread t owns
+    // descending positions 4t .. 4t+3.
+    constexpr int VS = vshift<DT>();
+    auto vkey_of = [vbase](int v) {
+      const unsigned int top = vbase + static_cast<unsigned int>(v);
+      return (top << VS) | (top < (0x80000000u >> VS) ? ((1u << VS) - 1u) : 0u);
+    };
+    auto cnt_of = [&](int t, int v) { return static_cast<unsigned int>(r0.vc16[t * nv + v]); };
+    unsigned int cv[4];
+    unsigned long long mv[4], msum4 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pos = 4 * tid + j, v = nv - 1 - pos;
+      unsigned int cnt = 0;
+      if (pos < nv)
+        for (int t = 0; t < S; ++t) cnt += cnt_of(t, v);
+      cv[j] = cnt;
+      mv[j] = cnt ? static_cast<unsigned long long>(cnt) * quant(wexp(key2f(vkey_of(v)), Mp)) : 0ull;
+      msum4 += mv[j];
+    }
     if (tid == 0) {
-      double W = 0.0;
-      for (int t = 0; t < S; ++t) W += sh.msum[t] * sh.scale[t];
-      sh.seld[2] = static_cast<double>(md.pr) * W;  // p * W, row units
-      sh.pos_hi = NBIN;
-      sh.pos_lo = NBIN;
+      sh.pos_hi = nv;
+      sh.pos_lo = nv;
       sh.pos_last = -1;
     }
-    double sA = 0.0, sU = 0.0;
+    // top-k rows: the k-th largest z' (position plim, counted from the top),
+    // the mass W_k of the values at or above it, and the nucleus target inside
+    // them (all of W_k when there is no top-p)
+    int plim = nv - 1;
+    if (khist) {
+      unsigned int csum = cv[0] + cv[1] + cv[2] + cv[3];
+      unsigned int cex, cin, ctot;
+      block_scan<unsigned int>(csum, reinterpret_cast<unsigned int*>(sh.rint), &cex, &cin, &ctot);
+      unsigned int crun = cex;
+      int fpos = nv;
 #pragma unroll
-    for (int q = 0; q < PB; ++q) {
-      sA += m[q];
-      sU += m[q] + e[q];
-    }
-    double exA, inA, totA, exU, inU, totU;
-    block_scan<double>(sA, sh.rd, &exA, &inA, &totA);
-    block_scan<double>(sU, sh.rd, &exU, &inU, &totU);
-    const double PW = sh.seld[2];
-    // first position whose cumulative upper bound reaches p*W: the boundary is
-    // not above it; first position whose cumulative lower bound reaches it:
-    // the boundary is not below it
-    const double t_hi = PW * (1.0 - 1e-9), t_lo = PW * (1.0 + 1e-9);
-    int ph = NBIN, pl = NBIN, last = -1;
-    double runA = exA, runU = exU;
-#pragma unroll
-    for (int q = 0; q < PB; ++q) {
-      runA += m[q];
-      runU += m[q] + e[q];
-      if (c[q] > 0) {
-        if (ph == NBIN && runU >= t_hi) ph = PB * tid + q;
-        if (pl == NBIN && runA >= t_lo) pl = PB * tid + q;
-        last = PB * tid + q;
+      for (int j = 0; j < 4; ++j) {
+        if (fpos == nv && cv[j] > 0 && crun + cv[j] >= kk) fpos = 4 * tid + j;
+        crun += cv[j];
       }
-    }
-    if (ph < NBIN) atomicMin(&sh.pos_hi, ph);
-    if (pl < NBIN) atomicMin(&sh.pos_lo, pl);
-    if (last >= 0) atomicMax(&sh.pos_last, last);
-    __syncthreads();
-    int p_hi = sh.pos_hi, p_lo = sh.pos_lo;
-    const int p_last = sh.pos_last < 0 ? NBIN - 1 : sh.pos_last;
-    if (p_hi > p_last) p_hi = p_last;
-    if (p_lo > p_last) p_lo = p_last;
-    // positions count down from the top bin: bhi = NBIN-1-p_hi >= blo = NBIN-1-p_lo
-    int ca = 0, cb = 0;
+      if (fpos < nv) atomicMin(&sh.pos_lo, fpos);
+      __syncthreads();
+      plim = sh.pos_lo < nv ? sh.pos_lo : nv - 1;
+      unsigned long long part = 0;
 #pragma unroll
-    for (int q = 0; q < PB; ++q) {
-      const int pos = PB * tid + q;
-      if (pos < p_hi) ca += static_cast<int>(c[q]);
-      if (pos > p_lo) cb += static_cast<int>(c[q]);
+      for (int j = 0; j < 4; ++j) part += (4 * tid + j <= plim) ? mv[j] : 0ull;
+      const unsigned long long wk = block_sum<unsigned long long>(part, sh.ru);
+      target = md.topp ? static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(wk)))
+                       : wk;
+      if (target == 0) target = 1;
     }
-    ca = block_sum<int>(ca, sh.rint);
-    cb = block_sum<int>(cb, sh.rint);
-    if (tid == 0) {
-      sh.sel[2] = NBIN - 1 - p_lo;  // blo
-      sh.sel[3] = NBIN - 1 - p_hi;  // bhi
-      sh.sel[7] = ca <= cb ? 1 : 2;  // sum the side with fewer elements
-    }
-    __syncthreads();
-  }
-
-  for (int attempt = 0; attempt < 2; ++attempt) {
-    // ---- B
-    if (tid == 0) {
-      const int blo = sh.sel[2], bhi = sh.sel[3];
-      const unsigned int klo_edge = max(static_cast<unsigned int>(blo) << 21, KEY_NEG_INF);
-      sh.sel[4] = static_cast<int>(attempt == 0 ? gkey<DT>(key2f(klo_edge), md.Tr) : 0u);
-      const unsigned int hi_edge = static_cast<unsigned int>(bhi + 1) << 21;
-      const bool has_hi = attempt == 0 && bhi < NBIN - 1 && hi_edge <= KEY_POS_INF;
-      sh.sel[5] = has_hi ? 1 : 0;
-      sh.sel[6] = static_cast<int>(has_hi ? gkey<DT>(key2f(hi_edge), md.Tr) : 0u);
-      sh.sel[8] = attempt == 0 ? sh.sel[7] : 0;  // R = whole row: no side to sum
-      sh.ncand = 0;
-    }
-    __syncthreads();
-    // ---- C
-    row_pass<DT, EPT, VECOK>(a, md, row, r, static_cast<unsigned int>(sh.sel[4]), sh.sel[5] != 0,
-                             static_cast<unsigned int>(sh.sel[6]), sh.sel[8], r0, r1, sh);
-    // ---- D
-    if (tid < S) {
-      double sd = 0.0;
-      unsigned long long sq = 0;
-      for (int w2 = 0; w2 < WAVES; ++w2) {
-        sd += r1.pass.sp[tid * WAVES + w2];
-        sq += r1.pass.sq[tid * WAVES + w2];
+    unsigned long long ex, in, tot;
+    block_scan<unsigned long long>(msum4, sh.ru, &ex, &in, &tot);
+    unsigned long long run = ex;
+    int found = nv, lastne = -1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pos = 4 * tid + j;
+      if (cv[j] > 0 && pos <= plim) {
+        if (found == nv && mv[j] > 0 && run + mv[j] >= target) found = pos;
+        lastne = pos;
       }
-      sh.side[tid] = sd;
-      sh.inR[tid] = sq;
-      sh.keepq[tid] = 0ull;
+      run += mv[j];
+    }
+    if (found < nv) atomicMin(&sh.pos_hi, found);
+    if (lastne >= 0) atomicMax(&sh.pos_last, lastne);
+    __syncthreads();
+    // the position of v* and the mass of the values above it; a top-k row
+    // without top-p keeps every tie of its k-th value
+    const bool whole = khist && !md.topp;
+    const int pstar = whole ? plim : (sh.pos_hi < nv ? sh.pos_hi : (sh.pos_last < 0 ? 0 : sh.pos_last));
+    if (pstar >= 4 * tid && pstar < 4 * tid + 4) {
+      unsigned long long pgt = ex;
+      for (int j = 0; j < pstar - 4 * tid; ++j) pgt += mv[j];
+      const int jj = pstar - 4 * tid;
+      const unsigned int cstar = cv[jj];
+      const unsigned long long wstar = cstar ? mv[jj] / cstar : 0ull;
+      unsigned long long t = cstar;
+      if (!whole && sh.pos_hi < nv && wstar > 0) {
+        const unsigned long long nd = target > pgt ? (target - pgt + wstar - 1) / wstar : 0ull;
+        t = nd < t ? nd : t;
+      }
+      if (t == 0) t = 1;
+      sh.selu[2] = t;
+      sh.sel[14] = static_cast<int>(cstar);
     }
     __syncthreads();
-    const int n = static_cast<int>(sh.ncand);
-    CandView cv;
-    cv.l = n <= CAND_LDS ? r0.cand : nullptr;
-    cv.g = a.cand + static_cast<size_t>(r) * S * a.L;
-    cv.off = nullptr;
-    cv.S = S;
-    cv.L = a.L;
-    const float Mp = sh.Mp;
-    auto wq = [Mp](uint2 e) { return quant(wexp(key2f(e.x), Mp)); };
-    if (tid == 0) {
-      const int side = sh.sel[8];
-      double pa = 0.0, inr_tot = 0.0;
+    const int vstar = nv - 1 - pstar;
+    vkey = vkey_of(vstar);
+    const unsigned int tties = static_cast<unsigned int>(sh.selu[2]);
+    const unsigned int cstar = static_cast<unsigned int>(sh.sel[14]);
+    if (tid == 0) {  // the slice holding the t-th tie and its rank there
+      unsigned int before = 0;
+      int st = S - 1;
       for (int t = 0; t < S; ++t) {
-        const double inr = static_cast<double>(sh.inR[t]) * QUNIT;
-        const double ab = side == 1 ? sh.side[t] : (side == 2 ? sh.msum[t] - sh.side[t] - inr : 0.0);
-        sh.keep[t] = ab < 0.0 ? 0.0 : ab;  // above-R mass, slice units
-        pa += sh.keep[t] * sh.scale[t];
-        inr_tot += inr * sh.scale[t];
+        const unsigned int ct = cnt_of(t, vstar);
+        if (before + ct >= tties) {
+          st = t;
+          break;
+        }
+        before += ct;
       }
-      const double need = sh.seld[2] - pa;  // nucleus mass still to cover inside R, row units
-      const bool bracketed = need > 0.0 && need <= inr_tot * (1.0 + 1e-9) + 1e-12;
-      sh.sel[9] = bracketed ? 1 : 0;
-      const double nq = need / QUNIT;
-      sh.selu[1] = nq <= 1.0 ? 1ull : static_cast<unsigned long long>(ceil(nq));
+      sh.sel[15] = st;
+      sh.selu[3] = tties - before;
     }
     __syncthreads();
-    if (sh.sel[9] == 0 && attempt == 0) {  // R missed the boundary: R = whole row
-      if (tid == 0) {
-        sh.sel[2] = 0;
-        sh.sel[3] = NBIN - 1;
+    const int st_tie = sh.sel[15];
+    const unsigned int rank = static_cast<unsigned int>(sh.selu[3]);
+    if (tties < cstar) {
+      // index of the rank-th element equal to v* in slice st_tie (thread t owns
+      // EPT consecutive elements)
+      const int b0 = st_tie * a.L, e0 = min(a.V, b0 + a.L);
+      const int my0 = b0 + tid * EPT;
+      unsigned int cnt = 0;
+#pragma unroll 2
+      for (int it = 0; it < EPT / VEC; ++it) {
+        float z[VEC];
+        load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j)
+          cnt += (my0 + it * VEC + j < e0 && f2key(fz<DT>(z[j], md.Tr)) == vkey) ? 1u : 0u;
+      }
+      unsigned int cex, cin, ctot;
+      block_scan<unsigned int>(cnt, reinterpret_cast<unsigned int*>(sh.rint), &cex, &cin, &ctot);
+      if (cex < rank && rank <= cin) {
+        unsigned int k = cex;
+        int pick = -1;
+        for (int it = 0; it < EPT / VEC && pick < 0; ++it) {
+          float z[VEC];
+          load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            const int i = my0 + it * VEC + j;
+            if (pick < 0 && i < e0 && f2key(fz<DT>(z[j], md.Tr)) == vkey && ++k == rank) pick = i;
+          }
+        }
+        sh.sel[1] = pick;
       }
       __syncthreads();
-      continue;
+      idx_cut = sh.sel[1];
     }
-    // ---- E
-    const unsigned long long target = sh.selu[1];
+    // kept in-bracket mass per slice: values above v*, and the ties up to the cut
+    for (int pidx = tid; pidx < S * nv; pidx += THREADS) {
+      const int t = pidx / nv, v = pidx - t * nv;
+      unsigned long long q = 0;
+      if (v >= vstar) {
+        unsigned int cnt = cnt_of(t, v);
+        if (v == vstar && tties < cstar) cnt = t < st_tie ? cnt : (t == st_tie ? rank : 0u);
+        if (cnt) q = static_cast<unsigned long long>(cnt) * quant(wexp(key2f(vkey_of(v)), sh.mps[t]));
+      }
+      if (q) atomicAdd(&sh.keepq[t], q);
+    }
+    __syncthreads();
+  } else {
+    // candidate mode: the bracket's elements, per-slice regions of a.cand
+    const int n = sh.off[S];
+    CandView cv;
+    cv.l = nullptr;
+    cv.g = a.cand + static_cast<size_t>(r) * S * a.L;
+    cv.off = sh.off;
+    cv.S = S;
+    cv.L = a.L;
+    if (n <= CAND_LDS) {  // gather into LDS
+      for (int t = 0; t < S; ++t) {
+        const int o = sh.off[t], cnt = sh.off[t + 1] - o;
+        const uint2* src = cv.g + static_cast<size_t>(t) * a.L;
+        for (int j = tid; j < cnt; j += THREADS) r0.cand[o + j] = ld_dev2(src + j);
+      }
+      __syncthreads();
+      cv.l = r0.cand;
+    }
+    if (khist) {  // k-th largest, top-p inside the top k, and the draw, on the candidates
+      const int id = resolve_topk(md, cv, n, Mp, sh);
+      write_sampled<DT>(a, md, row, r, id, sh);
+      if (tid == 0) stamped_take(a.gl + GL_ROWS, a.epoch, 0xffffffffu);
+      return;
+    }
+    auto wq = [Mp](uint2 e) { return quant(wexp(key2f(e.x), Mp)); };
     unsigned long long pgt, bef;
     unsigned int g_cnt;
     bool all_kept;
     auto any = [](uint2) { return true; };
-    const unsigned int vkey =
-        radix_select<true, true, true>(cv, n, any, wq, target, false, sh, &pgt, &g_cnt, &all_kept);
+    vkey = radix_select<true, true, true>(cv, n, any, wq, target, false, sh, &pgt, &g_cnt, &all_kept);
     const unsigned long long wstar = wq(make_uint2(vkey, 0u));
     unsigned long long tk = g_cnt;
     if (!all_kept && wstar > 0) {
@@ -973,9 +1309,9 @@ __device__ void finish_topp(const Args& a, const Mode& md, const void* row, int 
       tk = nd < tk ? nd : tk;
     }
     if (tk == 0) tk = 1;
-    int idx_cut = INT_MAX;
     if (tk < g_cnt) {
-      auto eq_v = [vkey](uint2 e) { return e.x == vkey; };
+      const unsigned int vk = vkey;
+      auto eq_v = [vk](uint2 e) { return e.x == vk; };
       unsigned int g2;
       bool none2;
       idx_cut = static_cast<int>(
@@ -995,19 +1331,19 @@ __device__ void finish_topp(const Args& a, const Mode& md, const void* row, int 
       lds_add_agg(sh.keepq, st, q, kept);
     }
     __syncthreads();
-    if (tid == 0) {
-      for (int t = 0; t < S; ++t) sh.keep[t] += static_cast<double>(sh.keepq[t]) * QUNIT;
-      int sst;
-      double rem;
-      pick_slice(sh.keep, sh.scale, S, md.u, &sst, &rem);
-      sh.sel[0] = sst;
-      sh.seld[1] = rem;
-    }
-    __syncthreads();
-    const int id = final_scan<DT, EPT, VECOK>(a, md, row, sh.sel[0], sh.seld[1], vkey, idx_cut, sh);
-    write_sampled<DT>(a, md, row, r, id, sh);
-    return;
   }
+  if (tid == 0) {
+    for (int t = 0; t < S; ++t) sh.keep[t] += static_cast<double>(sh.keepq[t]) * QUNIT;
+    int sst;
+    double rem;
+    pick_slice(sh.keep, sh.scale, S, md.u, &sst, &rem);
+    sh.sel[0] = sst;
+    sh.seld[1] = rem;
+  }
+  __syncthreads();
+  const int id = final_scan<DT, EPT, VECOK>(a, md, row, sh.sel[0], sh.seld[1], vkey, idx_cut, sh);
+  write_sampled<DT>(a, md, row, r, id, sh);
+  if (tid == 0) stamped_take(a.gl + GL_ROWS, a.epoch, 0xffffffffu);
 }
 
 // Everything the last slice of a row does.
@@ -1103,21 +1439,21 @@ __device__ __forceinline__ void finish_row(int r, Region0& r0, Region1& r1, Smal
     else
       finish_topk<DT, EPT, VECOK>(a, md, row, r, true, r0, r1, sh);
   } else if (md.kind == KIND_KHIST) {
-    finish_topk<DT, EPT, VECOK>(a, md, row, r, false, r0, r1, sh);
+    plan_topk<DT>(a, md, r, sh);
+    return;  // finished by its second pass
   } else if (md.kind == KIND_TOPP) {
-    finish_topp<DT, EPT, VECOK>(a, md, row, r, r0, r1, sh);
+    plan_topp<DT>(a, md, r, sh);
+    return;  // finished by its second pass
   }
+  if (tid == 0) stamped_take(a.gl + GL_ROWS, a.epoch, 0xffffffffu);
 }
 
 // =================================================================== kernel ==
 
+// First pass over slice s of row r; the row's last slice finishes the row
+// (returns true in that workgroup).
 template <int DT, int EPT, bool VECOK>
-__global__ __launch_bounds__(THREADS, 2) void k_sample(Args a) {
-  __shared__ Region0 r0;
-  __shared__ Region1 r1;
-  __shared__ Small sh;
-
-  const int s = blockIdx.x, r = blockIdx.y;
+__device__ __forceinline__ bool first_pass(const Args& a, int r, int s, Region0& r0, Region1& r1, Small& sh) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int S = a.S;
   const Mode md = decode<DT>(a, r);
@@ -1130,6 +1466,8 @@ __global__ __launch_bounds__(THREADS, 2) void k_sample(Args a) {
 #pragma unroll
   for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
 #define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
+  if (s == 0 && tid == 0 && (md.kind == KIND_TOPP || md.kind == KIND_KHIST))
+    st_dev(a.gl + GL_NEED, (static_cast<unsigned long long>(a.epoch) << 32) | 1u);
 
   // Histograms are cleared while the loads are in flight.  The pass has two
   // barriers: B1 publishes the wave maxima (and list thresholds), B2 the
@@ -1216,30 +1554,55 @@ __global__ __launch_bounds__(THREADS, 2) void k_sample(Args a) {
   }
 
   // ---- temperature-only / top-p: slice mass w = exp(z' - max z') and, for
-  // top-p, the (count, truncated w) histogram of z' keys
-  float mps = 0.0f;
+  // top-p, the exact (2^-42 units) mass histogram of z' keys with the range of
+  // occupied bins
+  const float mps = md.sampling ? fz<DT>(zmax, md.Tr) : 0.0f;  // the slice's weight reference
   if (md.kind == KIND_TEMP || md.kind == KIND_TOPP) {
-    mps = fz<DT>(zmax, md.Tr);
     const bool hist = md.kind == KIND_TOPP;
     double t = 0.0;
+    int bl = NBIN, bh = -1;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       if (MLXF_IDX(e) < end) {
         const float zp = fz<DT>(v[e], md.Tr);
         const float w = wexp(zp, mps);
         t += static_cast<double>(w);
-        if (hist)
-          atomicAdd(&r1.hist[f2key(zp) >> 21],
-                    (1ull << 40) +
-                        static_cast<unsigned long long>(static_cast<unsigned int>(w * 16777216.0f)));
+        if (hist) {
+          const int b = static_cast<int>(f2key(zp) >> 21);
+          bl = min(bl, b);
+          bh = max(bh, b);
+          const unsigned long long q = quant(w);
+          if (q) atomicAdd(&r1.hist[b], q);
+        }
       }
     }
     const double ws = wave_sum(t);
-    if (lane == 0) sh.rd2[wid] = ws;
+    if (hist) {
+      bl = wave_min(bl);
+      bh = wave_max(bh);
+    }
+    if (lane == 0) {
+      sh.rd2[wid] = ws;
+      sh.bmin[wid] = bl;
+      sh.bmax[wid] = bh;
+    }
   } else if (md.kind == KIND_KHIST) {
+    int bl = CNT_BINS, bh = -1;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e)
-      if (MLXF_IDX(e) < end) atomicAdd(&r1.cnt[f2key(v[e]) >> 20], 1u);
+    for (int e = 0; e < EPT; ++e) {
+      if (MLXF_IDX(e) < end) {
+        const int b = static_cast<int>(f2key(v[e]) >> 20);
+        bl = min(bl, b);
+        bh = max(bh, b);
+        atomicAdd(&r1.cnt[b], 1u);
+      }
+    }
+    bl = wave_min(bl);
+    bh = wave_max(bh);
+    if (lane == 0) {
+      sh.bmin[wid] = bl;
+      sh.bmax[wid] = bh;
+    }
   }
   {
     const int wa = wave_min(targ);
@@ -1318,47 +1681,28 @@ __global__ __launch_bounds__(THREADS, 2) void k_sample(Args a) {
 
   unsigned int ncand = 0;
   if (md.kind == KIND_TOPP) {
+    // only the occupied bins are stored; the range goes with the slice record
+    int bl = sh.bmin[0], bh = sh.bmax[0];
+#pragma unroll
+    for (int w2 = 1; w2 < WAVES; ++w2) {
+      bl = min(bl, sh.bmin[w2]);
+      bh = max(bh, sh.bmax[w2]);
+    }
     const size_t off = (static_cast<size_t>(r) * S + s) * NBIN;
-    for (int b = tid; b < NBIN; b += THREADS) st_dev(a.hist + off + b, r1.hist[b]);
+    for (int b = bl + tid; b <= bh; b += THREADS) st_dev(a.hist + off + b, r1.hist[b]);
+    ncand = bh < bl ? 0xffffu : static_cast<unsigned int>(bl) | (static_cast<unsigned int>(bh) << 16);
   } else if (md.kind == KIND_KHIST) {
-    // the bin of the slice's k-th largest z; thread t owns descending
-    // positions PC*t .. PC*t+PC-1
-    constexpr int PC = CNT_BINS / THREADS;
-    int cq[PC], sumq = 0;
+    // the occupied bins of the count histogram of z keys, as 32-bit counts
+    int bl = sh.bmin[0], bh = sh.bmax[0];
 #pragma unroll
-    for (int q = 0; q < PC; ++q) {
-      cq[q] = static_cast<int>(r1.cnt[CNT_BINS - 1 - (PC * tid + q)]);
-      sumq += cq[q];
+    for (int w2 = 1; w2 < WAVES; ++w2) {
+      bl = min(bl, sh.bmin[w2]);
+      bh = max(bh, sh.bmax[w2]);
     }
-    int total;
-    const int ex = block_excl_scan<int>(sumq, sh.rint, &total);
-    const int kk_s = md.kk < (end - beg) ? md.kk : (end - beg);
-    int run = ex;
-#pragma unroll
-    for (int q = 0; q < PC; ++q) {
-      if (run < kk_s && run + cq[q] >= kk_s) sh.sel[0] = CNT_BINS - 1 - (PC * tid + q);
-      run += cq[q];
-    }
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned int edge = max(static_cast<unsigned int>(sh.sel[0]) << 20, KEY_NEG_INF);
-      sh.sel[1] = static_cast<int>(gkey<DT>(fz<DT>(key2f(edge), md.Tr), md.Tr));
-    }
-    __syncthreads();
-    const unsigned int thr = static_cast<unsigned int>(sh.sel[1]);
-    int mine = 0;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && f2key(v[e]) >= thr) ? 1 : 0;
-    int ctot;
-    int pos = block_excl_scan<int>(mine, sh.rint, &ctot);
-    uint2* dst = a.cand + (static_cast<size_t>(r) * S + s) * a.L;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const int i = MLXF_IDX(e);
-      const unsigned int key = f2key(v[e]);
-      if (i < end && key >= thr) st_dev(dst + pos++, make_uint2(key, static_cast<unsigned int>(i)));
-    }
-    ncand = static_cast<unsigned int>(ctot);
+    unsigned int* hc = reinterpret_cast<unsigned int*>(a.hist + (static_cast<size_t>(r) * S + s) * NBIN);
+    for (int b = bl + tid; b <= bh; b += THREADS)
+      __hip_atomic_store(hc + b, r1.cnt[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ncand = bh < bl ? 0xffffu : static_cast<unsigned int>(bl) | (static_cast<unsigned int>(bh) << 16);
   }
 #undef MLXF_IDX
 
@@ -1377,7 +1721,7 @@ __global__ __launch_bounds__(THREADS, 2) void k_sample(Args a) {
   if (tid == 0)
     sh.ticket = __hip_atomic_fetch_add(a.ctr + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  if (sh.ticket != static_cast<unsigned int>(S - 1)) return;
+  if (sh.ticket != static_cast<unsigned int>(S - 1)) return false;
   if (tid == 0) {
     __hip_atomic_store(a.ctr + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
     sh.args = a;
@@ -1385,6 +1729,213 @@ __global__ __launch_bounds__(THREADS, 2) void k_sample(Args a) {
   }
   __syncthreads();
   finish_row<DT, EPT, VECOK>(r, r0, r1, sh);
+  return true;
+}
+
+// Second pass, one item = slice s of a queued row (top-p without top-k): the
+// slice's mass above the bracket (its own histogram's bins above bhi, exact)
+// and the bracket's elements, counted per z' value (value mode) or written out
+// as candidates.  The row's last item resolves the row.
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ void second_pass(const Args& a, int r, int s, Region0& r0, Region1& r1, Small& sh) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int S = a.S;
+  const Mode md = decode<DT>(a, r);
+  const void* row = row_ptr<DT>(a, r);
+  const unsigned long long* pl = a.plan + static_cast<size_t>(r) * PLAN_WORDS;
+  const unsigned long long wk = ld_dev(pl + PL_KEYS), wmode = ld_dev(pl + PL_MODE);
+  const unsigned int klo = static_cast<unsigned int>(wk), khi = static_cast<unsigned int>(wk >> 32);
+  const bool has_hi = (wmode & 1ull) != 0;
+  const bool khist = ((wmode >> 12) & 1ull) != 0;
+  const int bhi = static_cast<int>((wmode >> 1) & 0x7ffull);
+  const int nv = static_cast<int>((wmode >> 32) & 0x7ffull);
+  const unsigned int vbase = static_cast<unsigned int>(wmode >> 43);
+  const unsigned long long w1 =
+      ld_dev(reinterpret_cast<const unsigned long long*>(a.rec + (r * S + s)) + 1);
+  const unsigned int rg = static_cast<unsigned int>(w1 >> 32);
+  const int rlo = static_cast<int>(rg & 0xffffu), rhi = static_cast<int>(rg >> 16);
+  // mass above the bracket (top-p rows): this slice's histogram bins above bhi
+  unsigned long long ab = 0;
+  const unsigned long long* hs = a.hist + (static_cast<size_t>(r) * S + s) * NBIN;
+  if (!khist)
+    for (int b = max(bhi + 1, rlo) + tid; b <= rhi; b += THREADS) ab += ld_dev(hs + b);
+  if (nv > 0)
+    for (int v = tid; v < nv; v += THREADS) r0.vcnt[v] = 0u;
+  if (tid == 0) sh.ncand = 0u;
+  ab = block_sum<unsigned long long>(ab, sh.ru);  // (its barriers also publish the clears)
+  // the bracket's elements
+  const int beg = s * a.L, end = min(a.V, beg + a.L);
+  constexpr int NIT = EPT / VEC;
+  uint2* dst = a.cand + (static_cast<size_t>(r) * S + s) * a.L;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    float z[VEC];
+    const int i0 = beg + it * CHUNK + tid * VEC;
+    load8<DT, VECOK>(row, i0, end, z);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int i = i0 + j;
+      const unsigned int zk = f2key(z[j]);
+      const bool inr = i < end && zk >= klo && (!has_hi || zk < khi);
+      unsigned int zpk = 0;
+      if (inr) zpk = f2key(fz<DT>(z[j], md.Tr));
+      if (nv > 0) {
+        if (inr) atomicAdd(&r0.vcnt[(zpk >> vshift<DT>()) - vbase], 1u);
+      } else {
+        const unsigned long long bal = __ballot(inr);
+        if (bal) {
+          unsigned int basepos = 0;
+          if (lane == 0) basepos = atomicAdd(&sh.ncand, static_cast<unsigned int>(__popcll(bal)));
+          basepos = rdl(basepos, 0);
+          if (inr) {
+            const unsigned int pos =
+                basepos + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(bal >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(bal), 0u));
+            st_dev(dst + pos, make_uint2(zpk, static_cast<unsigned int>(i)));
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (nv > 0) {
+    for (int w = tid; w < nv / 2; w += THREADS)
+      st_dev(reinterpret_cast<unsigned long long*>(dst) + w, pack2(r0.vcnt[2 * w], r0.vcnt[2 * w + 1]));
+  } else if (tid == 0) {
+    __hip_atomic_store(a.ncand2 + (r * S + s), sh.ncand, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (tid == 0)
+    st_dev(a.above + (r * S + s),
+           static_cast<unsigned long long>(__double_as_longlong(static_cast<double>(ab) * QUNIT)));
+  // ticket: the row's last item resolves the row
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    sh.ticket = __hip_atomic_fetch_add(a.done2 + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (sh.ticket != static_cast<unsigned int>(S - 1)) return;
+  if (tid == 0) {
+    __hip_atomic_store(a.done2 + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+    sh.args = a;
+    sh.md = md;
+  }
+  if (tid < PLAN_WORDS) sh.plan[tid] = ld_dev(pl + tid);
+  __syncthreads();
+  resolve_row<DT, EPT, VECOK>(r, r0, r1, sh);
+}
+
+// Helpers: take second-pass items of any queued row, polling until every row is
+// finished or the idle bound runs out.  No row depends on helpers (see
+// drain_own); the workgroup that completes a row's last item resolves it.
+// Take the items of one row until none is left.  A row's last slice does this
+// for its own row after queueing it, so every item is taken by a running
+// workgroup whatever the helpers do.
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ void drain_own(const Args& a, int own_row, Region0& r0, Region1& r1, Small& sh) {
+  const int tid = threadIdx.x;
+  for (;;) {
+    __syncthreads();
+    if (tid == 0)
+      sh.qitem = static_cast<int>(stamped_take(a.next2 + own_row, a.epoch, static_cast<unsigned int>(a.S)));
+    __syncthreads();
+    const int qi = sh.qitem;
+    if (qi >= a.S) break;
+    second_pass<DT, EPT, VECOK>(a, own_row, qi, r0, r1, sh);
+  }
+}
+
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ void drain(const Args& a, Region0& r0, Region1& r1, Small& sh) {
+  constexpr bool wait = true;
+  const int tid = threadIdx.x;
+  const int S = a.S;
+  unsigned int cursor = 0;
+  int polls = 0;
+  for (;;) {
+    __syncthreads();
+    if (tid == 0) {
+      sh.rdone = stamped_get(a.gl + GL_ROWS, a.epoch);
+      sh.qn = stamped_get(a.gl + GL_QRES, a.epoch);
+      sh.qrow = static_cast<int>(stamped_get(a.gl + GL_HEAD, a.epoch));
+    }
+    __syncthreads();
+    const unsigned int qn = sh.qn, rdone = sh.rdone;
+    cursor = max(cursor, static_cast<unsigned int>(sh.qrow));
+    bool worked = false;
+    while (cursor < qn) {
+      __syncthreads();
+      if (tid == 0) {
+        // a reserved slot is written right after its reservation
+        unsigned int e = stamped_get(a.queue + cursor, a.epoch);
+        for (int spin = 0; e == 0u && spin < (1 << 20); ++spin) {
+          __builtin_amdgcn_s_sleep(2);
+          e = stamped_get(a.queue + cursor, a.epoch);
+        }
+        int item = S;
+        if (e != 0u) item = static_cast<int>(stamped_take(a.next2 + (e - 1u), a.epoch, static_cast<unsigned int>(S)));
+        sh.qrow = static_cast<int>(e) - 1;
+        sh.qitem = item;
+      }
+      __syncthreads();
+      const int qr = sh.qrow, qi = sh.qitem;
+      if (qr < 0 || qi >= S) {
+        // the row has no items left: move the shared head past it if it points here
+        if (tid == 0) {
+          unsigned long long w = (static_cast<unsigned long long>(a.epoch) << 32) | cursor;
+          __hip_atomic_compare_exchange_strong(a.gl + GL_HEAD, &w, w + 1ull, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+          if (cursor == 0u) {  // a head never stamped in this call reads as 0
+            unsigned long long z = ld_dev(a.gl + GL_HEAD);
+            if (static_cast<unsigned int>(z >> 32) != a.epoch)
+              __hip_atomic_compare_exchange_strong(a.gl + GL_HEAD, &z, w + 1ull, __ATOMIC_RELAXED,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+        ++cursor;
+        continue;
+      }
+      second_pass<DT, EPT, VECOK>(a, qr, qi, r0, r1, sh);
+      worked = true;
+    }
+    if (!wait || rdone >= static_cast<unsigned int>(a.B)) break;
+    if (worked) {
+      polls = 0;
+    } else {
+      if (++polls > IDLE_LIMIT) break;
+      // back off: idle helpers poll the shared counters less often
+      if (polls < 8)
+        __builtin_amdgcn_s_sleep(8);
+      else
+        __builtin_amdgcn_s_sleep(64);
+    }
+  }
+}
+
+// One launch: the first B*S workgroups run the first pass (row-major); those
+// that finish a row with a second pass then take that row's items.  The remaining
+// workgroups are helpers that only take second-pass items, and leave at once
+// unless some row of this call flagged a second pass.
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS, 2) void k_sample(Args a) {
+  __shared__ Region0 r0;
+  __shared__ Region1 r1;
+  __shared__ Small sh;
+  const int bid = static_cast<int>(blockIdx.x);
+  const int n1 = a.B * a.S;
+  if (bid < n1) {
+    const int r = bid / a.S;
+    if (first_pass<DT, EPT, VECOK>(a, r, bid - r * a.S, r0, r1, sh)) {
+      const int kind = sh.md.kind;
+      if (kind == KIND_TOPP && sh.md.pr > 0.0f)
+        drain_own<DT, EPT, VECOK>(a, r, r0, r1, sh);
+      else if (kind == KIND_KHIST)
+        drain_own<DT, EPT, VECOK>(a, r, r0, r1, sh);
+    }
+  } else {
+    if (threadIdx.x == 0) sh.qn = stamped_get(a.gl + GL_NEED, a.epoch);
+    __syncthreads();
+    if (sh.qn != 0u) drain<DT, EPT, VECOK>(a, r0, r1, sh);
+  }
 }
 
 // Zero the per-row counters of a fresh workspace.
@@ -1397,12 +1948,19 @@ __global__ void k_zero(unsigned int* p, size_t n) {
 
 struct Layout {
   int S, L, EPT;
-  size_t off_ctr, off_rec, off_list, off_hist, off_cand, total;
+  size_t off_ctr, off_done2, off_next2, off_gl, off_queue, off_rec, off_list, off_hist, off_cand,
+      off_plan, off_above, off_ncand2, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-constexpr size_t CTR_BYTES_MAX = 65536 * sizeof(unsigned int);
+// the zero-initialised head of the workspace: per-row tickets (two arrays of
+// 65536 32-bit counters), item counters and queue slots (65536 64-bit words
+// each) and the call-wide counters
+constexpr size_t ROWS_MAX = 65536;
+constexpr size_t CTR_BYTES_MAX =
+    2 * ROWS_MAX * sizeof(unsigned int) + 2 * ROWS_MAX * sizeof(unsigned long long) +
+    GL_WORDS * sizeof(unsigned long long);
 
 // EPT: the largest of {32, 16, 8} that still gives at least one workgroup
 // per CU (256) with at most MAX_S slices per row; otherwise the smallest EPT
@@ -1433,8 +1991,17 @@ Layout make_layout(int B, int V, int K_max) {
   l.S = (V + l.L - 1) / l.L;
   const size_t BS = static_cast<size_t>(B) * l.S;
   size_t o = 0;
-  l.off_ctr = o;  // first: mlxf_sampler_workspace_init zeroes the start of the buffer
-  o = align256(o + sizeof(unsigned int) * (B > 0 ? B : 1));
+  // First, at offsets that do not depend on the shape: the three per-row
+  // counter arrays, which must read zero before every call (the workspace is
+  // zeroed once; every call leaves them at zero).  Fixed offsets keep that true
+  // when one workspace serves calls of different shapes.
+  const size_t nb = B > 0 ? static_cast<size_t>(B) : 1;
+  l.off_ctr = 0;
+  l.off_done2 = ROWS_MAX * sizeof(unsigned int);
+  l.off_next2 = 2 * ROWS_MAX * sizeof(unsigned int);
+  l.off_queue = l.off_next2 + ROWS_MAX * sizeof(unsigned long long);
+  l.off_gl = l.off_queue + ROWS_MAX * sizeof(unsigned long long);
+  o = align256(CTR_BYTES_MAX);
   l.off_rec = o;
   o = align256(o + sizeof(SliceRec) * BS);
   l.off_list = o;
@@ -1443,8 +2010,24 @@ Layout make_layout(int B, int V, int K_max) {
   o = align256(o + sizeof(unsigned long long) * BS * NBIN);
   l.off_cand = o;
   o = align256(o + sizeof(uint2) * BS * l.L);
+  l.off_plan = o;
+  o = align256(o + sizeof(unsigned long long) * PLAN_WORDS * nb);
+  l.off_above = o;
+  o = align256(o + sizeof(double) * BS);
+  l.off_ncand2 = o;
+  o = align256(o + sizeof(unsigned int) * BS);
   l.total = o;
   return l;
+}
+
+// A fresh stamp per call (never 0, which a zeroed workspace holds).
+unsigned int next_epoch() {
+  static std::atomic<unsigned int> counter{0};
+  unsigned int e;
+  do {
+    e = counter.fetch_add(1u, std::memory_order_relaxed) + 1u;
+  } while (e == 0u);
+  return e;
 }
 
 void set_err(char** err, const std::string& msg) {
@@ -1474,9 +2057,13 @@ int check_shape(int B, int V, int K_max, int dtype, char** err) {
   return MLXF_OK;
 }
 
+// Helper workgroups (at most 256) are added when some row can have a second
+// pass (top-p without top-k, or top-k with k > 63).
 template <int DT, int EPT>
-hipError_t launch_ept(const Args& a, bool vecok, hipStream_t st) {
-  const dim3 grid(a.S, a.B);
+hipError_t launch_ept(Args a, bool vecok, hipStream_t st) {
+  const int n1 = a.B * a.S;
+  a.helpers = (a.T != nullptr && (a.p != nullptr || a.k != nullptr)) ? (n1 < 256 ? n1 : 256) : 0;
+  const dim3 grid(n1 + a.helpers);
   if (vecok)
     hipLaunchKernelGGL((k_sample<DT, EPT, true>), grid, dim3(THREADS), 0, st, a);
   else
@@ -1556,6 +2143,14 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
     a.out_top_ids = d_out_top_ids;
     a.out_top_lp = d_out_top_logprobs;
     a.ctr = reinterpret_cast<unsigned int*>(ws + l.off_ctr);
+    a.done2 = reinterpret_cast<unsigned int*>(ws + l.off_done2);
+    a.next2 = reinterpret_cast<unsigned long long*>(ws + l.off_next2);
+    a.queue = reinterpret_cast<unsigned long long*>(ws + l.off_queue);
+    a.gl = reinterpret_cast<unsigned long long*>(ws + l.off_gl);
+    a.epoch = next_epoch();
+    a.plan = reinterpret_cast<unsigned long long*>(ws + l.off_plan);
+    a.above = reinterpret_cast<double*>(ws + l.off_above);
+    a.ncand2 = reinterpret_cast<unsigned int*>(ws + l.off_ncand2);
     a.rec = reinterpret_cast<SliceRec*>(ws + l.off_rec);
     a.list = reinterpret_cast<unsigned long long*>(ws + l.off_list);
     a.hist = reinterpret_cast<unsigned long long*>(ws + l.off_hist);

@@ -213,6 +213,29 @@ def test_large_candidate_sets():
         gu.compare(g, o, dtype, label=f"large candidates {dtype}")
 
 
+def test_workspace_reuse_across_shapes():
+    """One workspace serves calls of different shapes in a row: B grows (the
+    per-row counters must still read zero), then shrinks, then grows again."""
+    ws = sampler.Workspace("cuda:0")
+    rng = np.random.default_rng(77)
+    for B, V, dtype in [(2, 3000, "bf16"), (40, 3000, "bf16"), (3, 20000, "f32"), (70, 5000, "f16"),
+                        (2, 3000, "bf16")]:
+        host, T, k, p, tlp, u = _random_case(rng, B, V, dtype)
+        p = np.where(rng.random(B) < 0.7, rng.uniform(0.3, 0.99, B), p).astype(np.float32)
+        k = np.where(p < 1.0, 0, k).astype(np.int32)  # mostly top-p-only rows
+        say(f"[parity] workspace reuse B={B} V={V} {dtype}")
+        dev = gu.to_device(host, dtype)
+        f = lambda a, t: torch.as_tensor(np.asarray(a), dtype=t).to("cuda:0")
+        res = sampler.sample_rows(dev, temperature=f(T, torch.float32), top_k=f(k, torch.int32),
+                                  top_p=f(p, torch.float32), top_logprobs=f(tlp, torch.int32),
+                                  uniforms=f(u, torch.float32), K_max=3, workspace=ws)
+        torch.cuda.synchronize()
+        g = dict(ids=res.tokens.cpu().numpy(), lp=res.logprobs.cpu().numpy(),
+                 top_ids=res.top_tokens.cpu().numpy(), top_lp=res.top_logprobs.cpu().numpy())
+        o = gu.oracle_sample(host, dtype, T=T, k=k, p=p, tlp=tlp, u=u, K_max=3)
+        gu.compare(g, o, dtype, tlp=tlp, label=f"workspace reuse B={B} V={V} {dtype}")
+
+
 def test_workspace_errors():
     from mlxforge_amd import _lib
     z = torch.zeros(2, 100, device="cuda:0")
