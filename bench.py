@@ -30,6 +30,13 @@ METRIC = ("µs/decode-step and sampled rows/sec at B=32,V=151936; achieved HBM G
 HBM_PEAK_GBPS = 8000.0
 ROTATE_BYTES = 512 << 20
 
+# HBM bytes per k_sample launch from rocprofv3 FETCH_SIZE and WRITE_SIZE runs
+# (separate passes), each scaled by what the counter reads for a plain device
+# copy of known size (--copy-calibration): profiles/k_sample_C3_hbm_traffic.md.
+# A counter run cannot share the timed process, so the figure is carried here.
+MEASURED_TRAFFIC_BYTES = {3: 20607094}
+COPY_CALIBRATION_BYTES = 256 << 20
+
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
@@ -115,7 +122,7 @@ def cpu_baseline(wl, seconds):
                    dtype=code, nthreads=threads)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= seconds or reps >= 200:
+        if el >= seconds:
             break
     rows_per_s = reps * wl.B / el
     return {"value": round(rows_per_s, 2), "unit": "rows/s", "cores": threads, "kind": "port",
@@ -133,7 +140,18 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs' lines")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run five plain 256 MiB device copies (counter scale factors)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        x = torch.ones(COPY_CALIBRATION_BYTES // 4, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": COPY_CALIBRATION_BYTES, "copies": 5}), flush=True)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, "
@@ -183,7 +201,8 @@ def main():
         "achieved_GBps_step": round(alg / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "kernel": "k_sample", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": MEASURED_TRAFFIC_BYTES.get(args.config),
                      "algorithmic_bytes_per_launch": alg,
                      "kernel_us": round(ms * 1e3, 2)},
     }

@@ -61,10 +61,15 @@ def build_lib() -> str:
 
 def build_kat() -> str:
     """C++ known-answer driver over the C++ wrapper; links the built library."""
+    # Host code only (no kernels): the system C++ compiler against the HIP
+    # runtime headers and library.
     tmp = KAT_BIN + ".tmp"
-    _run([hipcc(), "-O2", "-std=c++17", "-I", os.path.join(ROOT, "include"),
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    _run([shutil.which("g++") or "g++", "-O2", "-std=c++17", "-D__HIP_PLATFORM_AMD__",
+          "-I", os.path.join(rocm, "include"), "-I", os.path.join(ROOT, "include"),
           "-I", os.path.join(HERE, "include"), "-o", tmp, KAT_SRC, LIB,
-          f"-Wl,-rpath,{HERE}"])
+          "-L", os.path.join(rocm, "lib"), "-lamdhip64",
+          f"-Wl,-rpath,{HERE}", f"-Wl,-rpath,{os.path.join(rocm, 'lib')}"])
     os.replace(tmp, KAT_BIN)
     return KAT_BIN
 

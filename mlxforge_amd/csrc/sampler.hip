@@ -5,41 +5,49 @@
 // 141-166), run once per row by Worker::sample_rows (src/runtime/worker.cpp:
 // 448-486), with ONE kernel launch over all rows of a [B, V] logits matrix.
 //
-// Grid (S, B): row r is cut into S slices of L = 256 * EPT elements (EPT up to
-// 32); slice s is one 256-thread workgroup (4 waves, up to 256 VGPRs each, two
-// workgroups per CU) that loads its whole slice into registers with 16-byte
-// loads (one HBM read of the logits) and reduces it there:
+// One launch, a 1-D grid of B * S first-pass workgroups followed by up to 256
+// helper workgroups.  Row r is cut into S slices of L = 256 * EPT elements
+// (EPT in {8, 16, 32}); slice s is workgroup r * S + s (256 threads, 4 waves,
+// up to 256 VGPRs each, two workgroups per CU), which loads its whole slice
+// into registers with 16-byte loads (the one HBM read of the logits) and
+// reduces it there:
 //   * max and lowest-index argmax of z, and sum exp(z - max) when a logprob is
 //     wanted;
 //   * when top_logprobs or a top-k <= 63 is asked for: the slice's best 64
 //     entries by (z desc, index asc).  The 64th best of the 256 per-thread
 //     maxima bounds the slice's 64th best from below; the at most 64 * EPT
 //     elements at or above it are sorted in 64-entry chunks and merged;
-//   * top-k > 63: a 4096-bin count histogram of z keys gives the bin of the
-//     slice's k-th largest z; everything from the (temperature-mapped) lower
-//     edge of that bin up is written out as a candidate;
+//   * top-k > 63: a 4096-bin count histogram of z keys (the bins the slice
+//     occupies are recorded);
 //   * temperature-only and top-p rows: the sum of w = exp(z' - max z') over the
 //     slice (z' = z / T in the logits dtype), and for top-p a 2048-bin
-//     histogram of z' keys with (count, truncated w) packed in one 64-bit word.
+//     histogram of z' keys holding (count, exact 2^-42 fixed-point mass).
 // The slice then takes a ticket on the row's counter; the workgroup that draws
-// the row's last ticket finishes the row.  No workgroup ever waits for another.
+// the row's last ticket finishes the row:
 //   * greedy: argmax, logprob and top_logprobs from the slice summaries;
 //   * top-k <= 63: the merged best-64 list of the row decides everything in one
 //     wave (the k-th largest z', the nucleus prefix, the draw), after checking
 //     that the list holds every element at or above the k-th value of z';
-//   * top-k > 63: 8-bit radix selections over the candidates;
 //   * temperature-only: the slice that holds u * sum(w), then a walk of that
 //     slice in vocabulary order;
-//   * top-p: the combined histogram, with the bound of its truncation error,
-//     brackets the nucleus boundary in a range R of bins; a compare-only pass
-//     over the row collects R's elements and the exact mass of the smaller
-//     side of R; radix selections over R's elements give the cutoff value and
-//     the last kept index among its ties; then the walk of the one slice that
-//     holds the draw.
+//   * top-p and top-k > 63: the combined histograms bracket the cutoff in a
+//     narrow range of z' values, and the finisher writes a plan for a second
+//     pass and queues the row.
+// Second pass: one item per slice of a queued row, taken by the row's finisher
+// or by the helper workgroups (which poll the queue until every row of the
+// call is done).  An item re-reads its slice and keeps only what lies in the
+// bracket: per-value counts and masses when the bracket holds few distinct
+// 16-bit values, else the candidates themselves.  The row's last item resolves
+// the cutoff (the value, and the last kept index among its ties), the kept
+// mass, and the draw (the one slice holding u * kept mass, walked in
+// vocabulary order).  Nothing ever waits for a workgroup that may not have
+// started: the ticket holder does the work, and helpers only take queued work.
 // Masses that decide a cutoff are exact 64-bit fixed-point sums (2^-42 units)
 // or fp64 sums in a fixed order, so every result is reproducible bit for bit.
 // Data one workgroup leaves for another travels through device-coherent (sc1)
 // loads and stores, so no L2-wide write-back is ever needed.
+// Counters that must read zero at the start of a call are either reset by
+// their last user or stamped with a per-call epoch.
 // There is no MFMA anywhere: nothing here is a dense contraction.
 #include <hip/hip_runtime.h>
 #include <stdint.h>

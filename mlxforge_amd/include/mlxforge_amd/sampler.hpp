@@ -89,14 +89,14 @@ struct DeviceBuf {
   size_t n = 0;
   void reserve(size_t want) {
     if (want <= n) return;
-    if (p) hipFree(p);
+    if (p) (void)hipFree(p);
     p = nullptr;
     n = 0;
     hip_check(hipMalloc(reinterpret_cast<void**>(&p), want * sizeof(T) + 256), "hipMalloc");
     n = want;
   }
   ~DeviceBuf() {
-    if (p) hipFree(p);
+    if (p) (void)hipFree(p);
   }
 };
 }  // namespace detail
