@@ -3,56 +3,45 @@
 //
 // Replaces the per-row MLX graph of Sampler::sample (src/sample/sampler.cpp:
 // 141-166), run once per row by Worker::sample_rows (src/runtime/worker.cpp:
-// 448-486), with ONE kernel launch over all rows of a [B, V] logits matrix.
+// 448-486), with a short sequence of kernel launches over all rows of a
+// [B, V] logits matrix.  Row r is cut into S slices of L = 256 * EPT logits;
+// every launch is a 1-D grid of B * S workgroups of 256 threads, workgroup
+// r * S + s owning slice s of row r.
 //
-// One launch, a 1-D grid of B * S first-pass workgroups followed by up to 256
-// helper workgroups.  Row r is cut into S slices of L = 256 * EPT elements
-// (EPT in {8, 16, 32}); slice s is workgroup r * S + s (256 threads, 4 waves,
-// up to 256 VGPRs each, two workgroups per CU), which loads its whole slice
-// into registers with 16-byte loads (the one HBM read of the logits) and
-// reduces it there:
-//   * max and lowest-index argmax of z, and sum exp(z - max) when a logprob is
-//     wanted;
-//   * when top_logprobs or a top-k <= 63 is asked for: the slice's best 64
-//     entries by (z desc, index asc).  The 64th best of the 256 per-thread
-//     maxima bounds the slice's 64th best from below; the at most 64 * EPT
-//     elements at or above it are sorted in 64-entry chunks and merged;
-//   * top-k > 63: a 4096-bin count histogram of z keys (the bins the slice
-//     occupies are recorded);
-//   * temperature-only and top-p rows: the sum of w = exp(z' - max z') over the
-//     slice (z' = z / T in the logits dtype), and for top-p a 2048-bin
-//     histogram of z' keys holding (count, exact 2^-42 fixed-point mass).
-// The slice then takes a ticket on the row's counter; the workgroup that draws
-// the row's last ticket finishes the row:
-//   * greedy: argmax, logprob and top_logprobs from the slice summaries;
-//   * top-k <= 63: the merged best-64 list of the row decides everything in one
-//     wave (the k-th largest z', the nucleus prefix, the draw), after checking
-//     that the list holds every element at or above the k-th value of z';
-//   * temperature-only: the slice that holds u * sum(w), then a walk of that
-//     slice in vocabulary order;
-//   * top-p and top-k > 63: the combined histograms bracket the cutoff in a
-//     narrow range of z' values, and the finisher writes a plan for a second
-//     pass and queues the row.
-// Second pass: one item per slice of a queued row, taken by the row's finisher
-// or by the helper workgroups (which poll the queue until every row of the
-// call is done).  An item re-reads its slice and keeps only what lies in the
-// bracket: per-value counts and masses when the bracket holds few distinct
-// 16-bit values, else the candidates themselves.  The row's last item resolves
-// the cutoff (the value, and the last kept index among its ties), the kept
-// mass, and the draw (the one slice holding u * kept mass, walked in
-// vocabulary order).  Nothing ever waits for a workgroup that may not have
-// started: the ticket holder does the work, and helpers only take queued work.
-// Masses that decide a cutoff are exact 64-bit fixed-point sums (2^-42 units)
-// or fp64 sums in a fixed order, so every result is reproducible bit for bit.
-// Data one workgroup leaves for another travels through device-coherent (sc1)
-// loads and stores, so no L2-wide write-back is ever needed.
-// Counters that must read zero at the start of a call are either reset by
-// their last user or stamped with a per-call epoch.
+// k_first (one HBM read of every logit):
+//   * per slice: max and lowest-index argmax of z, the minimum of z, sum
+//     exp(z - max) when a logprob is wanted, and -- for top_logprobs or a
+//     top-k <= 63 -- the slice's best 64 entries by (z desc, index asc);
+//   * the slice's last workgroup to finish (a ticket on the row's counter)
+//     combines the row: argmax, log-sum-exp, top_logprobs, and for top-k <= 63
+//     the whole selection (k-th value, nucleus, draw) from the merged best-64
+//     list.  Every other sampling row gets a plan for the refine stages.
+//
+// k_refine (launched NSTAGE times): each stage narrows one selection per
+// unresolved row, all slices in parallel, and the row's last slice decides:
+//   COUNT   top-k: a 256-bin count histogram of z' over the current bracket;
+//   MASS    top-p: a 256-bin histogram of exact fixed-point masses
+//           w = exp(z' - max z') (2^-40 units) over the current bracket;
+//   GATHER  the bracket's elements themselves (at most CAP per row), resolved
+//           exactly by radix selections in LDS;
+//   DRAWSUM the kept mass of each slice (temperature-only rows, or top-k sets
+//           too large to gather).
+// The first histogram level bins z' on a value grid anchored at the row's max
+// (uniform in log-weight, so concentrated rows spread over many bins); later
+// levels take 8-bit digits of the z' key inside the chosen bin.  A row whose
+// cutoff value is known exactly draws: the slice holding u * (kept mass) is
+// found from per-slice kept masses and walked in vocabulary order.  The last
+// stage finishes any row still open by running the remaining levels over its
+// slices itself.
+//
+// Masses that decide a cutoff are sums of integers, so every result is
+// reproducible bit for bit and every level is consistent with the one before.
+// Data one workgroup hands to another travels through device-coherent (sc1)
+// loads and stores; nothing waits for a workgroup that may not have started.
 // There is no MFMA anywhere: nothing here is a dense contraction.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -65,20 +54,22 @@ namespace mlxf {
 namespace {
 
 enum { KIND_GREEDY = 0, KIND_TEMP = 1, KIND_KLIST = 2, KIND_KHIST = 3, KIND_TOPP = 4 };
+enum { PH_DONE = 0, PH_COUNT = 1, PH_MASS = 2, PH_GATHER = 3, PH_DRAWSUM = 4 };
+// FL_VGRID: the current level bins z' on the value grid (else key digits kb, sh)
+// FL_GALL:  the gather takes every element at or above the bracket's low edge;
+//           the top-k selection is finished on the candidates
+// FL_TOPP:  a nucleus selection follows the top-k selection
+enum { FL_VGRID = 1, FL_GALL = 2, FL_TOPP = 4 };
+enum { SL_FAST = 1 };  // slice record flag: the FMA-corrected division is exact for every z
+
 constexpr int LIST = 64;
 constexpr int KLIST_MAX = LIST - 1;  // top-k resolved from the best-64 lists
-constexpr int CAND_LDS = 4096;
-constexpr int CNT_BINS = 4096;  // z-key >> 20: the per-slice top-k threshold bins
-constexpr int RBINS = 256;      // radix digit
-
-struct SliceRec {  // four 64-bit words
-  float zmax;
-  int zarg;
-  float mps;  // max z' over the slice
-  unsigned int ncand;
-  double lse_s;  // sum exp(z - zmax) over the slice
-  double msum;   // sum w(z', mps) over the slice
-};
+constexpr int NB = 256;              // bins per histogram level
+constexpr int CAP = 4096;            // gathered candidates per row (LDS)
+constexpr int NSTAGE = 3;            // refine launches per call
+constexpr int SERIAL_MAX = 40;       // bound on the levels the last stage runs itself
+constexpr int SURV = 64 * 32;        // best-64 survivors of a slice (<= 64 * EPT)
+constexpr float MASS_LOG2_SPAN = 40.0f;  // weights below 2^-40 quantise to zero
 
 struct Args {
   const void* logits;
@@ -93,64 +84,24 @@ struct Args {
   float* out_lp;
   int* out_top_ids;
   float* out_top_lp;
-  unsigned int* ctr;          // [B] first-pass tickets
-  unsigned int* done2;        // [B] second-pass tickets
-  unsigned long long* next2;  // [B] second-pass items taken (epoch-stamped)
-  unsigned long long* gl;     // call-wide counters (GL_*, epoch-stamped)
-  unsigned long long* queue;  // [B] rows with second-pass items: (epoch, row + 1)
-  unsigned int epoch;         // this call's stamp (never 0)
-  int helpers;                // workgroups after the first B*S
-  SliceRec* rec;
-  unsigned long long* list;   // [B*S][64] packed (z bits, index)
-  unsigned long long* hist;   // [B*S][NBIN]
-  uint2* cand;                // [B*S][L]
-  unsigned long long* plan;   // [B][PLAN_WORDS]
-  double* above;              // [B*S] mass above the bracket, slice units
-  unsigned int* ncand2;       // [B*S] second-pass candidates per slice
+  unsigned int* actcnt;        // [4] rows on each stage's list (zero between calls, see below)
+  unsigned int* ncand;         // [B] gathered-candidate counters, zero between calls
+  unsigned int* actlist;       // [NSTAGE][B] rows still open before each refine stage
+  unsigned long long* rec;     // [B*S][4] slice records
+  unsigned long long* list;    // [B*S][64] (z bits, index)
+  unsigned long long* rowst;   // [B][8] row plans
+  unsigned int* hcnt;          // [B*S][256] histogram counts
+  unsigned long long* hmass;   // [B*S][256] histogram masses
+  unsigned long long* above;   // [B*S] kept mass above the bracket (MASS)
+  unsigned long long* dsum;    // [B*S] kept mass (DRAWSUM)
+  unsigned long long* cand;    // [B][CAP] (z' key, index)
 };
 
-// Call-wide counters: queue slots reserved, rows finished, whether any row of
-// the call has a second pass, and the first queue slot whose row may still have
-// items left.  These, the per-row item counters and the
-// queue slots are 64-bit words (epoch << 32 | value): a word stamped by another
-// call reads as zero, so nothing needs resetting between calls.  (The per-row
-// tickets ctr / done2 are plain counters, reset by their last user.)
-enum { GL_QRES = 0, GL_ROWS = 1, GL_NEED = 2, GL_HEAD = 3, GL_WORDS = 8 };
-constexpr int IDLE_LIMIT = 1 << 16;  // bound on a helper's idle polls (each sleeps up to ~2 us)
-
-__device__ __forceinline__ unsigned int stamped(unsigned long long w, unsigned int epoch) {
-  return static_cast<unsigned int>(w >> 32) == epoch ? static_cast<unsigned int>(w) : 0u;
-}
-__device__ __forceinline__ unsigned int stamped_get(const unsigned long long* p, unsigned int epoch) {
-  return stamped(ld_dev(p), epoch);
-}
-// Take the next value of a stamped counter: the first taker in a call claims
-// the word (compare-exchange from the stale stamp to (epoch, 1)), everyone
-// else adds 1.  Returns the value taken, or `limit` once it has reached limit
-// (the low half never reaches the stamp: there are far fewer takers than 2^32).
-__device__ __forceinline__ unsigned int stamped_take(unsigned long long* p, unsigned int epoch,
-                                                     unsigned int limit) {
-  unsigned long long w = ld_dev(p);
-  if (static_cast<unsigned int>(w >> 32) != epoch) {
-    const unsigned long long claim = (static_cast<unsigned long long>(epoch) << 32) | 1u;
-    if (__hip_atomic_compare_exchange_strong(p, &w, claim, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT))
-      return 0u < limit ? 0u : limit;
-    if (static_cast<unsigned int>(w >> 32) != epoch) return limit;  // (another call's stamp: not ours)
-  }
-  const unsigned long long old = __hip_atomic_fetch_add(p, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const unsigned int v = static_cast<unsigned int>(old);
-  return v < limit ? v : limit;
-}
-
-// The plan a row's first pass leaves for its second pass (64-bit words): bracket z-key range [klo, khi), has_hi, value
-// mode (nv > 0: nv z' values from value index vbase), the nucleus mass still to
-// cover inside the bracket (2^-42 row units), the row's LSE and max z'.
-enum { PL_KEYS = 0, PL_MODE = 1, PL_TARGET = 2, PL_LSE = 3, PL_MP = 4, PLAN_WORDS = 5 };
+// ------------------------------------------------------------ parameters --
 
 struct Mode {
-  int sampling, kk, topp, K, need_lse, want_lp, kind, need_list;
-  float Tr, pr, u;
+  int sampling, kk, topp, K, need_lse, want_lp, kind, need_list, tslow;
+  float Tr, pr, u, y;
 };
 
 // Per-row parameters with the reference's sentinels and the C ABI's
@@ -161,6 +112,8 @@ __device__ __forceinline__ Mode decode(const Args& a, int r) {
   const float T = a.T ? a.T[r] : 0.0f;
   m.Tr = round_dt<DT>(T);
   m.sampling = (__builtin_isfinite(T) && T > 0.0f && m.Tr > 0.0f) ? 1 : 0;
+  m.y = m.sampling ? 1.0f / m.Tr : 1.0f;  // correctly rounded (IEEE division)
+  m.tslow = (m.Tr >= 0x1p-24f && m.Tr <= 0x1p24f) ? 0 : 1;
   const int k = a.k ? a.k[r] : 0;
   m.kk = (m.sampling && k > 0) ? (k < a.V ? k : a.V) : 0;
   const float p = a.p ? a.p[r] : 1.0f;
@@ -193,152 +146,882 @@ __device__ __forceinline__ const void* row_ptr(const Args& a, int r) {
          static_cast<size_t>(r) * static_cast<size_t>(a.row_stride) * elem_size<DT>();
 }
 
+// ------------------------------------------------------ element functions --
+
+// z' = round_dtype(z / Tr) with the quotient correctly rounded (the temperature
+// division of src/sample/sampler.cpp:158).  The fast form is Markstein's
+// FMA-corrected quotient: with y = RN(1/Tr), q0 = RN(z * y) is within an ulp of
+// z / Tr, the remainder z - Tr * q0 is exact by FMA, and RN(q0 + r * y) is the
+// correctly rounded quotient (P. Markstein, IBM J. Res. Dev. 34(1), 1990).  It
+// is used only when no product, remainder or quotient can leave the normal
+// range: 2^-24 <= Tr <= 2^24 and every finite z of the slice has |z| = 0 or
+// 2^-96 <= |z| < 2^100 (the slice record's SL_FAST); +-inf passes through.
+// Zeros come out as +0, so equal values have equal keys.
+template <int DT>
+__device__ __forceinline__ float zdiv(float z, float Tr, float y, bool fast) {
+  float q;
+  if (fast) {
+    const float q0 = z * y;
+    const float rr = __builtin_fmaf(-q0, Tr, z);
+    const float q1 = __builtin_fmaf(rr, y, q0);
+    q = rr != rr ? q0 : q1;
+  } else {
+    q = z / Tr;
+  }
+  return round_dt<DT>(q) + 0.0f;
+}
+
+// Whether |z| lies outside the range the fast division covers (finite z only).
+__device__ __forceinline__ bool div_unsafe(float z) {
+  const unsigned int az = __float_as_uint(z) & 0x7fffffffu;
+  return (az - 1u < 0x0f800000u - 1u) | ((az >= 0x71800000u) & (az < 0x7f800000u));
+}
+
+// Monotone key of a z' value: 32 bits for fp32 logits, the 16-bit value's own
+// key for bf16 / f16 (z' is a value of the logits dtype).
+template <int DT>
+constexpr int keybits() {
+  return DT == MLXF_DTYPE_F32 ? 32 : 16;
+}
+template <int DT>
+__device__ __forceinline__ unsigned int zkey(float zp) {
+  if constexpr (DT == MLXF_DTYPE_F32) {
+    return f2key(zp);
+  } else if constexpr (DT == MLXF_DTYPE_BF16) {
+    return f2key(zp) >> 16;
+  } else {
+    const unsigned int h = __half_as_ushort(__float2half_rn(zp));
+    return (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+  }
+}
+template <int DT>
+__device__ __forceinline__ float kval(unsigned int k) {
+  if constexpr (DT == MLXF_DTYPE_F32) {
+    return key2f(k);
+  } else if constexpr (DT == MLXF_DTYPE_BF16) {
+    return key2f((k << 16) | ((k & 0x8000u) ? 0u : 0xffffu));
+  } else {
+    const unsigned int h = (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(h)));
+  }
+}
+template <int DT>
+__device__ __forceinline__ unsigned int key_lo() {  // key of -inf
+  return DT == MLXF_DTYPE_F32 ? 0x007fffffu : (DT == MLXF_DTYPE_BF16 ? 0x007fu : 0x03ffu);
+}
+template <int DT>
+__device__ __forceinline__ unsigned int key_hi() {  // key of +inf
+  return DT == MLXF_DTYPE_F32 ? 0xff800000u : (DT == MLXF_DTYPE_BF16 ? 0xff80u : 0xfc00u);
+}
+
+// log2 of the weight: (z' - Mp) * log2(e) as one FMA with nc = -RN(Mp * log2 e).
+// The rounding of nc scales every weight of the row by the same factor, which
+// cancels in every mass ratio.
+__device__ __forceinline__ float wlog2(float zp, float nc) { return __builtin_fmaf(zp, LOG2E, nc); }
+
+// w = exp(z' - Mp); for an infinite row max the limit (1 where z' == Mp, else 0).
+__device__ __forceinline__ float wfun(float zp, float Mp, float nc, bool minf) {
+  return minf ? (zp == Mp ? 1.0f : 0.0f) : __builtin_amdgcn_exp2f(wlog2(zp, nc));
+}
+
+// floor(w * 2^40) for w in [0, 1 + 2^-20]: exact fixed-point mass.
+__device__ __forceinline__ unsigned long long q40(float w) {
+  const float t = w * 256.0f;
+  const unsigned int hi = static_cast<unsigned int>(t);
+  const float fr = t - floorf(t);
+  const unsigned int lo = static_cast<unsigned int>(fr * 4294967296.0f);
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+// Value-grid bin of a z' (from its log2 weight x <= ~0): 0 at the row max, 255
+// at R2 = 255 / span below it and everything further down.  Non-increasing in z'.
+__device__ __forceinline__ int vbin_x(float x, float R2) {
+  return max(0, min(__float2int_rz(-x * R2), NB - 1));
+}
+
+// Smallest k in [lo, hi] with pred(k), for pred false then true over [lo, hi]
+// and true at hi: a 64-ary search, one candidate per lane (3 rounds for 16-bit
+// keys, 6 for 32-bit).  The whole wave calls it; every lane gets the result.
+template <typename PRED>
+__device__ unsigned int wave_search(unsigned int lo, unsigned int hi, PRED pred) {
+  const int lane = threadIdx.x & 63;
+  while (lo < hi) {
+    const unsigned long long span = static_cast<unsigned long long>(hi - lo) + 1ull;
+    const unsigned long long step = (span + 63ull) >> 6;
+    const unsigned long long k64 = static_cast<unsigned long long>(lo) + step * static_cast<unsigned long long>(lane);
+    const unsigned int k = k64 > hi ? hi : static_cast<unsigned int>(k64);
+    const unsigned long long bal = __ballot(pred(k));
+    if (bal == 0ull) {
+      lo = rdl(k, 63) + 1u;
+    } else {
+      const int f = __ffsll(static_cast<long long>(bal)) - 1;
+      const unsigned int kf = rdl(k, f);
+      if (f == 0) {
+        hi = kf;
+        lo = kf;
+      } else {
+        lo = rdl(k, f - 1) + 1u;
+        hi = kf;
+      }
+    }
+  }
+  return lo;
+}
+
+// Smallest z key whose z' reaches y (z' non-decreasing in z); 0xffffffff if
+// none.  Whole wave.
+template <int DT>
+__device__ unsigned int gkey(float y, float Tr) {
+  if (!(zdiv<DT>(INFINITY, Tr, 1.0f, false) >= y)) return 0xffffffffu;
+  return wave_search(KEY_NEG_INF, KEY_POS_INF,
+                     [&](unsigned int k) { return zdiv<DT>(key2f(k), Tr, 1.0f, false) >= y; });
+}
+
+// z-key bracket [zlo, zhi] of the elements whose z' key lies in [klo, khi].
+// Whole wave.
+template <int DT>
+__device__ void zbracket(unsigned int klo, unsigned int khi, float Tr, unsigned int* zlo,
+                         unsigned int* zhi) {
+  *zlo = gkey<DT>(kval<DT>(klo), Tr);
+  if (khi >= key_hi<DT>()) {
+    *zhi = KEY_POS_INF;
+  } else {
+    const unsigned int g = gkey<DT>(kval<DT>(khi + 1u), Tr);
+    *zhi = g == 0u ? 0u : g - 1u;
+  }
+}
+
 __device__ __forceinline__ unsigned long long pack_ent(float v, int i) {
   return pack2(__float_as_uint(v), static_cast<unsigned int>(i));
 }
 
-// 64-bit mass added to an LDS counter; one atomic per wave when every active
-// lane adds to the same counter (the common case: candidates come in slice
-// order, and ties share digits).
-__device__ __forceinline__ void lds_add_agg(unsigned long long* base, int idx, unsigned long long q,
-                                            bool act) {
-  const unsigned long long bal = __ballot(act);
-  if (!bal) return;
-  const int first = __ffsll(static_cast<long long>(bal)) - 1;
-  const int i0 = rdl(idx, first);
-  if (__ballot(act && idx != i0) == 0) {
-    const unsigned long long s = wave_sum(act ? q : 0ull);
-    if ((threadIdx.x & 63) == first && s) atomicAdd(base + i0, s);
-  } else if (act && q) {
-    atomicAdd(base + idx, q);
-  }
+__device__ __forceinline__ unsigned int ld_dev32(const unsigned int* p) {
+  return __hip_atomic_load(const_cast<unsigned int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void lds_cnt_agg(unsigned int* base, int idx, bool act) {
-  const unsigned long long bal = __ballot(act);
-  if (!bal) return;
-  const int first = __ffsll(static_cast<long long>(bal)) - 1;
-  const int i0 = rdl(idx, first);
-  if (__ballot(act && idx != i0) == 0) {
-    if ((threadIdx.x & 63) == first) atomicAdd(base + i0, static_cast<unsigned int>(__popcll(bal)));
-  } else if (act) {
-    atomicAdd(base + idx, 1u);
+__device__ __forceinline__ void st_dev32(unsigned int* p, unsigned int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sampled id (and its logprob) of row r.
+template <int DT>
+__device__ void write_out(const Args& a, int r, int id, double lse, bool want_lp) {
+  a.out_ids[r] = id;
+  if (a.out_lp) {
+    const void* row = row_ptr<DT>(a, r);
+    a.out_lp[r] = want_lp ? static_cast<float>(static_cast<double>(ld1<DT>(row, id)) - lse) : NAN;
   }
 }
 
-// ------------------------------------------------------------ shared memory --
+// Uniform draw over the whole vocabulary: what the reference's categorical
+// does when every logit left is -inf (all -inf rows, or a top-p of 0).
+__device__ __forceinline__ int uniform_id(float u, int V) {
+  const double x = floor(static_cast<double>(u) * static_cast<double>(V));
+  return x < V - 1 ? static_cast<int>(x) : V - 1;
+}
 
-union Region0 {  // 32 KB
-  uint2 cand[CAND_LDS];
-  unsigned int vcnt[2 * CAND_LDS];     // 16-bit counters, two per word
-  unsigned short vc16[4 * CAND_LDS];   // per (slice, z' value) counts
-  TopEnt surv[CAND_LDS];  // >= 64 * EPT: the most elements that can reach theta
+// ----------------------------------------------------------- row plans --
+
+// Row plan words (written by a row's finishing workgroup, read by every
+// workgroup of the row in the next stage).
+enum {
+  RS_PHASE = 0,  // phase | flags << 32
+  RS_ZB = 1,     // z-key bracket zlo | zhi << 32 (inclusive)
+  RS_DIG = 2,    // key digits: kb | sh << 32
+  RS_AUX = 3,    // cabove (participants above the bracket) | fkey (z' key filter) << 32
+  RS_GRID = 4,   // Mp bits | R2 bits << 32
+  RS_TGT = 5,    // remaining count / mass target inside the bracket (MASS: 0 = not set)
+  RS_LSE = 6,    // log-sum-exp of the row (fp64 bits)
+  RS_WORDS = 8
 };
-union Region1 {  // 16 KB
-  unsigned int cnt[CNT_BINS];
-  unsigned long long hist[NBIN];  // exact 2^-42 masses of w(z', mps) per z'-key bin
-  struct {
-    double sp[MAX_S * WAVES];
-    unsigned long long sq[MAX_S * WAVES];
-  } pass;
+
+struct Plan {
+  unsigned int phase, flags, zlo, zhi, kb, sh, cabove, fkey;
+  float Mp, R2;
+  unsigned long long target;
+  double lse;
 };
-struct Small {
-  Args args;
-  Mode md;
-  TopEnt lists[WAVES * LIST];  // tree merges
+
+__device__ __forceinline__ void plan_store(const Args& a, int r, const Plan& p) {
+  unsigned long long* w = a.rowst + static_cast<size_t>(r) * RS_WORDS;
+  st_dev(w + RS_PHASE, pack2(p.phase, p.flags));
+  st_dev(w + RS_ZB, pack2(p.zlo, p.zhi));
+  st_dev(w + RS_DIG, pack2(p.kb, p.sh));
+  st_dev(w + RS_AUX, pack2(p.cabove, p.fkey));
+  st_dev(w + RS_GRID, pack2(__float_as_uint(p.Mp), __float_as_uint(p.R2)));
+  st_dev(w + RS_TGT, p.target);
+  st_dev(w + RS_LSE, static_cast<unsigned long long>(__double_as_longlong(p.lse)));
+}
+__device__ __forceinline__ Plan plan_unpack(const unsigned long long* w) {
+  Plan p;
+  p.phase = static_cast<unsigned int>(w[RS_PHASE]);
+  p.flags = static_cast<unsigned int>(w[RS_PHASE] >> 32);
+  p.zlo = static_cast<unsigned int>(w[RS_ZB]);
+  p.zhi = static_cast<unsigned int>(w[RS_ZB] >> 32);
+  p.kb = static_cast<unsigned int>(w[RS_DIG]);
+  p.sh = static_cast<unsigned int>(w[RS_DIG] >> 32);
+  p.cabove = static_cast<unsigned int>(w[RS_AUX]);
+  p.fkey = static_cast<unsigned int>(w[RS_AUX] >> 32);
+  p.Mp = __uint_as_float(static_cast<unsigned int>(w[RS_GRID]));
+  p.R2 = __uint_as_float(static_cast<unsigned int>(w[RS_GRID] >> 32));
+  p.target = w[RS_TGT];
+  p.lse = __longlong_as_double(static_cast<long long>(w[RS_LSE]));
+  return p;
+}
+
+// First level of a selection over the z' keys >= fkey: the value grid when the
+// row max and the span below it are finite and positive, else the top 8 bits of
+// the key.  span2 is the span in log2-weight units.
+template <int DT>
+__device__ void plan_level1(Plan& p, float span2) {
+  if (__builtin_isfinite(p.Mp) && span2 > 0.0f && __builtin_isfinite(span2)) {
+    p.flags |= FL_VGRID;
+    p.R2 = 255.0f / span2;
+  } else {
+    p.flags &= ~static_cast<unsigned int>(FL_VGRID);
+    p.R2 = 0.0f;
+  }
+  p.kb = 0u;
+  p.sh = static_cast<unsigned int>(keybits<DT>() - 8);
+}
+
+// ================================================================ k_scan1 ==
+//
+// Stage 0, one workgroup per slice: the one HBM read of every logit.
+
+struct S1Lds {
+  TopEnt surv[SURV];
+  TopEnt lists[WAVES * LIST];
   float rf[WAVES];
+  float rmin[WAVES];
   int ri[WAVES];
-  double rd[WAVES + 1];
-  double rd2[WAVES];
-  unsigned long long ru[WAVES + 1];
-  int rint[WAVES + 1];
-  unsigned int ticket;
+  unsigned int rfl[WAVES];
+  double rd[WAVES];
+  unsigned int ncand;
   float thv;
   int thi;
-  float zmax;
-  int zarg;
-  double lse;
-  float Mp;
+};
+
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
+  __shared__ S1Lds sh;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int bid = static_cast<int>(blockIdx.x);
+  const int S = a.S;
+  const int r = bid / S, s = bid - r * S;
+  if (bid == 0 && tid == 0) a.actcnt[2] = 0u;  // the third stage list of the previous call is spent
+  const Mode md = decode<DT>(a, r);
+  const void* row = row_ptr<DT>(a, r);
+  const int beg = s * a.L;
+  const int end = min(a.V, beg + a.L);
+  constexpr int NIT = EPT / VEC;
+
+  float v[EPT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
+#define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
+  if (tid == 0) sh.ncand = 0u;
+
+  float tmax = v[0];
+#pragma unroll
+  for (int e = 1; e < EPT; ++e) tmax = fmaxf(tmax, v[e]);
+  {
+    const float wm = wave_max(tmax);
+    if (lane == 0) sh.rf[wid] = wm;
+  }
+  // minimum and division range of the slice (sampling rows)
+  if (md.sampling) {
+    float tmin = INFINITY;
+    bool bad = false;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const bool ok = MLXF_IDX(e) < end;
+      tmin = fminf(tmin, ok ? v[e] : INFINITY);
+      bad |= ok & div_unsafe(v[e]);
+    }
+    const float wmn = wave_min(tmin);
+    const bool wbad = __ballot(bad) != 0ull;
+    if (lane == 0) {
+      sh.rmin[wid] = wmn;
+      sh.rfl[wid] = wbad ? 1u : 0u;
+    }
+  }
+  // lowest index of the thread max; for list rows, the 64th best thread
+  // maximum (theta) bounds the slice's best 64
+  int tbi = INT_MAX;
+#pragma unroll
+  for (int e = EPT - 1; e >= 0; --e)
+    if (v[e] == tmax && MLXF_IDX(e) < end) tbi = MLXF_IDX(e);
+  if (md.need_list) {
+    float lv = tmax;
+    int li = tbi;
+    wave_sort(lv, li);
+    tree_merge(lv, li, sh.lists, WAVES);
+    if (tid == LIST - 1) {
+      sh.thv = lv;
+      sh.thi = li;
+    }
+  }
+  __syncthreads();
+  float zmax = sh.rf[0];
+#pragma unroll
+  for (int w2 = 1; w2 < WAVES; ++w2) zmax = fmaxf(zmax, sh.rf[w2]);
+  {
+    const int wa = wave_min(tmax == zmax ? tbi : INT_MAX);
+    if (lane == 0) sh.ri[wid] = wa;
+  }
+  if (md.need_lse) {
+    float t = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      if (MLXF_IDX(e) < end) t += wexp(v[e], zmax);
+    const double ws = wave_sum(static_cast<double>(t));
+    if (lane == 0) sh.rd[wid] = ws;
+  }
+  if (md.need_list) {
+    // survivors: every element at or before theta in (z desc, index asc) order;
+    // at most 64 threads hold one, so at most 64 * EPT of them
+    const float tv = sh.thv;
+    const int ti = sh.thi;
+    if (!better(tv, ti, tmax, tbi)) {
+      int mine = 0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && !better(tv, ti, v[e], MLXF_IDX(e))) ? 1 : 0;
+      int pos = static_cast<int>(atomicAdd(&sh.ncand, static_cast<unsigned int>(mine)));
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int i = MLXF_IDX(e);
+        if (i < end && !better(tv, ti, v[e], i)) {
+          sh.surv[pos].v = v[e];
+          sh.surv[pos].i = i;
+          ++pos;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  int zarg = sh.ri[0];
+#pragma unroll
+  for (int w2 = 1; w2 < WAVES; ++w2) zarg = min(zarg, sh.ri[w2]);
+  double lse_s = 0.0;
+  if (md.need_lse) {
+    lse_s = sh.rd[0];
+#pragma unroll
+    for (int w2 = 1; w2 < WAVES; ++w2) lse_s += sh.rd[w2];
+  }
+  float zmin = 0.0f;
+  unsigned int sfl = 0u;
+  if (md.sampling) {
+    zmin = sh.rmin[0];
+    unsigned int badw = sh.rfl[0];
+#pragma unroll
+    for (int w2 = 1; w2 < WAVES; ++w2) {
+      zmin = fminf(zmin, sh.rmin[w2]);
+      badw |= sh.rfl[w2];
+    }
+    sfl = badw ? 0u : static_cast<unsigned int>(SL_FAST);
+  }
+  if (md.need_list) {
+    // 64-entry chunks: wave w sorts chunks w, w + WAVES, ... into its own list
+    const int ntot = static_cast<int>(sh.ncand);
+    const int nch = (ntot + LIST - 1) / LIST;
+    float sv = -INFINITY;
+    int si = INT_MAX;
+    for (int ch = wid; ch < nch; ch += WAVES) {
+      const int c = ch * LIST + lane;
+      float cv = -INFINITY;
+      int ci = INT_MAX;
+      if (c < ntot) {
+        cv = sh.surv[c].v;
+        ci = sh.surv[c].i;
+      }
+      wave_sort(cv, ci);
+      wave_list_merge(sv, si, cv, ci);
+    }
+    tree_merge(sv, si, sh.lists, nch < WAVES ? (nch < 1 ? 1 : nch) : WAVES);
+    if (wid == 0) a.list[(static_cast<size_t>(r) * S + s) * LIST + lane] = pack_ent(sv, si);
+  }
+#undef MLXF_IDX
+  if (tid == 0) {
+    unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + s) * 4;
+    rp[0] = pack2(__float_as_uint(zmax), static_cast<unsigned int>(zarg));
+    rp[1] = pack2(__float_as_uint(zmin), sfl);
+    rp[2] = static_cast<unsigned long long>(__double_as_longlong(lse_s));
+  }
+}
+
+// ============================================================== k_decide1 ==
+//
+// Stage 0, one workgroup per row: argmax, log-sum-exp, top_logprobs, top-k <= 63
+// from the merged best-64 lists; a plan for every other sampling row.
+
+struct D1Lds {
+  unsigned long long lst[MAX_S * LIST];
+  TopEnt lists[WAVES * LIST];
+  TopEnt mlist[LIST];
   float szmax[MAX_S];
   int szarg[MAX_S];
+  float szmin[MAX_S];
   double slse[MAX_S];
-  unsigned int ncnd[MAX_S];
-  float mps[MAX_S];
-  double scale[MAX_S];
-  double msum[MAX_S];
-  int off[MAX_S + 1];
-  double side[MAX_S];
-  unsigned long long inR[MAX_S];
-  unsigned long long keepq[MAX_S];
-  double keep[MAX_S];
-  TopEnt mlist[LIST];  // the row's merged best-64
-  unsigned int rc[RBINS];
-  unsigned long long rm[RBINS];
-  int sel[16];
-  unsigned long long selu[4];
-  double seld[4];
-  unsigned int ncand;
-  unsigned int kmin, kmax;
-  int found;
-  int pos_hi, pos_lo, pos_last;
-  int bmin[WAVES], bmax[WAVES];
-  int rlo[MAX_S], rhi[MAX_S];  // occupied histogram bins per slice
-  unsigned long long plan[PLAN_WORDS];
-  int qrow, qitem;
-  unsigned int qn, rdone;
+  float zmax, zmin;
+  int zarg;
+  double lse;
+  int sel[4];
 };
 
-// A row's candidate list: in LDS, in global memory contiguous, or in global
-// memory as the per-slice regions of the first pass (located through off[]).
-struct CandView {
-  uint2* l;
-  uint2* g;
-  const int* off;  // nullptr: g is contiguous
-  int S, L;
-  __device__ __forceinline__ uint2* at(int c) const {
-    if (!off) return g + c;
-    int lo = 0, hi = S;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (off[mid] <= c)
-        lo = mid;
-      else
-        hi = mid;
-    }
-    return g + static_cast<size_t>(lo) * L + (c - off[lo]);
+// Top-k <= 63 from the row's merged best-64 list, by one wave.  Returns false
+// when the list may miss elements tied at the k-th value of z' (the caller then
+// plans a full top-k selection).  The nucleus and the draw follow
+// src/sample/sampler.cpp:63-85,165 on the list: (z' desc, index asc) order,
+// keep while the mass before an entry is < p * W_k, inverse CDF in vocabulary
+// order.
+template <int DT>
+__device__ bool klist_resolve(const Mode& md, float Mp, const TopEnt* ml, int* id_out) {
+  const int lane = threadIdx.x & 63;
+  const float lv = ml[lane].v;
+  const int li = ml[lane].i;
+  const bool real = li != INT_MAX;
+  const float zp = real ? zdiv<DT>(lv, md.Tr, md.y, false) : -INFINITY;
+  const float tau = rdl(zp, md.kk - 1);
+  const int last_i = rdl(li, LIST - 1);
+  const float last_zp = rdl(zp, LIST - 1);
+  if (last_i != INT_MAX && !(last_zp < tau)) return false;
+  const bool in_k = real && zp >= tau;
+  float sv = in_k ? zp : -INFINITY;
+  int si = in_k ? li : INT_MAX;
+  wave_sort(sv, si);  // (z' desc, index asc)
+  const bool k1 = si != INT_MAX;
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  const unsigned long long w = k1 ? q40(wfun(sv, Mp, nc, minf)) : 0ull;
+  const unsigned long long incl = wave_incl_scan(w);
+  const unsigned long long Wk = rdl(incl, 63);
+  bool keep = k1;
+  if (md.topp) {
+    const unsigned long long PW =
+        static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
+    keep = k1 && (incl - w) < PW;
   }
-  // candidate c (global entries may come from other workgroups)
-  __device__ __forceinline__ uint2 get(int c) const { return l ? l[c] : ld_dev2(at(c)); }
+  const unsigned long long wf = keep ? w : 0ull;
+  const unsigned long long Wf = wave_sum(wf);
+  unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(Wf));
+  if (Wf == 0)
+    Tu = 0;
+  else if (Tu >= Wf)
+    Tu = Wf - 1;
+  // kept mass at or before my index, in vocabulary order
+  unsigned long long cum = 0;
+  for (int q = 0; q < 64; ++q) {
+    const unsigned long long wq = rdl(wf, q);
+    const int iq = __builtin_amdgcn_readlane(si, q);
+    if (iq <= si) cum += wq;
+  }
+  const int cand = wave_min((keep && (Wf == 0 || (wf > 0 && cum > Tu))) ? si : INT_MAX);
+  *id_out = cand == INT_MAX ? rdl(si, 0) : cand;
+  return true;
+}
+
+// Put row r on the list of the next refine stage `stage` (0-based list index).
+__device__ __forceinline__ void enlist(const Args& a, int stage, int r) {
+  const unsigned int pos =
+      __hip_atomic_fetch_add(a.actcnt + stage, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  a.actlist[static_cast<size_t>(stage) * a.B + pos] = static_cast<unsigned int>(r);
+}
+
+template <int DT>
+__global__ __launch_bounds__(THREADS) void k_decide1(Args a) {
+  __shared__ D1Lds sh;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int r = static_cast<int>(blockIdx.x);
+  const int S = a.S;
+  const Mode md = decode<DT>(a, r);
+  if (tid < S) {
+    const unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + tid) * 4;
+    const unsigned long long w0 = rp[0], w1 = rp[1], w2 = rp[2];
+    sh.szmax[tid] = __uint_as_float(static_cast<unsigned int>(w0));
+    sh.szarg[tid] = static_cast<int>(w0 >> 32);
+    sh.szmin[tid] = __uint_as_float(static_cast<unsigned int>(w1));
+    sh.slse[tid] = __longlong_as_double(static_cast<long long>(w2));
+  }
+  if (md.need_list) {
+    const unsigned long long* src = a.list + static_cast<size_t>(r) * S * LIST;
+    for (int i = tid; i < S * LIST; i += THREADS) sh.lst[i] = src[i];
+  }
+  __syncthreads();
+  if (md.need_list) {
+    float lv = -INFINITY;
+    int li = INT_MAX;
+    for (int t = wid; t < S; t += WAVES) {
+      const unsigned long long w = sh.lst[t * LIST + lane];
+      wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
+    }
+    tree_merge(lv, li, sh.lists, S < WAVES ? S : WAVES);
+    if (wid == 0) {
+      sh.mlist[lane].v = lv;
+      sh.mlist[lane].i = li;
+    }
+  }
+  if (wid == 0) {
+    const float zm = lane < S ? sh.szmax[lane] : -INFINITY;
+    const int za = lane < S ? sh.szarg[lane] : INT_MAX;
+    float rm = zm;
+    int ra = za;
+    wave_best(rm, ra);
+    double part = (lane < S && md.need_lse) ? sh.slse[lane] * wexp_d(zm, rm) : 0.0;
+    part = wave_sum(part);
+    const float mn = wave_min(lane < S ? sh.szmin[lane] : INFINITY);
+    if (lane == 0) {
+      sh.zmax = rm;
+      sh.zarg = ra;
+      sh.zmin = mn;
+      sh.lse = md.need_lse ? static_cast<double>(rm) + log(part) : static_cast<double>(NAN);
+    }
+  }
+  __syncthreads();
+  const double lse = sh.lse;
+  if (a.K_max > 0 && tid < a.K_max) {  // top_logprobs: the first K of the best 64
+    const size_t o = static_cast<size_t>(r) * a.K_max + tid;
+    if (tid < md.K) {
+      a.out_top_ids[o] = sh.mlist[tid].i;
+      a.out_top_lp[o] = static_cast<float>(static_cast<double>(sh.mlist[tid].v) - lse);
+    } else {
+      a.out_top_ids[o] = -1;
+      a.out_top_lp[o] = -INFINITY;
+    }
+  }
+  Plan pl;
+  pl.phase = PH_DONE;
+  pl.flags = 0u;
+  pl.zlo = KEY_NEG_INF;
+  pl.zhi = KEY_POS_INF;
+  pl.kb = 0u;
+  pl.sh = 0u;
+  pl.cabove = 0u;
+  pl.fkey = key_lo<DT>();
+  pl.Mp = 0.0f;
+  pl.R2 = 0.0f;
+  pl.target = 0ull;
+  pl.lse = lse;
+  if (!md.sampling) {
+    if (tid == 0) write_out<DT>(a, r, sh.zarg, lse, md.want_lp);
+    return;
+  }
+  const float M = sh.zmax;
+  const float Mp = zdiv<DT>(M, md.Tr, md.y, false);  // max z' = z'(max z)
+  pl.Mp = Mp;
+  if (M == -INFINITY || (md.topp && !(md.pr > 0.0f))) {
+    // every logit left is -inf: the reference's draw is uniform
+    if (tid == 0) write_out<DT>(a, r, uniform_id(md.u, a.V), lse, md.want_lp);
+    return;
+  }
+  if (md.kind == KIND_KLIST) {
+    if (wid == 0) {
+      int id = -1;
+      const bool ok = klist_resolve<DT>(md, Mp, sh.mlist, &id);
+      if (lane == 0) {
+        sh.sel[0] = ok ? 1 : 0;
+        sh.sel[1] = id;
+      }
+    }
+    __syncthreads();
+    if (sh.sel[0]) {
+      if (tid == 0) write_out<DT>(a, r, sh.sel[1], lse, md.want_lp);
+      return;
+    }
+  }
+  const float nc = -(Mp * LOG2E);
+  const float zminp = zdiv<DT>(sh.zmin, md.Tr, md.y, false);
+  const float spanc = -wlog2(zminp, nc);  // full span of the row, log2 units
+  if (md.kind == KIND_KLIST || md.kind == KIND_KHIST) {
+    pl.phase = PH_COUNT;
+    pl.target = static_cast<unsigned long long>(md.kk);
+    if (md.topp) pl.flags |= FL_TOPP;
+    plan_level1<DT>(pl, spanc);
+  } else if (md.kind == KIND_TOPP) {
+    pl.phase = PH_MASS;
+    plan_level1<DT>(pl, fminf(spanc, MASS_LOG2_SPAN));
+    for (int t = tid; t < S; t += THREADS) a.above[static_cast<size_t>(r) * S + t] = 0ull;
+  } else {
+    pl.phase = PH_DRAWSUM;
+  }
+  if (tid == 0) {
+    plan_store(a, r, pl);
+    enlist(a, 0, r);
+  }
+}
+
+// =================================================================== stages ==
+
+// Shared memory of a stage's slice pass (kept small: it bounds the occupancy
+// of the streaming kernels).
+struct SLds {
+  unsigned long long pw[RS_WORDS];   // the row plan as read
+  unsigned int hc[NB];               // slice histogram: counts
+  unsigned long long hm[NB];         // slice histogram: masses
+  unsigned long long ru[WAVES + 1];
+  unsigned int rv[WAVES + 1];
+  unsigned int ncand;
+};
+// ... and of a deciding workgroup.
+struct RLds {
+  SLds sl;
+  unsigned long long cand[CAP];      // gathered candidates (z' key | index << 32)
+  unsigned long long kept[MAX_S];    // per-slice kept mass
+  unsigned int tcnt[MAX_S];          // per-slice ties / counts
+  int ri[WAVES + 1];
+  int sel[8];
+  unsigned long long selu[8];
+  unsigned int kmin, kmax, ncand;
+  int found;
 };
 
-// --------------------------------------------------- radix selection (block) --
-//
-// One selection over the candidates that satisfy `part(e)`, on the field
-// F(e) = e.x (key) or e.y (index), scanning values in descending or ascending
-// order, measuring either counts or fixed-point masses wq(e).  It returns the
-// first value v in scan order at which  before + measure(v) >= target
-// (> target when strict) with measure(v) > 0, where `before` is the measure of
-// the values that precede v; *before_out gets `before`, *gcount the number of
-// participants equal to v.  In mass mode, when no value qualifies (the target
-// exceeds the total), the last value in scan order is returned and *none is
-// set.  Rounds of 8-bit digits; the leading digits the participants all share
-// are skipped.  Must be called by the whole workgroup.
-template <bool BY_KEY, bool DESC, bool MASS, typename PART, typename WQ>
-__device__ unsigned int radix_select(const CandView& cv, int n, PART part, WQ wq,
-                                     unsigned long long target, bool strict, Small& sh,
-                                     unsigned long long* before_out, unsigned int* gcount,
-                                     bool* none) {
+// ---- one slice of one stage: the histogram, the gathered elements or the kept
+// mass of slice s of row r under the plan in sh.pw.  Results go to the
+// workspace with plain stores (read by the next kernel, or -- in the last
+// stage -- by this workgroup after a full wait and a barrier).
+template <int DT, int EPT, bool VECOK>
+__device__ void slice_stage(const Args& a, int r, int s, SLds& sh) {
+  const int tid = threadIdx.x;
+  const Plan pl = plan_unpack(sh.pw);
+  const Mode md = decode<DT>(a, r);
+  const void* row = row_ptr<DT>(a, r);
+  const int beg = s * a.L;
+  const int end = min(a.V, beg + a.L);
+  constexpr int NIT = EPT / VEC;
+  const unsigned int sfl = static_cast<unsigned int>(a.rec[(static_cast<size_t>(r) * a.S + s) * 4 + 1] >> 32);
+  const bool fast = !md.tslow && (sfl & SL_FAST);
+  const float Mp = pl.Mp;
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  const bool vgrid = (pl.flags & FL_VGRID) != 0;
+  const unsigned int zlo = pl.zlo, zhi = pl.zhi;
+
+  float v[EPT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
+#define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
+
+  if (pl.phase == PH_COUNT || pl.phase == PH_MASS) {
+    const bool mass = pl.phase == PH_MASS;
+    for (int b = tid; b < NB; b += THREADS) {
+      sh.hc[b] = 0u;
+      sh.hm[b] = 0ull;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const unsigned int zk = f2key(v[e]);
+      if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) {
+        const float zp = zdiv<DT>(v[e], md.Tr, md.y, fast);
+        const float x = wlog2(zp, nc);
+        unsigned long long q = 0;
+        if (mass) q = q40(minf ? (zp == Mp ? 1.0f : 0.0f) : __builtin_amdgcn_exp2f(x));
+        if (!mass || q) {
+          const int bin = vgrid ? vbin_x(x, pl.R2)
+                                : max(0, NB - 1 - static_cast<int>(min((zkey<DT>(zp) - pl.kb) >> pl.sh, 255u)));
+          atomicAdd(&sh.hc[bin], 1u);
+          if (mass) atomicAdd(&sh.hm[bin], q);
+        }
+      }
+    }
+    __syncthreads();
+    const size_t o = (static_cast<size_t>(r) * a.S + s) * NB;
+    for (int b = tid; b < NB; b += THREADS) {
+      a.hcnt[o + b] = sh.hc[b];
+      if (mass) a.hmass[o + b] = sh.hm[b];
+    }
+  } else if (pl.phase == PH_GATHER) {
+    // the slice's elements in the bracket: one reservation per workgroup
+    unsigned int mine = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const unsigned int zk = f2key(v[e]);
+      mine += (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) ? 1u : 0u;
+    }
+    unsigned int total;
+    unsigned int pos = block_excl_scan<unsigned int>(mine, sh.rv, &total);
+    if (tid == 0)
+      sh.ncand = total ? __hip_atomic_fetch_add(a.ncand + r, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+    __syncthreads();
+    pos += sh.ncand;
+    unsigned long long* dst = a.cand + static_cast<size_t>(r) * CAP;
+    if (mine) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const unsigned int zk = f2key(v[e]);
+        if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) {
+          const float zp = zdiv<DT>(v[e], md.Tr, md.y, fast);
+          if (pos < CAP) dst[pos] = pack2(zkey<DT>(zp), static_cast<unsigned int>(MLXF_IDX(e)));
+          ++pos;
+        }
+      }
+    }
+  } else if (pl.phase == PH_DRAWSUM) {
+    unsigned long long t = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const unsigned int zk = f2key(v[e]);
+      if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) {
+        const float zp = zdiv<DT>(v[e], md.Tr, md.y, fast);
+        t += q40(wfun(zp, Mp, nc, minf));
+      }
+    }
+    t = block_sum<unsigned long long>(t, sh.ru);
+    if (tid == 0) a.dsum[static_cast<size_t>(r) * a.S + s] = t;
+  }
+#undef MLXF_IDX
+}
+
+// ---- the draw: walk slice s in vocabulary order; kept elements are those with
+// z' key > tau, and the first tie_lim (in index order) of those equal to tau.
+// Returns the first kept element at which the running kept mass exceeds rem.
+template <int DT, int EPT, bool VECOK>
+__device__ int walk(const Args& a, int r, int s, float Mp, unsigned long long rem, unsigned int tau,
+                    unsigned int tie_lim, RLds& sh) {
+  const int tid = threadIdx.x;
+  const Mode md = decode<DT>(a, r);
+  const void* row = row_ptr<DT>(a, r);
+  const int b0 = s * a.L, e0 = min(a.V, b0 + a.L);
+  const int my0 = b0 + tid * EPT;
+  const unsigned int sfl = static_cast<unsigned int>(a.rec[(static_cast<size_t>(r) * a.S + s) * 4 + 1] >> 32);
+  const bool fast = !md.tslow && (sfl & SL_FAST);
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  // thread t owns EPT consecutive elements, held as z' keys
+  unsigned int kz[EPT];
+#pragma unroll
+  for (int it = 0; it < EPT / VEC; ++it) {
+    float z[VEC];
+    load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) kz[it * VEC + j] = zkey<DT>(zdiv<DT>(z[j], md.Tr, md.y, fast));
+  }
+  unsigned int nt = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) nt += (my0 + e < e0 && kz[e] == tau) ? 1u : 0u;
+  unsigned int tex, tin, ttot;
+  block_scan<unsigned int>(nt, sh.sl.rv, &tex, &tin, &ttot);
+  auto qof = [&](int e, unsigned int& rk) -> unsigned long long {
+    const bool valid = my0 + e < e0;
+    const bool tie = valid && kz[e] == tau;
+    const bool kept = valid && (kz[e] > tau || (tie && rk < tie_lim));
+    rk += tie ? 1u : 0u;
+    return kept ? q40(wfun(kval<DT>(kz[e]), Mp, nc, minf)) : 0ull;
+  };
+  unsigned long long qs = 0;
+  int last = -1;
+  {
+    unsigned int rk = tex;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const unsigned long long q = qof(e, rk);
+      qs += q;
+      if (q > 0) last = my0 + e;
+    }
+  }
+  unsigned long long ex, in, tot;
+  block_scan<unsigned long long>(qs, sh.sl.ru, &ex, &in, &tot);
+  if (tid == 0) sh.found = -1;
+  __syncthreads();
+  if (ex <= rem && rem < in) {
+    unsigned long long c = ex;
+    unsigned int rk = tex;
+    int pick = -1;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const unsigned long long q = qof(e, rk);
+      c += q;
+      if (pick < 0 && q > 0 && c > rem) pick = my0 + e;
+    }
+    sh.found = pick;
+  }
+  __syncthreads();
+  int id = sh.found;
+  if (id < 0) {  // rem reached no element: the last kept element with positive mass
+    const int lm = wave_max(last);
+    if ((tid & 63) == 0) sh.ri[tid >> 6] = lm;
+    __syncthreads();
+    if (tid == 0) {
+      int m = -1;
+      for (int w2 = 0; w2 < WAVES; ++w2) m = max(m, sh.ri[w2]);
+      sh.found = m < 0 ? b0 : m;
+    }
+    __syncthreads();
+    id = sh.found;
+  }
+  __syncthreads();
+  return id;
+}
+
+// Pick the slice holding the draw from per-slice kept masses sh.kept[0..S) and
+// walk it.  sh.tcnt[s] holds the kept ties of slice s unless all ties are kept.
+template <int DT, int EPT, bool VECOK>
+__device__ int draw(const Args& a, int r, const Mode& md, float Mp, unsigned int tau, bool all_ties,
+                    RLds& sh) {
+  const int tid = threadIdx.x;
+  const int S = a.S;
+  if (tid == 0) {
+    unsigned long long W = 0;
+    for (int t = 0; t < S; ++t) W += sh.kept[t];
+    unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(W));
+    if (W == 0)
+      Tu = 0;
+    else if (Tu >= W)
+      Tu = W - 1;
+    unsigned long long cum = 0;
+    int st = -1;
+    unsigned long long rem = 0;
+    for (int t = 0; t < S; ++t) {
+      if (sh.kept[t] > 0) {
+        st = t;
+        rem = Tu - cum;
+        if (cum + sh.kept[t] > Tu) break;
+      }
+      cum += sh.kept[t];
+    }
+    if (st < 0) {
+      st = 0;
+      rem = 0;
+    }
+    sh.sel[0] = st;
+    sh.selu[0] = rem;
+    sh.sel[1] = static_cast<int>(all_ties ? 0xffffffffu : sh.tcnt[st]);
+  }
+  __syncthreads();
+  const int st = sh.sel[0];
+  const unsigned long long rem = sh.selu[0];
+  const unsigned int tl = static_cast<unsigned int>(sh.sel[1]);
+  __syncthreads();
+  return walk<DT, EPT, VECOK>(a, r, st, Mp, rem, tau, tl, sh);
+}
+
+// ---- radix selection over the gathered candidates (LDS).  Over candidates
+// with pred(c), values of the field F (the z' key, scanned in descending
+// order, or the index, ascending) are scanned with measure 1 (counts) or the
+// candidate's fixed-point mass; returns the first value v at which
+// before + measure(v) >= target (> target when strict) with measure(v) > 0,
+// where before is the measure of the values scanned before v.  When no value
+// qualifies, the last value with a positive measure is returned.  *before_out
+// gets `before`, *gcount the number of candidates equal to v.  8-bit digits;
+// the leading bits all participants share are skipped.  Whole workgroup.
+template <int DT, bool BY_KEY, bool MASSM, typename PRED>
+__device__ unsigned int cselect(int n, PRED pred, float Mp, unsigned long long target, bool strict, RLds& sh,
+                                unsigned long long* before_out, unsigned int* gcount) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  // ---- range of the field over participants, and their count and measure
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  auto field = [](unsigned long long c) {
+    return BY_KEY ? static_cast<unsigned int>(c) : static_cast<unsigned int>(c >> 32);
+  };
+  auto meas = [&](unsigned long long c) -> unsigned long long {
+    if (!MASSM) return 1ull;
+    return q40(wfun(kval<DT>(static_cast<unsigned int>(c)), Mp, nc, minf));
+  };
   unsigned int lo = 0xffffffffu, hi = 0u;
-  unsigned long long cnt_all = 0, mass_all = 0;
   for (int c = tid; c < n; c += THREADS) {
-    const uint2 e = cv.get(c);
-    if (part(e)) {
-      const unsigned int f = BY_KEY ? e.x : e.y;
-      lo = min(lo, f);
-      hi = max(hi, f);
-      cnt_all += 1;
-      if (MASS) mass_all += wq(e);
+    const unsigned long long e = sh.cand[c];
+    if (pred(e) && meas(e) > 0) {
+      lo = min(lo, field(e));
+      hi = max(hi, field(e));
     }
   }
   lo = wave_min(lo);
@@ -352,1597 +1035,487 @@ __device__ unsigned int radix_select(const CandView& cv, int n, PART part, WQ wq
     atomicMin(&sh.kmin, lo);
     atomicMax(&sh.kmax, hi);
   }
-  cnt_all = block_sum<unsigned long long>(cnt_all, sh.ru);
-  if (MASS) mass_all = block_sum<unsigned long long>(mass_all, sh.ru);
+  __syncthreads();
   lo = sh.kmin;
   hi = sh.kmax;
   __syncthreads();
-  if (cnt_all == 0) {
+  if (lo > hi) {  // no participant with a positive measure
     *before_out = 0;
     *gcount = 0;
-    *none = true;
     return 0;
   }
-  const unsigned long long tot = MASS ? mass_all : cnt_all;
-  const bool reach = strict ? tot > target : tot >= target;
-  if (lo == hi) {  // a single value
-    *before_out = 0;
-    *gcount = static_cast<unsigned int>(cnt_all);
-    *none = MASS && !reach;
-    return lo;
-  }
-  if (MASS && !reach) {
-    // nothing qualifies: the last value in scan order, everything before it
-    const unsigned int v = DESC ? lo : hi;
-    unsigned long long cv_cnt = 0, cv_mass = 0;
-    for (int c = tid; c < n; c += THREADS) {
-      const uint2 e = cv.get(c);
-      if (part(e) && (BY_KEY ? e.x : e.y) == v) {
-        cv_cnt += 1;
-        cv_mass += wq(e);
-      }
-    }
-    cv_cnt = block_sum<unsigned long long>(cv_cnt, sh.ru);
-    cv_mass = block_sum<unsigned long long>(cv_mass, sh.ru);
-    *before_out = mass_all - cv_mass;
-    *gcount = static_cast<unsigned int>(cv_cnt);
-    *none = true;
-    return v;
-  }
-  const unsigned int diff = lo ^ hi;
-  const int top = 31 - __clz(static_cast<int>(diff));
-  int shift = (top >> 3) << 3;
+  int shift = 0;
+  if (lo != hi) shift = ((31 - __clz(static_cast<int>(lo ^ hi))) >> 3) << 3;
   unsigned int mask = shift + 8 >= 32 ? 0u : ~((1u << (shift + 8)) - 1u);
   unsigned int prefix = lo & mask;
   unsigned long long before = 0;
   unsigned int g = 0;
   for (; shift >= 0; shift -= 8) {
-    for (int d = tid; d < RBINS; d += THREADS) {
-      sh.rc[d] = 0u;
-      if (MASS) sh.rm[d] = 0ull;
+    for (int d = tid; d < NB; d += THREADS) {
+      sh.sl.hc[d] = 0u;
+      sh.sl.hm[d] = 0ull;
     }
     __syncthreads();
-    for (int base = 0; base < n; base += THREADS) {
-      const int c = base + tid;
-      uint2 e = make_uint2(0u, 0u);
-      bool act = false;
-      if (c < n) {
-        e = cv.get(c);
-        const unsigned int f = BY_KEY ? e.x : e.y;
-        act = part(e) && (f & mask) == prefix;
+    for (int c = tid; c < n; c += THREADS) {
+      const unsigned long long e = sh.cand[c];
+      const unsigned int f = field(e);
+      if (pred(e) && (f & mask) == prefix) {
+        const unsigned long long m = meas(e);
+        if (m > 0) {
+          const int d = static_cast<int>((f >> shift) & 255u);
+          const int pos = BY_KEY ? NB - 1 - d : d;
+          atomicAdd(&sh.sl.hc[pos], 1u);
+          if (MASSM) atomicAdd(&sh.sl.hm[pos], m);
+        }
       }
-      const unsigned int f = BY_KEY ? e.x : e.y;
-      const int d = static_cast<int>((f >> shift) & 255u);
-      lds_cnt_agg(sh.rc, d, act);
-      if (MASS) lds_add_agg(sh.rm, d, act ? wq(e) : 0ull, act);
     }
     __syncthreads();
     if (wid == 0) {
-      // lane l owns scan positions 4l..4l+3
       unsigned long long val[4];
       unsigned int cnt[4];
       unsigned long long sum = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int pos = 4 * lane + q;
-        const int d = DESC ? RBINS - 1 - pos : pos;
-        cnt[q] = sh.rc[d];
-        val[q] = MASS ? sh.rm[d] : static_cast<unsigned long long>(cnt[q]);
+        cnt[q] = sh.sl.hc[4 * lane + q];
+        val[q] = MASSM ? sh.sl.hm[4 * lane + q] : static_cast<unsigned long long>(cnt[q]);
         sum += val[q];
       }
       const unsigned long long inc = wave_incl_scan(sum);
-      unsigned long long run = inc - sum;
-      const unsigned long long tg = target > before ? target - before : 0ull;
-      int found = 4 * 64, lastne = -1;
+      unsigned long long run = before + inc - sum;
+      int found = NB, lastne = -1;
       unsigned long long bef = 0, bef_last = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int pos = 4 * lane + q;
-        if (found == 4 * 64 && val[q] > 0 && (strict ? run + val[q] > tg : run + val[q] >= tg)) {
+        if (found == NB && val[q] > 0 && (strict ? run + val[q] > target : run + val[q] >= target)) {
           found = pos;
           bef = run;
         }
-        if (cnt[q] > 0) {
+        if (val[q] > 0) {
           lastne = pos;
           bef_last = run;
         }
         run += val[q];
       }
       int best = wave_min(found);
-      const int lbest = wave_max(lastne);
-      // the total reaches the target, so some digit qualifies; the last
-      // non-empty digit only guards against a total that rounding made short
       unsigned long long b;
-      if (best < 4 * 64) {
+      if (best < NB) {
         b = rdl(bef, best >> 2);
       } else {
-        best = lbest < 0 ? 0 : lbest;
+        best = wave_max(lastne);
+        if (best < 0) best = 0;
         b = rdl(bef_last, best >> 2);
       }
       if (lane == 0) {
-        const int d = DESC ? RBINS - 1 - best : best;
-        sh.sel[0] = d;
-        sh.sel[2] = static_cast<int>(sh.rc[d]);
-        sh.selu[0] = b;
+        sh.sel[2] = best;
+        sh.sel[3] = static_cast<int>(sh.sl.hc[best]);
+        sh.selu[1] = b;
       }
     }
     __syncthreads();
-    prefix |= static_cast<unsigned int>(sh.sel[0]) << shift;
+    const int pos = sh.sel[2];
+    const unsigned int d = static_cast<unsigned int>(BY_KEY ? NB - 1 - pos : pos);
+    prefix |= d << shift;
     mask |= 255u << shift;
-    before += sh.selu[0];
-    g = static_cast<unsigned int>(sh.sel[2]);
+    before = sh.selu[1];
+    g = static_cast<unsigned int>(sh.sel[3]);
     __syncthreads();
   }
   *before_out = before;
   *gcount = g;
-  *none = false;
   return prefix;
 }
 
-// -------------------------------------------------- candidate-set finishing --
-
-// Top-k (then optionally top-p) and the draw, all on a candidate set that holds
-// every element whose z' reaches the row's k-th largest z' (keys are z' keys).
-// Returns the drawn index.
-__device__ int resolve_topk(const Mode& md, const CandView& cv, int n, float Mp, Small& sh) {
-  auto wq = [Mp](uint2 e) { return quant(wexp(key2f(e.x), Mp)); };
-  auto all = [](uint2) { return true; };
-  unsigned long long bef;
-  unsigned int g;
-  bool none;
-  // (1) k-th largest key, with multiplicity
-  const unsigned int tau = radix_select<true, true, false>(
-      cv, n, all, wq, static_cast<unsigned long long>(md.kk), false, sh, &bef, &g, &none);
-  // (2) mass of the top-k set
-  unsigned long long wk = 0;
+// Block sum of the fixed-point masses of the candidates with pred.
+template <int DT, typename PRED>
+__device__ unsigned long long cmass(int n, PRED pred, float Mp, RLds& sh) {
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  unsigned long long t = 0;
   for (int c = threadIdx.x; c < n; c += THREADS) {
-    const uint2 e = cv.get(c);
-    if (e.x >= tau) wk += wq(e);
+    const unsigned long long e = sh.cand[c];
+    if (pred(e)) t += q40(wfun(kval<DT>(static_cast<unsigned int>(e)), Mp, nc, minf));
   }
-  wk = block_sum<unsigned long long>(wk, sh.ru);
-  unsigned int vkey = tau;
-  int idx_cut = INT_MAX;
-  unsigned long long Wf = wk;
-  if (md.topp) {
-    // (3) nucleus cutoff: keep while the mass before an element is < p * W_k
-    const unsigned long long PW =
-        static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(wk)));
-    auto ge_tau = [tau](uint2 e) { return e.x >= tau; };
-    unsigned long long pgt;
-    vkey = radix_select<true, true, true>(cv, n, ge_tau, wq, PW, false, sh, &pgt, &g, &none);
-    const unsigned long long wstar = wq(make_uint2(vkey, 0u));
-    unsigned long long t = g;
-    if (!none && wstar > 0) {
-      const unsigned long long need = PW > pgt ? (PW - pgt + wstar - 1) / wstar : 0ull;
-      t = need < t ? need : t;
-    }
-    if (t == 0) t = 1;
-    if (t < g) {  // (4) the t-th smallest index among the ties at the cutoff
-      auto eq_v = [vkey](uint2 e) { return e.x == vkey; };
-      idx_cut = static_cast<int>(
-          radix_select<false, false, false>(cv, n, eq_v, wq, t, false, sh, &bef, &g, &none));
-    }
-    Wf = pgt + t * wstar;
-  }
-  // (5) inverse-CDF draw in vocabulary order over the kept set
-  unsigned long long T = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(Wf));
-  if (Wf == 0)
-    T = 0;
-  else if (T >= Wf)
-    T = Wf - 1;
-  auto kept = [vkey, idx_cut](uint2 e) {
-    return e.x > vkey || (e.x == vkey && static_cast<int>(e.y) <= idx_cut);
-  };
-  if (Wf == 0) {  // every kept weight underflowed: the lowest kept index
-    return static_cast<int>(radix_select<false, false, false>(cv, n, kept, wq, 1ull, false, sh, &bef,
-                                                              &g, &none));
-  }
-  return static_cast<int>(radix_select<false, false, true>(cv, n, kept, wq, T, true, sh, &bef, &g, &none));
+  return block_sum<unsigned long long>(t, sh.sl.ru);
 }
 
-// ------------------------------------------------------- last-block stages --
-
-// Walk slice s in vocabulary order; the first kept element at which the
-// running mass w(z', mps_s) exceeds rem is the draw.  Kept: key(z') > vkey, or
-// equal with index <= idx_cut.  Thread t owns EPT consecutive elements, read 8
-// at a time (the thread that holds the crossing reads its elements again; they
-// are in L2 by then).
-template <int DT, int EPT, bool VECOK>
-__device__ int final_scan(const Args& a, const Mode& md, const void* row, int s, double rem,
-                          unsigned int vkey, int idx_cut, Small& sh) {
-  const int tid = threadIdx.x;
-  const int b0 = s * a.L;
-  const int e0 = min(a.V, b0 + a.L);
-  const float mps = sh.mps[s];
-  const int my0 = b0 + tid * EPT;
-  auto weight = [&](float z, int i) {
-    const float zp = fz<DT>(z, md.Tr);
-    const unsigned int key = f2key(zp);
-    const bool kept = i < e0 && (key > vkey || (key == vkey && i <= idx_cut));
-    return kept ? wexp(zp, mps) : 0.0f;
-  };
-  double sum = 0.0;
-  int last_pos = -1;
-#pragma unroll 2
-  for (int it = 0; it < EPT / VEC; ++it) {
-    float z[VEC];
-    load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const float ww = weight(z[j], my0 + it * VEC + j);
-      sum += static_cast<double>(ww);
-      if (ww > 0.0f) last_pos = my0 + it * VEC + j;
-    }
+// Number of ties kept at a cutoff: the mass still to cover (need) in units of
+// one tie's mass (wt), at least 1, at most g.
+__device__ __forceinline__ unsigned int ties_kept(unsigned long long need, unsigned long long wt, unsigned int g) {
+  unsigned long long t = g;
+  if (wt > 0) {
+    const unsigned long long nd = (need + wt - 1) / wt;
+    t = nd < t ? nd : t;
   }
-  double ex, in, tot;
-  block_scan<double>(sum, sh.rd, &ex, &in, &tot);
-  if (tid == 0) sh.found = -1;
-  __syncthreads();
-  if (ex <= rem && rem < in) {
-    double c = ex;
-    int pick = -1;
-    for (int it = 0; it < EPT / VEC && pick < 0; ++it) {
-      float z[VEC];
-      load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const float ww = weight(z[j], my0 + it * VEC + j);
-        c += static_cast<double>(ww);
-        if (pick < 0 && c > rem && ww > 0.0f) pick = my0 + it * VEC + j;
-      }
+  if (t == 0) t = 1;
+  return static_cast<unsigned int>(t);
+}
+
+// Publish wave 0's bracket [klo, khi] -> z-key bracket to the workgroup.
+template <int DT>
+__device__ void set_bracket(Plan& pl, unsigned int klo, unsigned int khi, float Tr, RLds& sh) {
+  if ((threadIdx.x >> 6) == 0) {
+    unsigned int zl, zh;
+    zbracket<DT>(klo, khi, Tr, &zl, &zh);
+    if (threadIdx.x == 0) {
+      sh.sel[6] = static_cast<int>(zl);
+      sh.sel[7] = static_cast<int>(zh);
     }
-    sh.found = pick < 0 ? last_pos : pick;  // rounding inside the thread: its last positive element
   }
   __syncthreads();
-  int id = sh.found;
-  if (id < 0) {  // rem at or past the slice total (fp64 rounding): last kept element
-    const int lp = wave_max(last_pos);
-    if ((tid & 63) == 0) sh.rint[tid >> 6] = lp;
-    __syncthreads();
-    if (tid == 0) {
-      int m = -1;
-      for (int w2 = 0; w2 < WAVES; ++w2) m = max(m, sh.rint[w2]);
-      sh.found = m < 0 ? b0 : m;
-    }
-    __syncthreads();
-    id = sh.found;
-  }
-  return id;
-}
-
-template <int DT>
-__device__ void write_sampled(const Args& a, const Mode& md, const void* row, int r, int id,
-                              const Small& sh) {
-  if (threadIdx.x != 0) return;
-  a.out_ids[r] = id;
-  if (a.out_lp)
-    a.out_lp[r] = md.want_lp ? static_cast<float>(static_cast<double>(ld1<DT>(row, id)) - sh.lse)
-                             : NAN;
-}
-
-// Index of the slice holding u * (total kept mass) and the remaining target in
-// that slice's own units.  keep[t] are slice-unit masses, scale[t] converts them
-// to row units.
-__device__ void pick_slice(const double* keep, const double* scale, int S, float u, int* sst_out,
-                           double* rem_out) {
-  double W = 0.0;
-  for (int t = 0; t < S; ++t) W += keep[t] * scale[t];
-  const double T = static_cast<double>(u) * W;
-  double cum = 0.0, before = 0.0;
-  int sst = -1;
-  for (int t = 0; t < S; ++t) {
-    const double m = keep[t] * scale[t];
-    if (m > 0.0) {
-      sst = t;
-      before = cum;
-      if (cum + m > T) break;
-    }
-    cum += m;
-  }
-  if (sst < 0) {
-    sst = 0;
-    before = 0.0;
-  }
-  *sst_out = sst;
-  *rem_out = scale[sst] > 0.0 ? (T - before) / scale[sst] : 0.0;
-}
-
-// Temperature only: all elements kept.
-template <int DT, int EPT, bool VECOK>
-__device__ void finish_temp(const Args& a, const Mode& md, const void* row, int r, Small& sh) {
-  if (threadIdx.x == 0) {
-    int sst;
-    double rem;
-    pick_slice(sh.msum, sh.scale, a.S, md.u, &sst, &rem);
-    sh.sel[0] = sst;
-    sh.seld[0] = rem;
-  }
+  pl.zlo = static_cast<unsigned int>(sh.sel[6]);
+  pl.zhi = static_cast<unsigned int>(sh.sel[7]);
   __syncthreads();
-  const int id = final_scan<DT, EPT, VECOK>(a, md, row, sh.sel[0], sh.seld[0], 0u, INT_MAX, sh);
-  write_sampled<DT>(a, md, row, r, id, sh);
 }
 
-// Top-k <= 63 from the row's merged best-64 list, by one wave.  Returns false
-// when the list may miss elements tied at the k-th value of z' (then the caller
-// extracts the candidates from the row).
-template <int DT>
-__device__ bool klist_resolve(const Mode& md, float Mp, const Small& sh, int* id_out) {
-  const int lane = threadIdx.x & 63;
-  const float lv = sh.mlist[lane].v;
-  const int li = sh.mlist[lane].i;
-  const bool real = li != INT_MAX;
-  const float zp = real ? fz<DT>(lv, md.Tr) : -INFINITY;
-  const float tau = rdl(zp, md.kk - 1);
-  const int last_i = rdl(li, LIST - 1);
-  const float last_zp = rdl(zp, LIST - 1);
-  // every element with z' >= tau is in the list unless the list's last entry reaches tau
-  if (last_i != INT_MAX && !(last_zp < tau)) return false;
-  const bool in_k = real && zp >= tau;
-  float sv = in_k ? zp : -INFINITY;
-  int si = in_k ? li : INT_MAX;
-  wave_sort(sv, si);  // (z' desc, index asc)
-  const bool k1 = si != INT_MAX;
-  const unsigned long long w = k1 ? quant(wexp(sv, Mp)) : 0ull;
-  const unsigned long long incl = wave_incl_scan(w);
-  const unsigned long long Wk = rdl(incl, 63);
-  bool keep = k1;
-  if (md.topp) {
-    const unsigned long long PW =
-        static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
-    keep = k1 && (incl - w) < PW;
-  }
-  const unsigned long long wf = keep ? w : 0ull;
-  const unsigned long long Wf = wave_sum(wf);
-  unsigned long long T = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(Wf));
-  if (Wf == 0)
-    T = 0;
-  else if (T >= Wf)
-    T = Wf - 1;
-  // mass of kept entries with index <= mine, in vocabulary order
-  unsigned long long cum = 0;
-  for (int q = 0; q < 64; ++q) {
-    const unsigned int wlo = __builtin_amdgcn_readlane(static_cast<unsigned int>(wf), q);
-    const unsigned int whi = __builtin_amdgcn_readlane(static_cast<unsigned int>(wf >> 32), q);
-    const int iq = __builtin_amdgcn_readlane(si, q);
-    if (iq <= si) cum += pack2(wlo, whi);
-  }
-  const int cand = wave_min((keep && (Wf == 0 || (wf > 0 && cum > T))) ? si : INT_MAX);
-  *id_out = cand == INT_MAX ? rdl(si, 0) : cand;
-  return true;
+// Digit level over the key range [klo, khi]: 256 bins of 2^sh keys from kb.
+__device__ __forceinline__ void set_digits(Plan& pl, unsigned int klo, unsigned int khi) {
+  pl.flags &= ~static_cast<unsigned int>(FL_VGRID);
+  pl.kb = klo;
+  const unsigned int span = khi - klo;
+  const int bl = span ? 32 - __clz(static_cast<int>(span)) : 0;
+  pl.sh = static_cast<unsigned int>(bl > 8 ? bl - 8 : 0);
 }
 
-// z' value index shift for the 16-bit types: z' is a bf16 / f16 value held in
-// fp32, so its key's low VSHIFT bits carry no information.
-template <int DT>
-constexpr int vshift() {
-  return DT == MLXF_DTYPE_BF16 ? 16 : 13;
-}
-
-// Compare-only pass over the row (the finishing workgroup alone).  Elements
-// with z key in [klo, khi) are "in range"; their mass (2^-42 units of
-// w(z', mps_t)) goes to r1.pass.sq[t * WAVES + wave].  In candidate mode
-// (nv == 0) they become candidates (z' key, index); in value mode (nv > 0, the
-// 16-bit types) they are counted per (slice, z' value) in 16-bit counters
-// r0.vcnt (value index (z' key >> vshift) - vbase).  When `sum_side` is 1
-// (above: z key >= khi) or 2 (below: z key < klo) the mass of that side goes to
-// r1.pass.sp (fp64).  has_hi false: no upper bound.  The next slice's loads
-// are in flight while a slice is processed.
+// ---- the deciding step of a stage for row r (whole workgroup): reads the
+// slices' results, then either writes the sampled id or leaves the next plan in
+// sh.sl.pw and in the row's plan words.
 template <int DT, int EPT, bool VECOK>
-__device__ void row_pass(const Args& a, const Mode& md, const void* row, int r, unsigned int klo,
-                         bool has_hi, unsigned int khi, int sum_side, int nv, unsigned int vbase,
-                         Region0& r0, Region1& r1, Small& sh) {
-  constexpr int NIT = EPT / VEC;
+__device__ void finish_stage(const Args& a, int r, RLds& sh) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int S = a.S;
-  uint2* g = a.cand + static_cast<size_t>(r) * S * a.L;
-  if (nv > 0) {
-    for (int w = tid; w < (S * nv + 1) / 2; w += THREADS) r0.vcnt[w] = 0u;
-    __syncthreads();
-  }
-  // double buffer: slice t+1's loads are in flight while slice t is processed
-  Raw8<DT> cur[NIT], nxt[NIT];
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) load_raw<DT, VECOK>(row, it * CHUNK + tid * VEC, min(a.V, a.L), cur[it]);
-#pragma unroll 1
-  for (int t = 0; t < S; ++t) {
-    const int b0 = t * a.L, e0 = min(a.V, b0 + a.L);
-    if (t + 1 < S) {
-      const int nb0 = b0 + a.L, ne0 = min(a.V, nb0 + a.L);
-#pragma unroll
-      for (int it = 0; it < NIT; ++it) load_raw<DT, VECOK>(row, nb0 + it * CHUNK + tid * VEC, ne0, nxt[it]);
-    }
-    const float mps = sh.mps[t];
-    double part = 0.0;
-    unsigned long long pq = 0;
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      float z[VEC];
-      decode8<DT>(cur[it], z);
-      const int i0 = b0 + it * CHUNK + tid * VEC;
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const int i = i0 + j;
-        const bool valid = i < e0;
-        const unsigned int zk = f2key(z[j]);
-        const bool above = valid && has_hi && zk >= khi;
-        const bool inr = valid && !above && zk >= klo;
-        const bool side = sum_side == 1 ? above : (sum_side == 2 && valid && !above && !inr);
-        unsigned int zpk = 0;
-        if (side || inr) {  // most elements need neither the division nor the exp
-          const float zp = fz<DT>(z[j], md.Tr);
-          const float w = wexp(zp, mps);
-          if (side) part += static_cast<double>(w);
-          if (inr) pq += quant(w);
-          zpk = f2key(zp);
-        }
-        if (nv > 0) {
-          if (inr) {
-            const unsigned int c = static_cast<unsigned int>(t * nv) + ((zpk >> vshift<DT>()) - vbase);
-            atomicAdd(&r0.vcnt[c >> 1], 1u << (16 * (c & 1u)));
-          }
-        } else {
-          const unsigned long long bal = __ballot(inr);
-          if (bal) {
-            unsigned int basepos = 0;
-            if (lane == 0) basepos = atomicAdd(&sh.ncand, static_cast<unsigned int>(__popcll(bal)));
-            basepos = rdl(basepos, 0);
-            if (inr) {
-              const unsigned int pos =
-                  basepos + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(bal >> 32),
-                                                      __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(bal), 0u));
-              const uint2 ent = make_uint2(zpk, static_cast<unsigned int>(i));
-              st_dev(g + pos, ent);
-              if (pos < CAND_LDS) r0.cand[pos] = ent;
-            }
-          }
-        }
-      }
-    }
-    const double pd = wave_sum(part);
-    pq = wave_sum(pq);
-    if (lane == 0) {
-      r1.pass.sp[t * WAVES + wid] = pd;
-      r1.pass.sq[t * WAVES + wid] = pq;
-    }
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) cur[it] = nxt[it];
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // candidate stores complete before other waves read them
-  __syncthreads();
-}
+  Plan pl = plan_unpack(sh.sl.pw);
+  const Mode md = decode<DT>(a, r);
+  const float Mp = pl.Mp;
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  const unsigned int khi_all = key_hi<DT>(), klo_all = key_lo<DT>();
+  bool done = false;
+  int id = 0;
 
-// Top-k from candidates of the first pass (k > 63), or -- when the best-64 list
-// cannot decide a k <= 63 row -- from candidates extracted from the row now.
-template <int DT, int EPT, bool VECOK>
-__device__ void finish_topk(const Args& a, const Mode& md, const void* row, int r, bool from_row,
-                            Region0& r0, Region1& r1, Small& sh) {
-  const int tid = threadIdx.x;
-  const int S = a.S;
-  CandView cv;
-  int n;
-  if (from_row) {
-    // every element with z' >= z'(list entry k-1) -- i.e. z key >= g(that z')
-    if (tid == 0) {
-      const float tau_z = sh.mlist[md.kk - 1].v;
-      sh.sel[4] = static_cast<int>(gkey<DT>(fz<DT>(tau_z, md.Tr), md.Tr));
-      sh.ncand = 0;
-    }
-    __syncthreads();
-    row_pass<DT, EPT, VECOK>(a, md, row, r, static_cast<unsigned int>(sh.sel[4]), false, 0u, 0, 0, 0u,
-                             r0, r1, sh);
-    n = static_cast<int>(sh.ncand);
-    cv.l = n <= CAND_LDS ? r0.cand : nullptr;
-    cv.g = a.cand + static_cast<size_t>(r) * S * a.L;
-    cv.off = nullptr;
-  } else {
-    if (tid == 0) {
-      int o = 0;
-      for (int t = 0; t < S; ++t) {
-        sh.off[t] = o;
-        o += static_cast<int>(sh.ncnd[t]);
+  if (pl.phase == PH_COUNT || pl.phase == PH_MASS) {
+    const bool mass = pl.phase == PH_MASS;
+    // per-bin totals: thread t owns bin t; loads issued 8 slices at a time
+    unsigned int C = 0;
+    unsigned long long Mb = 0;
+    const size_t o0 = static_cast<size_t>(r) * S * NB;
+    for (int t0 = 0; t0 < S; t0 += 8) {
+      unsigned int c8[8];
+      unsigned long long m8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const size_t o = o0 + static_cast<size_t>(t0 + j) * NB + tid;
+        c8[j] = t0 + j < S ? ld_dev32(a.hcnt + o) : 0u;
+        m8[j] = (mass && t0 + j < S) ? ld_dev(a.hmass + o) : 0ull;
       }
-      sh.off[S] = o;
-    }
-    __syncthreads();
-    n = sh.off[S];
-    uint2* g = a.cand + static_cast<size_t>(r) * S * a.L;
-    const bool in_lds = n <= CAND_LDS;
-    for (int t = 0; t < S; ++t) {  // z key -> z' key
-      const int o = sh.off[t], cnt = sh.off[t + 1] - o;
-      uint2* src = g + static_cast<size_t>(t) * a.L;
-      for (int j = tid; j < cnt; j += THREADS) {
-        uint2 e = ld_dev2(src + j);
-        e.x = f2key(fz<DT>(key2f(e.x), md.Tr));
-        if (in_lds)
-          r0.cand[o + j] = e;
-        else
-          st_dev(src + j, e);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        C += c8[j];
+        Mb += m8[j];
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // global rewrites complete before other waves read them
-    __syncthreads();
-    cv.l = in_lds ? r0.cand : nullptr;
-    cv.g = g;
-    cv.off = sh.off;
-  }
-  cv.S = S;
-  cv.L = a.L;
-  const int id = resolve_topk(md, cv, n, sh.Mp, sh);
-  write_sampled<DT>(a, md, row, r, id, sh);
-}
-
-// Top-p without top-k, end of the first pass (the row's last slice): combine the
-// slices' exact mass histograms (occupied bins only) in row units, bracket the
-// nucleus boundary -- the bins [blo, bhi] whose cumulative mass from the top
-// reaches p * W within a relative 1e-12 -- and leave the plan for the second
-// pass: the bracket as z-key thresholds (no division in the comparisons),
-// value mode when the logits are 16-bit and the bracket holds few z' values,
-// p * W, the LSE and max z'; then queue the row for its second pass, whose S
-// items (one per slice) any workgroup may take.  Thread t owns descending
-// positions PB*t ..
-// PB*t+PB-1, i.e. the consecutive bins hb0 .. hb0+PB-1 (position PB*t+q is bin
-// hb0+PB-1-q); four slices' histograms are read per round.
-template <int DT>
-__device__ void plan_topp(const Args& a, const Mode& md, int r, Small& sh) {
-  const int tid = threadIdx.x;
-  const int S = a.S;
-  constexpr int PB = NBIN / THREADS;
-  if (tid < S) {
-    const unsigned int rg = sh.ncnd[tid];
-    sh.rlo[tid] = static_cast<int>(rg & 0xffffu);
-    sh.rhi[tid] = static_cast<int>(rg >> 16);
-  }
-  if (tid == 0) {
-    sh.pos_hi = NBIN;
-    sh.pos_lo = NBIN;
-    sh.pos_last = -1;
-  }
-  __syncthreads();
-  const unsigned long long* hrow = a.hist + static_cast<size_t>(r) * S * NBIN;
-  const int hb0 = NBIN - PB * (tid + 1);
-  double m[PB];
-#pragma unroll
-  for (int q = 0; q < PB; ++q) m[q] = 0.0;
-#pragma unroll 1
-  for (int t0 = 0; t0 < S; t0 += 4) {
-    unsigned long long h[4][PB];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int t = t0 + u;
-      const int lo = t < S ? sh.rlo[t] : NBIN, hi = t < S ? sh.rhi[t] : -1;
-#pragma unroll
-      for (int j = 0; j < PB; ++j) {
-        const int b = hb0 + j;
-        h[u][j] = (b >= lo && b <= hi) ? ld_dev(hrow + static_cast<size_t>(t) * NBIN + b) : 0ull;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const double sc = t0 + u < S ? sh.scale[t0 + u] * QUNIT : 0.0;
-#pragma unroll
-      for (int j = 0; j < PB; ++j) m[PB - 1 - j] += static_cast<double>(h[u][j]) * sc;
-    }
-  }
-  double sA = 0.0;
-#pragma unroll
-  for (int q = 0; q < PB; ++q) sA += m[q];
-  double exA, inA, W;
-  block_scan<double>(sA, sh.rd, &exA, &inA, &W);
-  const double PW = static_cast<double>(md.pr) * W;
-  const double t_hi = PW * (1.0 - 1e-12), t_lo = PW * (1.0 + 1e-12);
-  int ph = NBIN, pl = NBIN, last = -1;
-  double run = exA;
-#pragma unroll
-  for (int q = 0; q < PB; ++q) {
-    run += m[q];
-    if (m[q] > 0.0) {
-      if (ph == NBIN && run >= t_hi) ph = PB * tid + q;
-      if (pl == NBIN && run >= t_lo) pl = PB * tid + q;
-      last = PB * tid + q;
-    }
-  }
-  if (ph < NBIN) atomicMin(&sh.pos_hi, ph);
-  if (pl < NBIN) atomicMin(&sh.pos_lo, pl);
-  if (last >= 0) atomicMax(&sh.pos_last, last);
-  __syncthreads();
-  if (tid == 0) {
-    const int p_last = sh.pos_last < 0 ? NBIN - 1 : sh.pos_last;
-    const int p_hi = min(sh.pos_hi, p_last), p_lo = min(sh.pos_lo, p_last);
-    const int bhi = NBIN - 1 - p_hi, blo = NBIN - 1 - p_lo;
-    const unsigned int klo_edge = max(static_cast<unsigned int>(blo) << 21, KEY_NEG_INF);
-    const unsigned int klo = gkey<DT>(key2f(klo_edge), md.Tr);
-    const unsigned int hi_edge = static_cast<unsigned int>(bhi + 1) << 21;
-    const bool has_hi = bhi < NBIN - 1 && hi_edge <= KEY_POS_INF;
-    const unsigned int khi = has_hi ? gkey<DT>(key2f(hi_edge), md.Tr) : 0u;
-    // value mode: every z' in the bracket is one of nv 16-bit values, counted
-    // per (slice, value) in 16-bit LDS counters by the resolving workgroup
-    int nv = 0;
-    if (DT != MLXF_DTYPE_F32) {
-      const int vpb = 1 << (21 - vshift<DT>());
-      const int want = (bhi - blo + 1) * vpb;
-      if (want <= 1024 && want * S <= 4 * CAND_LDS) nv = want;
-    }
-    const unsigned int vbase = static_cast<unsigned int>(blo) << (21 - vshift<DT>());
-    unsigned long long* pl_ = a.plan + static_cast<size_t>(r) * PLAN_WORDS;
-    st_dev(pl_ + PL_KEYS, pack2(klo, khi));
-    st_dev(pl_ + PL_MODE, pack2(static_cast<unsigned int>(has_hi ? 1 : 0) | (static_cast<unsigned int>(bhi) << 1),
-                                static_cast<unsigned int>(nv) | (vbase << 11)));  // kind bit 12 clear: top-p
-    st_dev(pl_ + PL_TARGET, static_cast<unsigned long long>(__double_as_longlong(PW)));
-    st_dev(pl_ + PL_LSE, static_cast<unsigned long long>(__double_as_longlong(sh.lse)));
-    st_dev(pl_ + PL_MP, static_cast<unsigned long long>(__float_as_uint(sh.Mp)));
-    __builtin_amdgcn_s_waitcnt(0);  // the plan is complete before the row is queued
-    const unsigned int qp = stamped_take(a.gl + GL_QRES, a.epoch, 0xffffffffu);
-    st_dev(a.queue + qp, (static_cast<unsigned long long>(a.epoch) << 32) | (static_cast<unsigned int>(r) + 1u));
-  }
-}
-
-// Top-k with k > 63, end of the first pass: the z-key bin that holds the
-// row's k-th largest z, from the slices' count histograms (occupied bins only);
-// the plan's bracket is every element whose z' reaches the z' of that bin's
-// lower edge (z key >= klo, no upper bound).  Value mode when the logits are
-// 16-bit and few z' values lie between that edge and the row's max z'.  Then
-// queue the row for its second pass.  Thread t owns descending positions
-// PC*t .. PC*t+PC-1 (bins cb0 .. cb0+PC-1).
-template <int DT>
-__device__ void plan_topk(const Args& a, const Mode& md, int r, Small& sh) {
-  const int tid = threadIdx.x;
-  const int S = a.S;
-  constexpr int PC = CNT_BINS / THREADS;
-  if (tid < S) {
-    const unsigned int rg = sh.ncnd[tid];
-    sh.rlo[tid] = static_cast<int>(rg & 0xffffu);
-    sh.rhi[tid] = static_cast<int>(rg >> 16);
-  }
-  if (tid == 0) sh.pos_hi = CNT_BINS;
-  __syncthreads();
-  const unsigned int* hrow = reinterpret_cast<const unsigned int*>(a.hist + static_cast<size_t>(r) * S * NBIN);
-  const int cb0 = CNT_BINS - PC * (tid + 1);
-  unsigned int c[PC];
-#pragma unroll
-  for (int q = 0; q < PC; ++q) c[q] = 0u;
-#pragma unroll 1
-  for (int t0 = 0; t0 < S; t0 += 2) {
-    unsigned int h[2][PC];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int t = t0 + u;
-      const int lo = t < S ? sh.rlo[t] : CNT_BINS, hi = t < S ? sh.rhi[t] : -1;
-#pragma unroll
-      for (int j = 0; j < PC; ++j) {
-        const int b = cb0 + j;
-        h[u][j] = (b >= lo && b <= hi)
-                      ? __hip_atomic_load(hrow + static_cast<size_t>(t) * CNT_BINS + b, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT)
-                      : 0u;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int j = 0; j < PC; ++j) c[PC - 1 - j] += h[u][j];
-  }
-  unsigned int sum = 0;
-#pragma unroll
-  for (int q = 0; q < PC; ++q) sum += c[q];
-  unsigned int ex, in, tot;
-  block_scan<unsigned int>(sum, reinterpret_cast<unsigned int*>(sh.rint), &ex, &in, &tot);
-  const unsigned int kk = static_cast<unsigned int>(md.kk);
-  unsigned int run = ex;
-  int found = CNT_BINS;
-#pragma unroll
-  for (int q = 0; q < PC; ++q) {
-    if (found == CNT_BINS && c[q] > 0 && run + c[q] >= kk) found = PC * tid + q;
-    run += c[q];
-  }
-  if (found < CNT_BINS) atomicMin(&sh.pos_hi, found);
-  __syncthreads();
-  if (tid == 0) {
-    const int pos = sh.pos_hi < CNT_BINS ? sh.pos_hi : CNT_BINS - 1;  // (k <= V: always found)
-    const int bstar = CNT_BINS - 1 - pos;
-    const unsigned int edge = max(static_cast<unsigned int>(bstar) << 20, KEY_NEG_INF);
-    const unsigned int klo = gkey<DT>(fz<DT>(key2f(edge), md.Tr), md.Tr);
-    int nv = 0;
-    unsigned int vbase = 0;
-    if (DT != MLXF_DTYPE_F32) {
-      const unsigned int vlo = f2key(fz<DT>(key2f(klo), md.Tr)) >> vshift<DT>();
-      const unsigned int vhi = f2key(sh.Mp) >> vshift<DT>();
-      const int want = static_cast<int>(vhi - vlo + 2) & ~1;  // whole pairs of counters
-      if (vhi >= vlo && want <= 1024 && want * S <= 4 * CAND_LDS) {
-        nv = want;
-        vbase = vlo;
-      }
-    }
-    unsigned long long* pl_ = a.plan + static_cast<size_t>(r) * PLAN_WORDS;
-    st_dev(pl_ + PL_KEYS, pack2(klo, 0u));
-    st_dev(pl_ + PL_MODE, pack2(static_cast<unsigned int>(NBIN - 1) << 1 | (1u << 12),  // kind bit: top-k
-                                static_cast<unsigned int>(nv) | (vbase << 11)));
-    st_dev(pl_ + PL_TARGET, static_cast<unsigned long long>(kk));
-    st_dev(pl_ + PL_LSE, static_cast<unsigned long long>(__double_as_longlong(sh.lse)));
-    st_dev(pl_ + PL_MP, static_cast<unsigned long long>(__float_as_uint(sh.Mp)));
-    __builtin_amdgcn_s_waitcnt(0);  // the plan is complete before the row is queued
-    const unsigned int qp = stamped_take(a.gl + GL_QRES, a.epoch, 0xffffffffu);
-    st_dev(a.queue + qp, (static_cast<unsigned long long>(a.epoch) << 32) | (static_cast<unsigned int>(r) + 1u));
-  }
-}
-
-// Second pass, the row's last item: the exact nucleus cutoff inside the
-// bracket and the draw.  Value mode (16-bit logits): per (slice, z' value)
-// counts give the cutoff value v*, the number t of its ties that are kept
-// (lowest indices first), the slice holding the t-th tie (scanned for its
-// index) and every slice's kept mass.  Candidate mode: radix selections over
-// the bracket's elements.  Then the slice that holds the draw is walked.
-template <int DT, int EPT, bool VECOK>
-__device__ void resolve_row(int r, Region0& r0, Region1& r1, Small& sh) {
-  const Args& a = sh.args;
-  const Mode& md = sh.md;
-  const void* row = row_ptr<DT>(a, r);
-  const int tid = threadIdx.x;
-  const int S = a.S;
-  const unsigned long long wmode = sh.plan[PL_MODE];
-  const bool khist = ((wmode >> 12) & 1ull) != 0;  // top-k (k > 63) row, else top-p
-  const int nv = static_cast<int>((wmode >> 32) & 0x7ffu);
-  const unsigned int vbase = static_cast<unsigned int>(wmode >> 43);
-  const double PW = khist ? 0.0 : __longlong_as_double(static_cast<long long>(sh.plan[PL_TARGET]));
-  const unsigned int kk = khist ? static_cast<unsigned int>(sh.plan[PL_TARGET]) : 0u;
-  const float Mp = __uint_as_float(static_cast<unsigned int>(sh.plan[PL_MP]));
-  if (tid == 0) {
-    sh.lse = __longlong_as_double(static_cast<long long>(sh.plan[PL_LSE]));
-    sh.Mp = Mp;
-  }
-  if (tid < S) {
-    const unsigned long long* rp = reinterpret_cast<const unsigned long long*>(a.rec + (r * S + tid));
-    const float mps = __uint_as_float(static_cast<unsigned int>(ld_dev(rp + 1)));
-    sh.mps[tid] = mps;
-    sh.scale[tid] = wexp_d(mps, Mp);
-    sh.keep[tid] = __longlong_as_double(static_cast<long long>(ld_dev(a.above + (r * S + tid))));
-    sh.keepq[tid] = 0ull;
-    sh.ncnd[tid] = nv > 0 ? 0u : __hip_atomic_load(a.ncand2 + (r * S + tid), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    double pa = 0.0;
-    for (int t = 0; t < S; ++t) pa += sh.keep[t] * sh.scale[t];
-    const double nq = (PW - pa) / QUNIT;  // nucleus mass still to cover inside the bracket
-    sh.selu[1] = nq <= 1.0 ? 1ull : static_cast<unsigned long long>(ceil(nq));
-    int o = 0;
-    for (int t = 0; t < S; ++t) {
-      sh.off[t] = o;
-      o += static_cast<int>(sh.ncnd[t]);
-    }
-    sh.off[S] = o;
-  }
-  __syncthreads();
-  unsigned long long target = sh.selu[1];
-  unsigned int vkey;
-  int idx_cut = INT_MAX;
-  if (nv > 0) {
-    // per (slice, value) counts: slice t left nv/2 words of two 32-bit counts
-    const int words = nv / 2;
-#pragma unroll 4
-    for (int idx = tid; idx < S * words; idx += THREADS) {
-      const int t = idx / words, w = idx - t * words;
-      const unsigned long long x =
-          ld_dev(reinterpret_cast<const unsigned long long*>(a.cand + (static_cast<size_t>(r) * S + t) * a.L) + w);
-      r0.vc16[t * nv + 2 * w] = static_cast<unsigned short>(x);
-      r0.vc16[t * nv + 2 * w + 1] = static_cast<unsigned short>(x >> 32);
-    }
-    __syncthreads();
-    // Values are scanned from the top (value index nv-1) down; thread t owns
-    // descending positions 4t .. 4t+3.
-    constexpr int VS = vshift<DT>();
-    auto vkey_of = [vbase](int v) {
-      const unsigned int top = vbase + static_cast<unsigned int>(v);
-      return (top << VS) | (top < (0x80000000u >> VS) ? ((1u << VS) - 1u) : 0u);
-    };
-    auto cnt_of = [&](int t, int v) { return static_cast<unsigned int>(r0.vc16[t * nv + v]); };
-    unsigned int cv[4];
-    unsigned long long mv[4], msum4 = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int pos = 4 * tid + j, v = nv - 1 - pos;
-      unsigned int cnt = 0;
-      if (pos < nv)
-        for (int t = 0; t < S; ++t) cnt += cnt_of(t, v);
-      cv[j] = cnt;
-      mv[j] = cnt ? static_cast<unsigned long long>(cnt) * quant(wexp(key2f(vkey_of(v)), Mp)) : 0ull;
-      msum4 += mv[j];
+    const unsigned long long meas = mass ? Mb : static_cast<unsigned long long>(C);
+    unsigned long long mex, min_, mtot;
+    block_scan<unsigned long long>(meas, sh.sl.ru, &mex, &min_, &mtot);
+    unsigned int cex, cin, ctot;
+    block_scan<unsigned int>(C, sh.sl.rv, &cex, &cin, &ctot);
+    if (mass && pl.target == 0) {
+      // first mass level: the nucleus target p * W over the participants
+      const unsigned long long PW =
+          static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(mtot)));
+      pl.target = PW < 1 ? 1 : PW;
     }
     if (tid == 0) {
-      sh.pos_hi = nv;
-      sh.pos_lo = nv;
-      sh.pos_last = -1;
+      sh.sel[4] = NB;
+      sh.sel[5] = -1;
     }
-    // top-k rows: the k-th largest z' (position plim, counted from the top),
-    // the mass W_k of the values at or above it, and the nucleus target inside
-    // them (all of W_k when there is no top-p)
-    int plim = nv - 1;
-    if (khist) {
-      unsigned int csum = cv[0] + cv[1] + cv[2] + cv[3];
-      unsigned int cex, cin, ctot;
-      block_scan<unsigned int>(csum, reinterpret_cast<unsigned int*>(sh.rint), &cex, &cin, &ctot);
-      unsigned int crun = cex;
-      int fpos = nv;
+    __syncthreads();
+    if (meas > 0 && min_ >= pl.target) atomicMin(&sh.sel[4], tid);
+    if (meas > 0) atomicMax(&sh.sel[5], tid);
+    __syncthreads();
+    const int bstar = sh.sel[4] < NB ? sh.sel[4] : (sh.sel[5] >= 0 ? sh.sel[5] : NB - 1);
+    if (tid == bstar) {
+      sh.selu[2] = mex;                                   // measure above the bin
+      sh.selu[3] = static_cast<unsigned long long>(cex);  // participants above the bin
+      sh.selu[4] = static_cast<unsigned long long>(C);    // participants in the bin
+    }
+    // per slice: the mass above the bin (MASS) and the participants in the bin;
+    // wave w takes slices w, w + WAVES, ..., four at a time
+    for (int t0 = wid * 4; t0 < S; t0 += WAVES * 4) {
+      unsigned long long part[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if (fpos == nv && cv[j] > 0 && crun + cv[j] >= kk) fpos = 4 * tid + j;
-        crun += cv[j];
-      }
-      if (fpos < nv) atomicMin(&sh.pos_lo, fpos);
-      __syncthreads();
-      plim = sh.pos_lo < nv ? sh.pos_lo : nv - 1;
-      unsigned long long part = 0;
+        part[j] = 0;
+        const int t = t0 + j;
+        if (mass && t < S) {
+          const size_t ob = o0 + static_cast<size_t>(t) * NB;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) part += (4 * tid + j <= plim) ? mv[j] : 0ull;
-      const unsigned long long wk = block_sum<unsigned long long>(part, sh.ru);
-      target = md.topp ? static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(wk)))
-                       : wk;
-      if (target == 0) target = 1;
-    }
-    unsigned long long ex, in, tot;
-    block_scan<unsigned long long>(msum4, sh.ru, &ex, &in, &tot);
-    unsigned long long run = ex;
-    int found = nv, lastne = -1;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int pos = 4 * tid + j;
-      if (cv[j] > 0 && pos <= plim) {
-        if (found == nv && mv[j] > 0 && run + mv[j] >= target) found = pos;
-        lastne = pos;
-      }
-      run += mv[j];
-    }
-    if (found < nv) atomicMin(&sh.pos_hi, found);
-    if (lastne >= 0) atomicMax(&sh.pos_last, lastne);
-    __syncthreads();
-    // the position of v* and the mass of the values above it; a top-k row
-    // without top-p keeps every tie of its k-th value
-    const bool whole = khist && !md.topp;
-    const int pstar = whole ? plim : (sh.pos_hi < nv ? sh.pos_hi : (sh.pos_last < 0 ? 0 : sh.pos_last));
-    if (pstar >= 4 * tid && pstar < 4 * tid + 4) {
-      unsigned long long pgt = ex;
-      for (int j = 0; j < pstar - 4 * tid; ++j) pgt += mv[j];
-      const int jj = pstar - 4 * tid;
-      const unsigned int cstar = cv[jj];
-      const unsigned long long wstar = cstar ? mv[jj] / cstar : 0ull;
-      unsigned long long t = cstar;
-      if (!whole && sh.pos_hi < nv && wstar > 0) {
-        const unsigned long long nd = target > pgt ? (target - pgt + wstar - 1) / wstar : 0ull;
-        t = nd < t ? nd : t;
-      }
-      if (t == 0) t = 1;
-      sh.selu[2] = t;
-      sh.sel[14] = static_cast<int>(cstar);
-    }
-    __syncthreads();
-    const int vstar = nv - 1 - pstar;
-    vkey = vkey_of(vstar);
-    const unsigned int tties = static_cast<unsigned int>(sh.selu[2]);
-    const unsigned int cstar = static_cast<unsigned int>(sh.sel[14]);
-    if (tid == 0) {  // the slice holding the t-th tie and its rank there
-      unsigned int before = 0;
-      int st = S - 1;
-      for (int t = 0; t < S; ++t) {
-        const unsigned int ct = cnt_of(t, vstar);
-        if (before + ct >= tties) {
-          st = t;
-          break;
-        }
-        before += ct;
-      }
-      sh.sel[15] = st;
-      sh.selu[3] = tties - before;
-    }
-    __syncthreads();
-    const int st_tie = sh.sel[15];
-    const unsigned int rank = static_cast<unsigned int>(sh.selu[3]);
-    if (tties < cstar) {
-      // index of the rank-th element equal to v* in slice st_tie (thread t owns
-      // EPT consecutive elements)
-      const int b0 = st_tie * a.L, e0 = min(a.V, b0 + a.L);
-      const int my0 = b0 + tid * EPT;
-      unsigned int cnt = 0;
-#pragma unroll 2
-      for (int it = 0; it < EPT / VEC; ++it) {
-        float z[VEC];
-        load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
-#pragma unroll
-        for (int j = 0; j < VEC; ++j)
-          cnt += (my0 + it * VEC + j < e0 && f2key(fz<DT>(z[j], md.Tr)) == vkey) ? 1u : 0u;
-      }
-      unsigned int cex, cin, ctot;
-      block_scan<unsigned int>(cnt, reinterpret_cast<unsigned int*>(sh.rint), &cex, &cin, &ctot);
-      if (cex < rank && rank <= cin) {
-        unsigned int k = cex;
-        int pick = -1;
-        for (int it = 0; it < EPT / VEC && pick < 0; ++it) {
-          float z[VEC];
-          load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) {
-            const int i = my0 + it * VEC + j;
-            if (pick < 0 && i < e0 && f2key(fz<DT>(z[j], md.Tr)) == vkey && ++k == rank) pick = i;
-          }
-        }
-        sh.sel[1] = pick;
-      }
-      __syncthreads();
-      idx_cut = sh.sel[1];
-    }
-    // kept in-bracket mass per slice: values above v*, and the ties up to the cut
-    for (int pidx = tid; pidx < S * nv; pidx += THREADS) {
-      const int t = pidx / nv, v = pidx - t * nv;
-      unsigned long long q = 0;
-      if (v >= vstar) {
-        unsigned int cnt = cnt_of(t, v);
-        if (v == vstar && tties < cstar) cnt = t < st_tie ? cnt : (t == st_tie ? rank : 0u);
-        if (cnt) q = static_cast<unsigned long long>(cnt) * quant(wexp(key2f(vkey_of(v)), sh.mps[t]));
-      }
-      if (q) atomicAdd(&sh.keepq[t], q);
-    }
-    __syncthreads();
-  } else {
-    // candidate mode: the bracket's elements, per-slice regions of a.cand
-    const int n = sh.off[S];
-    CandView cv;
-    cv.l = nullptr;
-    cv.g = a.cand + static_cast<size_t>(r) * S * a.L;
-    cv.off = sh.off;
-    cv.S = S;
-    cv.L = a.L;
-    if (n <= CAND_LDS) {  // gather into LDS
-      for (int t = 0; t < S; ++t) {
-        const int o = sh.off[t], cnt = sh.off[t + 1] - o;
-        const uint2* src = cv.g + static_cast<size_t>(t) * a.L;
-        for (int j = tid; j < cnt; j += THREADS) r0.cand[o + j] = ld_dev2(src + j);
-      }
-      __syncthreads();
-      cv.l = r0.cand;
-    }
-    if (khist) {  // k-th largest, top-p inside the top k, and the draw, on the candidates
-      const int id = resolve_topk(md, cv, n, Mp, sh);
-      write_sampled<DT>(a, md, row, r, id, sh);
-      if (tid == 0) stamped_take(a.gl + GL_ROWS, a.epoch, 0xffffffffu);
-      return;
-    }
-    auto wq = [Mp](uint2 e) { return quant(wexp(key2f(e.x), Mp)); };
-    unsigned long long pgt, bef;
-    unsigned int g_cnt;
-    bool all_kept;
-    auto any = [](uint2) { return true; };
-    vkey = radix_select<true, true, true>(cv, n, any, wq, target, false, sh, &pgt, &g_cnt, &all_kept);
-    const unsigned long long wstar = wq(make_uint2(vkey, 0u));
-    unsigned long long tk = g_cnt;
-    if (!all_kept && wstar > 0) {
-      const unsigned long long nd = target > pgt ? (target - pgt + wstar - 1) / wstar : 0ull;
-      tk = nd < tk ? nd : tk;
-    }
-    if (tk == 0) tk = 1;
-    if (tk < g_cnt) {
-      const unsigned int vk = vkey;
-      auto eq_v = [vk](uint2 e) { return e.x == vk; };
-      unsigned int g2;
-      bool none2;
-      idx_cut = static_cast<int>(
-          radix_select<false, false, false>(cv, n, eq_v, wq, tk, false, sh, &bef, &g2, &none2));
-    }
-    for (int base = 0; base < n; base += THREADS) {
-      const int c = base + tid;
-      bool kept = false;
-      int st = 0;
-      unsigned long long q = 0;
-      if (c < n) {
-        const uint2 e = cv.get(c);
-        kept = e.x > vkey || (e.x == vkey && static_cast<int>(e.y) <= idx_cut);
-        st = static_cast<int>(e.y) / a.L;
-        q = kept ? quant(wexp(key2f(e.x), sh.mps[st])) : 0ull;
-      }
-      lds_add_agg(sh.keepq, st, q, kept);
-    }
-    __syncthreads();
-  }
-  if (tid == 0) {
-    for (int t = 0; t < S; ++t) sh.keep[t] += static_cast<double>(sh.keepq[t]) * QUNIT;
-    int sst;
-    double rem;
-    pick_slice(sh.keep, sh.scale, S, md.u, &sst, &rem);
-    sh.sel[0] = sst;
-    sh.seld[1] = rem;
-  }
-  __syncthreads();
-  const int id = final_scan<DT, EPT, VECOK>(a, md, row, sh.sel[0], sh.seld[1], vkey, idx_cut, sh);
-  write_sampled<DT>(a, md, row, r, id, sh);
-  if (tid == 0) stamped_take(a.gl + GL_ROWS, a.epoch, 0xffffffffu);
-}
-
-// Everything the last slice of a row does.
-template <int DT, int EPT, bool VECOK>
-__device__ __forceinline__ void finish_row(int r, Region0& r0, Region1& r1, Small& sh) {
-  const Args& a = sh.args;
-  const Mode& md = sh.md;  // in LDS: callees that are not inlined take it by reference
-  const void* row = row_ptr<DT>(a, r);
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int S = a.S;
-
-  if (tid < S) {
-    const unsigned long long* rp = reinterpret_cast<const unsigned long long*>(a.rec + (r * S + tid));
-    const unsigned long long w0 = ld_dev(rp + 0), w1 = ld_dev(rp + 1);
-    sh.szmax[tid] = __uint_as_float(static_cast<unsigned int>(w0));
-    sh.szarg[tid] = static_cast<int>(w0 >> 32);
-    sh.mps[tid] = __uint_as_float(static_cast<unsigned int>(w1));
-    sh.ncnd[tid] = static_cast<unsigned int>(w1 >> 32);
-    sh.slse[tid] = __longlong_as_double(static_cast<long long>(ld_dev(rp + 2)));
-    sh.msum[tid] = __longlong_as_double(static_cast<long long>(ld_dev(rp + 3)));
-  }
-  // the row's best 64: wave w merges the lists of slices w, w + 16, ...; then a tree
-  if (md.need_list) {
-    float lv = -INFINITY;
-    int li = INT_MAX;
-    for (int t = wid; t < S; t += WAVES) {
-      const unsigned long long w = ld_dev(a.list + (static_cast<size_t>(r) * S + t) * LIST + lane);
-      wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
-    }
-    tree_merge(lv, li, sh.lists, S < WAVES ? S : WAVES);
-    if (wid == 0) {
-      sh.mlist[lane].v = lv;
-      sh.mlist[lane].i = li;
-    }
-  }
-  __syncthreads();
-  if (wid == 0) {
-    const float zm = lane < S ? sh.szmax[lane] : -INFINITY;
-    const int za = lane < S ? sh.szarg[lane] : INT_MAX;
-    float rm = zm;
-    int ra = za;
-    wave_best(rm, ra);
-    double part = (lane < S && md.need_lse) ? sh.slse[lane] * wexp_d(zm, rm) : 0.0;
-    part = wave_sum(part);
-    const float Mp = md.sampling ? fz<DT>(rm, md.Tr) : 0.0f;
-    if (lane < S && md.sampling) sh.scale[lane] = wexp_d(sh.mps[lane], Mp);
-    if (lane == 0) {
-      sh.zmax = rm;
-      sh.zarg = ra;
-      sh.lse = md.need_lse ? static_cast<double>(rm) + log(part) : static_cast<double>(NAN);
-      sh.Mp = Mp;
-    }
-  }
-  __syncthreads();
-
-  if (tid == 0 && md.kind == KIND_GREEDY) {
-    a.out_ids[r] = sh.zarg;
-    if (a.out_lp)
-      a.out_lp[r] = md.want_lp ? static_cast<float>(static_cast<double>(sh.zmax) - sh.lse) : NAN;
-  }
-  if (a.K_max > 0 && tid < a.K_max) {  // top_logprobs: the first K of the best-64
-    const size_t o = static_cast<size_t>(r) * a.K_max + tid;
-    if (tid < md.K) {
-      a.out_top_ids[o] = sh.mlist[tid].i;
-      a.out_top_lp[o] = static_cast<float>(static_cast<double>(sh.mlist[tid].v) - sh.lse);
-    } else {
-      a.out_top_ids[o] = -1;
-      a.out_top_lp[o] = -INFINITY;
-    }
-  }
-
-  if (md.topp && !(md.pr > 0.0f)) {
-    // p rounds to 0 in the logits dtype: the nucleus keeps nothing, every
-    // logit is masked, and the draw is uniform over the vocabulary
-    if (tid == 0) {
-      const double x = floor(static_cast<double>(md.u) * static_cast<double>(a.V));
-      write_sampled<DT>(a, md, row, r, x < a.V - 1 ? static_cast<int>(x) : a.V - 1, sh);
-    }
-  } else if (md.kind == KIND_TEMP) {
-    finish_temp<DT, EPT, VECOK>(a, md, row, r, sh);
-  } else if (md.kind == KIND_KLIST) {
-    if (wid == 0) {
-      int id = -1;
-      const bool ok = klist_resolve<DT>(md, sh.Mp, sh, &id);
-      if (lane == 0) {
-        sh.sel[10] = ok ? 1 : 0;
-        sh.sel[11] = id;
-      }
-    }
-    __syncthreads();
-    if (sh.sel[10])
-      write_sampled<DT>(a, md, row, r, sh.sel[11], sh);
-    else
-      finish_topk<DT, EPT, VECOK>(a, md, row, r, true, r0, r1, sh);
-  } else if (md.kind == KIND_KHIST) {
-    plan_topk<DT>(a, md, r, sh);
-    return;  // finished by its second pass
-  } else if (md.kind == KIND_TOPP) {
-    plan_topp<DT>(a, md, r, sh);
-    return;  // finished by its second pass
-  }
-  if (tid == 0) stamped_take(a.gl + GL_ROWS, a.epoch, 0xffffffffu);
-}
-
-// =================================================================== kernel ==
-
-// First pass over slice s of row r; the row's last slice finishes the row
-// (returns true in that workgroup).
-template <int DT, int EPT, bool VECOK>
-__device__ __forceinline__ bool first_pass(const Args& a, int r, int s, Region0& r0, Region1& r1, Small& sh) {
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int S = a.S;
-  const Mode md = decode<DT>(a, r);
-  const void* row = row_ptr<DT>(a, r);
-  const int beg = s * a.L;
-  const int end = min(a.V, beg + a.L);
-  constexpr int NIT = EPT / VEC;
-
-  float v[EPT];
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
-#define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
-  if (s == 0 && tid == 0 && (md.kind == KIND_TOPP || md.kind == KIND_KHIST))
-    st_dev(a.gl + GL_NEED, (static_cast<unsigned long long>(a.epoch) << 32) | 1u);
-
-  // Histograms are cleared while the loads are in flight.  The pass has two
-  // barriers: B1 publishes the wave maxima (and list thresholds), B2 the
-  // argmax, the sums and the survivors.
-  if (md.kind == KIND_TOPP) {
-    for (int b = tid; b < NBIN; b += THREADS) r1.hist[b] = 0ull;
-  } else if (md.kind == KIND_KHIST) {
-    for (int b = tid; b < CNT_BINS; b += THREADS) r1.cnt[b] = 0u;
-  }
-  if (tid == 0) sh.ncand = 0u;
-
-  // ---- thread max; each wave's max and, for the best-64 list, the wave's 16th
-  // largest thread maximum (a bisection on the key with ballots)
-  float tmax = v[0];
-#pragma unroll
-  for (int e = 1; e < EPT; ++e) tmax = fmaxf(tmax, v[e]);
-  unsigned int tw = 0u;
-  if (md.need_list) {
-    const unsigned int k = f2key(tmax);
-#pragma unroll 4
-    for (int b = 31; b >= 0; --b) {
-      const unsigned int c = tw | (1u << b);
-      if (__popcll(__ballot(k >= c)) >= LIST / WAVES) tw = c;
-    }
-  }
-  {
-    const float wm = wave_max(tmax);
-    if (lane == 0) {
-      sh.rf[wid] = wm;
-      sh.rint[wid] = static_cast<int>(tw);
-    }
-  }
-  __syncthreads();  // B1
-  float zmax = sh.rf[0];
-#pragma unroll
-  for (int w2 = 1; w2 < WAVES; ++w2) zmax = fmaxf(zmax, sh.rf[w2]);
-
-  // ---- lowest index holding the max: only threads that hold it look.  Entries
-  // at or past `end` read as -inf and come after the thread's valid entries.
-  int targ = INT_MAX;
-  if (tmax == zmax) {
-#pragma unroll
-    for (int e = EPT - 1; e >= 0; --e)
-      if (v[e] == zmax && MLXF_IDX(e) < end) targ = MLXF_IDX(e);
-  }
-
-  // ---- log-sum-exp partial
-  if (md.need_lse) {
-    float t = 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e)
-      if (MLXF_IDX(e) < end) t += wexp(v[e], zmax);
-    const double ws = wave_sum(static_cast<double>(t));
-    if (lane == 0) sh.rd[wid] = ws;
-  }
-
-  // ---- best-64 survivors.  theta, the smallest wave threshold, is reached by
-  // at least 64 elements (16 thread maxima per wave), so the slice's best 64
-  // all reach it.  Survivors are appended in LDS with one atomic per thread.
-  if (md.need_list) {
-    unsigned int tk = static_cast<unsigned int>(sh.rint[0]);
-#pragma unroll
-    for (int w2 = 1; w2 < WAVES; ++w2) tk = min(tk, static_cast<unsigned int>(sh.rint[w2]));
-    const float thv = key2f(tk < KEY_NEG_INF ? KEY_NEG_INF : tk);
-    if (tmax >= thv) {
-      int mine = 0;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) mine += (v[e] >= thv && MLXF_IDX(e) < end) ? 1 : 0;
-      if (mine > 0) {
-        int pos = static_cast<int>(atomicAdd(&sh.ncand, static_cast<unsigned int>(mine)));
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) {
-          const int i = MLXF_IDX(e);
-          if (v[e] >= thv && i < end) {
-            if (pos < CAND_LDS) {
-              r0.surv[pos].v = v[e];
-              r0.surv[pos].i = i;
-            }
-            ++pos;
+          for (int q = 0; q < NB / 64; ++q) {
+            const int b = lane + 64 * q;
+            part[j] += b < bstar ? ld_dev(a.hmass + ob + b) : 0ull;
           }
         }
       }
-    }
-  }
-
-  // ---- temperature-only / top-p: slice mass w = exp(z' - max z') and, for
-  // top-p, the exact (2^-42 units) mass histogram of z' keys with the range of
-  // occupied bins
-  const float mps = md.sampling ? fz<DT>(zmax, md.Tr) : 0.0f;  // the slice's weight reference
-  if (md.kind == KIND_TEMP || md.kind == KIND_TOPP) {
-    const bool hist = md.kind == KIND_TOPP;
-    double t = 0.0;
-    int bl = NBIN, bh = -1;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      if (MLXF_IDX(e) < end) {
-        const float zp = fz<DT>(v[e], md.Tr);
-        const float w = wexp(zp, mps);
-        t += static_cast<double>(w);
-        if (hist) {
-          const int b = static_cast<int>(f2key(zp) >> 21);
-          bl = min(bl, b);
-          bh = max(bh, b);
-          const unsigned long long q = quant(w);
-          if (q) atomicAdd(&r1.hist[b], q);
+      for (int j = 0; j < 4; ++j) {
+        const int t = t0 + j;
+        const unsigned long long ps = wave_sum(part[j]);
+        if (lane == 0 && t < S) {
+          if (mass) {
+            const unsigned long long ab = ld_dev(a.above + static_cast<size_t>(r) * S + t) + ps;
+            st_dev(a.above + static_cast<size_t>(r) * S + t, ab);
+            sh.kept[t] = ab;
+          }
+          sh.tcnt[t] = ld_dev32(a.hcnt + o0 + static_cast<size_t>(t) * NB + bstar);
         }
       }
     }
-    const double ws = wave_sum(t);
-    if (hist) {
-      bl = wave_min(bl);
-      bh = wave_max(bh);
-    }
-    if (lane == 0) {
-      sh.rd2[wid] = ws;
-      sh.bmin[wid] = bl;
-      sh.bmax[wid] = bh;
-    }
-  } else if (md.kind == KIND_KHIST) {
-    int bl = CNT_BINS, bh = -1;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      if (MLXF_IDX(e) < end) {
-        const int b = static_cast<int>(f2key(v[e]) >> 20);
-        bl = min(bl, b);
-        bh = max(bh, b);
-        atomicAdd(&r1.cnt[b], 1u);
-      }
-    }
-    bl = wave_min(bl);
-    bh = wave_max(bh);
-    if (lane == 0) {
-      sh.bmin[wid] = bl;
-      sh.bmax[wid] = bh;
-    }
-  }
-  {
-    const int wa = wave_min(targ);
-    if (lane == 0) sh.ri[wid] = wa;
-  }
-  __syncthreads();  // B2
-  int zarg = sh.ri[0];
-#pragma unroll
-  for (int w2 = 1; w2 < WAVES; ++w2) zarg = min(zarg, sh.ri[w2]);
-  double lse_s = 0.0, msum = 0.0;
-  if (md.need_lse) {
-    lse_s = sh.rd[0];
-#pragma unroll
-    for (int w2 = 1; w2 < WAVES; ++w2) lse_s += sh.rd[w2];
-  }
-  if (md.kind == KIND_TEMP || md.kind == KIND_TOPP) {
-    msum = sh.rd2[0];
-#pragma unroll
-    for (int w2 = 1; w2 < WAVES; ++w2) msum += sh.rd2[w2];
-  }
-
-  // ---- best 64 of the slice from the survivors
-  if (md.need_list) {
-    int ntot = static_cast<int>(sh.ncand);
-    if (ntot > CAND_LDS) {
-      // Heavy ties at theta: the exact (value desc, index asc) 64th best thread
-      // maximum instead, which at most 64 * EPT elements reach.
-      int tbi = INT_MAX;
-#pragma unroll
-      for (int e = EPT - 1; e >= 0; --e)
-        if (v[e] == tmax && MLXF_IDX(e) < end) tbi = MLXF_IDX(e);
-      float lv = tmax;
-      int li = tbi;
-      wave_sort(lv, li);
-      tree_merge(lv, li, sh.lists, WAVES);
-      if (tid == LIST - 1) {
-        sh.thv = lv;
-        sh.thi = li;
-      }
-      __syncthreads();
-      const float tv = sh.thv;
-      const int ti = sh.thi;
-      int mine = 0;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && !better(tv, ti, v[e], MLXF_IDX(e))) ? 1 : 0;
-      int pos = block_excl_scan<int>(mine, sh.rint, &ntot);
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const int i = MLXF_IDX(e);
-        if (i < end && !better(tv, ti, v[e], i)) {
-          r0.surv[pos].v = v[e];
-          r0.surv[pos].i = i;
-          ++pos;
+    // key range [klo, khi] of the chosen bin (wave 0)
+    if (wid == 0) {
+      unsigned int klo, khi;
+      if (pl.flags & FL_VGRID) {
+        auto vb = [&](unsigned int k) { return vbin_x(wlog2(kval<DT>(k), nc), pl.R2); };
+        klo = wave_search(klo_all, khi_all, [&](unsigned int k) { return vb(k) <= bstar; });
+        if (bstar == 0) {
+          khi = khi_all;
+        } else {
+          const unsigned int nx = wave_search(klo_all, khi_all, [&](unsigned int k) { return vb(k) <= bstar - 1; });
+          khi = nx > klo ? nx - 1u : klo;
         }
-      }
-      __syncthreads();
-    }
-    // 64-entry chunks: wave w sorts chunks w, w + WAVES, ... into its own list
-    const int nch = (ntot + LIST - 1) / LIST;
-    float sv = -INFINITY;
-    int si = INT_MAX;
-    for (int ch = wid; ch < nch; ch += WAVES) {
-      const int c = ch * LIST + lane;
-      float cv = -INFINITY;
-      int ci = INT_MAX;
-      if (c < ntot) {
-        cv = r0.surv[c].v;
-        ci = r0.surv[c].i;
-      }
-      wave_sort(cv, ci);
-      wave_list_merge(sv, si, cv, ci);
-    }
-    tree_merge(sv, si, sh.lists, nch < WAVES ? nch : WAVES);
-    if (wid == 0) st_dev(a.list + (static_cast<size_t>(r) * S + s) * LIST + lane, pack_ent(sv, si));
-  }
-
-  unsigned int ncand = 0;
-  if (md.kind == KIND_TOPP) {
-    // only the occupied bins are stored; the range goes with the slice record
-    int bl = sh.bmin[0], bh = sh.bmax[0];
-#pragma unroll
-    for (int w2 = 1; w2 < WAVES; ++w2) {
-      bl = min(bl, sh.bmin[w2]);
-      bh = max(bh, sh.bmax[w2]);
-    }
-    const size_t off = (static_cast<size_t>(r) * S + s) * NBIN;
-    for (int b = bl + tid; b <= bh; b += THREADS) st_dev(a.hist + off + b, r1.hist[b]);
-    ncand = bh < bl ? 0xffffu : static_cast<unsigned int>(bl) | (static_cast<unsigned int>(bh) << 16);
-  } else if (md.kind == KIND_KHIST) {
-    // the occupied bins of the count histogram of z keys, as 32-bit counts
-    int bl = sh.bmin[0], bh = sh.bmax[0];
-#pragma unroll
-    for (int w2 = 1; w2 < WAVES; ++w2) {
-      bl = min(bl, sh.bmin[w2]);
-      bh = max(bh, sh.bmax[w2]);
-    }
-    unsigned int* hc = reinterpret_cast<unsigned int*>(a.hist + (static_cast<size_t>(r) * S + s) * NBIN);
-    for (int b = bl + tid; b <= bh; b += THREADS)
-      __hip_atomic_store(hc + b, r1.cnt[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ncand = bh < bl ? 0xffffu : static_cast<unsigned int>(bl) | (static_cast<unsigned int>(bh) << 16);
-  }
-#undef MLXF_IDX
-
-  if (tid == 0) {
-    unsigned long long* rp = reinterpret_cast<unsigned long long*>(a.rec + (r * S + s));
-    st_dev(rp + 0, pack2(__float_as_uint(zmax), static_cast<unsigned int>(zarg)));
-    st_dev(rp + 1, pack2(__float_as_uint(mps), ncand));
-    st_dev(rp + 2, static_cast<unsigned long long>(__double_as_longlong(lse_s)));
-    st_dev(rp + 3, static_cast<unsigned long long>(__double_as_longlong(msum)));
-  }
-
-  // ---- ticket: the last slice of the row finishes it.  Every wave waits for
-  // its device-coherent stores to complete before the ticket is drawn.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0)
-    sh.ticket = __hip_atomic_fetch_add(a.ctr + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (sh.ticket != static_cast<unsigned int>(S - 1)) return false;
-  if (tid == 0) {
-    __hip_atomic_store(a.ctr + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
-    sh.args = a;
-    sh.md = md;
-  }
-  __syncthreads();
-  finish_row<DT, EPT, VECOK>(r, r0, r1, sh);
-  return true;
-}
-
-// Second pass, one item = slice s of a queued row (top-p without top-k): the
-// slice's mass above the bracket (its own histogram's bins above bhi, exact)
-// and the bracket's elements, counted per z' value (value mode) or written out
-// as candidates.  The row's last item resolves the row.
-template <int DT, int EPT, bool VECOK>
-__device__ __forceinline__ void second_pass(const Args& a, int r, int s, Region0& r0, Region1& r1, Small& sh) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int S = a.S;
-  const Mode md = decode<DT>(a, r);
-  const void* row = row_ptr<DT>(a, r);
-  const unsigned long long* pl = a.plan + static_cast<size_t>(r) * PLAN_WORDS;
-  const unsigned long long wk = ld_dev(pl + PL_KEYS), wmode = ld_dev(pl + PL_MODE);
-  const unsigned int klo = static_cast<unsigned int>(wk), khi = static_cast<unsigned int>(wk >> 32);
-  const bool has_hi = (wmode & 1ull) != 0;
-  const bool khist = ((wmode >> 12) & 1ull) != 0;
-  const int bhi = static_cast<int>((wmode >> 1) & 0x7ffull);
-  const int nv = static_cast<int>((wmode >> 32) & 0x7ffull);
-  const unsigned int vbase = static_cast<unsigned int>(wmode >> 43);
-  const unsigned long long w1 =
-      ld_dev(reinterpret_cast<const unsigned long long*>(a.rec + (r * S + s)) + 1);
-  const unsigned int rg = static_cast<unsigned int>(w1 >> 32);
-  const int rlo = static_cast<int>(rg & 0xffffu), rhi = static_cast<int>(rg >> 16);
-  // mass above the bracket (top-p rows): this slice's histogram bins above bhi
-  unsigned long long ab = 0;
-  const unsigned long long* hs = a.hist + (static_cast<size_t>(r) * S + s) * NBIN;
-  if (!khist)
-    for (int b = max(bhi + 1, rlo) + tid; b <= rhi; b += THREADS) ab += ld_dev(hs + b);
-  if (nv > 0)
-    for (int v = tid; v < nv; v += THREADS) r0.vcnt[v] = 0u;
-  if (tid == 0) sh.ncand = 0u;
-  ab = block_sum<unsigned long long>(ab, sh.ru);  // (its barriers also publish the clears)
-  // the bracket's elements
-  const int beg = s * a.L, end = min(a.V, beg + a.L);
-  constexpr int NIT = EPT / VEC;
-  uint2* dst = a.cand + (static_cast<size_t>(r) * S + s) * a.L;
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    float z[VEC];
-    const int i0 = beg + it * CHUNK + tid * VEC;
-    load8<DT, VECOK>(row, i0, end, z);
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const int i = i0 + j;
-      const unsigned int zk = f2key(z[j]);
-      const bool inr = i < end && zk >= klo && (!has_hi || zk < khi);
-      unsigned int zpk = 0;
-      if (inr) zpk = f2key(fz<DT>(z[j], md.Tr));
-      if (nv > 0) {
-        if (inr) atomicAdd(&r0.vcnt[(zpk >> vshift<DT>()) - vbase], 1u);
       } else {
-        const unsigned long long bal = __ballot(inr);
-        if (bal) {
-          unsigned int basepos = 0;
-          if (lane == 0) basepos = atomicAdd(&sh.ncand, static_cast<unsigned int>(__popcll(bal)));
-          basepos = rdl(basepos, 0);
-          if (inr) {
-            const unsigned int pos =
-                basepos + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(bal >> 32),
-                                                    __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(bal), 0u));
-            st_dev(dst + pos, make_uint2(zpk, static_cast<unsigned int>(i)));
-          }
-        }
+        const unsigned long long lo64 =
+            static_cast<unsigned long long>(pl.kb) + (static_cast<unsigned long long>(NB - 1 - bstar) << pl.sh);
+        const unsigned long long hi64 = lo64 + (1ull << pl.sh) - 1ull;
+        klo = static_cast<unsigned int>(lo64);
+        khi = static_cast<unsigned int>(hi64 < khi_all ? hi64 : khi_all);
+      }
+      if (klo < pl.fkey) klo = pl.fkey;
+      if (mass) {
+        // elements whose mass quantises to zero never count: start the bracket
+        // at the first key with a positive mass
+        const unsigned int kq = wave_search(klo_all, khi_all, [&](unsigned int k) {
+          return q40(wfun(kval<DT>(k), Mp, nc, minf)) > 0;
+        });
+        if (klo < kq) klo = kq;
+      }
+      if (khi < klo) khi = klo;
+      if (lane == 0) {
+        sh.sel[6] = static_cast<int>(klo);
+        sh.sel[7] = static_cast<int>(khi);
       }
     }
+    __syncthreads();
+    const unsigned long long abv = sh.selu[2];
+    const unsigned int cabv = static_cast<unsigned int>(sh.selu[3]);
+    const unsigned int cstar = static_cast<unsigned int>(sh.selu[4]);
+    const unsigned int klo = static_cast<unsigned int>(sh.sel[6]);
+    const unsigned int khi = static_cast<unsigned int>(sh.sel[7]);
+    __syncthreads();
+    const bool exact = klo == khi;
+    const unsigned long long rest = pl.target > abv ? pl.target - abv : 1ull;  // still to cover in the bin
+    if (!mass) {
+      const unsigned int nge = pl.cabove + cabv + cstar;  // participants with key >= klo
+      if (nge <= CAP) {
+        // gather everything from the bin's low edge up: the k-th largest, the
+        // nucleus and the draw are then decided on the candidates
+        pl.phase = PH_GATHER;
+        pl.flags |= FL_GALL;
+        set_bracket<DT>(pl, klo, khi_all, md.Tr, sh);
+        pl.target = static_cast<unsigned long long>(md.kk);
+      } else if (exact) {
+        // the k-th largest z' is klo; every tie is kept
+        pl.fkey = klo;
+        pl.cabove = 0u;
+        set_bracket<DT>(pl, klo, khi_all, md.Tr, sh);
+        pl.target = 0;
+        if (pl.flags & FL_TOPP) {
+          pl.phase = PH_MASS;
+          pl.flags &= ~static_cast<unsigned int>(FL_TOPP);
+          plan_level1<DT>(pl, fminf(-wlog2(kval<DT>(klo), nc), MASS_LOG2_SPAN));
+          for (int t = tid; t < S; t += THREADS) st_dev(a.above + static_cast<size_t>(r) * S + t, 0ull);
+        } else {
+          pl.phase = PH_DRAWSUM;
+        }
+      } else {
+        set_digits(pl, klo, khi);
+        pl.cabove += cabv;
+        pl.target = rest;
+        set_bracket<DT>(pl, klo, khi, md.Tr, sh);
+      }
+    } else {
+      if (exact) {
+        // cutoff value klo: its first t ties (lowest indices) are kept
+        const unsigned long long wt = q40(wfun(kval<DT>(klo), Mp, nc, minf));
+        const unsigned int t = ties_kept(rest, wt, cstar);
+        if (tid == 0) {
+          unsigned int before = 0;
+          for (int s2 = 0; s2 < S; ++s2) {
+            const unsigned int c = sh.tcnt[s2];
+            const unsigned int kt = t > before ? (t - before < c ? t - before : c) : 0u;
+            before += c;
+            sh.tcnt[s2] = kt;
+            sh.kept[s2] += static_cast<unsigned long long>(kt) * wt;
+          }
+        }
+        __syncthreads();
+        id = draw<DT, EPT, VECOK>(a, r, md, Mp, klo, false, sh);
+        done = true;
+      } else if (cstar <= CAP) {
+        pl.phase = PH_GATHER;
+        pl.target = rest;
+        set_bracket<DT>(pl, klo, khi, md.Tr, sh);
+      } else {
+        set_digits(pl, klo, khi);
+        pl.target = rest;
+        set_bracket<DT>(pl, klo, khi, md.Tr, sh);
+      }
+    }
+  } else if (pl.phase == PH_DRAWSUM) {
+    for (int t = tid; t < S; t += THREADS) sh.kept[t] = ld_dev(a.dsum + static_cast<size_t>(r) * S + t);
+    __syncthreads();
+    id = draw<DT, EPT, VECOK>(a, r, md, Mp, pl.fkey, true, sh);
+    done = true;
+  } else if (pl.phase == PH_GATHER) {
+    if (tid == 0) {
+      const unsigned int n = ld_dev32(a.ncand + r);
+      sh.ncand = n < CAP ? n : CAP;
+      st_dev32(a.ncand + r, 0u);
+    }
+    __syncthreads();
+    const int n = static_cast<int>(sh.ncand);
+    for (int c = tid; c < n; c += THREADS) sh.cand[c] = ld_dev(a.cand + static_cast<size_t>(r) * CAP + c);
+    __syncthreads();
+    unsigned long long bef;
+    unsigned int g;
+    if (pl.flags & FL_GALL) {
+      // k-th largest z' (with multiplicity), then the nucleus inside the top k
+      auto all = [](unsigned long long) { return true; };
+      const unsigned int tk = cselect<DT, true, false>(n, all, Mp, pl.target, false, sh, &bef, &g);
+      unsigned int tau = tk;
+      unsigned int cut = 0xffffffffu;  // last kept index among the ties at tau
+      if (pl.flags & FL_TOPP) {
+        auto ink = [tk](unsigned long long e) { return static_cast<unsigned int>(e) >= tk; };
+        const unsigned long long Wk = cmass<DT>(n, ink, Mp, sh);
+        unsigned long long PW =
+            static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
+        if (PW < 1) PW = 1;
+        unsigned long long pgt;
+        tau = cselect<DT, true, true>(n, ink, Mp, PW, false, sh, &pgt, &g);
+        const unsigned long long wt = q40(wfun(kval<DT>(tau), Mp, nc, minf));
+        const unsigned int t = ties_kept(PW > pgt ? PW - pgt : 0ull, wt, g);
+        if (t < g) {
+          auto eq = [tau](unsigned long long e) { return static_cast<unsigned int>(e) == tau; };
+          cut = cselect<DT, false, false>(n, eq, Mp, t, false, sh, &bef, &g);
+        }
+      }
+      auto kept = [tau, cut](unsigned long long e) {
+        const unsigned int k = static_cast<unsigned int>(e);
+        return k > tau || (k == tau && static_cast<unsigned int>(e >> 32) <= cut);
+      };
+      const unsigned long long Wf = cmass<DT>(n, kept, Mp, sh);
+      unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(Wf));
+      if (Wf == 0)
+        Tu = 0;
+      else if (Tu >= Wf)
+        Tu = Wf - 1;
+      id = static_cast<int>(cselect<DT, false, true>(n, kept, Mp, Tu, true, sh, &bef, &g));
+      done = true;
+    } else {
+      // nucleus cutoff inside the bin: the remaining target over the candidates
+      auto all = [](unsigned long long) { return true; };
+      unsigned long long pgt;
+      const unsigned int tau = cselect<DT, true, true>(n, all, Mp, pl.target, false, sh, &pgt, &g);
+      const unsigned long long wt = q40(wfun(kval<DT>(tau), Mp, nc, minf));
+      const unsigned int t = ties_kept(pl.target > pgt ? pl.target - pgt : 0ull, wt, g);
+      unsigned int cut = 0xffffffffu;
+      if (t < g) {
+        auto eq = [tau](unsigned long long e) { return static_cast<unsigned int>(e) == tau; };
+        cut = cselect<DT, false, false>(n, eq, Mp, t, false, sh, &bef, &g);
+      }
+      // per-slice kept mass: above the bin, plus the kept candidates
+      for (int t2 = tid; t2 < S; t2 += THREADS) {
+        sh.kept[t2] = ld_dev(a.above + static_cast<size_t>(r) * S + t2);
+        sh.tcnt[t2] = 0u;
+      }
+      __syncthreads();
+      for (int c = tid; c < n; c += THREADS) {
+        const unsigned long long e = sh.cand[c];
+        const unsigned int k = static_cast<unsigned int>(e);
+        const unsigned int i = static_cast<unsigned int>(e >> 32);
+        const int st = static_cast<int>(i) / a.L;
+        if (k > tau || (k == tau && i <= cut)) {
+          atomicAdd(&sh.kept[st], q40(wfun(kval<DT>(k), Mp, nc, minf)));
+          if (k == tau) atomicAdd(&sh.tcnt[st], 1u);
+        }
+      }
+      __syncthreads();
+      id = draw<DT, EPT, VECOK>(a, r, md, Mp, tau, false, sh);
+      done = true;
+    }
   }
-  __syncthreads();
-  if (nv > 0) {
-    for (int w = tid; w < nv / 2; w += THREADS)
-      st_dev(reinterpret_cast<unsigned long long*>(dst) + w, pack2(r0.vcnt[2 * w], r0.vcnt[2 * w + 1]));
-  } else if (tid == 0) {
-    __hip_atomic_store(a.ncand2 + (r * S + s), sh.ncand, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (done) pl.phase = PH_DONE;
+  if (tid == 0) {
+    if (done) write_out<DT>(a, r, id, pl.lse, md.want_lp);
+    plan_store(a, r, pl);
+    sh.sl.pw[RS_PHASE] = pack2(pl.phase, pl.flags);
+    sh.sl.pw[RS_ZB] = pack2(pl.zlo, pl.zhi);
+    sh.sl.pw[RS_DIG] = pack2(pl.kb, pl.sh);
+    sh.sl.pw[RS_AUX] = pack2(pl.cabove, pl.fkey);
+    sh.sl.pw[RS_GRID] = pack2(__float_as_uint(pl.Mp), __float_as_uint(pl.R2));
+    sh.sl.pw[RS_TGT] = pl.target;
   }
-  if (tid == 0)
-    st_dev(a.above + (r * S + s),
-           static_cast<unsigned long long>(__double_as_longlong(static_cast<double>(ab) * QUNIT)));
-  // ticket: the row's last item resolves the row
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (tid == 0)
-    sh.ticket = __hip_atomic_fetch_add(a.done2 + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (sh.ticket != static_cast<unsigned int>(S - 1)) return;
-  if (tid == 0) {
-    __hip_atomic_store(a.done2 + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
-    sh.args = a;
-    sh.md = md;
-  }
-  if (tid < PLAN_WORDS) sh.plan[tid] = ld_dev(pl + tid);
-  __syncthreads();
-  resolve_row<DT, EPT, VECOK>(r, r0, r1, sh);
 }
 
-// Helpers: take second-pass items of any queued row, polling until every row is
-// finished or the idle bound runs out.  No row depends on helpers (see
-// drain_own); the workgroup that completes a row's last item resolves it.
-// Take the items of one row until none is left.  A row's last slice does this
-// for its own row after queueing it, so every item is taken by a running
-// workgroup whatever the helpers do.
+// Refine stage `stage` (0-based), one workgroup per slice of each row on the
+// stage's list.  The list and the plans come from the previous kernel.
 template <int DT, int EPT, bool VECOK>
-__device__ __forceinline__ void drain_own(const Args& a, int own_row, Region0& r0, Region1& r1, Small& sh) {
+__global__ __launch_bounds__(THREADS) void k_scan(Args a, int stage) {
+  __shared__ SLds sh;
   const int tid = threadIdx.x;
-  for (;;) {
-    __syncthreads();
-    if (tid == 0)
-      sh.qitem = static_cast<int>(stamped_take(a.next2 + own_row, a.epoch, static_cast<unsigned int>(a.S)));
-    __syncthreads();
-    const int qi = sh.qitem;
-    if (qi >= a.S) break;
-    second_pass<DT, EPT, VECOK>(a, own_row, qi, r0, r1, sh);
-  }
-}
-
-template <int DT, int EPT, bool VECOK>
-__device__ __forceinline__ void drain(const Args& a, Region0& r0, Region1& r1, Small& sh) {
-  constexpr bool wait = true;
-  const int tid = threadIdx.x;
-  const int S = a.S;
-  unsigned int cursor = 0;
-  int polls = 0;
-  for (;;) {
-    __syncthreads();
-    if (tid == 0) {
-      sh.rdone = stamped_get(a.gl + GL_ROWS, a.epoch);
-      sh.qn = stamped_get(a.gl + GL_QRES, a.epoch);
-      sh.qrow = static_cast<int>(stamped_get(a.gl + GL_HEAD, a.epoch));
-    }
-    __syncthreads();
-    const unsigned int qn = sh.qn, rdone = sh.rdone;
-    cursor = max(cursor, static_cast<unsigned int>(sh.qrow));
-    bool worked = false;
-    while (cursor < qn) {
-      __syncthreads();
-      if (tid == 0) {
-        // a reserved slot is written right after its reservation
-        unsigned int e = stamped_get(a.queue + cursor, a.epoch);
-        for (int spin = 0; e == 0u && spin < (1 << 20); ++spin) {
-          __builtin_amdgcn_s_sleep(2);
-          e = stamped_get(a.queue + cursor, a.epoch);
-        }
-        int item = S;
-        if (e != 0u) item = static_cast<int>(stamped_take(a.next2 + (e - 1u), a.epoch, static_cast<unsigned int>(S)));
-        sh.qrow = static_cast<int>(e) - 1;
-        sh.qitem = item;
-      }
-      __syncthreads();
-      const int qr = sh.qrow, qi = sh.qitem;
-      if (qr < 0 || qi >= S) {
-        // the row has no items left: move the shared head past it if it points here
-        if (tid == 0) {
-          unsigned long long w = (static_cast<unsigned long long>(a.epoch) << 32) | cursor;
-          __hip_atomic_compare_exchange_strong(a.gl + GL_HEAD, &w, w + 1ull, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-          if (cursor == 0u) {  // a head never stamped in this call reads as 0
-            unsigned long long z = ld_dev(a.gl + GL_HEAD);
-            if (static_cast<unsigned int>(z >> 32) != a.epoch)
-              __hip_atomic_compare_exchange_strong(a.gl + GL_HEAD, &z, w + 1ull, __ATOMIC_RELAXED,
-                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-        ++cursor;
-        continue;
-      }
-      second_pass<DT, EPT, VECOK>(a, qr, qi, r0, r1, sh);
-      worked = true;
-    }
-    if (!wait || rdone >= static_cast<unsigned int>(a.B)) break;
-    if (worked) {
-      polls = 0;
-    } else {
-      if (++polls > IDLE_LIMIT) break;
-      // back off: idle helpers poll the shared counters less often
-      if (polls < 8)
-        __builtin_amdgcn_s_sleep(8);
-      else
-        __builtin_amdgcn_s_sleep(64);
-    }
-  }
-}
-
-// One launch: the first B*S workgroups run the first pass (row-major); those
-// that finish a row with a second pass then take that row's items.  The remaining
-// workgroups are helpers that only take second-pass items, and leave at once
-// unless some row of this call flagged a second pass.
-template <int DT, int EPT, bool VECOK>
-__global__ __launch_bounds__(THREADS, 2) void k_sample(Args a) {
-  __shared__ Region0 r0;
-  __shared__ Region1 r1;
-  __shared__ Small sh;
   const int bid = static_cast<int>(blockIdx.x);
-  const int n1 = a.B * a.S;
-  if (bid < n1) {
-    const int r = bid / a.S;
-    if (first_pass<DT, EPT, VECOK>(a, r, bid - r * a.S, r0, r1, sh)) {
-      const int kind = sh.md.kind;
-      if (kind == KIND_TOPP && sh.md.pr > 0.0f)
-        drain_own<DT, EPT, VECOK>(a, r, r0, r1, sh);
-      else if (kind == KIND_KHIST)
-        drain_own<DT, EPT, VECOK>(a, r, r0, r1, sh);
+  const int S = a.S;
+  // the list two stages back has been read by its decide kernel: clear its count
+  if (stage >= 1 && bid == 0 && tid == 0) a.actcnt[stage - 1] = 0u;
+  const unsigned int n = a.actcnt[stage];
+  if (static_cast<unsigned int>(bid) >= n * static_cast<unsigned int>(S)) return;
+  const int r = static_cast<int>(a.actlist[static_cast<size_t>(stage) * a.B + bid / S]);
+  const int s = bid % S;
+  if (tid < RS_WORDS) sh.pw[tid] = a.rowst[static_cast<size_t>(r) * RS_WORDS + tid];
+  __syncthreads();
+  slice_stage<DT, EPT, VECOK>(a, r, s, sh);
+}
+
+// Refine stage `stage`, one workgroup per row on the stage's list: decide, and
+// put the row on the next stage's list if it is still open.  The last stage
+// finishes every row itself: this workgroup runs the remaining levels over the
+// row's slices.  Each level narrows the bracket or advances the phase, so the
+// loop ends; its bound is a guard.
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS) void k_decide(Args a, int stage) {
+  __shared__ RLds sh;
+  const int tid = threadIdx.x;
+  const int bid = static_cast<int>(blockIdx.x);
+  const int S = a.S;
+  const unsigned int n = a.actcnt[stage];
+  if (static_cast<unsigned int>(bid) >= n) return;
+  const int r = static_cast<int>(a.actlist[static_cast<size_t>(stage) * a.B + bid]);
+  if (tid < RS_WORDS) sh.sl.pw[tid] = a.rowst[static_cast<size_t>(r) * RS_WORDS + tid];
+  __syncthreads();
+  finish_stage<DT, EPT, VECOK>(a, r, sh);
+  if (static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) == PH_DONE) return;
+  if (stage + 1 < NSTAGE) {
+    if (tid == 0) enlist(a, stage + 1, r);
+    return;
+  }
+  for (int it = 0; it < SERIAL_MAX && static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) != PH_DONE; ++it) {
+    for (int s2 = 0; s2 < S; ++s2) {
+      slice_stage<DT, EPT, VECOK>(a, r, s2, sh.sl);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
     }
-  } else {
-    if (threadIdx.x == 0) sh.qn = stamped_get(a.gl + GL_NEED, a.epoch);
-    __syncthreads();
-    if (sh.qn != 0u) drain<DT, EPT, VECOK>(a, r0, r1, sh);
+    finish_stage<DT, EPT, VECOK>(a, r, sh);
   }
 }
 
@@ -1956,23 +1529,24 @@ __global__ void k_zero(unsigned int* p, size_t n) {
 
 struct Layout {
   int S, L, EPT;
-  size_t off_ctr, off_done2, off_next2, off_gl, off_queue, off_rec, off_list, off_hist, off_cand,
-      off_plan, off_above, off_ncand2, total;
+  size_t off_ncand, off_actcnt, off_actlist, off_rec, off_list, off_rowst, off_hcnt, off_hmass, off_above,
+      off_dsum, off_cand, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-// the zero-initialised head of the workspace: per-row tickets (two arrays of
-// 65536 32-bit counters), item counters and queue slots (65536 64-bit words
-// each) and the call-wide counters
+// The zero-initialised head of the workspace, at offsets that do not depend on
+// the shape (so one workspace serves calls of every shape): per-row gathered-
+// candidate counters (65536 32-bit words) and the stage-list counts.  Every
+// call leaves them ready for the next: a decide kernel clears the candidate
+// counters it read, and each stage-list count is cleared by the scan kernel
+// that runs once its list has been read.
 constexpr size_t ROWS_MAX = 65536;
-constexpr size_t CTR_BYTES_MAX =
-    2 * ROWS_MAX * sizeof(unsigned int) + 2 * ROWS_MAX * sizeof(unsigned long long) +
-    GL_WORDS * sizeof(unsigned long long);
+constexpr size_t CTR_BYTES_MAX = ROWS_MAX * sizeof(unsigned int) + 256;
 
-// EPT: the largest of {32, 16, 8} that still gives at least one workgroup
-// per CU (256) with at most MAX_S slices per row; otherwise the smallest EPT
-// with S <= MAX_S (short batches: as many slices as allowed).
+// EPT: the largest of {32, 16, 8} that still gives at least one workgroup per
+// CU (256) with at most MAX_S slices per row; otherwise the smallest EPT with
+// S <= MAX_S.
 Layout make_layout(int B, int V, int K_max) {
   (void)K_max;
   Layout l;
@@ -1998,44 +1572,30 @@ Layout make_layout(int B, int V, int K_max) {
   l.L = THREADS * ept;
   l.S = (V + l.L - 1) / l.L;
   const size_t BS = static_cast<size_t>(B) * l.S;
-  size_t o = 0;
-  // First, at offsets that do not depend on the shape: the three per-row
-  // counter arrays, which must read zero before every call (the workspace is
-  // zeroed once; every call leaves them at zero).  Fixed offsets keep that true
-  // when one workspace serves calls of different shapes.
   const size_t nb = B > 0 ? static_cast<size_t>(B) : 1;
-  l.off_ctr = 0;
-  l.off_done2 = ROWS_MAX * sizeof(unsigned int);
-  l.off_next2 = 2 * ROWS_MAX * sizeof(unsigned int);
-  l.off_queue = l.off_next2 + ROWS_MAX * sizeof(unsigned long long);
-  l.off_gl = l.off_queue + ROWS_MAX * sizeof(unsigned long long);
-  o = align256(CTR_BYTES_MAX);
+  l.off_ncand = 0;
+  l.off_actcnt = ROWS_MAX * sizeof(unsigned int);
+  size_t o = align256(CTR_BYTES_MAX);
+  l.off_actlist = o;
+  o = align256(o + sizeof(unsigned int) * NSTAGE * nb);
   l.off_rec = o;
-  o = align256(o + sizeof(SliceRec) * BS);
+  o = align256(o + 4 * sizeof(unsigned long long) * BS);
   l.off_list = o;
   o = align256(o + sizeof(unsigned long long) * BS * LIST);
-  l.off_hist = o;
-  o = align256(o + sizeof(unsigned long long) * BS * NBIN);
-  l.off_cand = o;
-  o = align256(o + sizeof(uint2) * BS * l.L);
-  l.off_plan = o;
-  o = align256(o + sizeof(unsigned long long) * PLAN_WORDS * nb);
+  l.off_rowst = o;
+  o = align256(o + sizeof(unsigned long long) * RS_WORDS * nb);
+  l.off_hcnt = o;
+  o = align256(o + sizeof(unsigned int) * BS * NB);
+  l.off_hmass = o;
+  o = align256(o + sizeof(unsigned long long) * BS * NB);
   l.off_above = o;
-  o = align256(o + sizeof(double) * BS);
-  l.off_ncand2 = o;
-  o = align256(o + sizeof(unsigned int) * BS);
+  o = align256(o + sizeof(unsigned long long) * BS);
+  l.off_dsum = o;
+  o = align256(o + sizeof(unsigned long long) * BS);
+  l.off_cand = o;
+  o = align256(o + sizeof(unsigned long long) * nb * CAP);
   l.total = o;
   return l;
-}
-
-// A fresh stamp per call (never 0, which a zeroed workspace holds).
-unsigned int next_epoch() {
-  static std::atomic<unsigned int> counter{0};
-  unsigned int e;
-  do {
-    e = counter.fetch_add(1u, std::memory_order_relaxed) + 1u;
-  } while (e == 0u);
-  return e;
 }
 
 void set_err(char** err, const std::string& msg) {
@@ -2065,17 +1625,19 @@ int check_shape(int B, int V, int K_max, int dtype, char** err) {
   return MLXF_OK;
 }
 
-// Helper workgroups (at most 256) are added when some row can have a second
-// pass (top-p without top-k, or top-k with k > 63).
-template <int DT, int EPT>
-hipError_t launch_ept(Args a, bool vecok, hipStream_t st) {
-  const int n1 = a.B * a.S;
-  a.helpers = (a.T != nullptr && (a.p != nullptr || a.k != nullptr)) ? (n1 < 256 ? n1 : 256) : 0;
-  const dim3 grid(n1 + a.helpers);
-  if (vecok)
-    hipLaunchKernelGGL((k_sample<DT, EPT, true>), grid, dim3(THREADS), 0, st, a);
-  else
-    hipLaunchKernelGGL((k_sample<DT, EPT, false>), grid, dim3(THREADS), 0, st, a);
+// Stage 0 (scan, decide), then NSTAGE refine stages (scan, decide) when any row
+// may sample.
+template <int DT, int EPT, bool VECOK>
+hipError_t launch_ept(const Args& a, hipStream_t st) {
+  const dim3 slices(static_cast<unsigned int>(a.B * a.S)), rows(static_cast<unsigned int>(a.B));
+  hipLaunchKernelGGL((k_scan1<DT, EPT, VECOK>), slices, dim3(THREADS), 0, st, a);
+  hipLaunchKernelGGL((k_decide1<DT>), rows, dim3(THREADS), 0, st, a);
+  if (a.T) {
+    for (int i = 0; i < NSTAGE; ++i) {
+      hipLaunchKernelGGL((k_scan<DT, EPT, VECOK>), slices, dim3(THREADS), 0, st, a, i);
+      hipLaunchKernelGGL((k_decide<DT, EPT, VECOK>), rows, dim3(THREADS), 0, st, a, i);
+    }
+  }
   return hipGetLastError();
 }
 
@@ -2083,11 +1645,11 @@ template <int DT>
 hipError_t launch_dt(const Args& a, int ept, bool vecok, hipStream_t st) {
   switch (ept) {
     case 8:
-      return launch_ept<DT, 8>(a, vecok, st);
+      return vecok ? launch_ept<DT, 8, true>(a, st) : launch_ept<DT, 8, false>(a, st);
     case 16:
-      return launch_ept<DT, 16>(a, vecok, st);
+      return vecok ? launch_ept<DT, 16, true>(a, st) : launch_ept<DT, 16, false>(a, st);
     default:
-      return launch_ept<DT, 32>(a, vecok, st);
+      return vecok ? launch_ept<DT, 32, true>(a, st) : launch_ept<DT, 32, false>(a, st);
   }
 }
 
@@ -2150,19 +1712,17 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
     a.out_lp = d_out_logprobs;
     a.out_top_ids = d_out_top_ids;
     a.out_top_lp = d_out_top_logprobs;
-    a.ctr = reinterpret_cast<unsigned int*>(ws + l.off_ctr);
-    a.done2 = reinterpret_cast<unsigned int*>(ws + l.off_done2);
-    a.next2 = reinterpret_cast<unsigned long long*>(ws + l.off_next2);
-    a.queue = reinterpret_cast<unsigned long long*>(ws + l.off_queue);
-    a.gl = reinterpret_cast<unsigned long long*>(ws + l.off_gl);
-    a.epoch = next_epoch();
-    a.plan = reinterpret_cast<unsigned long long*>(ws + l.off_plan);
-    a.above = reinterpret_cast<double*>(ws + l.off_above);
-    a.ncand2 = reinterpret_cast<unsigned int*>(ws + l.off_ncand2);
-    a.rec = reinterpret_cast<SliceRec*>(ws + l.off_rec);
+    a.ncand = reinterpret_cast<unsigned int*>(ws + l.off_ncand);
+    a.actcnt = reinterpret_cast<unsigned int*>(ws + l.off_actcnt);
+    a.actlist = reinterpret_cast<unsigned int*>(ws + l.off_actlist);
+    a.rec = reinterpret_cast<unsigned long long*>(ws + l.off_rec);
     a.list = reinterpret_cast<unsigned long long*>(ws + l.off_list);
-    a.hist = reinterpret_cast<unsigned long long*>(ws + l.off_hist);
-    a.cand = reinterpret_cast<uint2*>(ws + l.off_cand);
+    a.rowst = reinterpret_cast<unsigned long long*>(ws + l.off_rowst);
+    a.hcnt = reinterpret_cast<unsigned int*>(ws + l.off_hcnt);
+    a.hmass = reinterpret_cast<unsigned long long*>(ws + l.off_hmass);
+    a.above = reinterpret_cast<unsigned long long*>(ws + l.off_above);
+    a.dsum = reinterpret_cast<unsigned long long*>(ws + l.off_dsum);
+    a.cand = reinterpret_cast<unsigned long long*>(ws + l.off_cand);
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e;
     if (dtype == MLXF_DTYPE_F32)
