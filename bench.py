@@ -45,7 +45,7 @@ def log(msg):
 class Step:
     """Pre-allocated device state for one workload; run() issues one mlxf_sample."""
 
-    def __init__(self, wl, torch, lib, rotate=True):
+    def __init__(self, wl, torch, lib, rotate=True, hinted=True):
         import numpy as np
         self.wl, self.torch, self.lib = wl, torch, lib
         dev = torch.device("cuda:0")
@@ -80,6 +80,9 @@ class Step:
                           P(self.ws.data_ptr()), self.ws_bytes, self.stream]
         self.row_bytes = wl.V * wl.elem_size
         self.i = 0
+        # refine stages from the host-side parameters (what a serving loop
+        # knows about its rows); unhinted = the generic mlxf_sample path
+        self.stages = _lib.refine_stages(B, wl.V, self.code, wl.T, wl.k, wl.p) if hinted else 3
 
     def _logits(self):
         p = self.buf[self.i % self.R].data_ptr()
@@ -88,8 +91,9 @@ class Step:
 
     def run(self):
         err = ctypes.c_void_p()
-        rc = self.lib.mlxf_sample(self._logits(), self.code, self.wl.B, self.wl.V, self.wl.V,
-                                  *self.args_tail, ctypes.byref(err))
+        rc = self.lib.mlxf_sample_staged(self._logits(), self.code, self.wl.B, self.wl.V, self.wl.V,
+                                         *self.args_tail[:-1], self.stages, self.args_tail[-1],
+                                         ctypes.byref(err))
         if rc:
             from mlxforge_amd import _lib
             _lib.check(rc, err)
@@ -169,14 +173,16 @@ def main():
         wl = workloads.make(cfg)
         st = Step(wl, torch, lib)
         ms = time_steps(st, torch, warmup, steps)
+        st.stages, stages = 3, st.stages
+        ms_all = time_steps(st, torch, warmup, steps)
         st_hot = Step(wl, torch, lib, rotate=False)
         ms_hot = time_steps(st_hot, torch, warmup, steps)
         del st, st_hot
         torch.cuda.empty_cache()
-        return wl, ms, ms_hot
+        return wl, ms, ms_hot, ms_all, stages
 
     log(f"[bench] config C{args.config}: warmup {args.warmup}, steps {args.steps}")
-    wl, ms, ms_hot = measure(args.config, args.steps, args.warmup)
+    wl, ms, ms_hot, ms_all, stages = measure(args.config, args.steps, args.warmup)
     alg = wl.algorithmic_bytes()
     # one kernel per step: its algorithmic bytes are the step's (logits read
     # once, ids / logprobs / top-K written, per-row parameters read)
@@ -198,6 +204,8 @@ def main():
                    "logits_dtype": wl.dtype, "input_rotation": "cold (>512 MB of copies)"},
         "us_per_step": round(ms * 1e3, 2),
         "us_per_step_hot": round(ms_hot * 1e3, 2),
+        "refine_stages": stages,
+        "us_per_step_all_stages": round(ms_all * 1e3, 2),
         "achieved_GBps_step": round(alg / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "kernel": "k_sample", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -215,9 +223,10 @@ def main():
             if cfg == args.config:
                 continue
             log(f"[bench] extra config C{cfg}")
-            w2, m2, mh2 = measure(cfg, min(args.steps, 100), min(args.warmup, 10))
+            w2, m2, mh2, ma2, st2 = measure(cfg, min(args.steps, 100), min(args.warmup, 10))
             extra[f"C{cfg}"] = {"workload": w2.name, "us_per_step": round(m2 * 1e3, 2),
                                 "us_per_step_hot": round(mh2 * 1e3, 2),
+                                "refine_stages": st2, "us_per_step_all_stages": round(ma2 * 1e3, 2),
                                 "rows_per_s": round(w2.B / (m2 * 1e-3), 1),
                                 "achieved_GBps_step": round(w2.algorithmic_bytes() / (m2 * 1e-3) / 1e9, 1),
                                 "hbm_frac": round(w2.algorithmic_bytes() / (m2 * 1e-3) / 1e9

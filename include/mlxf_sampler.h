@@ -110,6 +110,29 @@ int mlxf_sample(const void* d_logits, int dtype, int B, int V, int64_t row_strid
                 float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
                 int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err);
 
+/* mlxf_sample with the number of refine stages to launch (0..3) given by the
+ * caller.  mlxf_sample launches all three, which any mix of parameters needs;
+ * a caller that knows its rows' parameters on the host (as Worker::sample_rows
+ * does, src/runtime/worker.cpp:453-473) passes
+ * mlxf_sampler_refine_stages(...) instead and skips launches no row can use.
+ * Results are identical for every count >= that value: rows still open after
+ * the last stage launched are finished by its deciding kernel.  No reference
+ * counterpart (the reference builds one MLX graph per row). */
+int mlxf_sample_staged(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                       const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                       const int32_t* d_top_logprobs, const float* d_uniforms, int32_t* d_out_ids,
+                       float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
+                       int K_max, void* d_workspace, size_t workspace_bytes, int refine_stages,
+                       void* stream, char** err);
+
+/* Refine stages a call needs, from HOST copies of the per-row temperature,
+ * top_k and top_p (NULL = the sentinel: greedy / off / off), with the same
+ * sanitisation as mlxf_sample (src/sample/sampler.h:16-29,
+ * src/capi/mlxforge.cpp:43-70): 0 when every row is greedy or has a top-k of
+ * at most 63, 1 when every other row is temperature-only, else 3. */
+int mlxf_sampler_refine_stages(int B, int V, int dtype, const float* h_temperature,
+                               const int32_t* h_top_k, const float* h_top_p);
+
 /* argmax over each row, lowest index on ties: Sampler::greedy
  * (src/sample/sampler.h:61, src/sample/sampler.cpp:59-61). */
 int mlxf_greedy(const void* d_logits, int dtype, int B, int V, int64_t row_stride,

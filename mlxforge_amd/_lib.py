@@ -21,6 +21,8 @@ SYMBOLS = (
     "mlxf_sampler_abi_version",
     "mlxf_sampler_workspace_size",
     "mlxf_sample",
+    "mlxf_sample_staged",
+    "mlxf_sampler_refine_stages",
     "mlxf_greedy",
     "mlxf_string_free",
     "mlxf_sampler_workspace_init",
@@ -51,6 +53,10 @@ def load() -> ctypes.CDLL:
     L.mlxf_sampler_workspace_size.restype = I
     L.mlxf_sample.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, I, P, SZ, P, PP]
     L.mlxf_sample.restype = I
+    L.mlxf_sample_staged.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, I, P, SZ, I, P, PP]
+    L.mlxf_sample_staged.restype = I
+    L.mlxf_sampler_refine_stages.argtypes = [I, I, I, P, P, P]
+    L.mlxf_sampler_refine_stages.restype = I
     L.mlxf_greedy.argtypes = [P, I, I, I, I64, P, P, SZ, P, PP]
     L.mlxf_greedy.restype = I
     L.mlxf_sampler_workspace_init.argtypes = [P, SZ, P, PP]
@@ -82,3 +88,20 @@ def workspace_size(B: int, V: int, K_max: int, dtype: int) -> int:
     rc = load().mlxf_sampler_workspace_size(B, V, K_max, dtype, ctypes.byref(n), ctypes.byref(err))
     check(rc, err)
     return n.value
+
+
+def refine_stages(B: int, V: int, dtype: int, T=None, k=None, p=None) -> int:
+    """Refine stages a call needs, from host arrays of the per-row temperature,
+    top_k and top_p (numpy float32 / int32 / float32, or None for the sentinel)."""
+    import numpy as np
+
+    def ptr(a, t):
+        if a is None:
+            return None, None
+        a = np.ascontiguousarray(a, dtype=t)
+        return a, a.ctypes.data_as(ctypes.c_void_p)
+
+    Ta, Tp = ptr(T, np.float32)
+    ka, kp = ptr(k, np.int32)
+    pa, pp = ptr(p, np.float32)
+    return load().mlxf_sampler_refine_stages(B, V, dtype, Tp, kp, pp)

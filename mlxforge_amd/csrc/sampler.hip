@@ -295,6 +295,8 @@ __device__ __forceinline__ unsigned long long pack_ent(float v, int i) {
   return pack2(__float_as_uint(v), static_cast<unsigned int>(i));
 }
 
+__device__ __forceinline__ unsigned long long LDP(const unsigned long long* p) { return *p; }
+
 __device__ __forceinline__ unsigned int ld_dev32(const unsigned int* p) {
   return __hip_atomic_load(const_cast<unsigned int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -343,13 +345,13 @@ struct Plan {
 
 __device__ __forceinline__ void plan_store(const Args& a, int r, const Plan& p) {
   unsigned long long* w = a.rowst + static_cast<size_t>(r) * RS_WORDS;
-  st_dev(w + RS_PHASE, pack2(p.phase, p.flags));
-  st_dev(w + RS_ZB, pack2(p.zlo, p.zhi));
-  st_dev(w + RS_DIG, pack2(p.kb, p.sh));
-  st_dev(w + RS_AUX, pack2(p.cabove, p.fkey));
-  st_dev(w + RS_GRID, pack2(__float_as_uint(p.Mp), __float_as_uint(p.R2)));
-  st_dev(w + RS_TGT, p.target);
-  st_dev(w + RS_LSE, static_cast<unsigned long long>(__double_as_longlong(p.lse)));
+  w[RS_PHASE] = pack2(p.phase, p.flags);
+  w[RS_ZB] = pack2(p.zlo, p.zhi);
+  w[RS_DIG] = pack2(p.kb, p.sh);
+  w[RS_AUX] = pack2(p.cabove, p.fkey);
+  w[RS_GRID] = pack2(__float_as_uint(p.Mp), __float_as_uint(p.R2));
+  w[RS_TGT] = p.target;
+  w[RS_LSE] = static_cast<unsigned long long>(__double_as_longlong(p.lse));
 }
 __device__ __forceinline__ Plan plan_unpack(const unsigned long long* w) {
   Plan p;
@@ -390,11 +392,12 @@ __device__ void plan_level1(Plan& p, float span2) {
 
 struct S1Lds {
   TopEnt surv[SURV];
-  TopEnt lists[WAVES * LIST];
+  TopEnt lists[WAVES * LIST];  // bitonic fallback for many survivors
   float rf[WAVES];
   float rmin[WAVES];
   int ri[WAVES];
-  unsigned int rfl[WAVES];
+  unsigned int ramin[WAVES];
+  int ramax[WAVES];
   double rd[WAVES];
   unsigned int ncand;
   float thv;
@@ -408,18 +411,28 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
   const int bid = static_cast<int>(blockIdx.x);
   const int S = a.S;
   const int r = bid / S, s = bid - r * S;
-  if (bid == 0 && tid == 0) a.actcnt[2] = 0u;  // the third stage list of the previous call is spent
+  // a new call: the stage lists of the previous call (whatever number of stages
+  // it launched) are spent
+  if (bid == 0 && tid < NSTAGE) a.actcnt[tid] = 0u;
   const Mode md = decode<DT>(a, r);
   const void* row = row_ptr<DT>(a, r);
   const int beg = s * a.L;
   const int end = min(a.V, beg + a.L);
   constexpr int NIT = EPT / VEC;
+  // rows that reach the refine stages: the division range of the slice, and
+  // (top-k rows) its minimum
+  const bool refine = md.kind == KIND_TEMP || md.kind == KIND_TOPP || md.kind == KIND_KHIST;
+  const bool want_min = md.kind == KIND_KHIST || md.kind == KIND_TOPP;
 
   float v[EPT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
 #define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
-  if (tid == 0) sh.ncand = 0u;
+  if (tid == 0) {
+    sh.ncand = 0u;
+    sh.thv = -INFINITY;
+    sh.thi = INT_MAX;
+  }
 
   float tmax = v[0];
 #pragma unroll
@@ -428,30 +441,38 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
     const float wm = wave_max(tmax);
     if (lane == 0) sh.rf[wid] = wm;
   }
-  // minimum and division range of the slice (sampling rows)
-  if (md.sampling) {
+  if (refine) {
+    // smallest nonzero |z| (as bits - 1, so zeros wrap past every value) and
+    // largest finite |z| (as bits + 2^23: infinities wrap negative)
+    unsigned int amin = 0xffffffffu;
+    int amax = 0;
     float tmin = INFINITY;
-    bool bad = false;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       const bool ok = MLXF_IDX(e) < end;
-      tmin = fminf(tmin, ok ? v[e] : INFINITY);
-      bad |= ok & div_unsafe(v[e]);
+      const unsigned int az = __float_as_uint(v[e]) & 0x7fffffffu;
+      amin = min(amin, ok ? az - 1u : 0xffffffffu);
+      amax = max(amax, ok ? static_cast<int>(az + 0x00800000u) : 0);
+      if (want_min) tmin = fminf(tmin, ok ? v[e] : INFINITY);
     }
-    const float wmn = wave_min(tmin);
-    const bool wbad = __ballot(bad) != 0ull;
+    amin = wave_min(amin);
+    amax = wave_max(amax);
+    if (want_min) tmin = wave_min(tmin);
     if (lane == 0) {
-      sh.rmin[wid] = wmn;
-      sh.rfl[wid] = wbad ? 1u : 0u;
+      sh.ramin[wid] = amin;
+      sh.ramax[wid] = amax;
+      sh.rmin[wid] = tmin;
     }
   }
-  // lowest index of the thread max; for list rows, the 64th best thread
-  // maximum (theta) bounds the slice's best 64
+  // lowest index of the thread max
   int tbi = INT_MAX;
 #pragma unroll
   for (int e = EPT - 1; e >= 0; --e)
     if (v[e] == tmax && MLXF_IDX(e) < end) tbi = MLXF_IDX(e);
   if (md.need_list) {
+    // theta: the 64th best thread maximum (bitonic sort of each wave's 64 and a
+    // tree merge).  With fewer than 64 threads holding elements it is the
+    // sentinel and every element survives: fewer than 64 * EPT of them.
     float lv = tmax;
     int li = tbi;
     wave_sort(lv, li);
@@ -477,6 +498,7 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
     const double ws = wave_sum(static_cast<double>(t));
     if (lane == 0) sh.rd[wid] = ws;
   }
+  __syncthreads();
   if (md.need_list) {
     // survivors: every element at or before theta in (z desc, index asc) order;
     // at most 64 threads hold one, so at most 64 * EPT of them
@@ -510,35 +532,52 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
   }
   float zmin = 0.0f;
   unsigned int sfl = 0u;
-  if (md.sampling) {
+  if (refine) {
+    unsigned int amin = sh.ramin[0];
+    int amax = sh.ramax[0];
     zmin = sh.rmin[0];
-    unsigned int badw = sh.rfl[0];
 #pragma unroll
     for (int w2 = 1; w2 < WAVES; ++w2) {
+      amin = min(amin, sh.ramin[w2]);
+      amax = max(amax, sh.ramax[w2]);
       zmin = fminf(zmin, sh.rmin[w2]);
-      badw |= sh.rfl[w2];
     }
-    sfl = badw ? 0u : static_cast<unsigned int>(SL_FAST);
+    // the FMA-corrected division is exact when every nonzero |z| >= 2^-96 and
+    // every finite |z| < 2^100
+    sfl = (amin >= 0x0f7fffffu && amax < static_cast<int>(0x71800000u + 0x00800000u)) ? static_cast<unsigned int>(SL_FAST) : 0u;
   }
   if (md.need_list) {
-    // 64-entry chunks: wave w sorts chunks w, w + WAVES, ... into its own list
+    unsigned long long* dst = a.list + (static_cast<size_t>(r) * S + s) * LIST;
     const int ntot = static_cast<int>(sh.ncand);
-    const int nch = (ntot + LIST - 1) / LIST;
-    float sv = -INFINITY;
-    int si = INT_MAX;
-    for (int ch = wid; ch < nch; ch += WAVES) {
-      const int c = ch * LIST + lane;
-      float cv = -INFINITY;
-      int ci = INT_MAX;
-      if (c < ntot) {
-        cv = sh.surv[c].v;
-        ci = sh.surv[c].i;
+    if (ntot <= THREADS) {
+      // rank of each survivor among the survivors: its place in the list
+      if (tid < LIST && tid >= ntot) dst[tid] = pack_ent(-INFINITY, INT_MAX);
+      if (tid < ntot) {
+        const float mv = sh.surv[tid].v;
+        const int mi = sh.surv[tid].i;
+        int rank = 0;
+        for (int j = 0; j < ntot; ++j) rank += better(sh.surv[j].v, sh.surv[j].i, mv, mi) ? 1 : 0;
+        if (rank < LIST) dst[rank] = pack_ent(mv, mi);
       }
-      wave_sort(cv, ci);
-      wave_list_merge(sv, si, cv, ci);
+    } else {
+      // many survivors (heavy ties at theta): 64-entry chunks sorted and merged
+      const int nch = (ntot + LIST - 1) / LIST;
+      float sv = -INFINITY;
+      int si = INT_MAX;
+      for (int ch = wid; ch < nch; ch += WAVES) {
+        const int c = ch * LIST + lane;
+        float cv = -INFINITY;
+        int ci = INT_MAX;
+        if (c < ntot) {
+          cv = sh.surv[c].v;
+          ci = sh.surv[c].i;
+        }
+        wave_sort(cv, ci);
+        wave_list_merge(sv, si, cv, ci);
+      }
+      tree_merge(sv, si, sh.lists, nch < WAVES ? nch : WAVES);
+      if (wid == 0) dst[lane] = pack_ent(sv, si);
     }
-    tree_merge(sv, si, sh.lists, nch < WAVES ? (nch < 1 ? 1 : nch) : WAVES);
-    if (wid == 0) a.list[(static_cast<size_t>(r) * S + s) * LIST + lane] = pack_ent(sv, si);
   }
 #undef MLXF_IDX
   if (tid == 0) {
@@ -555,7 +594,7 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
 // from the merged best-64 lists; a plan for every other sampling row.
 
 struct D1Lds {
-  unsigned long long lst[MAX_S * LIST];
+  unsigned long long lst[MAX_S * LIST];  // (the per-slice lists; dead once merged)
   TopEnt lists[WAVES * LIST];
   TopEnt mlist[LIST];
   float szmax[MAX_S];
@@ -625,128 +664,6 @@ __device__ __forceinline__ void enlist(const Args& a, int stage, int r) {
   const unsigned int pos =
       __hip_atomic_fetch_add(a.actcnt + stage, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   a.actlist[static_cast<size_t>(stage) * a.B + pos] = static_cast<unsigned int>(r);
-}
-
-template <int DT>
-__global__ __launch_bounds__(THREADS) void k_decide1(Args a) {
-  __shared__ D1Lds sh;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int r = static_cast<int>(blockIdx.x);
-  const int S = a.S;
-  const Mode md = decode<DT>(a, r);
-  if (tid < S) {
-    const unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + tid) * 4;
-    const unsigned long long w0 = rp[0], w1 = rp[1], w2 = rp[2];
-    sh.szmax[tid] = __uint_as_float(static_cast<unsigned int>(w0));
-    sh.szarg[tid] = static_cast<int>(w0 >> 32);
-    sh.szmin[tid] = __uint_as_float(static_cast<unsigned int>(w1));
-    sh.slse[tid] = __longlong_as_double(static_cast<long long>(w2));
-  }
-  if (md.need_list) {
-    const unsigned long long* src = a.list + static_cast<size_t>(r) * S * LIST;
-    for (int i = tid; i < S * LIST; i += THREADS) sh.lst[i] = src[i];
-  }
-  __syncthreads();
-  if (md.need_list) {
-    float lv = -INFINITY;
-    int li = INT_MAX;
-    for (int t = wid; t < S; t += WAVES) {
-      const unsigned long long w = sh.lst[t * LIST + lane];
-      wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
-    }
-    tree_merge(lv, li, sh.lists, S < WAVES ? S : WAVES);
-    if (wid == 0) {
-      sh.mlist[lane].v = lv;
-      sh.mlist[lane].i = li;
-    }
-  }
-  if (wid == 0) {
-    const float zm = lane < S ? sh.szmax[lane] : -INFINITY;
-    const int za = lane < S ? sh.szarg[lane] : INT_MAX;
-    float rm = zm;
-    int ra = za;
-    wave_best(rm, ra);
-    double part = (lane < S && md.need_lse) ? sh.slse[lane] * wexp_d(zm, rm) : 0.0;
-    part = wave_sum(part);
-    const float mn = wave_min(lane < S ? sh.szmin[lane] : INFINITY);
-    if (lane == 0) {
-      sh.zmax = rm;
-      sh.zarg = ra;
-      sh.zmin = mn;
-      sh.lse = md.need_lse ? static_cast<double>(rm) + log(part) : static_cast<double>(NAN);
-    }
-  }
-  __syncthreads();
-  const double lse = sh.lse;
-  if (a.K_max > 0 && tid < a.K_max) {  // top_logprobs: the first K of the best 64
-    const size_t o = static_cast<size_t>(r) * a.K_max + tid;
-    if (tid < md.K) {
-      a.out_top_ids[o] = sh.mlist[tid].i;
-      a.out_top_lp[o] = static_cast<float>(static_cast<double>(sh.mlist[tid].v) - lse);
-    } else {
-      a.out_top_ids[o] = -1;
-      a.out_top_lp[o] = -INFINITY;
-    }
-  }
-  Plan pl;
-  pl.phase = PH_DONE;
-  pl.flags = 0u;
-  pl.zlo = KEY_NEG_INF;
-  pl.zhi = KEY_POS_INF;
-  pl.kb = 0u;
-  pl.sh = 0u;
-  pl.cabove = 0u;
-  pl.fkey = key_lo<DT>();
-  pl.Mp = 0.0f;
-  pl.R2 = 0.0f;
-  pl.target = 0ull;
-  pl.lse = lse;
-  if (!md.sampling) {
-    if (tid == 0) write_out<DT>(a, r, sh.zarg, lse, md.want_lp);
-    return;
-  }
-  const float M = sh.zmax;
-  const float Mp = zdiv<DT>(M, md.Tr, md.y, false);  // max z' = z'(max z)
-  pl.Mp = Mp;
-  if (M == -INFINITY || (md.topp && !(md.pr > 0.0f))) {
-    // every logit left is -inf: the reference's draw is uniform
-    if (tid == 0) write_out<DT>(a, r, uniform_id(md.u, a.V), lse, md.want_lp);
-    return;
-  }
-  if (md.kind == KIND_KLIST) {
-    if (wid == 0) {
-      int id = -1;
-      const bool ok = klist_resolve<DT>(md, Mp, sh.mlist, &id);
-      if (lane == 0) {
-        sh.sel[0] = ok ? 1 : 0;
-        sh.sel[1] = id;
-      }
-    }
-    __syncthreads();
-    if (sh.sel[0]) {
-      if (tid == 0) write_out<DT>(a, r, sh.sel[1], lse, md.want_lp);
-      return;
-    }
-  }
-  const float nc = -(Mp * LOG2E);
-  const float zminp = zdiv<DT>(sh.zmin, md.Tr, md.y, false);
-  const float spanc = -wlog2(zminp, nc);  // full span of the row, log2 units
-  if (md.kind == KIND_KLIST || md.kind == KIND_KHIST) {
-    pl.phase = PH_COUNT;
-    pl.target = static_cast<unsigned long long>(md.kk);
-    if (md.topp) pl.flags |= FL_TOPP;
-    plan_level1<DT>(pl, spanc);
-  } else if (md.kind == KIND_TOPP) {
-    pl.phase = PH_MASS;
-    plan_level1<DT>(pl, fminf(spanc, MASS_LOG2_SPAN));
-    for (int t = tid; t < S; t += THREADS) a.above[static_cast<size_t>(r) * S + t] = 0ull;
-  } else {
-    pl.phase = PH_DRAWSUM;
-  }
-  if (tid == 0) {
-    plan_store(a, r, pl);
-    enlist(a, 0, r);
-  }
 }
 
 // =================================================================== stages ==
@@ -1205,8 +1122,8 @@ __device__ void finish_stage(const Args& a, int r, RLds& sh) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const size_t o = o0 + static_cast<size_t>(t0 + j) * NB + tid;
-        c8[j] = t0 + j < S ? ld_dev32(a.hcnt + o) : 0u;
-        m8[j] = (mass && t0 + j < S) ? ld_dev(a.hmass + o) : 0ull;
+        c8[j] = t0 + j < S ? a.hcnt[o] : 0u;
+        m8[j] = (mass && t0 + j < S) ? LDP(a.hmass + o) : 0ull;
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -1252,7 +1169,7 @@ __device__ void finish_stage(const Args& a, int r, RLds& sh) {
 #pragma unroll
           for (int q = 0; q < NB / 64; ++q) {
             const int b = lane + 64 * q;
-            part[j] += b < bstar ? ld_dev(a.hmass + ob + b) : 0ull;
+            part[j] += b < bstar ? LDP(a.hmass + ob + b) : 0ull;
           }
         }
       }
@@ -1262,11 +1179,11 @@ __device__ void finish_stage(const Args& a, int r, RLds& sh) {
         const unsigned long long ps = wave_sum(part[j]);
         if (lane == 0 && t < S) {
           if (mass) {
-            const unsigned long long ab = ld_dev(a.above + static_cast<size_t>(r) * S + t) + ps;
-            st_dev(a.above + static_cast<size_t>(r) * S + t, ab);
+            const unsigned long long ab = LDP(a.above + static_cast<size_t>(r) * S + t) + ps;
+            a.above[static_cast<size_t>(r) * S + t] = ab;
             sh.kept[t] = ab;
           }
-          sh.tcnt[t] = ld_dev32(a.hcnt + o0 + static_cast<size_t>(t) * NB + bstar);
+          sh.tcnt[t] = a.hcnt[o0 + static_cast<size_t>(t) * NB + bstar];
         }
       }
     }
@@ -1332,7 +1249,7 @@ __device__ void finish_stage(const Args& a, int r, RLds& sh) {
           pl.phase = PH_MASS;
           pl.flags &= ~static_cast<unsigned int>(FL_TOPP);
           plan_level1<DT>(pl, fminf(-wlog2(kval<DT>(klo), nc), MASS_LOG2_SPAN));
-          for (int t = tid; t < S; t += THREADS) st_dev(a.above + static_cast<size_t>(r) * S + t, 0ull);
+          for (int t = tid; t < S; t += THREADS) a.above[static_cast<size_t>(r) * S + t] = 0ull;
         } else {
           pl.phase = PH_DRAWSUM;
         }
@@ -1371,19 +1288,19 @@ __device__ void finish_stage(const Args& a, int r, RLds& sh) {
       }
     }
   } else if (pl.phase == PH_DRAWSUM) {
-    for (int t = tid; t < S; t += THREADS) sh.kept[t] = ld_dev(a.dsum + static_cast<size_t>(r) * S + t);
+    for (int t = tid; t < S; t += THREADS) sh.kept[t] = LDP(a.dsum + static_cast<size_t>(r) * S + t);
     __syncthreads();
     id = draw<DT, EPT, VECOK>(a, r, md, Mp, pl.fkey, true, sh);
     done = true;
   } else if (pl.phase == PH_GATHER) {
     if (tid == 0) {
-      const unsigned int n = ld_dev32(a.ncand + r);
+      const unsigned int n = a.ncand[r];
       sh.ncand = n < CAP ? n : CAP;
-      st_dev32(a.ncand + r, 0u);
+      a.ncand[r] = 0u;
     }
     __syncthreads();
     const int n = static_cast<int>(sh.ncand);
-    for (int c = tid; c < n; c += THREADS) sh.cand[c] = ld_dev(a.cand + static_cast<size_t>(r) * CAP + c);
+    for (int c = tid; c < n; c += THREADS) sh.cand[c] = LDP(a.cand + static_cast<size_t>(r) * CAP + c);
     __syncthreads();
     unsigned long long bef;
     unsigned int g;
@@ -1434,7 +1351,7 @@ __device__ void finish_stage(const Args& a, int r, RLds& sh) {
       }
       // per-slice kept mass: above the bin, plus the kept candidates
       for (int t2 = tid; t2 < S; t2 += THREADS) {
-        sh.kept[t2] = ld_dev(a.above + static_cast<size_t>(r) * S + t2);
+        sh.kept[t2] = LDP(a.above + static_cast<size_t>(r) * S + t2);
         sh.tcnt[t2] = 0u;
       }
       __syncthreads();
@@ -1476,8 +1393,6 @@ __global__ __launch_bounds__(THREADS) void k_scan(Args a, int stage) {
   const int tid = threadIdx.x;
   const int bid = static_cast<int>(blockIdx.x);
   const int S = a.S;
-  // the list two stages back has been read by its decide kernel: clear its count
-  if (stage >= 1 && bid == 0 && tid == 0) a.actcnt[stage - 1] = 0u;
   const unsigned int n = a.actcnt[stage];
   if (static_cast<unsigned int>(bid) >= n * static_cast<unsigned int>(S)) return;
   const int r = static_cast<int>(a.actlist[static_cast<size_t>(stage) * a.B + bid / S]);
@@ -1487,17 +1402,33 @@ __global__ __launch_bounds__(THREADS) void k_scan(Args a, int stage) {
   slice_stage<DT, EPT, VECOK>(a, r, s, sh);
 }
 
+// Finish row r here: run the remaining levels over the row's slices in this
+// workgroup (the row plan is in sh.sl.pw).  Each level narrows the bracket or
+// advances the phase, so the loop ends; its bound is a guard.
+template <int DT, int EPT, bool VECOK>
+__device__ void serial_finish(const Args& a, int r, RLds& sh) {
+  for (int it = 0; it < SERIAL_MAX && static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) != PH_DONE; ++it) {
+    for (int s2 = 0; s2 < a.S; ++s2) {
+      slice_stage<DT, EPT, VECOK>(a, r, s2, sh.sl);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    // the slice passes' stores are complete; drop stale L1 lines before the
+    // plain loads of the deciding step
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    finish_stage<DT, EPT, VECOK>(a, r, sh);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+}
+
 // Refine stage `stage`, one workgroup per row on the stage's list: decide, and
 // put the row on the next stage's list if it is still open.  The last stage
-// finishes every row itself: this workgroup runs the remaining levels over the
-// row's slices.  Each level narrows the bracket or advances the phase, so the
-// loop ends; its bound is a guard.
+// launched finishes every row itself.
 template <int DT, int EPT, bool VECOK>
-__global__ __launch_bounds__(THREADS) void k_decide(Args a, int stage) {
+__global__ __launch_bounds__(THREADS) void k_decide(Args a, int stage, int last) {
   __shared__ RLds sh;
   const int tid = threadIdx.x;
   const int bid = static_cast<int>(blockIdx.x);
-  const int S = a.S;
   const unsigned int n = a.actcnt[stage];
   if (static_cast<unsigned int>(bid) >= n) return;
   const int r = static_cast<int>(a.actlist[static_cast<size_t>(stage) * a.B + bid]);
@@ -1505,19 +1436,162 @@ __global__ __launch_bounds__(THREADS) void k_decide(Args a, int stage) {
   __syncthreads();
   finish_stage<DT, EPT, VECOK>(a, r, sh);
   if (static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) == PH_DONE) return;
-  if (stage + 1 < NSTAGE) {
+  if (!last) {
     if (tid == 0) enlist(a, stage + 1, r);
     return;
   }
-  for (int it = 0; it < SERIAL_MAX && static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) != PH_DONE; ++it) {
-    for (int s2 = 0; s2 < S; ++s2) {
-      slice_stage<DT, EPT, VECOK>(a, r, s2, sh.sl);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-    finish_stage<DT, EPT, VECOK>(a, r, sh);
-  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  serial_finish<DT, EPT, VECOK>(a, r, sh);
 }
+
+// Shared memory of k_decide1: the list stage, then (when no refine stage is
+// launched) the refine state of a row finished here.
+union D1Shared {
+  D1Lds d;
+  RLds r;
+};
+
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS) void k_decide1(Args a, int nstage) {
+  __shared__ D1Shared shu;
+  D1Lds& sh = shu.d;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int r = static_cast<int>(blockIdx.x);
+  const int S = a.S;
+  const Mode md = decode<DT>(a, r);
+  if (tid < S) {
+    const unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + tid) * 4;
+    const unsigned long long w0 = rp[0], w1 = rp[1], w2 = rp[2];
+    sh.szmax[tid] = __uint_as_float(static_cast<unsigned int>(w0));
+    sh.szarg[tid] = static_cast<int>(w0 >> 32);
+    sh.szmin[tid] = __uint_as_float(static_cast<unsigned int>(w1));
+    sh.slse[tid] = __longlong_as_double(static_cast<long long>(w2));
+  }
+  if (md.need_list) {
+    const unsigned long long* src = a.list + static_cast<size_t>(r) * S * LIST;
+    for (int i = tid; i < S * LIST; i += THREADS) sh.lst[i] = src[i];
+  }
+  __syncthreads();
+  if (md.need_list) {
+    float lv = -INFINITY;
+    int li = INT_MAX;
+    for (int t = wid; t < S; t += WAVES) {
+      const unsigned long long w = sh.lst[t * LIST + lane];
+      wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
+    }
+    tree_merge(lv, li, sh.lists, S < WAVES ? S : WAVES);
+    if (wid == 0) {
+      sh.mlist[lane].v = lv;
+      sh.mlist[lane].i = li;
+    }
+  }
+  if (wid == 0) {
+    const float zm = lane < S ? sh.szmax[lane] : -INFINITY;
+    const int za = lane < S ? sh.szarg[lane] : INT_MAX;
+    float rm = zm;
+    int ra = za;
+    wave_best(rm, ra);
+    double part = (lane < S && md.need_lse) ? sh.slse[lane] * wexp_d(zm, rm) : 0.0;
+    part = wave_sum(part);
+    const float mn = wave_min(lane < S ? sh.szmin[lane] : INFINITY);
+    if (lane == 0) {
+      sh.zmax = rm;
+      sh.zarg = ra;
+      sh.zmin = mn;
+      sh.lse = md.need_lse ? static_cast<double>(rm) + log(part) : static_cast<double>(NAN);
+    }
+  }
+  __syncthreads();
+  const double lse = sh.lse;
+  if (a.K_max > 0 && tid < a.K_max) {  // top_logprobs: the first K of the best 64
+    const size_t o = static_cast<size_t>(r) * a.K_max + tid;
+    if (tid < md.K) {
+      a.out_top_ids[o] = sh.mlist[tid].i;
+      a.out_top_lp[o] = static_cast<float>(static_cast<double>(sh.mlist[tid].v) - lse);
+    } else {
+      a.out_top_ids[o] = -1;
+      a.out_top_lp[o] = -INFINITY;
+    }
+  }
+  Plan pl;
+  pl.phase = PH_DONE;
+  pl.flags = 0u;
+  pl.zlo = KEY_NEG_INF;
+  pl.zhi = KEY_POS_INF;
+  pl.kb = 0u;
+  pl.sh = 0u;
+  pl.cabove = 0u;
+  pl.fkey = key_lo<DT>();
+  pl.Mp = 0.0f;
+  pl.R2 = 0.0f;
+  pl.target = 0ull;
+  pl.lse = lse;
+  if (!md.sampling) {
+    if (tid == 0) write_out<DT>(a, r, sh.zarg, lse, md.want_lp);
+    return;
+  }
+  const float M = sh.zmax;
+  const float Mp = zdiv<DT>(M, md.Tr, md.y, false);  // max z' = z'(max z)
+  pl.Mp = Mp;
+  if (M == -INFINITY || (md.topp && !(md.pr > 0.0f))) {
+    // every logit left is -inf: the reference's draw is uniform
+    if (tid == 0) write_out<DT>(a, r, uniform_id(md.u, a.V), lse, md.want_lp);
+    return;
+  }
+  if (md.kind == KIND_KLIST) {
+    if (wid == 0) {
+      int id = -1;
+      const bool ok = klist_resolve<DT>(md, Mp, sh.mlist, &id);
+      if (lane == 0) {
+        sh.sel[0] = ok ? 1 : 0;
+        sh.sel[1] = id;
+      }
+    }
+    __syncthreads();
+    if (sh.sel[0]) {
+      if (tid == 0) write_out<DT>(a, r, sh.sel[1], lse, md.want_lp);
+      return;
+    }
+  }
+  const float nc = -(Mp * LOG2E);
+  // full span of the row in log2 units (unknown, i.e. infinite, when the scan
+  // did not take the minimum)
+  const float spanc = sh.zmin == INFINITY ? INFINITY : -wlog2(zdiv<DT>(sh.zmin, md.Tr, md.y, false), nc);
+  if (md.kind == KIND_KLIST || md.kind == KIND_KHIST) {
+    pl.phase = PH_COUNT;
+    pl.target = static_cast<unsigned long long>(md.kk);
+    if (md.topp) pl.flags |= FL_TOPP;
+    plan_level1<DT>(pl, spanc);
+  } else if (md.kind == KIND_TOPP) {
+    pl.phase = PH_MASS;
+    plan_level1<DT>(pl, fminf(spanc, MASS_LOG2_SPAN));
+    for (int t = tid; t < S; t += THREADS) a.above[static_cast<size_t>(r) * S + t] = 0ull;
+  } else {
+    pl.phase = PH_DRAWSUM;
+  }
+  if (tid == 0) plan_store(a, r, pl);
+  if (nstage > 0) {
+    if (tid == 0) enlist(a, 0, r);
+    return;
+  }
+  // no refine stage is launched (the caller's parameters promised top-k <= 63
+  // or greedy rows only): finish the row here
+  __syncthreads();
+  if (tid == 0) {
+    shu.r.sl.pw[RS_PHASE] = pack2(pl.phase, pl.flags);
+    shu.r.sl.pw[RS_ZB] = pack2(pl.zlo, pl.zhi);
+    shu.r.sl.pw[RS_DIG] = pack2(pl.kb, pl.sh);
+    shu.r.sl.pw[RS_AUX] = pack2(pl.cabove, pl.fkey);
+    shu.r.sl.pw[RS_GRID] = pack2(__float_as_uint(pl.Mp), __float_as_uint(pl.R2));
+    shu.r.sl.pw[RS_TGT] = pl.target;
+    shu.r.sl.pw[RS_LSE] = static_cast<unsigned long long>(__double_as_longlong(pl.lse));
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  serial_finish<DT, EPT, VECOK>(a, r, shu.r);
+}
+
 
 // Zero the per-row counters of a fresh workspace.
 __global__ void k_zero(unsigned int* p, size_t n) {
@@ -1537,10 +1611,9 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 
 // The zero-initialised head of the workspace, at offsets that do not depend on
 // the shape (so one workspace serves calls of every shape): per-row gathered-
-// candidate counters (65536 32-bit words) and the stage-list counts.  Every
-// call leaves them ready for the next: a decide kernel clears the candidate
-// counters it read, and each stage-list count is cleared by the scan kernel
-// that runs once its list has been read.
+// candidate counters (65536 32-bit words) and the stage-list counts.  A
+// decide kernel clears the candidate counters it read; the first kernel of a
+// call clears the stage-list counts.
 constexpr size_t ROWS_MAX = 65536;
 constexpr size_t CTR_BYTES_MAX = ROWS_MAX * sizeof(unsigned int) + 256;
 
@@ -1625,39 +1698,75 @@ int check_shape(int B, int V, int K_max, int dtype, char** err) {
   return MLXF_OK;
 }
 
-// Stage 0 (scan, decide), then NSTAGE refine stages (scan, decide) when any row
-// may sample.
+// Stage 0 (scan, decide), then `nst` refine stages (scan, decide); the last
+// deciding kernel launched finishes every row still open.
 template <int DT, int EPT, bool VECOK>
-hipError_t launch_ept(const Args& a, hipStream_t st) {
+hipError_t launch_ept(const Args& a, int nst, hipStream_t st) {
   const dim3 slices(static_cast<unsigned int>(a.B * a.S)), rows(static_cast<unsigned int>(a.B));
   hipLaunchKernelGGL((k_scan1<DT, EPT, VECOK>), slices, dim3(THREADS), 0, st, a);
-  hipLaunchKernelGGL((k_decide1<DT>), rows, dim3(THREADS), 0, st, a);
-  if (a.T) {
-    for (int i = 0; i < NSTAGE; ++i) {
-      hipLaunchKernelGGL((k_scan<DT, EPT, VECOK>), slices, dim3(THREADS), 0, st, a, i);
-      hipLaunchKernelGGL((k_decide<DT, EPT, VECOK>), rows, dim3(THREADS), 0, st, a, i);
-    }
+  hipLaunchKernelGGL((k_decide1<DT, EPT, VECOK>), rows, dim3(THREADS), 0, st, a, nst);
+  for (int i = 0; i < nst; ++i) {
+    hipLaunchKernelGGL((k_scan<DT, EPT, VECOK>), slices, dim3(THREADS), 0, st, a, i);
+    hipLaunchKernelGGL((k_decide<DT, EPT, VECOK>), rows, dim3(THREADS), 0, st, a, i, i == nst - 1 ? 1 : 0);
   }
   return hipGetLastError();
 }
 
 template <int DT>
-hipError_t launch_dt(const Args& a, int ept, bool vecok, hipStream_t st) {
+hipError_t launch_dt(const Args& a, int ept, bool vecok, int nst, hipStream_t st) {
   switch (ept) {
     case 8:
-      return vecok ? launch_ept<DT, 8, true>(a, st) : launch_ept<DT, 8, false>(a, st);
+      return vecok ? launch_ept<DT, 8, true>(a, nst, st) : launch_ept<DT, 8, false>(a, nst, st);
     case 16:
-      return vecok ? launch_ept<DT, 16, true>(a, st) : launch_ept<DT, 16, false>(a, st);
+      return vecok ? launch_ept<DT, 16, true>(a, nst, st) : launch_ept<DT, 16, false>(a, nst, st);
     default:
-      return vecok ? launch_ept<DT, 32, true>(a, st) : launch_ept<DT, 32, false>(a, st);
+      return vecok ? launch_ept<DT, 32, true>(a, nst, st) : launch_ept<DT, 32, false>(a, nst, st);
   }
+}
+
+// Refine stages a call needs, from host copies of the per-row parameters with
+// the same sanitisation as the kernels: 0 when every row is greedy or has a
+// top-k <= 63 (decided from the best-64 lists; a row whose k-th value has more
+// ties than the list holds is finished by the first deciding kernel itself), 1
+// when the other rows are temperature-only, else NSTAGE.  A null array reads
+// as the sentinel (T: greedy; k: off; p: off).
+int host_refine_stages(int B, int V, int dtype, const float* T, const int32_t* k, const float* p) {
+  if (!T) return 0;
+  auto rnd = [dtype](float x) {
+    if (dtype == MLXF_DTYPE_F32) return x;
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    if (dtype == MLXF_DTYPE_BF16) {
+      u += 0x7fffu + ((u >> 16) & 1u);
+      u &= 0xffff0000u;
+      float y;
+      std::memcpy(&y, &u, 4);
+      return y;
+    }
+    return static_cast<float>(static_cast<_Float16>(x));
+  };
+  int need = 0;
+  for (int r = 0; r < B; ++r) {
+    const float t = T[r];
+    if (!(std::isfinite(t) && t > 0.0f && rnd(t) > 0.0f)) continue;  // greedy
+    const int kk = k ? k[r] : 0;
+    const float pp = p ? p[r] : 1.0f;
+    const int kc = kk > 0 ? (kk < V ? kk : V) : 0;
+    if (kc > 0 && kc <= KLIST_MAX) continue;
+    if (kc == 0 && !(pp > 0.0f && pp < 1.0f)) {
+      need = need > 1 ? need : 1;
+      continue;
+    }
+    return NSTAGE;
+  }
+  return need;
 }
 
 int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
                const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
                const int32_t* d_top_logprobs, const float* d_uniforms, int32_t* d_out_ids,
                float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
-               int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err) {
+               int K_max, void* d_workspace, size_t workspace_bytes, void* stream, int nst, char** err) {
   try {
     int rc = check_shape(B, V, K_max, dtype, err);
     if (rc) return rc;
@@ -1723,14 +1832,19 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
     a.above = reinterpret_cast<unsigned long long*>(ws + l.off_above);
     a.dsum = reinterpret_cast<unsigned long long*>(ws + l.off_dsum);
     a.cand = reinterpret_cast<unsigned long long*>(ws + l.off_cand);
+    if (nst < 0 || nst > NSTAGE) {
+      set_err(err, "mlxf: refine_stages must be in [0, 3]");
+      return MLXF_EINVAL;
+    }
+    if (!d_temperature) nst = 0;  // every row greedy
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e;
     if (dtype == MLXF_DTYPE_F32)
-      e = launch_dt<MLXF_DTYPE_F32>(a, l.EPT, vecok, st);
+      e = launch_dt<MLXF_DTYPE_F32>(a, l.EPT, vecok, nst, st);
     else if (dtype == MLXF_DTYPE_BF16)
-      e = launch_dt<MLXF_DTYPE_BF16>(a, l.EPT, vecok, st);
+      e = launch_dt<MLXF_DTYPE_BF16>(a, l.EPT, vecok, nst, st);
     else
-      e = launch_dt<MLXF_DTYPE_F16>(a, l.EPT, vecok, st);
+      e = launch_dt<MLXF_DTYPE_F16>(a, l.EPT, vecok, nst, st);
     if (e != hipSuccess) {
       set_err(err, std::string("mlxf: kernel launch failed: ") + hipGetErrorString(e));
       return MLXF_EHIP;
@@ -1798,14 +1912,30 @@ int mlxf_sample(const void* d_logits, int dtype, int B, int V, int64_t row_strid
                 int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err) {
   return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p,
                     d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
-                    d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, err);
+                    d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, mlxf::NSTAGE, err);
+}
+
+int mlxf_sample_staged(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                       const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                       const int32_t* d_top_logprobs, const float* d_uniforms, int32_t* d_out_ids,
+                       float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
+                       int K_max, void* d_workspace, size_t workspace_bytes, int refine_stages,
+                       void* stream, char** err) {
+  return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p,
+                    d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
+                    d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, refine_stages, err);
+}
+
+int mlxf_sampler_refine_stages(int B, int V, int dtype, const float* h_temperature,
+                               const int32_t* h_top_k, const float* h_top_p) {
+  return mlxf::host_refine_stages(B, V, dtype, h_temperature, h_top_k, h_top_p);
 }
 
 int mlxf_greedy(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
                 int32_t* d_out_ids, void* d_workspace, size_t workspace_bytes, void* stream,
                 char** err) {
   return run_sample(d_logits, dtype, B, V, row_stride, nullptr, nullptr, nullptr, nullptr, nullptr,
-                    d_out_ids, nullptr, nullptr, nullptr, 0, d_workspace, workspace_bytes, stream,
+                    d_out_ids, nullptr, nullptr, nullptr, 0, d_workspace, workspace_bytes, stream, 0,
                     err);
 }
 

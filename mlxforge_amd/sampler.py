@@ -86,13 +86,27 @@ def _param(x, B, dtype, device):
     return x
 
 
+def _host_view(x, B):
+    """Host copy of a per-row parameter given as a scalar / sequence / numpy
+    array; None when it is a device tensor (then the host does not know it)."""
+    import numpy as np
+    if x is None:
+        return "off"
+    if torch.is_tensor(x):
+        return None
+    return np.broadcast_to(np.asarray(x), (B,))
+
+
 def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
                 top_logprobs=None, uniforms=None, K_max: int = 0, V: int | None = None,
-                workspace: Workspace | None = None) -> SampleResult:
+                workspace: Workspace | None = None, refine_stages: int | None = None) -> SampleResult:
     """Sample one token per row of a [B, row_stride] logits view.
 
-    Per-row parameters are device tensors of length B (or Python scalars, which
-    are broadcast); None disables the knob (temperature None = all greedy).
+    Per-row parameters are device tensors of length B (or Python scalars /
+    host sequences, which are copied); None disables the knob (temperature
+    None = all greedy).  refine_stages: refine stages to launch (0..3); by
+    default derived from the parameters when they are all known on the host
+    (mlxf_sampler_refine_stages), else 3.
     """
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be a [B, V] view with unit stride along V")
@@ -101,6 +115,14 @@ def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
     dev = logits.device
     B = logits.shape[0]
     V = logits.shape[1] if V is None else V
+    code = _DTYPES[logits.dtype]
+    if refine_stages is None:
+        hv = [_host_view(x, B) for x in (temperature, top_k, top_p)]
+        if any(h is None for h in hv):
+            refine_stages = 3
+        else:
+            hv = [None if isinstance(h, str) else h for h in hv]
+            refine_stages = _lib.refine_stages(B, V, code, *hv)
     T = _param(temperature, B, torch.float32, dev)
     k = _param(top_k, B, torch.int32, dev)
     p = _param(top_p, B, torch.float32, dev)
@@ -110,16 +132,15 @@ def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
     lp = torch.empty(B, dtype=torch.float32, device=dev)
     top_ids = torch.empty((B, K_max), dtype=torch.int32, device=dev)
     top_lp = torch.empty((B, K_max), dtype=torch.float32, device=dev)
-    code = _DTYPES[logits.dtype]
     if workspace is None:
         workspace = _default_ws.setdefault(dev, Workspace(dev))
     ws = workspace.get(B, V, K_max, code)
     stream = torch.cuda.current_stream(dev).cuda_stream
     err = ctypes.c_void_p()
-    rc = _lib.load().mlxf_sample(
+    rc = _lib.load().mlxf_sample_staged(
         _ptr(logits), code, B, V, logits.stride(0), _ptr(T), _ptr(k), _ptr(p), _ptr(tlp), _ptr(u),
         _ptr(ids), _ptr(lp), _ptr(top_ids) if K_max else None, _ptr(top_lp) if K_max else None,
-        K_max, _ptr(ws), ws.numel(), ctypes.c_void_p(stream), ctypes.byref(err))
+        K_max, _ptr(ws), ws.numel(), int(refine_stages), ctypes.c_void_p(stream), ctypes.byref(err))
     _lib.check(rc, err)
     return SampleResult(ids, lp, top_ids, top_lp)
 

@@ -29,12 +29,15 @@ def to_device(host: np.ndarray, dtype: str, device="cuda:0") -> torch.Tensor:
     return t.to(device)
 
 
-def gpu_sample(logits_dev, T=None, k=None, p=None, tlp=None, u=None, K_max=0, V=None):
+def gpu_sample(logits_dev, T=None, k=None, p=None, tlp=None, u=None, K_max=0, V=None,
+               stages=None):
+    """stages: refine stages to launch (None: all three, the generic path)."""
     dev = logits_dev.device
     f = lambda a, t: None if a is None else torch.as_tensor(np.asarray(a), dtype=t).to(dev)
     res = sampler.sample_rows(logits_dev, temperature=f(T, torch.float32), top_k=f(k, torch.int32),
                               top_p=f(p, torch.float32), top_logprobs=f(tlp, torch.int32),
-                              uniforms=f(u, torch.float32), K_max=K_max, V=V)
+                              uniforms=f(u, torch.float32), K_max=K_max, V=V,
+                              refine_stages=3 if stages is None else stages)
     torch.cuda.synchronize()
     return dict(ids=res.tokens.cpu().numpy(), lp=res.logprobs.cpu().numpy(),
                 top_ids=res.top_tokens.cpu().numpy(), top_lp=res.top_logprobs.cpu().numpy())

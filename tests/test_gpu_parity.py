@@ -39,6 +39,12 @@ def test_config_parity(cfg):
                          K_max=wl.K_max)
     rep = gu.compare(g, o, wl.dtype, tlp=wl.tlp, label=f"C{cfg}")
     say(f"[parity] config {cfg}: {rep}")
+    # the stage count the host-side parameters call for gives the same results
+    from mlxforge_amd import _lib
+    code = {"f32": _lib.DTYPE_F32, "bf16": _lib.DTYPE_BF16, "f16": _lib.DTYPE_F16}[wl.dtype]
+    st = _lib.refine_stages(wl.B, wl.V, code, wl.T, wl.k, wl.p)
+    gh = gu.gpu_sample(dev, T=wl.T, k=wl.k, p=wl.p, tlp=wl.tlp, u=wl.u, K_max=wl.K_max, stages=st)
+    assert np.array_equal(g["ids"], gh["ids"]), f"C{cfg}: {st} stages differ from 3"
     # determinism: a second run is bit-identical
     g2 = gu.gpu_sample(dev, T=wl.T, k=wl.k, p=wl.p, tlp=wl.tlp, u=wl.u, K_max=wl.K_max)
     assert np.array_equal(g["ids"], g2["ids"])
@@ -249,3 +255,21 @@ def test_workspace_errors():
                                  16, None, ctypes.byref(err))
     assert rc == _lib.EWORKSPACE
     _lib.load().mlxf_string_free(err)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_stage_counts_agree(dtype):
+    """Rows still open after the last refine stage launched are finished by its
+    deciding kernel: every stage count gives bit-identical results."""
+    rng = np.random.default_rng(77 + len(dtype))
+    for V in (3000, 20000):
+        host, T, k, p, tlp, u = _random_case(rng, 6, V, dtype)
+        dev = gu.to_device(host, dtype)
+        say(f"[parity] stage counts dtype={dtype} V={V}")
+        ref = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=3, stages=3)
+        o = gu.oracle_sample(host, dtype, T=T, k=k, p=p, tlp=tlp, u=u, K_max=3)
+        gu.compare(ref, o, dtype, tlp=tlp, label=f"stages {dtype} V={V}")
+        for st in (0, 1, 2):
+            g = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=3, stages=st)
+            assert np.array_equal(g["ids"], ref["ids"]), (st, g["ids"], ref["ids"])
+            assert np.array_equal(g["lp"].view(np.uint32), ref["lp"].view(np.uint32))
