@@ -90,8 +90,8 @@ struct Args {
   unsigned long long* rec;     // [B*S][4] slice records
   unsigned long long* list;    // [B*S][64] (z bits, index)
   unsigned long long* rowst;   // [B][8] row plans
-  unsigned int* hcnt;          // [B*S][256] histogram counts
-  unsigned long long* hmass;   // [B*S][256] histogram masses
+  unsigned int* hcnt;          // [B*S][256] histogram counts, cumulative from bin 0 (the top)
+  unsigned long long* hmass;   // [B*S][256] histogram masses, cumulative from bin 0
   unsigned long long* above;   // [B*S] kept mass above the bracket (MASS)
   unsigned long long* dsum;    // [B*S] kept mass (DRAWSUM)
   unsigned long long* cand;    // [B][CAP] (z' key, index)
@@ -243,7 +243,7 @@ __device__ __forceinline__ int vbin_x(float x, float R2) {
 // and true at hi: a 64-ary search, one candidate per lane (3 rounds for 16-bit
 // keys, 6 for 32-bit).  The whole wave calls it; every lane gets the result.
 template <typename PRED>
-__device__ unsigned int wave_search(unsigned int lo, unsigned int hi, PRED pred) {
+__device__ __forceinline__ unsigned int wave_search(unsigned int lo, unsigned int hi, PRED pred) {
   const int lane = threadIdx.x & 63;
   while (lo < hi) {
     const unsigned long long span = static_cast<unsigned long long>(hi - lo) + 1ull;
@@ -271,7 +271,7 @@ __device__ unsigned int wave_search(unsigned int lo, unsigned int hi, PRED pred)
 // Smallest z key whose z' reaches y (z' non-decreasing in z); 0xffffffff if
 // none.  Whole wave.
 template <int DT>
-__device__ unsigned int gkey(float y, float Tr) {
+__device__ __forceinline__ unsigned int gkey(float y, float Tr) {
   if (!(zdiv<DT>(INFINITY, Tr, 1.0f, false) >= y)) return 0xffffffffu;
   return wave_search(KEY_NEG_INF, KEY_POS_INF,
                      [&](unsigned int k) { return zdiv<DT>(key2f(k), Tr, 1.0f, false) >= y; });
@@ -280,7 +280,7 @@ __device__ unsigned int gkey(float y, float Tr) {
 // z-key bracket [zlo, zhi] of the elements whose z' key lies in [klo, khi].
 // Whole wave.
 template <int DT>
-__device__ void zbracket(unsigned int klo, unsigned int khi, float Tr, unsigned int* zlo,
+__device__ __forceinline__ void zbracket(unsigned int klo, unsigned int khi, float Tr, unsigned int* zlo,
                          unsigned int* zhi) {
   *zlo = gkey<DT>(kval<DT>(klo), Tr);
   if (khi >= key_hi<DT>()) {
@@ -306,7 +306,7 @@ __device__ __forceinline__ void st_dev32(unsigned int* p, unsigned int v) {
 
 // Sampled id (and its logprob) of row r.
 template <int DT>
-__device__ void write_out(const Args& a, int r, int id, double lse, bool want_lp) {
+__device__ __forceinline__ void write_out(const Args& a, int r, int id, double lse, bool want_lp) {
   a.out_ids[r] = id;
   if (a.out_lp) {
     const void* row = row_ptr<DT>(a, r);
@@ -353,7 +353,7 @@ __device__ __forceinline__ void plan_store(const Args& a, int r, const Plan& p) 
   w[RS_TGT] = p.target;
   w[RS_LSE] = static_cast<unsigned long long>(__double_as_longlong(p.lse));
 }
-__device__ __forceinline__ Plan plan_unpack(const unsigned long long* w) {
+__device__ __forceinline__ Plan plan_unpack(const unsigned long long* w) {  // (LDS or global)
   Plan p;
   p.phase = static_cast<unsigned int>(w[RS_PHASE]);
   p.flags = static_cast<unsigned int>(w[RS_PHASE] >> 32);
@@ -374,7 +374,7 @@ __device__ __forceinline__ Plan plan_unpack(const unsigned long long* w) {
 // row max and the span below it are finite and positive, else the top 8 bits of
 // the key.  span2 is the span in log2-weight units.
 template <int DT>
-__device__ void plan_level1(Plan& p, float span2) {
+__device__ __forceinline__ void plan_level1(Plan& p, float span2) {
   if (__builtin_isfinite(p.Mp) && span2 > 0.0f && __builtin_isfinite(span2)) {
     p.flags |= FL_VGRID;
     p.R2 = 255.0f / span2;
@@ -614,7 +614,7 @@ struct D1Lds {
 // keep while the mass before an entry is < p * W_k, inverse CDF in vocabulary
 // order.
 template <int DT>
-__device__ bool klist_resolve(const Mode& md, float Mp, const TopEnt* ml, int* id_out) {
+__device__ __forceinline__ bool klist_resolve(const Mode& md, float Mp, const TopEnt* ml, int* id_out) {
   const int lane = threadIdx.x & 63;
   const float lv = ml[lane].v;
   const int li = ml[lane].i;
@@ -659,11 +659,12 @@ __device__ bool klist_resolve(const Mode& md, float Mp, const TopEnt* ml, int* i
   return true;
 }
 
-// Put row r on the list of the next refine stage `stage` (0-based list index).
-__device__ __forceinline__ void enlist(const Args& a, int stage, int r) {
+// Put row r (its next phase in the high half) on the list of refine stage
+// `stage` (0-based).
+__device__ __forceinline__ void enlist(const Args& a, int stage, int r, unsigned int phase) {
   const unsigned int pos =
       __hip_atomic_fetch_add(a.actcnt + stage, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  a.actlist[static_cast<size_t>(stage) * a.B + pos] = static_cast<unsigned int>(r);
+  a.actlist[static_cast<size_t>(stage) * a.B + pos] = static_cast<unsigned int>(r) | (phase << 16);
 }
 
 // =================================================================== stages ==
@@ -696,9 +697,8 @@ struct RLds {
 // workspace with plain stores (read by the next kernel, or -- in the last
 // stage -- by this workgroup after a full wait and a barrier).
 template <int DT, int EPT, bool VECOK>
-__device__ void slice_stage(const Args& a, int r, int s, SLds& sh) {
+__device__ __forceinline__ void slice_stage(const Args& a, int r, int s, const Plan& pl, SLds& sh) {
   const int tid = threadIdx.x;
-  const Plan pl = plan_unpack(sh.pw);
   const Mode md = decode<DT>(a, r);
   const void* row = row_ptr<DT>(a, r);
   const int beg = s * a.L;
@@ -741,10 +741,16 @@ __device__ void slice_stage(const Args& a, int r, int s, SLds& sh) {
       }
     }
     __syncthreads();
+    // cumulative from the top bin down: the deciding step reads a bin's total
+    // and everything above it in one word
     const size_t o = (static_cast<size_t>(r) * a.S + s) * NB;
-    for (int b = tid; b < NB; b += THREADS) {
-      a.hcnt[o + b] = sh.hc[b];
-      if (mass) a.hmass[o + b] = sh.hm[b];
+    unsigned int cex, cin, ctot;
+    block_scan<unsigned int>(sh.hc[tid], sh.rv, &cex, &cin, &ctot);
+    a.hcnt[o + tid] = cin;
+    if (mass) {
+      unsigned long long mex, min_, mtot;
+      block_scan<unsigned long long>(sh.hm[tid], sh.ru, &mex, &min_, &mtot);
+      a.hmass[o + tid] = min_;
     }
   } else if (pl.phase == PH_GATHER) {
     // the slice's elements in the bracket: one reservation per workgroup
@@ -792,7 +798,7 @@ __device__ void slice_stage(const Args& a, int r, int s, SLds& sh) {
 // z' key > tau, and the first tie_lim (in index order) of those equal to tau.
 // Returns the first kept element at which the running kept mass exceeds rem.
 template <int DT, int EPT, bool VECOK>
-__device__ int walk(const Args& a, int r, int s, float Mp, unsigned long long rem, unsigned int tau,
+__device__ __forceinline__ int walk(const Args& a, int r, int s, float Mp, unsigned long long rem, unsigned int tau,
                     unsigned int tie_lim, RLds& sh) {
   const int tid = threadIdx.x;
   const Mode md = decode<DT>(a, r);
@@ -872,7 +878,7 @@ __device__ int walk(const Args& a, int r, int s, float Mp, unsigned long long re
 // Pick the slice holding the draw from per-slice kept masses sh.kept[0..S) and
 // walk it.  sh.tcnt[s] holds the kept ties of slice s unless all ties are kept.
 template <int DT, int EPT, bool VECOK>
-__device__ int draw(const Args& a, int r, const Mode& md, float Mp, unsigned int tau, bool all_ties,
+__device__ __forceinline__ int draw(const Args& a, int r, const Mode& md, float Mp, unsigned int tau, bool all_ties,
                     RLds& sh) {
   const int tid = threadIdx.x;
   const int S = a.S;
@@ -921,7 +927,7 @@ __device__ int draw(const Args& a, int r, const Mode& md, float Mp, unsigned int
 // gets `before`, *gcount the number of candidates equal to v.  8-bit digits;
 // the leading bits all participants share are skipped.  Whole workgroup.
 template <int DT, bool BY_KEY, bool MASSM, typename PRED>
-__device__ unsigned int cselect(int n, PRED pred, float Mp, unsigned long long target, bool strict, RLds& sh,
+__device__ __forceinline__ unsigned int cselect(int n, PRED pred, float Mp, unsigned long long target, bool strict, RLds& sh,
                                 unsigned long long* before_out, unsigned int* gcount) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const float nc = -(Mp * LOG2E);
@@ -1045,7 +1051,7 @@ __device__ unsigned int cselect(int n, PRED pred, float Mp, unsigned long long t
 
 // Block sum of the fixed-point masses of the candidates with pred.
 template <int DT, typename PRED>
-__device__ unsigned long long cmass(int n, PRED pred, float Mp, RLds& sh) {
+__device__ __forceinline__ unsigned long long cmass(int n, PRED pred, float Mp, RLds& sh) {
   const float nc = -(Mp * LOG2E);
   const bool minf = !__builtin_isfinite(Mp);
   unsigned long long t = 0;
@@ -1070,7 +1076,7 @@ __device__ __forceinline__ unsigned int ties_kept(unsigned long long need, unsig
 
 // Publish wave 0's bracket [klo, khi] -> z-key bracket to the workgroup.
 template <int DT>
-__device__ void set_bracket(Plan& pl, unsigned int klo, unsigned int khi, float Tr, RLds& sh) {
+__device__ __forceinline__ void set_bracket(Plan& pl, unsigned int klo, unsigned int khi, float Tr, RLds& sh) {
   if ((threadIdx.x >> 6) == 0) {
     unsigned int zl, zh;
     zbracket<DT>(klo, khi, Tr, &zl, &zh);
@@ -1098,10 +1104,41 @@ __device__ __forceinline__ void set_digits(Plan& pl, unsigned int klo, unsigned 
 // slices' results, then either writes the sampled id or leaves the next plan in
 // sh.sl.pw and in the row's plan words.
 template <int DT, int EPT, bool VECOK>
-__device__ void finish_stage(const Args& a, int r, RLds& sh) {
+__device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int ph, const unsigned long long* pwsrc,
+                                             RLds& sh) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int S = a.S;
-  Plan pl = plan_unpack(sh.sl.pw);
+  // The slices' results for phase ph, requested together with the plan words
+  // (pwsrc: the row's plan in global memory, or its copy in LDS): thread t owns
+  // histogram bin t and sums every slice's cumulative count and mass at t;
+  // thread t < S holds slice t's mass above the bracket so far, or its kept mass.
+  const bool hist = ph == PH_COUNT || ph == PH_MASS;
+  const bool mass = ph == PH_MASS;
+  const size_t o0 = static_cast<size_t>(r) * S * NB;
+  unsigned int Cc = 0;
+  unsigned long long Mc = 0;
+  for (int t0 = 0; t0 < S; t0 += 32) {
+    unsigned int cc[32];
+    unsigned long long mc[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const size_t o = o0 + static_cast<size_t>(t0 + j) * NB + tid;
+      cc[j] = (hist && t0 + j < S) ? a.hcnt[o] : 0u;
+      mc[j] = (mass && t0 + j < S) ? a.hmass[o] : 0ull;
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      Cc += cc[j];
+      Mc += mc[j];
+    }
+  }
+  unsigned long long pre = 0;
+  if (tid < S) {
+    if (mass) pre = a.above[static_cast<size_t>(r) * S + tid];
+    if (ph == PH_DRAWSUM) pre = a.dsum[static_cast<size_t>(r) * S + tid];
+  }
+  const unsigned int ng = (ph == PH_GATHER && tid == 0) ? a.ncand[r] : 0u;
+  Plan pl = plan_unpack(pwsrc);
   const Mode md = decode<DT>(a, r);
   const float Mp = pl.Mp;
   const float nc = -(Mp * LOG2E);
@@ -1110,121 +1147,90 @@ __device__ void finish_stage(const Args& a, int r, RLds& sh) {
   bool done = false;
   int id = 0;
 
-  if (pl.phase == PH_COUNT || pl.phase == PH_MASS) {
-    const bool mass = pl.phase == PH_MASS;
-    // per-bin totals: thread t owns bin t; loads issued 8 slices at a time
-    unsigned int C = 0;
-    unsigned long long Mb = 0;
-    const size_t o0 = static_cast<size_t>(r) * S * NB;
-    for (int t0 = 0; t0 < S; t0 += 8) {
-      unsigned int c8[8];
-      unsigned long long m8[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const size_t o = o0 + static_cast<size_t>(t0 + j) * NB + tid;
-        c8[j] = t0 + j < S ? a.hcnt[o] : 0u;
-        m8[j] = (mass && t0 + j < S) ? LDP(a.hmass + o) : 0ull;
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        C += c8[j];
-        Mb += m8[j];
-      }
-    }
-    const unsigned long long meas = mass ? Mb : static_cast<unsigned long long>(C);
-    unsigned long long mex, min_, mtot;
-    block_scan<unsigned long long>(meas, sh.sl.ru, &mex, &min_, &mtot);
-    unsigned int cex, cin, ctot;
-    block_scan<unsigned int>(C, sh.sl.rv, &cex, &cin, &ctot);
+  if (hist) {
+    const unsigned long long abp = pre;
+    const unsigned long long mcum = mass ? Mc : static_cast<unsigned long long>(Cc);
+    sh.sl.hc[tid] = Cc;
+    sh.sl.hm[tid] = mcum;
+    if (tid == 0) sh.sel[4] = NB;
+    __syncthreads();
     if (mass && pl.target == 0) {
       // first mass level: the nucleus target p * W over the participants
       const unsigned long long PW =
-          static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(mtot)));
+          static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(sh.sl.hm[NB - 1])));
       pl.target = PW < 1 ? 1 : PW;
     }
-    if (tid == 0) {
-      sh.sel[4] = NB;
-      sh.sel[5] = -1;
+    // the chosen bin: the first whose cumulative measure reaches the target
+    // (the total, should rounding leave the target out of reach)
+    {
+      const unsigned long long tgt = pl.target < sh.sl.hm[NB - 1] ? pl.target : sh.sl.hm[NB - 1];
+      const unsigned long long bal = __ballot(mcum >= tgt);
+      if (bal && lane == 0) atomicMin(&sh.sel[4], wid * 64 + __ffsll(static_cast<long long>(bal)) - 1);
     }
     __syncthreads();
-    if (meas > 0 && min_ >= pl.target) atomicMin(&sh.sel[4], tid);
-    if (meas > 0) atomicMax(&sh.sel[5], tid);
-    __syncthreads();
-    const int bstar = sh.sel[4] < NB ? sh.sel[4] : (sh.sel[5] >= 0 ? sh.sel[5] : NB - 1);
-    if (tid == bstar) {
-      sh.selu[2] = mex;                                   // measure above the bin
-      sh.selu[3] = static_cast<unsigned long long>(cex);  // participants above the bin
-      sh.selu[4] = static_cast<unsigned long long>(C);    // participants in the bin
-    }
-    // per slice: the mass above the bin (MASS) and the participants in the bin;
-    // wave w takes slices w, w + WAVES, ..., four at a time
-    for (int t0 = wid * 4; t0 < S; t0 += WAVES * 4) {
-      unsigned long long part[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        part[j] = 0;
-        const int t = t0 + j;
-        if (mass && t < S) {
-          const size_t ob = o0 + static_cast<size_t>(t) * NB;
-#pragma unroll
-          for (int q = 0; q < NB / 64; ++q) {
-            const int b = lane + 64 * q;
-            part[j] += b < bstar ? LDP(a.hmass + ob + b) : 0ull;
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = t0 + j;
-        const unsigned long long ps = wave_sum(part[j]);
-        if (lane == 0 && t < S) {
-          if (mass) {
-            const unsigned long long ab = LDP(a.above + static_cast<size_t>(r) * S + t) + ps;
-            a.above[static_cast<size_t>(r) * S + t] = ab;
-            sh.kept[t] = ab;
-          }
-          sh.tcnt[t] = a.hcnt[o0 + static_cast<size_t>(t) * NB + bstar];
-        }
-      }
-    }
-    // key range [klo, khi] of the chosen bin (wave 0)
-    if (wid == 0) {
-      unsigned int klo, khi;
-      if (pl.flags & FL_VGRID) {
-        auto vb = [&](unsigned int k) { return vbin_x(wlog2(kval<DT>(k), nc), pl.R2); };
-        klo = wave_search(klo_all, khi_all, [&](unsigned int k) { return vb(k) <= bstar; });
-        if (bstar == 0) {
-          khi = khi_all;
-        } else {
-          const unsigned int nx = wave_search(klo_all, khi_all, [&](unsigned int k) { return vb(k) <= bstar - 1; });
-          khi = nx > klo ? nx - 1u : klo;
-        }
-      } else {
-        const unsigned long long lo64 =
-            static_cast<unsigned long long>(pl.kb) + (static_cast<unsigned long long>(NB - 1 - bstar) << pl.sh);
-        const unsigned long long hi64 = lo64 + (1ull << pl.sh) - 1ull;
-        klo = static_cast<unsigned int>(lo64);
-        khi = static_cast<unsigned int>(hi64 < khi_all ? hi64 : khi_all);
-      }
-      if (klo < pl.fkey) klo = pl.fkey;
+    const int bstar = sh.sel[4] < NB ? sh.sel[4] : NB - 1;
+    const unsigned long long abv = bstar > 0 ? sh.sl.hm[bstar - 1] : 0ull;  // measure above the bin
+    const unsigned int cabv = bstar > 0 ? sh.sl.hc[bstar - 1] : 0u;         // participants above it
+    const unsigned int cstar = sh.sl.hc[bstar] - cabv;                     // participants in it
+    // per slice (thread t < S for slice t): the participants in the bin, and
+    // the mass above it (MASS); the cumulative words around the bin are re-read
+    // (they are in L2 by now)
+    if (tid < S) {
+      const size_t os = o0 + static_cast<size_t>(tid) * NB;
+      const unsigned int cb = a.hcnt[os + bstar];
+      const unsigned int cb1 = bstar > 0 ? a.hcnt[os + bstar - 1] : 0u;
+      const unsigned long long mb1 = (mass && bstar > 0) ? a.hmass[os + bstar - 1] : 0ull;
+      sh.tcnt[tid] = cb - cb1;
       if (mass) {
-        // elements whose mass quantises to zero never count: start the bracket
-        // at the first key with a positive mass
-        const unsigned int kq = wave_search(klo_all, khi_all, [&](unsigned int k) {
-          return q40(wfun(kval<DT>(k), Mp, nc, minf)) > 0;
-        });
-        if (klo < kq) klo = kq;
+        sh.kept[tid] = abp + mb1;
+        a.above[static_cast<size_t>(r) * S + tid] = abp + mb1;
       }
+    }
+    // key range [klo, khi] of the chosen bin: wave 0 the low edge, wave 1 the
+    // high edge, wave 2 the first key with a positive mass
+    if (tid == 0) {
+      sh.sel[6] = 0;
+      sh.sel[7] = static_cast<int>(khi_all);
+      sh.sel[3] = static_cast<int>(klo_all);
+    }
+    __syncthreads();
+    if (pl.flags & FL_VGRID) {
+      auto vb = [&](unsigned int k) { return vbin_x(wlog2(kval<DT>(k), nc), pl.R2); };
+      if (wid == 0) {
+        const unsigned int klo = wave_search(klo_all, khi_all, [&](unsigned int k) { return vb(k) <= bstar; });
+        if (lane == 0) sh.sel[6] = static_cast<int>(klo);
+      } else if (wid == 1 && bstar > 0) {
+        const unsigned int nx = wave_search(klo_all, khi_all, [&](unsigned int k) { return vb(k) <= bstar - 1; });
+        if (lane == 0) sh.sel[7] = static_cast<int>(nx > klo_all ? nx - 1u : klo_all);
+      }
+    } else if (tid == 0) {
+      const unsigned long long lo64 =
+          static_cast<unsigned long long>(pl.kb) + (static_cast<unsigned long long>(NB - 1 - bstar) << pl.sh);
+      const unsigned long long hi64 = lo64 + (1ull << pl.sh) - 1ull;
+      sh.sel[6] = static_cast<int>(lo64);
+      sh.sel[7] = static_cast<int>(hi64 < khi_all ? hi64 : khi_all);
+    }
+    if (mass && wid == 2) {
+      // elements whose mass quantises to zero never count: the bracket starts
+      // at the first key with a positive mass
+      const unsigned int kq = wave_search(klo_all, khi_all, [&](unsigned int k) {
+        return q40(wfun(kval<DT>(k), Mp, nc, minf)) > 0;
+      });
+      if (lane == 0) sh.sel[3] = static_cast<int>(kq);
+    }
+    __syncthreads();
+    {
+      unsigned int klo = static_cast<unsigned int>(sh.sel[6]), khi = static_cast<unsigned int>(sh.sel[7]);
+      if (klo < pl.fkey) klo = pl.fkey;
+      if (klo < static_cast<unsigned int>(sh.sel[3])) klo = static_cast<unsigned int>(sh.sel[3]);
       if (khi < klo) khi = klo;
-      if (lane == 0) {
+      __syncthreads();
+      if (tid == 0) {
         sh.sel[6] = static_cast<int>(klo);
         sh.sel[7] = static_cast<int>(khi);
       }
     }
     __syncthreads();
-    const unsigned long long abv = sh.selu[2];
-    const unsigned int cabv = static_cast<unsigned int>(sh.selu[3]);
-    const unsigned int cstar = static_cast<unsigned int>(sh.selu[4]);
     const unsigned int klo = static_cast<unsigned int>(sh.sel[6]);
     const unsigned int khi = static_cast<unsigned int>(sh.sel[7]);
     __syncthreads();
@@ -1287,15 +1293,14 @@ __device__ void finish_stage(const Args& a, int r, RLds& sh) {
         set_bracket<DT>(pl, klo, khi, md.Tr, sh);
       }
     }
-  } else if (pl.phase == PH_DRAWSUM) {
-    for (int t = tid; t < S; t += THREADS) sh.kept[t] = LDP(a.dsum + static_cast<size_t>(r) * S + t);
+  } else if (ph == PH_DRAWSUM) {
+    if (tid < S) sh.kept[tid] = pre;
     __syncthreads();
     id = draw<DT, EPT, VECOK>(a, r, md, Mp, pl.fkey, true, sh);
     done = true;
-  } else if (pl.phase == PH_GATHER) {
+  } else if (ph == PH_GATHER) {
     if (tid == 0) {
-      const unsigned int n = a.ncand[r];
-      sh.ncand = n < CAP ? n : CAP;
+      sh.ncand = ng < CAP ? ng : CAP;
       a.ncand[r] = 0u;
     }
     __syncthreads();
@@ -1380,6 +1385,7 @@ __device__ void finish_stage(const Args& a, int r, RLds& sh) {
     sh.sl.pw[RS_AUX] = pack2(pl.cabove, pl.fkey);
     sh.sl.pw[RS_GRID] = pack2(__float_as_uint(pl.Mp), __float_as_uint(pl.R2));
     sh.sl.pw[RS_TGT] = pl.target;
+    sh.sl.pw[RS_LSE] = static_cast<unsigned long long>(__double_as_longlong(pl.lse));
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -1390,33 +1396,32 @@ __device__ void finish_stage(const Args& a, int r, RLds& sh) {
 template <int DT, int EPT, bool VECOK>
 __global__ __launch_bounds__(THREADS) void k_scan(Args a, int stage) {
   __shared__ SLds sh;
-  const int tid = threadIdx.x;
   const int bid = static_cast<int>(blockIdx.x);
   const int S = a.S;
   const unsigned int n = a.actcnt[stage];
+  const unsigned int e = a.actlist[static_cast<size_t>(stage) * a.B + bid / S];
   if (static_cast<unsigned int>(bid) >= n * static_cast<unsigned int>(S)) return;
-  const int r = static_cast<int>(a.actlist[static_cast<size_t>(stage) * a.B + bid / S]);
-  const int s = bid % S;
-  if (tid < RS_WORDS) sh.pw[tid] = a.rowst[static_cast<size_t>(r) * RS_WORDS + tid];
-  __syncthreads();
-  slice_stage<DT, EPT, VECOK>(a, r, s, sh);
+  const int r = static_cast<int>(e & 0xffffu);
+  const Plan pl = plan_unpack(a.rowst + static_cast<size_t>(r) * RS_WORDS);
+  slice_stage<DT, EPT, VECOK>(a, r, bid % S, pl, sh);
 }
 
 // Finish row r here: run the remaining levels over the row's slices in this
 // workgroup (the row plan is in sh.sl.pw).  Each level narrows the bracket or
 // advances the phase, so the loop ends; its bound is a guard.
 template <int DT, int EPT, bool VECOK>
-__device__ void serial_finish(const Args& a, int r, RLds& sh) {
+__device__ __forceinline__ void serial_finish(const Args& a, int r, RLds& sh) {
   for (int it = 0; it < SERIAL_MAX && static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) != PH_DONE; ++it) {
+    const Plan pl = plan_unpack(sh.sl.pw);
     for (int s2 = 0; s2 < a.S; ++s2) {
-      slice_stage<DT, EPT, VECOK>(a, r, s2, sh.sl);
+      slice_stage<DT, EPT, VECOK>(a, r, s2, pl, sh.sl);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
     // the slice passes' stores are complete; drop stale L1 lines before the
     // plain loads of the deciding step
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    finish_stage<DT, EPT, VECOK>(a, r, sh);
+    finish_stage<DT, EPT, VECOK>(a, r, pl.phase, sh.sl.pw, sh);
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
 }
@@ -1425,19 +1430,18 @@ __device__ void serial_finish(const Args& a, int r, RLds& sh) {
 // put the row on the next stage's list if it is still open.  The last stage
 // launched finishes every row itself.
 template <int DT, int EPT, bool VECOK>
-__global__ __launch_bounds__(THREADS) void k_decide(Args a, int stage, int last) {
+__global__ __launch_bounds__(THREADS, 1) void k_decide(Args a, int stage, int last) {
   __shared__ RLds sh;
   const int tid = threadIdx.x;
   const int bid = static_cast<int>(blockIdx.x);
   const unsigned int n = a.actcnt[stage];
+  const unsigned int e = a.actlist[static_cast<size_t>(stage) * a.B + bid];
   if (static_cast<unsigned int>(bid) >= n) return;
-  const int r = static_cast<int>(a.actlist[static_cast<size_t>(stage) * a.B + bid]);
-  if (tid < RS_WORDS) sh.sl.pw[tid] = a.rowst[static_cast<size_t>(r) * RS_WORDS + tid];
-  __syncthreads();
-  finish_stage<DT, EPT, VECOK>(a, r, sh);
+  const int r = static_cast<int>(e & 0xffffu);
+  finish_stage<DT, EPT, VECOK>(a, r, e >> 16, a.rowst + static_cast<size_t>(r) * RS_WORDS, sh);
   if (static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) == PH_DONE) return;
   if (!last) {
-    if (tid == 0) enlist(a, stage + 1, r);
+    if (tid == 0) enlist(a, stage + 1, r, static_cast<unsigned int>(sh.sl.pw[RS_PHASE]));
     return;
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
@@ -1452,7 +1456,7 @@ union D1Shared {
 };
 
 template <int DT, int EPT, bool VECOK>
-__global__ __launch_bounds__(THREADS) void k_decide1(Args a, int nstage) {
+__global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
   __shared__ D1Shared shu;
   D1Lds& sh = shu.d;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -1571,7 +1575,7 @@ __global__ __launch_bounds__(THREADS) void k_decide1(Args a, int nstage) {
   }
   if (tid == 0) plan_store(a, r, pl);
   if (nstage > 0) {
-    if (tid == 0) enlist(a, 0, r);
+    if (tid == 0) enlist(a, 0, r, pl.phase);
     return;
   }
   // no refine stage is launched (the caller's parameters promised top-k <= 63
