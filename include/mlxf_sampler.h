@@ -133,6 +133,16 @@ int mlxf_sample_staged(const void* d_logits, int dtype, int B, int V, int64_t ro
 int mlxf_sampler_refine_stages(int B, int V, int dtype, const float* h_temperature,
                                const int32_t* h_top_k, const float* h_top_p);
 
+/* The first kernel of mlxf_sample alone -- the one HBM read of the logits
+ * (per-slice maxima, log-sum-exp partials, best-64 lists), which dominates a
+ * decode step -- with the same arguments; writes no output.  For measuring
+ * that kernel in isolation.  No reference counterpart. */
+int mlxf_sampler_first_pass(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                            const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                            const int32_t* d_top_logprobs, const float* d_uniforms, int32_t* d_out_ids,
+                            float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
+                            int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err);
+
 /* argmax over each row, lowest index on ties: Sampler::greedy
  * (src/sample/sampler.h:61, src/sample/sampler.cpp:59-61). */
 int mlxf_greedy(const void* d_logits, int dtype, int B, int V, int64_t row_stride,

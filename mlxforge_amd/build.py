@@ -1,7 +1,9 @@
 """Build recipe for the HIP sampler library (gfx950).
 
 Produces ``mlxforge_amd/libmlxf_sampler.so`` in-tree from
-``mlxforge_amd/csrc/sampler.hip`` with hipcc, and the C++ known-answer test
+``mlxforge_amd/csrc/sampler.hip`` (host side) and ``sampler_{f32,bf16,f16}.hip``
+(one logits dtype's kernels each, compiled in parallel) with hipcc, and the C++
+known-answer test
 driver ``mlxforge_amd/sampler_kat`` (tests/cpp/sampler_kat.cpp) that exercises
 the C++ host wrapper (mlxforge_amd/include/mlxforge_amd/sampler.hpp).
 
@@ -22,7 +24,8 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRC = os.path.join(HERE, "csrc", "sampler.hip")
+CSRC = os.path.join(HERE, "csrc")
+SRCS = [os.path.join(CSRC, f) for f in ("sampler.hip", "sampler_f32.hip", "sampler_bf16.hip", "sampler_f16.hip")]
 LIB = os.path.join(HERE, "libmlxf_sampler.so")
 KAT_SRC = os.path.join(ROOT, "tests", "cpp", "sampler_kat.cpp")
 KAT_BIN = os.path.join(HERE, "sampler_kat")
@@ -44,6 +47,10 @@ def hipcc() -> str:
 
 def _run(cmd):
     proc = subprocess.run(cmd, capture_output=True, text=True)
+    _report(cmd, proc)
+
+
+def _report(cmd, proc):
     # hipcc's host pass does not know the packed-fp32 feature and says so; drop that line.
     noise = [l for l in proc.stderr.splitlines() if "packed-fp32-ops" not in l]
     if proc.returncode != 0:
@@ -53,8 +60,19 @@ def _run(cmd):
 
 
 def build_lib() -> str:
-    tmp = LIB + ".tmp"
-    _run([hipcc(), *HIP_FLAGS, "-shared", "-I", os.path.join(ROOT, "include"), "-o", tmp, SRC])
+    import tempfile
+    objs, procs = [], []
+    with tempfile.TemporaryDirectory() as tmpd:
+        for src in SRCS:
+            obj = os.path.join(tmpd, os.path.basename(src) + ".o")
+            cmd = [hipcc(), *HIP_FLAGS, "-c", "-I", os.path.join(ROOT, "include"), "-o", obj, src]
+            procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+            objs.append(obj)
+        for cmd, pr in procs:
+            out, err = pr.communicate()
+            _report(cmd, subprocess.CompletedProcess(cmd, pr.returncode, out, err))
+        tmp = LIB + ".tmp"
+        _run([hipcc(), *HIP_FLAGS, "-shared", "-o", tmp, *objs])
     os.replace(tmp, LIB)
     return LIB
 

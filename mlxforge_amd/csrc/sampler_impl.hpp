@@ -1,0 +1,1675 @@
+#pragma once
+// sampler_impl.hpp -- device code of the MI355X (gfx950) batched token
+// sampler: the kernels and their launch sequence.  Each sampler_<dtype>.hip
+// instantiates it for one logits dtype (the three build in parallel); the host
+// side (sampler.hip) calls them through launch_<dtype>.
+//
+// Replaces the per-row MLX graph of Sampler::sample (src/sample/sampler.cpp:
+// 141-166), run once per row by Worker::sample_rows (src/runtime/worker.cpp:
+// 448-486), with a short sequence of kernels over all rows of a [B, V] logits
+// matrix.  Row r is cut into S slices of L = 256 * EPT logits.  A call is
+//
+//   k_scan1   one workgroup per slice: the one HBM read of every logit.  Max
+//             and lowest-index argmax of z, sum exp(z - max) when a logprob is
+//             wanted, the slice minimum and division range for rows that go on
+//             to the refine stages, and -- for top_logprobs or top-k <= 63 --
+//             the slice's best 64 entries by (z desc, index asc);
+//   k_decide1 one workgroup per row: argmax, log-sum-exp, top_logprobs, and
+//             for top-k <= 63 the whole selection (k-th value, nucleus, draw)
+//             from the merged best-64 lists; every other sampling row gets a
+//             plan and goes on the first stage's list;
+//   then up to NSTAGE refine stages, each a scan over the slices of the rows on
+//   its list and a deciding kernel per row:
+//     COUNT   top-k: a 256-bin count histogram of z' over the current bracket;
+//     MASS    top-p: a 256-bin histogram of exact fixed-point masses
+//             w = exp(z' - max z') (2^-40 units) over the current bracket;
+//     GATHER  the bracket's elements themselves (at most CAP per row), resolved
+//             exactly by radix selections in LDS;
+//     DRAWSUM the kept mass of each slice (temperature-only rows, or top-k sets
+//             too large to gather).
+//   The first histogram level bins z' on a value grid anchored at the row max
+//   (uniform in log-weight, so concentrated rows spread over many bins); later
+//   levels take 8-bit digits of the z' key inside the chosen bin.  A row whose
+//   cutoff value is known exactly draws: the slice holding u * (kept mass) is
+//   found from per-slice kept masses and walked in vocabulary order.  The last
+//   stage launched finishes any row still open by running the remaining levels
+//   over its slices in its deciding workgroup.
+//
+// Masses that decide a cutoff are sums of integers, so every result is
+// reproducible bit for bit and every level is consistent with the one before.
+// Kernels hand data on through the workspace (kernel boundaries order it);
+// nothing waits for a workgroup that may not have started.  There is no MFMA
+// anywhere: nothing here is a dense contraction.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "device_common.hpp"
+#include "mlxf_sampler.h"
+
+namespace mlxf {
+
+enum { KIND_GREEDY = 0, KIND_TEMP = 1, KIND_KLIST = 2, KIND_KHIST = 3, KIND_TOPP = 4 };
+enum { PH_DONE = 0, PH_COUNT = 1, PH_MASS = 2, PH_GATHER = 3, PH_DRAWSUM = 4 };
+// FL_VGRID: the current level bins z' on the value grid (else key digits kb, sh)
+// FL_GALL:  the gather takes every element at or above the bracket's low edge;
+//           the top-k selection is finished on the candidates
+// FL_TOPP:  a nucleus selection follows the top-k selection
+enum { FL_VGRID = 1, FL_GALL = 2, FL_TOPP = 4 };
+enum { SL_FAST = 1 };  // slice record flag: the FMA-corrected division is exact for every z
+
+constexpr int LIST = 64;
+constexpr int KLIST_MAX = LIST - 1;  // top-k resolved from the best-64 lists
+constexpr int NB = 256;              // bins per histogram level
+constexpr int CAP = 4096;            // gathered candidates per row (LDS)
+constexpr int NSTAGE = 3;            // refine launches per call
+constexpr int SERIAL_MAX = 40;       // bound on the levels the last stage runs itself
+constexpr int SURV = 64 * 32;        // best-64 survivors of a slice (<= 64 * EPT)
+constexpr float MASS_LOG2_SPAN = 40.0f;  // weights below 2^-40 quantise to zero
+
+
+// ------------------------------------------------------------ parameters --
+
+struct Args {
+  const void* logits;
+  long long row_stride;
+  int B, V, K_max, S, L;
+  const float* T;
+  const int* k;
+  const float* p;
+  const int* tlp;
+  const float* u;
+  int* out_ids;
+  float* out_lp;
+  int* out_top_ids;
+  float* out_top_lp;
+  unsigned int* actcnt;        // [4] rows on each stage's list (zero between calls, see below)
+  unsigned int* ncand;         // [B] gathered-candidate counters, zero between calls
+  unsigned int* actlist;       // [NSTAGE][B] rows still open before each refine stage
+  unsigned long long* rec;     // [B*S][4] slice records
+  unsigned long long* list;    // [B*S][64] (z bits, index)
+  unsigned long long* rowst;   // [B][8] row plans
+  unsigned int* hcnt;          // [B*S][256] histogram counts, cumulative from bin 0 (the top)
+  unsigned long long* hmass;   // [B*S][256] histogram masses, cumulative from bin 0
+  unsigned long long* above;   // [B*S] kept mass above the bracket (MASS)
+  unsigned long long* dsum;    // [B*S] kept mass (DRAWSUM)
+  unsigned long long* cand;    // [B][CAP] (z' key, index)
+};
+
+
+// One dtype's launch sequence (defined in sampler_<dtype>.hip).
+hipError_t launch_f32(const Args& a, int ept, bool vecok, int nst, hipStream_t st);
+hipError_t launch_bf16(const Args& a, int ept, bool vecok, int nst, hipStream_t st);
+hipError_t launch_f16(const Args& a, int ept, bool vecok, int nst, hipStream_t st);
+
+namespace {
+
+
+struct Mode {
+  int sampling, kk, topp, K, need_lse, want_lp, kind, need_list, tslow;
+  float Tr, pr, u, y;
+};
+
+// Per-row parameters with the reference's sentinels and the C ABI's
+// sanitisation (src/sample/sampler.h:15-29, src/capi/mlxforge.cpp:43-70).
+template <int DT>
+__device__ __forceinline__ Mode decode(const Args& a, int r) {
+  Mode m;
+  const float T = a.T ? a.T[r] : 0.0f;
+  m.Tr = round_dt<DT>(T);
+  m.sampling = (__builtin_isfinite(T) && T > 0.0f && m.Tr > 0.0f) ? 1 : 0;
+  m.y = m.sampling ? 1.0f / m.Tr : 1.0f;  // correctly rounded (IEEE division)
+  m.tslow = (m.Tr >= 0x1p-24f && m.Tr <= 0x1p24f) ? 0 : 1;
+  const int k = a.k ? a.k[r] : 0;
+  m.kk = (m.sampling && k > 0) ? (k < a.V ? k : a.V) : 0;
+  const float p = a.p ? a.p[r] : 1.0f;
+  m.topp = (m.sampling && p > 0.0f && p < 1.0f) ? 1 : 0;
+  m.pr = round_dt<DT>(p);
+  const int tlp = a.tlp ? a.tlp[r] : -1;
+  int K = tlp > 0 ? tlp : 0;
+  K = K < a.K_max ? K : a.K_max;
+  K = K < a.V ? K : a.V;
+  m.K = K;
+  m.want_lp = (a.out_lp != nullptr && tlp >= 0) ? 1 : 0;
+  m.need_lse = (tlp >= 0 && (a.out_lp != nullptr || K > 0)) ? 1 : 0;
+  float u = a.u ? a.u[r] : 0.0f;
+  if (!(u >= 0.0f)) u = 0.0f;
+  if (u >= 1.0f) u = 0x1.fffffep-1f;
+  m.u = u;
+  if (!m.sampling)
+    m.kind = KIND_GREEDY;
+  else if (m.kk > 0)
+    m.kind = m.kk <= KLIST_MAX ? KIND_KLIST : KIND_KHIST;
+  else
+    m.kind = m.topp ? KIND_TOPP : KIND_TEMP;
+  m.need_list = (K > 0 || m.kind == KIND_KLIST) ? 1 : 0;
+  return m;
+}
+
+template <int DT>
+__device__ __forceinline__ const void* row_ptr(const Args& a, int r) {
+  return static_cast<const char*>(a.logits) +
+         static_cast<size_t>(r) * static_cast<size_t>(a.row_stride) * elem_size<DT>();
+}
+
+// ------------------------------------------------------ element functions --
+
+// z' = round_dtype(z / Tr) with the quotient correctly rounded (the temperature
+// division of src/sample/sampler.cpp:158).  The fast form is Markstein's
+// FMA-corrected quotient: with y = RN(1/Tr), q0 = RN(z * y) is within an ulp of
+// z / Tr, the remainder z - Tr * q0 is exact by FMA, and RN(q0 + r * y) is the
+// correctly rounded quotient (P. Markstein, IBM J. Res. Dev. 34(1), 1990).  It
+// is used only when no product, remainder or quotient can leave the normal
+// range: 2^-24 <= Tr <= 2^24 and every finite z of the slice has |z| = 0 or
+// 2^-96 <= |z| < 2^100 (the slice record's SL_FAST); +-inf passes through.
+// Zeros come out as +0, so equal values have equal keys.
+template <int DT>
+__device__ __forceinline__ float zdiv(float z, float Tr, float y, bool fast) {
+  float q;
+  if (fast) {
+    const float q0 = z * y;
+    const float rr = __builtin_fmaf(-q0, Tr, z);
+    const float q1 = __builtin_fmaf(rr, y, q0);
+    q = rr != rr ? q0 : q1;
+  } else {
+    q = z / Tr;
+  }
+  return round_dt<DT>(q) + 0.0f;
+}
+
+// Whether |z| lies outside the range the fast division covers (finite z only).
+__device__ __forceinline__ bool div_unsafe(float z) {
+  const unsigned int az = __float_as_uint(z) & 0x7fffffffu;
+  return (az - 1u < 0x0f800000u - 1u) | ((az >= 0x71800000u) & (az < 0x7f800000u));
+}
+
+// Monotone key of a z' value: 32 bits for fp32 logits, the 16-bit value's own
+// key for bf16 / f16 (z' is a value of the logits dtype).
+template <int DT>
+constexpr int keybits() {
+  return DT == MLXF_DTYPE_F32 ? 32 : 16;
+}
+template <int DT>
+__device__ __forceinline__ unsigned int zkey(float zp) {
+  if constexpr (DT == MLXF_DTYPE_F32) {
+    return f2key(zp);
+  } else if constexpr (DT == MLXF_DTYPE_BF16) {
+    return f2key(zp) >> 16;
+  } else {
+    const unsigned int h = __half_as_ushort(__float2half_rn(zp));
+    return (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+  }
+}
+template <int DT>
+__device__ __forceinline__ float kval(unsigned int k) {
+  if constexpr (DT == MLXF_DTYPE_F32) {
+    return key2f(k);
+  } else if constexpr (DT == MLXF_DTYPE_BF16) {
+    return key2f((k << 16) | ((k & 0x8000u) ? 0u : 0xffffu));
+  } else {
+    const unsigned int h = (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(h)));
+  }
+}
+template <int DT>
+__device__ __forceinline__ unsigned int key_lo() {  // key of -inf
+  return DT == MLXF_DTYPE_F32 ? 0x007fffffu : (DT == MLXF_DTYPE_BF16 ? 0x007fu : 0x03ffu);
+}
+template <int DT>
+__device__ __forceinline__ unsigned int key_hi() {  // key of +inf
+  return DT == MLXF_DTYPE_F32 ? 0xff800000u : (DT == MLXF_DTYPE_BF16 ? 0xff80u : 0xfc00u);
+}
+
+// log2 of the weight: (z' - Mp) * log2(e) as one FMA with nc = -RN(Mp * log2 e).
+// The rounding of nc scales every weight of the row by the same factor, which
+// cancels in every mass ratio.
+__device__ __forceinline__ float wlog2(float zp, float nc) { return __builtin_fmaf(zp, LOG2E, nc); }
+
+// w = exp(z' - Mp); for an infinite row max the limit (1 where z' == Mp, else 0).
+__device__ __forceinline__ float wfun(float zp, float Mp, float nc, bool minf) {
+  return minf ? (zp == Mp ? 1.0f : 0.0f) : __builtin_amdgcn_exp2f(wlog2(zp, nc));
+}
+
+// floor(w * 2^40) for w in [0, 1 + 2^-20]: exact fixed-point mass.
+__device__ __forceinline__ unsigned long long q40(float w) {
+  const float t = w * 256.0f;
+  const unsigned int hi = static_cast<unsigned int>(t);
+  const float fr = t - floorf(t);
+  const unsigned int lo = static_cast<unsigned int>(fr * 4294967296.0f);
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+// Value-grid bin of a z' (from its log2 weight x <= ~0): 0 at the row max, 255
+// at R2 = 255 / span below it and everything further down.  Non-increasing in z'.
+__device__ __forceinline__ int vbin_x(float x, float R2) {
+  return max(0, min(__float2int_rz(-x * R2), NB - 1));
+}
+
+// Smallest k in [lo, hi] with pred(k), for pred false then true over [lo, hi]
+// and true at hi: a 64-ary search, one candidate per lane (3 rounds for 16-bit
+// keys, 6 for 32-bit).  The whole wave calls it; every lane gets the result.
+template <typename PRED>
+__device__ __forceinline__ unsigned int wave_search(unsigned int lo, unsigned int hi, PRED pred) {
+  const int lane = threadIdx.x & 63;
+  while (lo < hi) {
+    const unsigned long long span = static_cast<unsigned long long>(hi - lo) + 1ull;
+    const unsigned long long step = (span + 63ull) >> 6;
+    const unsigned long long k64 = static_cast<unsigned long long>(lo) + step * static_cast<unsigned long long>(lane);
+    const unsigned int k = k64 > hi ? hi : static_cast<unsigned int>(k64);
+    const unsigned long long bal = __ballot(pred(k));
+    if (bal == 0ull) {
+      lo = rdl(k, 63) + 1u;
+    } else {
+      const int f = __ffsll(static_cast<long long>(bal)) - 1;
+      const unsigned int kf = rdl(k, f);
+      if (f == 0) {
+        hi = kf;
+        lo = kf;
+      } else {
+        lo = rdl(k, f - 1) + 1u;
+        hi = kf;
+      }
+    }
+  }
+  return lo;
+}
+
+// Smallest z key whose z' reaches y (z' non-decreasing in z); 0xffffffff if
+// none.  Whole wave.
+template <int DT>
+__device__ __forceinline__ unsigned int gkey(float y, float Tr) {
+  if (!(zdiv<DT>(INFINITY, Tr, 1.0f, false) >= y)) return 0xffffffffu;
+  return wave_search(KEY_NEG_INF, KEY_POS_INF,
+                     [&](unsigned int k) { return zdiv<DT>(key2f(k), Tr, 1.0f, false) >= y; });
+}
+
+// z-key bracket [zlo, zhi] of the elements whose z' key lies in [klo, khi].
+// Whole wave.
+template <int DT>
+__device__ __forceinline__ void zbracket(unsigned int klo, unsigned int khi, float Tr, unsigned int* zlo,
+                         unsigned int* zhi) {
+  *zlo = gkey<DT>(kval<DT>(klo), Tr);
+  if (khi >= key_hi<DT>()) {
+    *zhi = KEY_POS_INF;
+  } else {
+    const unsigned int g = gkey<DT>(kval<DT>(khi + 1u), Tr);
+    *zhi = g == 0u ? 0u : g - 1u;
+  }
+}
+
+__device__ __forceinline__ unsigned long long pack_ent(float v, int i) {
+  return pack2(__float_as_uint(v), static_cast<unsigned int>(i));
+}
+
+__device__ __forceinline__ unsigned long long LDP(const unsigned long long* p) { return *p; }
+
+__device__ __forceinline__ unsigned int ld_dev32(const unsigned int* p) {
+  return __hip_atomic_load(const_cast<unsigned int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev32(unsigned int* p, unsigned int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sampled id (and its logprob) of row r.
+template <int DT>
+__device__ __forceinline__ void write_out(const Args& a, int r, int id, double lse, bool want_lp) {
+  a.out_ids[r] = id;
+  if (a.out_lp) {
+    const void* row = row_ptr<DT>(a, r);
+    a.out_lp[r] = want_lp ? static_cast<float>(static_cast<double>(ld1<DT>(row, id)) - lse) : NAN;
+  }
+}
+
+// Uniform draw over the whole vocabulary: what the reference's categorical
+// does when every logit left is -inf (all -inf rows, or a top-p of 0).
+__device__ __forceinline__ int uniform_id(float u, int V) {
+  const double x = floor(static_cast<double>(u) * static_cast<double>(V));
+  return x < V - 1 ? static_cast<int>(x) : V - 1;
+}
+
+// ----------------------------------------------------------- row plans --
+
+// Row plan words (written by a row's finishing workgroup, read by every
+// workgroup of the row in the next stage).
+enum {
+  RS_PHASE = 0,  // phase | flags << 32
+  RS_ZB = 1,     // z-key bracket zlo | zhi << 32 (inclusive)
+  RS_DIG = 2,    // key digits: kb | sh << 32
+  RS_AUX = 3,    // cabove (participants above the bracket) | fkey (z' key filter) << 32
+  RS_GRID = 4,   // Mp bits | R2 bits << 32
+  RS_TGT = 5,    // remaining count / mass target inside the bracket (MASS: 0 = not set)
+  RS_LSE = 6,    // log-sum-exp of the row (fp64 bits)
+  RS_WORDS = 8
+};
+
+struct Plan {
+  unsigned int phase, flags, zlo, zhi, kb, sh, cabove, fkey;
+  float Mp, R2;
+  unsigned long long target;
+  double lse;
+};
+
+__device__ __forceinline__ void plan_store(const Args& a, int r, const Plan& p) {
+  unsigned long long* w = a.rowst + static_cast<size_t>(r) * RS_WORDS;
+  w[RS_PHASE] = pack2(p.phase, p.flags);
+  w[RS_ZB] = pack2(p.zlo, p.zhi);
+  w[RS_DIG] = pack2(p.kb, p.sh);
+  w[RS_AUX] = pack2(p.cabove, p.fkey);
+  w[RS_GRID] = pack2(__float_as_uint(p.Mp), __float_as_uint(p.R2));
+  w[RS_TGT] = p.target;
+  w[RS_LSE] = static_cast<unsigned long long>(__double_as_longlong(p.lse));
+}
+__device__ __forceinline__ Plan plan_unpack(const unsigned long long* w) {  // (LDS or global)
+  Plan p;
+  p.phase = static_cast<unsigned int>(w[RS_PHASE]);
+  p.flags = static_cast<unsigned int>(w[RS_PHASE] >> 32);
+  p.zlo = static_cast<unsigned int>(w[RS_ZB]);
+  p.zhi = static_cast<unsigned int>(w[RS_ZB] >> 32);
+  p.kb = static_cast<unsigned int>(w[RS_DIG]);
+  p.sh = static_cast<unsigned int>(w[RS_DIG] >> 32);
+  p.cabove = static_cast<unsigned int>(w[RS_AUX]);
+  p.fkey = static_cast<unsigned int>(w[RS_AUX] >> 32);
+  p.Mp = __uint_as_float(static_cast<unsigned int>(w[RS_GRID]));
+  p.R2 = __uint_as_float(static_cast<unsigned int>(w[RS_GRID] >> 32));
+  p.target = w[RS_TGT];
+  p.lse = __longlong_as_double(static_cast<long long>(w[RS_LSE]));
+  return p;
+}
+
+// First level of a selection over the z' keys >= fkey: the value grid when the
+// row max and the span below it are finite and positive, else the top 8 bits of
+// the key.  span2 is the span in log2-weight units.
+template <int DT>
+__device__ __forceinline__ void plan_level1(Plan& p, float span2) {
+  if (__builtin_isfinite(p.Mp) && span2 > 0.0f && __builtin_isfinite(span2)) {
+    p.flags |= FL_VGRID;
+    p.R2 = 255.0f / span2;
+  } else {
+    p.flags &= ~static_cast<unsigned int>(FL_VGRID);
+    p.R2 = 0.0f;
+  }
+  p.kb = 0u;
+  p.sh = static_cast<unsigned int>(keybits<DT>() - 8);
+}
+
+// ================================================================ k_scan1 ==
+//
+// Stage 0, one workgroup per slice: the one HBM read of every logit.
+
+struct S1Lds {
+  TopEnt surv[SURV];
+  TopEnt lists[WAVES * LIST];  // bitonic fallback for many survivors
+  float rf[WAVES];
+  float rmin[WAVES];
+  int ri[WAVES];
+  unsigned int ramin[WAVES];
+  int ramax[WAVES];
+  double rd[WAVES];
+  unsigned int rth[WAVES];
+  int rsc[WAVES + 1];
+  float thv;
+  int thi;
+};
+
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
+  __shared__ S1Lds sh;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int bid = static_cast<int>(blockIdx.x);
+  const int S = a.S;
+  const int r = bid / S, s = bid - r * S;
+  // a new call: the stage lists of the previous call (whatever number of stages
+  // it launched) are spent
+  if (bid == 0 && tid < NSTAGE) a.actcnt[tid] = 0u;
+  const Mode md = decode<DT>(a, r);
+  const void* row = row_ptr<DT>(a, r);
+  const int beg = s * a.L;
+  const int end = min(a.V, beg + a.L);
+  constexpr int NIT = EPT / VEC;
+  // rows that reach the refine stages: the division range of the slice, and
+  // (top-k rows) its minimum
+  const bool refine = md.kind == KIND_TEMP || md.kind == KIND_TOPP || md.kind == KIND_KHIST;
+  const bool want_min = md.kind == KIND_KHIST || md.kind == KIND_TOPP;
+
+  float v[EPT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
+#define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
+
+  float tmax = v[0];
+#pragma unroll
+  for (int e = 1; e < EPT; ++e) tmax = fmaxf(tmax, v[e]);
+  {
+    const float wm = wave_max(tmax);
+    if (lane == 0) sh.rf[wid] = wm;
+  }
+  if (refine) {
+    // smallest nonzero |z| (as bits - 1, so zeros wrap past every value) and
+    // largest finite |z| (as bits + 2^23: infinities wrap negative)
+    unsigned int amin = 0xffffffffu;
+    int amax = 0;
+    float tmin = INFINITY;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const bool ok = MLXF_IDX(e) < end;
+      const unsigned int az = __float_as_uint(v[e]) & 0x7fffffffu;
+      amin = min(amin, ok ? az - 1u : 0xffffffffu);
+      amax = max(amax, ok ? static_cast<int>(az + 0x00800000u) : 0);
+      if (want_min) tmin = fminf(tmin, ok ? v[e] : INFINITY);
+    }
+    amin = wave_min(amin);
+    amax = wave_max(amax);
+    if (want_min) tmin = wave_min(tmin);
+    if (lane == 0) {
+      sh.ramin[wid] = amin;
+      sh.ramax[wid] = amax;
+      sh.rmin[wid] = tmin;
+    }
+  }
+  // lowest index of the thread max
+  int tbi = INT_MAX;
+#pragma unroll
+  for (int e = EPT - 1; e >= 0; --e)
+    if (v[e] == tmax && MLXF_IDX(e) < end) tbi = MLXF_IDX(e);
+  if (md.need_list) {
+    // theta: each wave's 16th largest thread-maximum key, by bisection on the
+    // key bits with ballots; the smallest of the four is reached by at least 64
+    // elements (16 thread maxima per wave), so the slice's best 64 all reach it.
+    // (A thread with no element in the slice counts as key 0, below every key.)
+    const unsigned int kt = tbi != INT_MAX ? f2key(tmax) : 0u;
+    unsigned int tw = 0u;
+    for (int b = 31; b >= 0; --b) {
+      const unsigned int c = tw | (1u << b);
+      if (__popcll(__ballot(kt >= c)) >= LIST / WAVES) tw = c;
+    }
+    if (lane == 0) sh.rth[wid] = tw;
+  }
+  __syncthreads();
+  float zmax = sh.rf[0];
+#pragma unroll
+  for (int w2 = 1; w2 < WAVES; ++w2) zmax = fmaxf(zmax, sh.rf[w2]);
+  {
+    const int wa = wave_min(tmax == zmax ? tbi : INT_MAX);
+    if (lane == 0) sh.ri[wid] = wa;
+  }
+  if (md.need_lse) {
+    float t = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      if (MLXF_IDX(e) < end) t += wexp(v[e], zmax);
+    const double ws = wave_sum(static_cast<double>(t));
+    if (lane == 0) sh.rd[wid] = ws;
+  }
+  __syncthreads();
+  int nsurv = 0;
+  if (md.need_list) {
+    // survivors: every element whose key reaches theta, in slots from a block
+    // scan of the per-thread counts
+    unsigned int th = sh.rth[0];
+#pragma unroll
+    for (int w2 = 1; w2 < WAVES; ++w2) th = min(th, sh.rth[w2]);
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && f2key(v[e]) >= th) ? 1 : 0;
+    int pos = block_excl_scan<int>(mine, sh.rsc, &nsurv);
+    if (nsurv <= SURV) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int i = MLXF_IDX(e);
+        if (i < end && f2key(v[e]) >= th) {
+          sh.surv[pos].v = v[e];
+          sh.surv[pos].i = i;
+          ++pos;
+        }
+      }
+    } else {
+      // (heavy ties at theta) the exact 64th best thread maximum instead, which
+      // at most 64 * EPT elements reach: bitonic sort of each wave's 64 and a
+      // tree merge; with fewer than 64 threads holding elements it is the
+      // sentinel and every element survives
+      float lv = tmax;
+      int li = tbi;
+      wave_sort(lv, li);
+      tree_merge(lv, li, sh.lists, WAVES);
+      if (tid == LIST - 1) {
+        sh.thv = lv;
+        sh.thi = li;
+      }
+      __syncthreads();
+      const float tv = sh.thv;
+      const int ti = sh.thi;
+      mine = 0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && !better(tv, ti, v[e], MLXF_IDX(e))) ? 1 : 0;
+      pos = block_excl_scan<int>(mine, sh.rsc, &nsurv);
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int i = MLXF_IDX(e);
+        if (i < end && !better(tv, ti, v[e], i)) {
+          sh.surv[pos].v = v[e];
+          sh.surv[pos].i = i;
+          ++pos;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  int zarg = sh.ri[0];
+#pragma unroll
+  for (int w2 = 1; w2 < WAVES; ++w2) zarg = min(zarg, sh.ri[w2]);
+  double lse_s = 0.0;
+  if (md.need_lse) {
+    lse_s = sh.rd[0];
+#pragma unroll
+    for (int w2 = 1; w2 < WAVES; ++w2) lse_s += sh.rd[w2];
+  }
+  float zmin = 0.0f;
+  unsigned int sfl = 0u;
+  if (refine) {
+    unsigned int amin = sh.ramin[0];
+    int amax = sh.ramax[0];
+    zmin = sh.rmin[0];
+#pragma unroll
+    for (int w2 = 1; w2 < WAVES; ++w2) {
+      amin = min(amin, sh.ramin[w2]);
+      amax = max(amax, sh.ramax[w2]);
+      zmin = fminf(zmin, sh.rmin[w2]);
+    }
+    // the FMA-corrected division is exact when every nonzero |z| >= 2^-96 and
+    // every finite |z| < 2^100
+    sfl = (amin >= 0x0f7fffffu && amax < static_cast<int>(0x71800000u + 0x00800000u)) ? static_cast<unsigned int>(SL_FAST) : 0u;
+  }
+  if (md.need_list) {
+    unsigned long long* dst = a.list + (static_cast<size_t>(r) * S + s) * LIST;
+    const int ntot = nsurv;
+    if (ntot <= THREADS) {
+      // rank of each survivor among the survivors: its place in the list
+      if (tid < LIST && tid >= ntot) dst[tid] = pack_ent(-INFINITY, INT_MAX);
+      if (tid < ntot) {
+        const float mv = sh.surv[tid].v;
+        const int mi = sh.surv[tid].i;
+        int rank = 0;
+#pragma unroll 16
+        for (int j = 0; j < ntot; ++j) rank += better(sh.surv[j].v, sh.surv[j].i, mv, mi) ? 1 : 0;
+        if (rank < LIST) dst[rank] = pack_ent(mv, mi);
+      }
+    } else {
+      // many survivors (heavy ties at theta): 64-entry chunks sorted and merged
+      const int nch = (ntot + LIST - 1) / LIST;
+      float sv = -INFINITY;
+      int si = INT_MAX;
+      for (int ch = wid; ch < nch; ch += WAVES) {
+        const int c = ch * LIST + lane;
+        float cv = -INFINITY;
+        int ci = INT_MAX;
+        if (c < ntot) {
+          cv = sh.surv[c].v;
+          ci = sh.surv[c].i;
+        }
+        wave_sort(cv, ci);
+        wave_list_merge(sv, si, cv, ci);
+      }
+      tree_merge(sv, si, sh.lists, nch < WAVES ? nch : WAVES);
+      if (wid == 0) dst[lane] = pack_ent(sv, si);
+    }
+  }
+#undef MLXF_IDX
+  if (tid == 0) {
+    unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + s) * 4;
+    rp[0] = pack2(__float_as_uint(zmax), static_cast<unsigned int>(zarg));
+    rp[1] = pack2(__float_as_uint(zmin), sfl);
+    rp[2] = static_cast<unsigned long long>(__double_as_longlong(lse_s));
+  }
+}
+
+// ============================================================== k_decide1 ==
+//
+// Stage 0, one workgroup per row: argmax, log-sum-exp, top_logprobs, top-k <= 63
+// from the merged best-64 lists; a plan for every other sampling row.
+
+struct D1Lds {
+  unsigned long long lst[MAX_S * LIST];  // (the per-slice lists; dead once merged)
+  TopEnt lists[WAVES * LIST];
+  TopEnt mlist[LIST];
+  float szmax[MAX_S];
+  int szarg[MAX_S];
+  float szmin[MAX_S];
+  double slse[MAX_S];
+  float zmax, zmin;
+  int zarg;
+  double lse;
+  int sel[4];
+};
+
+// Top-k <= 63 from the row's merged best-64 list, by one wave.  Returns false
+// when the list may miss elements tied at the k-th value of z' (the caller then
+// plans a full top-k selection).  The nucleus and the draw follow
+// src/sample/sampler.cpp:63-85,165 on the list: (z' desc, index asc) order,
+// keep while the mass before an entry is < p * W_k, inverse CDF in vocabulary
+// order.
+template <int DT>
+__device__ __forceinline__ bool klist_resolve(const Mode& md, float Mp, const TopEnt* ml, int* id_out) {
+  const int lane = threadIdx.x & 63;
+  const float lv = ml[lane].v;
+  const int li = ml[lane].i;
+  const bool real = li != INT_MAX;
+  const float zp = real ? zdiv<DT>(lv, md.Tr, md.y, false) : -INFINITY;
+  const float tau = rdl(zp, md.kk - 1);
+  const int last_i = rdl(li, LIST - 1);
+  const float last_zp = rdl(zp, LIST - 1);
+  if (last_i != INT_MAX && !(last_zp < tau)) return false;
+  const bool in_k = real && zp >= tau;
+  float sv = in_k ? zp : -INFINITY;
+  int si = in_k ? li : INT_MAX;
+  // (z' desc, index asc): the list is in (z desc, index asc) order and z' is
+  // non-decreasing in z, so only entries whose z' the rounding made equal can be
+  // out of order -- and then some neighbouring pair is
+  const float nsv = __shfl_down(sv, 1, 64);
+  const int nsi = __shfl_down(si, 1, 64);
+  if (__ballot(lane < 63 && sv == nsv && si > nsi)) wave_sort(sv, si);
+  const bool k1 = si != INT_MAX;
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  const unsigned long long w = k1 ? q40(wfun(sv, Mp, nc, minf)) : 0ull;
+  const unsigned long long incl = wave_incl_scan(w);
+  const unsigned long long Wk = rdl(incl, 63);
+  bool keep = k1;
+  if (md.topp) {
+    const unsigned long long PW =
+        static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
+    keep = k1 && (incl - w) < PW;
+  }
+  const unsigned long long wf = keep ? w : 0ull;
+  const unsigned long long Wf = wave_sum(wf);
+  unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(Wf));
+  if (Wf == 0)
+    Tu = 0;
+  else if (Tu >= Wf)
+    Tu = Wf - 1;
+  // kept mass at or before my index, in vocabulary order
+  unsigned long long cum = 0;
+  for (int q = 0; q < 64; ++q) {
+    const unsigned long long wq = rdl(wf, q);
+    const int iq = __builtin_amdgcn_readlane(si, q);
+    if (iq <= si) cum += wq;
+  }
+  const int cand = wave_min((keep && (Wf == 0 || (wf > 0 && cum > Tu))) ? si : INT_MAX);
+  *id_out = cand == INT_MAX ? rdl(si, 0) : cand;
+  return true;
+}
+
+// Put row r (its next phase in the high half) on the list of refine stage
+// `stage` (0-based).
+__device__ __forceinline__ void enlist(const Args& a, int stage, int r, unsigned int phase) {
+  const unsigned int pos =
+      __hip_atomic_fetch_add(a.actcnt + stage, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  a.actlist[static_cast<size_t>(stage) * a.B + pos] = static_cast<unsigned int>(r) | (phase << 16);
+}
+
+// =================================================================== stages ==
+
+// Shared memory of a stage's slice pass (kept small: it bounds the occupancy
+// of the streaming kernels).
+struct SLds {
+  unsigned long long pw[RS_WORDS];   // the row plan as read
+  unsigned int hc[NB];               // slice histogram: counts
+  unsigned long long hm[NB];         // slice histogram: masses
+  unsigned long long ru[WAVES + 1];
+  unsigned int rv[WAVES + 1];
+  unsigned int ncand;
+};
+// ... and of a deciding workgroup.
+struct RLds {
+  SLds sl;
+  unsigned long long cand[CAP];      // gathered candidates (z' key | index << 32)
+  unsigned long long kept[MAX_S];    // per-slice kept mass
+  unsigned int tcnt[MAX_S];          // per-slice ties / counts
+  int ri[WAVES + 1];
+  int sel[8];
+  unsigned long long selu[8];
+  unsigned int kmin, kmax, ncand;
+  int found;
+};
+
+// ---- one slice of one stage: the histogram, the gathered elements or the kept
+// mass of slice s of row r under the plan in sh.pw.  Results go to the
+// workspace with plain stores (read by the next kernel, or -- in the last
+// stage -- by this workgroup after a full wait and a barrier).
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ void slice_stage(const Args& a, int r, int s, const Plan& pl, SLds& sh) {
+  const int tid = threadIdx.x;
+  const Mode md = decode<DT>(a, r);
+  const void* row = row_ptr<DT>(a, r);
+  const int beg = s * a.L;
+  const int end = min(a.V, beg + a.L);
+  constexpr int NIT = EPT / VEC;
+  const unsigned int sfl = static_cast<unsigned int>(a.rec[(static_cast<size_t>(r) * a.S + s) * 4 + 1] >> 32);
+  const bool fast = !md.tslow && (sfl & SL_FAST);
+  const float Mp = pl.Mp;
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  const bool vgrid = (pl.flags & FL_VGRID) != 0;
+  const unsigned int zlo = pl.zlo, zhi = pl.zhi;
+
+  float v[EPT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
+#define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
+
+  if (pl.phase == PH_COUNT || pl.phase == PH_MASS) {
+    const bool mass = pl.phase == PH_MASS;
+    for (int b = tid; b < NB; b += THREADS) {
+      sh.hc[b] = 0u;
+      sh.hm[b] = 0ull;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const unsigned int zk = f2key(v[e]);
+      if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) {
+        const float zp = zdiv<DT>(v[e], md.Tr, md.y, fast);
+        const float x = wlog2(zp, nc);
+        unsigned long long q = 0;
+        if (mass) q = q40(minf ? (zp == Mp ? 1.0f : 0.0f) : __builtin_amdgcn_exp2f(x));
+        if (!mass || q) {
+          const int bin = vgrid ? vbin_x(x, pl.R2)
+                                : max(0, NB - 1 - static_cast<int>(min((zkey<DT>(zp) - pl.kb) >> pl.sh, 255u)));
+          atomicAdd(&sh.hc[bin], 1u);
+          if (mass) atomicAdd(&sh.hm[bin], q);
+        }
+      }
+    }
+    __syncthreads();
+    // cumulative from the top bin down: the deciding step reads a bin's total
+    // and everything above it in one word
+    const size_t o = (static_cast<size_t>(r) * a.S + s) * NB;
+    unsigned int cex, cin, ctot;
+    block_scan<unsigned int>(sh.hc[tid], sh.rv, &cex, &cin, &ctot);
+    a.hcnt[o + tid] = cin;
+    if (mass) {
+      unsigned long long mex, min_, mtot;
+      block_scan<unsigned long long>(sh.hm[tid], sh.ru, &mex, &min_, &mtot);
+      a.hmass[o + tid] = min_;
+    }
+  } else if (pl.phase == PH_GATHER) {
+    // the slice's elements in the bracket: one reservation per workgroup
+    unsigned int mine = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const unsigned int zk = f2key(v[e]);
+      mine += (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) ? 1u : 0u;
+    }
+    unsigned int total;
+    unsigned int pos = block_excl_scan<unsigned int>(mine, sh.rv, &total);
+    if (tid == 0)
+      sh.ncand = total ? __hip_atomic_fetch_add(a.ncand + r, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+    __syncthreads();
+    pos += sh.ncand;
+    unsigned long long* dst = a.cand + static_cast<size_t>(r) * CAP;
+    if (mine) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const unsigned int zk = f2key(v[e]);
+        if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) {
+          const float zp = zdiv<DT>(v[e], md.Tr, md.y, fast);
+          if (pos < CAP) dst[pos] = pack2(zkey<DT>(zp), static_cast<unsigned int>(MLXF_IDX(e)));
+          ++pos;
+        }
+      }
+    }
+  } else if (pl.phase == PH_DRAWSUM) {
+    unsigned long long t = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const unsigned int zk = f2key(v[e]);
+      if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) {
+        const float zp = zdiv<DT>(v[e], md.Tr, md.y, fast);
+        t += q40(wfun(zp, Mp, nc, minf));
+      }
+    }
+    t = block_sum<unsigned long long>(t, sh.ru);
+    if (tid == 0) a.dsum[static_cast<size_t>(r) * a.S + s] = t;
+  }
+#undef MLXF_IDX
+}
+
+// ---- the draw: walk slice s in vocabulary order; kept elements are those with
+// z' key > tau, and the first tie_lim (in index order) of those equal to tau.
+// Returns the first kept element at which the running kept mass exceeds rem.
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ int walk(const Args& a, int r, int s, float Mp, unsigned long long rem, unsigned int tau,
+                    unsigned int tie_lim, RLds& sh) {
+  const int tid = threadIdx.x;
+  const Mode md = decode<DT>(a, r);
+  const void* row = row_ptr<DT>(a, r);
+  const int b0 = s * a.L, e0 = min(a.V, b0 + a.L);
+  const int my0 = b0 + tid * EPT;
+  const unsigned int sfl = static_cast<unsigned int>(a.rec[(static_cast<size_t>(r) * a.S + s) * 4 + 1] >> 32);
+  const bool fast = !md.tslow && (sfl & SL_FAST);
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  // thread t owns EPT consecutive elements, held as z' keys
+  unsigned int kz[EPT];
+#pragma unroll
+  for (int it = 0; it < EPT / VEC; ++it) {
+    float z[VEC];
+    load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) kz[it * VEC + j] = zkey<DT>(zdiv<DT>(z[j], md.Tr, md.y, fast));
+  }
+  unsigned int nt = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) nt += (my0 + e < e0 && kz[e] == tau) ? 1u : 0u;
+  unsigned int tex, tin, ttot;
+  block_scan<unsigned int>(nt, sh.sl.rv, &tex, &tin, &ttot);
+  auto qof = [&](int e, unsigned int& rk) -> unsigned long long {
+    const bool valid = my0 + e < e0;
+    const bool tie = valid && kz[e] == tau;
+    const bool kept = valid && (kz[e] > tau || (tie && rk < tie_lim));
+    rk += tie ? 1u : 0u;
+    return kept ? q40(wfun(kval<DT>(kz[e]), Mp, nc, minf)) : 0ull;
+  };
+  unsigned long long qs = 0;
+  int last = -1;
+  {
+    unsigned int rk = tex;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const unsigned long long q = qof(e, rk);
+      qs += q;
+      if (q > 0) last = my0 + e;
+    }
+  }
+  unsigned long long ex, in, tot;
+  block_scan<unsigned long long>(qs, sh.sl.ru, &ex, &in, &tot);
+  if (tid == 0) sh.found = -1;
+  __syncthreads();
+  if (ex <= rem && rem < in) {
+    unsigned long long c = ex;
+    unsigned int rk = tex;
+    int pick = -1;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const unsigned long long q = qof(e, rk);
+      c += q;
+      if (pick < 0 && q > 0 && c > rem) pick = my0 + e;
+    }
+    sh.found = pick;
+  }
+  __syncthreads();
+  int id = sh.found;
+  if (id < 0) {  // rem reached no element: the last kept element with positive mass
+    const int lm = wave_max(last);
+    if ((tid & 63) == 0) sh.ri[tid >> 6] = lm;
+    __syncthreads();
+    if (tid == 0) {
+      int m = -1;
+      for (int w2 = 0; w2 < WAVES; ++w2) m = max(m, sh.ri[w2]);
+      sh.found = m < 0 ? b0 : m;
+    }
+    __syncthreads();
+    id = sh.found;
+  }
+  __syncthreads();
+  return id;
+}
+
+// Pick the slice holding the draw from per-slice kept masses sh.kept[0..S) and
+// walk it.  sh.tcnt[s] holds the kept ties of slice s unless all ties are kept.
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ int draw(const Args& a, int r, const Mode& md, float Mp, unsigned int tau, bool all_ties,
+                    RLds& sh) {
+  const int tid = threadIdx.x;
+  const int S = a.S;
+  if (tid == 0) {
+    unsigned long long W = 0;
+    for (int t = 0; t < S; ++t) W += sh.kept[t];
+    unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(W));
+    if (W == 0)
+      Tu = 0;
+    else if (Tu >= W)
+      Tu = W - 1;
+    unsigned long long cum = 0;
+    int st = -1;
+    unsigned long long rem = 0;
+    for (int t = 0; t < S; ++t) {
+      if (sh.kept[t] > 0) {
+        st = t;
+        rem = Tu - cum;
+        if (cum + sh.kept[t] > Tu) break;
+      }
+      cum += sh.kept[t];
+    }
+    if (st < 0) {
+      st = 0;
+      rem = 0;
+    }
+    sh.sel[0] = st;
+    sh.selu[0] = rem;
+    sh.sel[1] = static_cast<int>(all_ties ? 0xffffffffu : sh.tcnt[st]);
+  }
+  __syncthreads();
+  const int st = sh.sel[0];
+  const unsigned long long rem = sh.selu[0];
+  const unsigned int tl = static_cast<unsigned int>(sh.sel[1]);
+  __syncthreads();
+  return walk<DT, EPT, VECOK>(a, r, st, Mp, rem, tau, tl, sh);
+}
+
+// ---- radix selection over the gathered candidates (LDS).  Over candidates
+// with pred(c), values of the field F (the z' key, scanned in descending
+// order, or the index, ascending) are scanned with measure 1 (counts) or the
+// candidate's fixed-point mass; returns the first value v at which
+// before + measure(v) >= target (> target when strict) with measure(v) > 0,
+// where before is the measure of the values scanned before v.  When no value
+// qualifies, the last value with a positive measure is returned.  *before_out
+// gets `before`, *gcount the number of candidates equal to v.  8-bit digits;
+// the leading bits all participants share are skipped.  Whole workgroup.
+template <int DT, bool BY_KEY, bool MASSM, typename PRED>
+__device__ __forceinline__ unsigned int cselect(int n, PRED pred, float Mp, unsigned long long target, bool strict, RLds& sh,
+                                unsigned long long* before_out, unsigned int* gcount) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  auto field = [](unsigned long long c) {
+    return BY_KEY ? static_cast<unsigned int>(c) : static_cast<unsigned int>(c >> 32);
+  };
+  auto meas = [&](unsigned long long c) -> unsigned long long {
+    if (!MASSM) return 1ull;
+    return q40(wfun(kval<DT>(static_cast<unsigned int>(c)), Mp, nc, minf));
+  };
+  unsigned int lo = 0xffffffffu, hi = 0u;
+  for (int c = tid; c < n; c += THREADS) {
+    const unsigned long long e = sh.cand[c];
+    if (pred(e) && meas(e) > 0) {
+      lo = min(lo, field(e));
+      hi = max(hi, field(e));
+    }
+  }
+  lo = wave_min(lo);
+  hi = wave_max(hi);
+  if (tid == 0) {
+    sh.kmin = 0xffffffffu;
+    sh.kmax = 0u;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    atomicMin(&sh.kmin, lo);
+    atomicMax(&sh.kmax, hi);
+  }
+  __syncthreads();
+  lo = sh.kmin;
+  hi = sh.kmax;
+  __syncthreads();
+  if (lo > hi) {  // no participant with a positive measure
+    *before_out = 0;
+    *gcount = 0;
+    return 0;
+  }
+  int shift = 0;
+  if (lo != hi) shift = ((31 - __clz(static_cast<int>(lo ^ hi))) >> 3) << 3;
+  unsigned int mask = shift + 8 >= 32 ? 0u : ~((1u << (shift + 8)) - 1u);
+  unsigned int prefix = lo & mask;
+  unsigned long long before = 0;
+  unsigned int g = 0;
+  for (; shift >= 0; shift -= 8) {
+    for (int d = tid; d < NB; d += THREADS) {
+      sh.sl.hc[d] = 0u;
+      sh.sl.hm[d] = 0ull;
+    }
+    __syncthreads();
+    for (int c = tid; c < n; c += THREADS) {
+      const unsigned long long e = sh.cand[c];
+      const unsigned int f = field(e);
+      if (pred(e) && (f & mask) == prefix) {
+        const unsigned long long m = meas(e);
+        if (m > 0) {
+          const int d = static_cast<int>((f >> shift) & 255u);
+          const int pos = BY_KEY ? NB - 1 - d : d;
+          atomicAdd(&sh.sl.hc[pos], 1u);
+          if (MASSM) atomicAdd(&sh.sl.hm[pos], m);
+        }
+      }
+    }
+    __syncthreads();
+    if (wid == 0) {
+      unsigned long long val[4];
+      unsigned int cnt[4];
+      unsigned long long sum = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        cnt[q] = sh.sl.hc[4 * lane + q];
+        val[q] = MASSM ? sh.sl.hm[4 * lane + q] : static_cast<unsigned long long>(cnt[q]);
+        sum += val[q];
+      }
+      const unsigned long long inc = wave_incl_scan(sum);
+      unsigned long long run = before + inc - sum;
+      int found = NB, lastne = -1;
+      unsigned long long bef = 0, bef_last = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int pos = 4 * lane + q;
+        if (found == NB && val[q] > 0 && (strict ? run + val[q] > target : run + val[q] >= target)) {
+          found = pos;
+          bef = run;
+        }
+        if (val[q] > 0) {
+          lastne = pos;
+          bef_last = run;
+        }
+        run += val[q];
+      }
+      int best = wave_min(found);
+      unsigned long long b;
+      if (best < NB) {
+        b = rdl(bef, best >> 2);
+      } else {
+        best = wave_max(lastne);
+        if (best < 0) best = 0;
+        b = rdl(bef_last, best >> 2);
+      }
+      if (lane == 0) {
+        sh.sel[2] = best;
+        sh.sel[3] = static_cast<int>(sh.sl.hc[best]);
+        sh.selu[1] = b;
+      }
+    }
+    __syncthreads();
+    const int pos = sh.sel[2];
+    const unsigned int d = static_cast<unsigned int>(BY_KEY ? NB - 1 - pos : pos);
+    prefix |= d << shift;
+    mask |= 255u << shift;
+    before = sh.selu[1];
+    g = static_cast<unsigned int>(sh.sel[3]);
+    __syncthreads();
+  }
+  *before_out = before;
+  *gcount = g;
+  return prefix;
+}
+
+// Block sum of the fixed-point masses of the candidates with pred.
+template <int DT, typename PRED>
+__device__ __forceinline__ unsigned long long cmass(int n, PRED pred, float Mp, RLds& sh) {
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  unsigned long long t = 0;
+  for (int c = threadIdx.x; c < n; c += THREADS) {
+    const unsigned long long e = sh.cand[c];
+    if (pred(e)) t += q40(wfun(kval<DT>(static_cast<unsigned int>(e)), Mp, nc, minf));
+  }
+  return block_sum<unsigned long long>(t, sh.sl.ru);
+}
+
+// Number of ties kept at a cutoff: the mass still to cover (need) in units of
+// one tie's mass (wt), at least 1, at most g.
+__device__ __forceinline__ unsigned int ties_kept(unsigned long long need, unsigned long long wt, unsigned int g) {
+  unsigned long long t = g;
+  if (wt > 0) {
+    const unsigned long long nd = (need + wt - 1) / wt;
+    t = nd < t ? nd : t;
+  }
+  if (t == 0) t = 1;
+  return static_cast<unsigned int>(t);
+}
+
+// Publish wave 0's bracket [klo, khi] -> z-key bracket to the workgroup.
+template <int DT>
+__device__ __forceinline__ void set_bracket(Plan& pl, unsigned int klo, unsigned int khi, float Tr, RLds& sh) {
+  if ((threadIdx.x >> 6) == 0) {
+    unsigned int zl, zh;
+    zbracket<DT>(klo, khi, Tr, &zl, &zh);
+    if (threadIdx.x == 0) {
+      sh.sel[6] = static_cast<int>(zl);
+      sh.sel[7] = static_cast<int>(zh);
+    }
+  }
+  __syncthreads();
+  pl.zlo = static_cast<unsigned int>(sh.sel[6]);
+  pl.zhi = static_cast<unsigned int>(sh.sel[7]);
+  __syncthreads();
+}
+
+// Digit level over the key range [klo, khi]: 256 bins of 2^sh keys from kb.
+__device__ __forceinline__ void set_digits(Plan& pl, unsigned int klo, unsigned int khi) {
+  pl.flags &= ~static_cast<unsigned int>(FL_VGRID);
+  pl.kb = klo;
+  const unsigned int span = khi - klo;
+  const int bl = span ? 32 - __clz(static_cast<int>(span)) : 0;
+  pl.sh = static_cast<unsigned int>(bl > 8 ? bl - 8 : 0);
+}
+
+// ---- the deciding step of a stage for row r (whole workgroup): reads the
+// slices' results, then either writes the sampled id or leaves the next plan in
+// sh.sl.pw and in the row's plan words.
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int ph, const unsigned long long* pwsrc,
+                                             RLds& sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int S = a.S;
+  // The slices' results for phase ph, requested together with the plan words
+  // (pwsrc: the row's plan in global memory, or its copy in LDS): thread t owns
+  // histogram bin t and sums every slice's cumulative count and mass at t;
+  // thread t < S holds slice t's mass above the bracket so far, or its kept mass.
+  const bool hist = ph == PH_COUNT || ph == PH_MASS;
+  const bool mass = ph == PH_MASS;
+  const size_t o0 = static_cast<size_t>(r) * S * NB;
+  unsigned int Cc = 0;
+  unsigned long long Mc = 0;
+  for (int t0 = 0; t0 < S; t0 += 32) {
+    unsigned int cc[32];
+    unsigned long long mc[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const size_t o = o0 + static_cast<size_t>(t0 + j) * NB + tid;
+      cc[j] = (hist && t0 + j < S) ? a.hcnt[o] : 0u;
+      mc[j] = (mass && t0 + j < S) ? a.hmass[o] : 0ull;
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      Cc += cc[j];
+      Mc += mc[j];
+    }
+  }
+  unsigned long long pre = 0;
+  if (tid < S) {
+    if (mass) pre = a.above[static_cast<size_t>(r) * S + tid];
+    if (ph == PH_DRAWSUM) pre = a.dsum[static_cast<size_t>(r) * S + tid];
+  }
+  const unsigned int ng = (ph == PH_GATHER && tid == 0) ? a.ncand[r] : 0u;
+  Plan pl = plan_unpack(pwsrc);
+  const Mode md = decode<DT>(a, r);
+  const float Mp = pl.Mp;
+  const float nc = -(Mp * LOG2E);
+  const bool minf = !__builtin_isfinite(Mp);
+  const unsigned int khi_all = key_hi<DT>(), klo_all = key_lo<DT>();
+  bool done = false;
+  int id = 0;
+
+  if (hist) {
+    const unsigned long long abp = pre;
+    const unsigned long long mcum = mass ? Mc : static_cast<unsigned long long>(Cc);
+    sh.sl.hc[tid] = Cc;
+    sh.sl.hm[tid] = mcum;
+    if (tid == 0) sh.sel[4] = NB;
+    __syncthreads();
+    if (mass && pl.target == 0) {
+      // first mass level: the nucleus target p * W over the participants
+      const unsigned long long PW =
+          static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(sh.sl.hm[NB - 1])));
+      pl.target = PW < 1 ? 1 : PW;
+    }
+    // the chosen bin: the first whose cumulative measure reaches the target
+    // (the total, should rounding leave the target out of reach)
+    {
+      const unsigned long long tgt = pl.target < sh.sl.hm[NB - 1] ? pl.target : sh.sl.hm[NB - 1];
+      const unsigned long long bal = __ballot(mcum >= tgt);
+      if (bal && lane == 0) atomicMin(&sh.sel[4], wid * 64 + __ffsll(static_cast<long long>(bal)) - 1);
+    }
+    __syncthreads();
+    const int bstar = sh.sel[4] < NB ? sh.sel[4] : NB - 1;
+    const unsigned long long abv = bstar > 0 ? sh.sl.hm[bstar - 1] : 0ull;  // measure above the bin
+    const unsigned int cabv = bstar > 0 ? sh.sl.hc[bstar - 1] : 0u;         // participants above it
+    const unsigned int cstar = sh.sl.hc[bstar] - cabv;                     // participants in it
+    // per slice (thread t < S for slice t): the participants in the bin, and
+    // the mass above it (MASS); the cumulative words around the bin are re-read
+    // (they are in L2 by now)
+    if (tid < S) {
+      const size_t os = o0 + static_cast<size_t>(tid) * NB;
+      const unsigned int cb = a.hcnt[os + bstar];
+      const unsigned int cb1 = bstar > 0 ? a.hcnt[os + bstar - 1] : 0u;
+      const unsigned long long mb1 = (mass && bstar > 0) ? a.hmass[os + bstar - 1] : 0ull;
+      sh.tcnt[tid] = cb - cb1;
+      if (mass) {
+        sh.kept[tid] = abp + mb1;
+        a.above[static_cast<size_t>(r) * S + tid] = abp + mb1;
+      }
+    }
+    // key range [klo, khi] of the chosen bin: wave 0 the low edge, wave 1 the
+    // high edge, wave 2 the first key with a positive mass
+    if (tid == 0) {
+      sh.sel[6] = 0;
+      sh.sel[7] = static_cast<int>(khi_all);
+      sh.sel[3] = static_cast<int>(klo_all);
+    }
+    __syncthreads();
+    if (pl.flags & FL_VGRID) {
+      auto vb = [&](unsigned int k) { return vbin_x(wlog2(kval<DT>(k), nc), pl.R2); };
+      if (wid == 0) {
+        const unsigned int klo = wave_search(klo_all, khi_all, [&](unsigned int k) { return vb(k) <= bstar; });
+        if (lane == 0) sh.sel[6] = static_cast<int>(klo);
+      } else if (wid == 1 && bstar > 0) {
+        const unsigned int nx = wave_search(klo_all, khi_all, [&](unsigned int k) { return vb(k) <= bstar - 1; });
+        if (lane == 0) sh.sel[7] = static_cast<int>(nx > klo_all ? nx - 1u : klo_all);
+      }
+    } else if (tid == 0) {
+      const unsigned long long lo64 =
+          static_cast<unsigned long long>(pl.kb) + (static_cast<unsigned long long>(NB - 1 - bstar) << pl.sh);
+      const unsigned long long hi64 = lo64 + (1ull << pl.sh) - 1ull;
+      sh.sel[6] = static_cast<int>(lo64);
+      sh.sel[7] = static_cast<int>(hi64 < khi_all ? hi64 : khi_all);
+    }
+    if (mass && wid == 2) {
+      // elements whose mass quantises to zero never count: the bracket starts
+      // at the first key with a positive mass
+      const unsigned int kq = wave_search(klo_all, khi_all, [&](unsigned int k) {
+        return q40(wfun(kval<DT>(k), Mp, nc, minf)) > 0;
+      });
+      if (lane == 0) sh.sel[3] = static_cast<int>(kq);
+    }
+    __syncthreads();
+    {
+      unsigned int klo = static_cast<unsigned int>(sh.sel[6]), khi = static_cast<unsigned int>(sh.sel[7]);
+      if (klo < pl.fkey) klo = pl.fkey;
+      if (klo < static_cast<unsigned int>(sh.sel[3])) klo = static_cast<unsigned int>(sh.sel[3]);
+      if (khi < klo) khi = klo;
+      __syncthreads();
+      if (tid == 0) {
+        sh.sel[6] = static_cast<int>(klo);
+        sh.sel[7] = static_cast<int>(khi);
+      }
+    }
+    __syncthreads();
+    const unsigned int klo = static_cast<unsigned int>(sh.sel[6]);
+    const unsigned int khi = static_cast<unsigned int>(sh.sel[7]);
+    __syncthreads();
+    const bool exact = klo == khi;
+    const unsigned long long rest = pl.target > abv ? pl.target - abv : 1ull;  // still to cover in the bin
+    if (!mass) {
+      const unsigned int nge = pl.cabove + cabv + cstar;  // participants with key >= klo
+      if (nge <= CAP) {
+        // gather everything from the bin's low edge up: the k-th largest, the
+        // nucleus and the draw are then decided on the candidates
+        pl.phase = PH_GATHER;
+        pl.flags |= FL_GALL;
+        set_bracket<DT>(pl, klo, khi_all, md.Tr, sh);
+        pl.target = static_cast<unsigned long long>(md.kk);
+      } else if (exact) {
+        // the k-th largest z' is klo; every tie is kept
+        pl.fkey = klo;
+        pl.cabove = 0u;
+        set_bracket<DT>(pl, klo, khi_all, md.Tr, sh);
+        pl.target = 0;
+        if (pl.flags & FL_TOPP) {
+          pl.phase = PH_MASS;
+          pl.flags &= ~static_cast<unsigned int>(FL_TOPP);
+          plan_level1<DT>(pl, fminf(-wlog2(kval<DT>(klo), nc), MASS_LOG2_SPAN));
+          for (int t = tid; t < S; t += THREADS) a.above[static_cast<size_t>(r) * S + t] = 0ull;
+        } else {
+          pl.phase = PH_DRAWSUM;
+        }
+      } else {
+        set_digits(pl, klo, khi);
+        pl.cabove += cabv;
+        pl.target = rest;
+        set_bracket<DT>(pl, klo, khi, md.Tr, sh);
+      }
+    } else {
+      if (exact) {
+        // cutoff value klo: its first t ties (lowest indices) are kept
+        const unsigned long long wt = q40(wfun(kval<DT>(klo), Mp, nc, minf));
+        const unsigned int t = ties_kept(rest, wt, cstar);
+        if (tid == 0) {
+          unsigned int before = 0;
+          for (int s2 = 0; s2 < S; ++s2) {
+            const unsigned int c = sh.tcnt[s2];
+            const unsigned int kt = t > before ? (t - before < c ? t - before : c) : 0u;
+            before += c;
+            sh.tcnt[s2] = kt;
+            sh.kept[s2] += static_cast<unsigned long long>(kt) * wt;
+          }
+        }
+        __syncthreads();
+        id = draw<DT, EPT, VECOK>(a, r, md, Mp, klo, false, sh);
+        done = true;
+      } else if (cstar <= CAP) {
+        pl.phase = PH_GATHER;
+        pl.target = rest;
+        set_bracket<DT>(pl, klo, khi, md.Tr, sh);
+      } else {
+        set_digits(pl, klo, khi);
+        pl.target = rest;
+        set_bracket<DT>(pl, klo, khi, md.Tr, sh);
+      }
+    }
+  } else if (ph == PH_DRAWSUM) {
+    if (tid < S) sh.kept[tid] = pre;
+    __syncthreads();
+    id = draw<DT, EPT, VECOK>(a, r, md, Mp, pl.fkey, true, sh);
+    done = true;
+  } else if (ph == PH_GATHER) {
+    if (tid == 0) {
+      sh.ncand = ng < CAP ? ng : CAP;
+      a.ncand[r] = 0u;
+    }
+    __syncthreads();
+    const int n = static_cast<int>(sh.ncand);
+    for (int c = tid; c < n; c += THREADS) sh.cand[c] = LDP(a.cand + static_cast<size_t>(r) * CAP + c);
+    __syncthreads();
+    unsigned long long bef;
+    unsigned int g;
+    if (pl.flags & FL_GALL) {
+      // k-th largest z' (with multiplicity), then the nucleus inside the top k
+      auto all = [](unsigned long long) { return true; };
+      const unsigned int tk = cselect<DT, true, false>(n, all, Mp, pl.target, false, sh, &bef, &g);
+      unsigned int tau = tk;
+      unsigned int cut = 0xffffffffu;  // last kept index among the ties at tau
+      if (pl.flags & FL_TOPP) {
+        auto ink = [tk](unsigned long long e) { return static_cast<unsigned int>(e) >= tk; };
+        const unsigned long long Wk = cmass<DT>(n, ink, Mp, sh);
+        unsigned long long PW =
+            static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
+        if (PW < 1) PW = 1;
+        unsigned long long pgt;
+        tau = cselect<DT, true, true>(n, ink, Mp, PW, false, sh, &pgt, &g);
+        const unsigned long long wt = q40(wfun(kval<DT>(tau), Mp, nc, minf));
+        const unsigned int t = ties_kept(PW > pgt ? PW - pgt : 0ull, wt, g);
+        if (t < g) {
+          auto eq = [tau](unsigned long long e) { return static_cast<unsigned int>(e) == tau; };
+          cut = cselect<DT, false, false>(n, eq, Mp, t, false, sh, &bef, &g);
+        }
+      }
+      auto kept = [tau, cut](unsigned long long e) {
+        const unsigned int k = static_cast<unsigned int>(e);
+        return k > tau || (k == tau && static_cast<unsigned int>(e >> 32) <= cut);
+      };
+      const unsigned long long Wf = cmass<DT>(n, kept, Mp, sh);
+      unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(Wf));
+      if (Wf == 0)
+        Tu = 0;
+      else if (Tu >= Wf)
+        Tu = Wf - 1;
+      id = static_cast<int>(cselect<DT, false, true>(n, kept, Mp, Tu, true, sh, &bef, &g));
+      done = true;
+    } else {
+      // nucleus cutoff inside the bin: the remaining target over the candidates
+      auto all = [](unsigned long long) { return true; };
+      unsigned long long pgt;
+      const unsigned int tau = cselect<DT, true, true>(n, all, Mp, pl.target, false, sh, &pgt, &g);
+      const unsigned long long wt = q40(wfun(kval<DT>(tau), Mp, nc, minf));
+      const unsigned int t = ties_kept(pl.target > pgt ? pl.target - pgt : 0ull, wt, g);
+      unsigned int cut = 0xffffffffu;
+      if (t < g) {
+        auto eq = [tau](unsigned long long e) { return static_cast<unsigned int>(e) == tau; };
+        cut = cselect<DT, false, false>(n, eq, Mp, t, false, sh, &bef, &g);
+      }
+      // per-slice kept mass: above the bin, plus the kept candidates
+      for (int t2 = tid; t2 < S; t2 += THREADS) {
+        sh.kept[t2] = LDP(a.above + static_cast<size_t>(r) * S + t2);
+        sh.tcnt[t2] = 0u;
+      }
+      __syncthreads();
+      for (int c = tid; c < n; c += THREADS) {
+        const unsigned long long e = sh.cand[c];
+        const unsigned int k = static_cast<unsigned int>(e);
+        const unsigned int i = static_cast<unsigned int>(e >> 32);
+        const int st = static_cast<int>(i) / a.L;
+        if (k > tau || (k == tau && i <= cut)) {
+          atomicAdd(&sh.kept[st], q40(wfun(kval<DT>(k), Mp, nc, minf)));
+          if (k == tau) atomicAdd(&sh.tcnt[st], 1u);
+        }
+      }
+      __syncthreads();
+      id = draw<DT, EPT, VECOK>(a, r, md, Mp, tau, false, sh);
+      done = true;
+    }
+  }
+  if (done) pl.phase = PH_DONE;
+  if (tid == 0) {
+    if (done) write_out<DT>(a, r, id, pl.lse, md.want_lp);
+    plan_store(a, r, pl);
+    sh.sl.pw[RS_PHASE] = pack2(pl.phase, pl.flags);
+    sh.sl.pw[RS_ZB] = pack2(pl.zlo, pl.zhi);
+    sh.sl.pw[RS_DIG] = pack2(pl.kb, pl.sh);
+    sh.sl.pw[RS_AUX] = pack2(pl.cabove, pl.fkey);
+    sh.sl.pw[RS_GRID] = pack2(__float_as_uint(pl.Mp), __float_as_uint(pl.R2));
+    sh.sl.pw[RS_TGT] = pl.target;
+    sh.sl.pw[RS_LSE] = static_cast<unsigned long long>(__double_as_longlong(pl.lse));
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
+// Refine stage `stage` (0-based), one workgroup per slice of each row on the
+// stage's list.  The list and the plans come from the previous kernel.
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS) void k_scan(Args a, int stage) {
+  __shared__ SLds sh;
+  const int bid = static_cast<int>(blockIdx.x);
+  const int S = a.S;
+  const unsigned int n = a.actcnt[stage];
+  const unsigned int e = a.actlist[static_cast<size_t>(stage) * a.B + bid / S];
+  if (static_cast<unsigned int>(bid) >= n * static_cast<unsigned int>(S)) return;
+  const int r = static_cast<int>(e & 0xffffu);
+  const Plan pl = plan_unpack(a.rowst + static_cast<size_t>(r) * RS_WORDS);
+  slice_stage<DT, EPT, VECOK>(a, r, bid % S, pl, sh);
+}
+
+// Finish row r here: run the remaining levels over the row's slices in this
+// workgroup (the row plan is in sh.sl.pw).  Each level narrows the bracket or
+// advances the phase, so the loop ends; its bound is a guard.
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ void serial_finish(const Args& a, int r, RLds& sh) {
+  for (int it = 0; it < SERIAL_MAX && static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) != PH_DONE; ++it) {
+    const Plan pl = plan_unpack(sh.sl.pw);
+    for (int s2 = 0; s2 < a.S; ++s2) {
+      slice_stage<DT, EPT, VECOK>(a, r, s2, pl, sh.sl);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    // the slice passes' stores are complete; drop stale L1 lines before the
+    // plain loads of the deciding step
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    finish_stage<DT, EPT, VECOK>(a, r, pl.phase, sh.sl.pw, sh);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+}
+
+// Refine stage `stage`, one workgroup per row on the stage's list: decide, and
+// put the row on the next stage's list if it is still open.  The last stage
+// launched finishes every row itself.
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS, 1) void k_decide(Args a, int stage, int last) {
+  __shared__ RLds sh;
+  const int tid = threadIdx.x;
+  const int bid = static_cast<int>(blockIdx.x);
+  const unsigned int n = a.actcnt[stage];
+  const unsigned int e = a.actlist[static_cast<size_t>(stage) * a.B + bid];
+  if (static_cast<unsigned int>(bid) >= n) return;
+  const int r = static_cast<int>(e & 0xffffu);
+  finish_stage<DT, EPT, VECOK>(a, r, e >> 16, a.rowst + static_cast<size_t>(r) * RS_WORDS, sh);
+  if (static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) == PH_DONE) return;
+  if (!last) {
+    if (tid == 0) enlist(a, stage + 1, r, static_cast<unsigned int>(sh.sl.pw[RS_PHASE]));
+    return;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  serial_finish<DT, EPT, VECOK>(a, r, sh);
+}
+
+// Shared memory of k_decide1: the list stage, then (when no refine stage is
+// launched) the refine state of a row finished here.
+union D1Shared {
+  D1Lds d;
+  RLds r;
+};
+
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
+  __shared__ D1Shared shu;
+  D1Lds& sh = shu.d;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int r = static_cast<int>(blockIdx.x);
+  const int S = a.S;
+  const Mode md = decode<DT>(a, r);
+  if (tid < S) {
+    const unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + tid) * 4;
+    const unsigned long long w0 = rp[0], w1 = rp[1], w2 = rp[2];
+    sh.szmax[tid] = __uint_as_float(static_cast<unsigned int>(w0));
+    sh.szarg[tid] = static_cast<int>(w0 >> 32);
+    sh.szmin[tid] = __uint_as_float(static_cast<unsigned int>(w1));
+    sh.slse[tid] = __longlong_as_double(static_cast<long long>(w2));
+  }
+  if (md.need_list) {
+    const unsigned long long* src = a.list + static_cast<size_t>(r) * S * LIST;
+    for (int i = tid; i < S * LIST; i += THREADS) sh.lst[i] = src[i];
+  }
+  __syncthreads();
+  if (md.need_list) {
+    float lv = -INFINITY;
+    int li = INT_MAX;
+    for (int t = wid; t < S; t += WAVES) {
+      const unsigned long long w = sh.lst[t * LIST + lane];
+      wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
+    }
+    tree_merge(lv, li, sh.lists, S < WAVES ? S : WAVES);
+    if (wid == 0) {
+      sh.mlist[lane].v = lv;
+      sh.mlist[lane].i = li;
+    }
+  }
+  if (wid == 0) {
+    const float zm = lane < S ? sh.szmax[lane] : -INFINITY;
+    const int za = lane < S ? sh.szarg[lane] : INT_MAX;
+    float rm = zm;
+    int ra = za;
+    wave_best(rm, ra);
+    double part = (lane < S && md.need_lse) ? sh.slse[lane] * wexp_d(zm, rm) : 0.0;
+    part = wave_sum(part);
+    const float mn = wave_min(lane < S ? sh.szmin[lane] : INFINITY);
+    if (lane == 0) {
+      sh.zmax = rm;
+      sh.zarg = ra;
+      sh.zmin = mn;
+      sh.lse = md.need_lse ? static_cast<double>(rm) + log(part) : static_cast<double>(NAN);
+    }
+  }
+  __syncthreads();
+  const double lse = sh.lse;
+  if (a.K_max > 0 && tid < a.K_max) {  // top_logprobs: the first K of the best 64
+    const size_t o = static_cast<size_t>(r) * a.K_max + tid;
+    if (tid < md.K) {
+      a.out_top_ids[o] = sh.mlist[tid].i;
+      a.out_top_lp[o] = static_cast<float>(static_cast<double>(sh.mlist[tid].v) - lse);
+    } else {
+      a.out_top_ids[o] = -1;
+      a.out_top_lp[o] = -INFINITY;
+    }
+  }
+  Plan pl;
+  pl.phase = PH_DONE;
+  pl.flags = 0u;
+  pl.zlo = KEY_NEG_INF;
+  pl.zhi = KEY_POS_INF;
+  pl.kb = 0u;
+  pl.sh = 0u;
+  pl.cabove = 0u;
+  pl.fkey = key_lo<DT>();
+  pl.Mp = 0.0f;
+  pl.R2 = 0.0f;
+  pl.target = 0ull;
+  pl.lse = lse;
+  if (!md.sampling) {
+    if (tid == 0) write_out<DT>(a, r, sh.zarg, lse, md.want_lp);
+    return;
+  }
+  const float M = sh.zmax;
+  const float Mp = zdiv<DT>(M, md.Tr, md.y, false);  // max z' = z'(max z)
+  pl.Mp = Mp;
+  if (M == -INFINITY || (md.topp && !(md.pr > 0.0f))) {
+    // every logit left is -inf: the reference's draw is uniform
+    if (tid == 0) write_out<DT>(a, r, uniform_id(md.u, a.V), lse, md.want_lp);
+    return;
+  }
+  if (md.kind == KIND_KLIST) {
+    if (wid == 0) {
+      int id = -1;
+      const bool ok = klist_resolve<DT>(md, Mp, sh.mlist, &id);
+      if (lane == 0) {
+        sh.sel[0] = ok ? 1 : 0;
+        sh.sel[1] = id;
+      }
+    }
+    __syncthreads();
+    if (sh.sel[0]) {
+      if (tid == 0) write_out<DT>(a, r, sh.sel[1], lse, md.want_lp);
+      return;
+    }
+  }
+  const float nc = -(Mp * LOG2E);
+  // full span of the row in log2 units (unknown, i.e. infinite, when the scan
+  // did not take the minimum)
+  const float spanc = sh.zmin == INFINITY ? INFINITY : -wlog2(zdiv<DT>(sh.zmin, md.Tr, md.y, false), nc);
+  if (md.kind == KIND_KLIST || md.kind == KIND_KHIST) {
+    pl.phase = PH_COUNT;
+    pl.target = static_cast<unsigned long long>(md.kk);
+    if (md.topp) pl.flags |= FL_TOPP;
+    plan_level1<DT>(pl, spanc);
+  } else if (md.kind == KIND_TOPP) {
+    pl.phase = PH_MASS;
+    plan_level1<DT>(pl, fminf(spanc, MASS_LOG2_SPAN));
+    for (int t = tid; t < S; t += THREADS) a.above[static_cast<size_t>(r) * S + t] = 0ull;
+  } else {
+    pl.phase = PH_DRAWSUM;
+  }
+  if (tid == 0) plan_store(a, r, pl);
+  if (nstage > 0) {
+    if (tid == 0) enlist(a, 0, r, pl.phase);
+    return;
+  }
+  // no refine stage is launched (the caller's parameters promised top-k <= 63
+  // or greedy rows only): finish the row here
+  __syncthreads();
+  if (tid == 0) {
+    shu.r.sl.pw[RS_PHASE] = pack2(pl.phase, pl.flags);
+    shu.r.sl.pw[RS_ZB] = pack2(pl.zlo, pl.zhi);
+    shu.r.sl.pw[RS_DIG] = pack2(pl.kb, pl.sh);
+    shu.r.sl.pw[RS_AUX] = pack2(pl.cabove, pl.fkey);
+    shu.r.sl.pw[RS_GRID] = pack2(__float_as_uint(pl.Mp), __float_as_uint(pl.R2));
+    shu.r.sl.pw[RS_TGT] = pl.target;
+    shu.r.sl.pw[RS_LSE] = static_cast<unsigned long long>(__double_as_longlong(pl.lse));
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  serial_finish<DT, EPT, VECOK>(a, r, shu.r);
+}
+
+
+
+// ================================================================ host side ==
+
+// Stage 0 (scan, decide), then `nst` refine stages (scan, decide); the last
+// deciding kernel launched finishes every row still open.  nst < 0: the first
+// scan only.
+template <int DT, int EPT, bool VECOK>
+hipError_t launch_ept(const Args& a, int nst, hipStream_t st) {
+  const dim3 slices(static_cast<unsigned int>(a.B * a.S)), rows(static_cast<unsigned int>(a.B));
+  hipLaunchKernelGGL((k_scan1<DT, EPT, VECOK>), slices, dim3(THREADS), 0, st, a);
+  if (nst < 0) return hipGetLastError();  // the first pass alone (profiling)
+  hipLaunchKernelGGL((k_decide1<DT, EPT, VECOK>), rows, dim3(THREADS), 0, st, a, nst);
+  for (int i = 0; i < nst; ++i) {
+    hipLaunchKernelGGL((k_scan<DT, EPT, VECOK>), slices, dim3(THREADS), 0, st, a, i);
+    hipLaunchKernelGGL((k_decide<DT, EPT, VECOK>), rows, dim3(THREADS), 0, st, a, i, i == nst - 1 ? 1 : 0);
+  }
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_dt(const Args& a, int ept, bool vecok, int nst, hipStream_t st) {
+  switch (ept) {
+    case 8:
+      return vecok ? launch_ept<DT, 8, true>(a, nst, st) : launch_ept<DT, 8, false>(a, nst, st);
+    case 16:
+      return vecok ? launch_ept<DT, 16, true>(a, nst, st) : launch_ept<DT, 16, false>(a, nst, st);
+    default:
+      return vecok ? launch_ept<DT, 32, true>(a, nst, st) : launch_ept<DT, 32, false>(a, nst, st);
+  }
+}
+
+}  // namespace
+}  // namespace mlxf

@@ -203,10 +203,14 @@ class Sampler {
     const size_t BK = static_cast<size_t>(B) * (K_max > 0 ? K_max : 1);
     top_ids_.reserve(BK);
     top_lp_.reserve(BK);
+    // the parameters are on the host here, so only the refine stages some row
+    // can need are launched
+    const int stages = mlxf_sampler_refine_stages(B, V, logits.dtype, T, k, p);
     err = nullptr;
-    detail::check(mlxf_sample(logits.data, logits.dtype, B, V, stride, T_.p, k_.p, p_.p, tlp_.p, u_.p,
-                              ids_.p, lp_.p, K_max ? top_ids_.p : nullptr, K_max ? top_lp_.p : nullptr,
-                              K_max, ws_.p, ws_bytes_, stream_, &err),
+    detail::check(mlxf_sample_staged(logits.data, logits.dtype, B, V, stride, T_.p, k_.p, p_.p, tlp_.p,
+                                     u_.p, ids_.p, lp_.p, K_max ? top_ids_.p : nullptr,
+                                     K_max ? top_lp_.p : nullptr, K_max, ws_.p, ws_bytes_, stages,
+                                     stream_, &err),
                   err);
     SampleResult res;
     res.K = K_max;
