@@ -353,6 +353,38 @@ __device__ __forceinline__ T block_excl_scan(T x, T* lds, T* total) {
   return ex;
 }
 
+// Inclusive scan of an int over the wave on the VALU: shifts within each row
+// of 16 lanes, then the rows' last lanes broadcast forward (row_bcast:15 into
+// rows 1 and 3, row_bcast:31 into rows 2 and 3).  Whole wave active.
+__device__ __forceinline__ int wave_incl_scan_dpp(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
+}
+
+// Exclusive block scan of an int for an lds array that no thread of the block
+// has read since the last barrier: one barrier, no LDS round trips inside the
+// waves.  lds: WAVES entries.
+__device__ __forceinline__ int block_excl_scan_fresh(int x, int* lds, int* total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int inc = wave_incl_scan_dpp(x);
+  if (lane == 63) lds[wid] = inc;
+  __syncthreads();
+  int off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    const int t = lds[w];
+    off += w < wid ? t : 0;
+    tot += t;
+  }
+  *total = tot;
+  return inc - x + off;
+}
+
 // Block sum in a fixed order (deterministic for floating T).  lds: WAVES entries.
 template <typename T>
 __device__ __forceinline__ T block_sum(T x, T* lds) {

@@ -470,17 +470,13 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
       sh.rmin[wid] = tmin;
     }
   }
-  // lowest index of the thread max
-  int tbi = INT_MAX;
-#pragma unroll
-  for (int e = EPT - 1; e >= 0; --e)
-    if (v[e] == tmax && MLXF_IDX(e) < end) tbi = MLXF_IDX(e);
   if (md.need_list) {
     // theta: each wave's 16th largest thread-maximum key, by bisection on the
     // key bits with ballots; the smallest of the four is reached by at least 64
     // elements (16 thread maxima per wave), so the slice's best 64 all reach it.
-    // (A thread with no element in the slice counts as key 0, below every key.)
-    const unsigned int kt = tbi != INT_MAX ? f2key(tmax) : 0u;
+    // (A thread with no element in the slice counts as key 0, below every key;
+    // its first element, at beg + tid * VEC, is its lowest index.)
+    const unsigned int kt = beg + tid * VEC < end ? f2key(tmax) : 0u;
     unsigned int tw = 0u;
     for (int b = 31; b >= 0; --b) {
       const unsigned int c = tw | (1u << b);
@@ -493,37 +489,61 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
 #pragma unroll
   for (int w2 = 1; w2 < WAVES; ++w2) zmax = fmaxf(zmax, sh.rf[w2]);
   {
-    const int wa = wave_min(tmax == zmax ? tbi : INT_MAX);
+    // lowest index of the slice max: only threads holding it look
+    int tbi = INT_MAX;
+    if (tmax == zmax) {
+#pragma unroll
+      for (int e = EPT - 1; e >= 0; --e)
+        if (v[e] == zmax && MLXF_IDX(e) < end) tbi = MLXF_IDX(e);
+    }
+    const int wa = wave_min(tbi);
     if (lane == 0) sh.ri[wid] = wa;
   }
   if (md.need_lse) {
     float t = 0.0f;
+    if (__builtin_isfinite(zmax)) {
+      // entries past the row end read as -inf and weigh 0
 #pragma unroll
-    for (int e = 0; e < EPT; ++e)
-      if (MLXF_IDX(e) < end) t += wexp(v[e], zmax);
+      for (int e = 0; e < EPT; ++e) t += __builtin_amdgcn_exp2f((v[e] - zmax) * LOG2E);
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e)
+        if (MLXF_IDX(e) < end) t += wexp(v[e], zmax);
+    }
     const double ws = wave_sum(static_cast<double>(t));
     if (lane == 0) sh.rd[wid] = ws;
   }
-  __syncthreads();
   int nsurv = 0;
   if (md.need_list) {
-    // survivors: every element whose key reaches theta, in slots from a block
-    // scan of the per-thread counts
+    // survivors: every element at or above theta, in slots from a block scan of
+    // the per-thread counts (its barrier also publishes sh.ri and sh.rd).  The
+    // float compare keeps -0 with +0, which (value desc, index asc) order ties.
     unsigned int th = sh.rth[0];
 #pragma unroll
     for (int w2 = 1; w2 < WAVES; ++w2) th = min(th, sh.rth[w2]);
+    const float thf = th <= KEY_NEG_INF ? -INFINITY : key2f(th);
+    // entries past the row end read as -inf: they need the bounds check only
+    // when theta is -inf
+    const bool nochk = end - beg == a.L || thf > -INFINITY;
     int mine = 0;
+    if (nochk) {
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && f2key(v[e]) >= th) ? 1 : 0;
-    int pos = block_excl_scan<int>(mine, sh.rsc, &nsurv);
+      for (int e = 0; e < EPT; ++e) mine += v[e] >= thf ? 1 : 0;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && v[e] >= thf) ? 1 : 0;
+    }
+    int pos = block_excl_scan_fresh(mine, sh.rsc, &nsurv);
     if (nsurv <= SURV) {
+      if (mine) {
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const int i = MLXF_IDX(e);
-        if (i < end && f2key(v[e]) >= th) {
-          sh.surv[pos].v = v[e];
-          sh.surv[pos].i = i;
-          ++pos;
+        for (int e = 0; e < EPT; ++e) {
+          const int i = MLXF_IDX(e);
+          if ((nochk || i < end) && v[e] >= thf) {
+            sh.surv[pos].v = v[e];
+            sh.surv[pos].i = i;
+            ++pos;
+          }
         }
       }
     } else {
@@ -531,8 +551,12 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
       // at most 64 * EPT elements reach: bitonic sort of each wave's 64 and a
       // tree merge; with fewer than 64 threads holding elements it is the
       // sentinel and every element survives
-      float lv = tmax;
-      int li = tbi;
+      float lv = -INFINITY;
+      int li = INT_MAX;
+#pragma unroll
+      for (int e = EPT - 1; e >= 0; --e)
+        if (v[e] == tmax && MLXF_IDX(e) < end) li = MLXF_IDX(e);
+      if (li != INT_MAX) lv = tmax;
       wave_sort(lv, li);
       tree_merge(lv, li, sh.lists, WAVES);
       if (tid == LIST - 1) {
@@ -545,7 +569,7 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
       mine = 0;
 #pragma unroll
       for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && !better(tv, ti, v[e], MLXF_IDX(e))) ? 1 : 0;
-      pos = block_excl_scan<int>(mine, sh.rsc, &nsurv);
+      pos = block_excl_scan_fresh(mine, sh.rsc, &nsurv);
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
         const int i = MLXF_IDX(e);
@@ -584,38 +608,24 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
     sfl = (amin >= 0x0f7fffffu && amax < static_cast<int>(0x71800000u + 0x00800000u)) ? static_cast<unsigned int>(SL_FAST) : 0u;
   }
   if (md.need_list) {
+    // the survivors sorted: 64-entry chunks sorted by the waves and merged
     unsigned long long* dst = a.list + (static_cast<size_t>(r) * S + s) * LIST;
-    const int ntot = nsurv;
-    if (ntot <= THREADS) {
-      // rank of each survivor among the survivors: its place in the list
-      if (tid < LIST && tid >= ntot) dst[tid] = pack_ent(-INFINITY, INT_MAX);
-      if (tid < ntot) {
-        const float mv = sh.surv[tid].v;
-        const int mi = sh.surv[tid].i;
-        int rank = 0;
-#pragma unroll 16
-        for (int j = 0; j < ntot; ++j) rank += better(sh.surv[j].v, sh.surv[j].i, mv, mi) ? 1 : 0;
-        if (rank < LIST) dst[rank] = pack_ent(mv, mi);
+    const int nch = (nsurv + LIST - 1) / LIST;
+    float sv = -INFINITY;
+    int si = INT_MAX;
+    for (int ch = wid; ch < nch; ch += WAVES) {
+      const int c = ch * LIST + lane;
+      float cv = -INFINITY;
+      int ci = INT_MAX;
+      if (c < nsurv) {
+        cv = sh.surv[c].v;
+        ci = sh.surv[c].i;
       }
-    } else {
-      // many survivors (heavy ties at theta): 64-entry chunks sorted and merged
-      const int nch = (ntot + LIST - 1) / LIST;
-      float sv = -INFINITY;
-      int si = INT_MAX;
-      for (int ch = wid; ch < nch; ch += WAVES) {
-        const int c = ch * LIST + lane;
-        float cv = -INFINITY;
-        int ci = INT_MAX;
-        if (c < ntot) {
-          cv = sh.surv[c].v;
-          ci = sh.surv[c].i;
-        }
-        wave_sort(cv, ci);
-        wave_list_merge(sv, si, cv, ci);
-      }
-      tree_merge(sv, si, sh.lists, nch < WAVES ? nch : WAVES);
-      if (wid == 0) dst[lane] = pack_ent(sv, si);
+      wave_sort(cv, ci);
+      wave_list_merge(sv, si, cv, ci);
     }
+    if (nch > 1) tree_merge(sv, si, sh.lists, nch < WAVES ? nch : WAVES);
+    if (wid == 0) dst[lane] = pack_ent(sv, si);
   }
 #undef MLXF_IDX
   if (tid == 0) {
