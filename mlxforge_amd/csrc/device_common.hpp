@@ -271,6 +271,12 @@ __device__ __forceinline__ unsigned int rdl(unsigned int v, int src) {
 __device__ __forceinline__ float rdl(float v, int src) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
 }
+__device__ __forceinline__ double rdl(double v, int src) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane(static_cast<int>(b), src);
+  const int hi = __builtin_amdgcn_readlane(static_cast<int>(b >> 32), src);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
 __device__ __forceinline__ unsigned long long rdl(unsigned long long v, int src) {
   const unsigned int lo = rdl(static_cast<unsigned int>(v), src);
   const unsigned int hi = rdl(static_cast<unsigned int>(v >> 32), src);
@@ -366,6 +372,68 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int x) {
   return x;
 }
 
+// Lane move of a double by DPP control CTRL (row mask RM; lanes without a
+// source, or outside RM, read 0.0).
+template <int CTRL, int RM, bool BC>
+__device__ __forceinline__ double dpp_d(double x) {
+  const long long b = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(b), CTRL, RM, 0xf, BC);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(b >> 32), CTRL, RM, 0xf, BC);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+
+// Inclusive scan of a double over the wave, same lane pattern as
+// wave_incl_scan_dpp.  Exact for integer values whose sums stay below 2^53.
+__device__ __forceinline__ double wave_incl_scan_dpp(double x) {
+  x += dpp_d<0x111, 0xf, true>(x);
+  x += dpp_d<0x112, 0xf, true>(x);
+  x += dpp_d<0x114, 0xf, true>(x);
+  x += dpp_d<0x118, 0xf, true>(x);
+  x += dpp_d<0x142, 0xa, false>(x);
+  x += dpp_d<0x143, 0xc, false>(x);
+  return x;
+}
+
+// Lane move of a 64-bit integer by DPP control CTRL (as dpp_d).
+template <int CTRL, int RM, bool BC>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long x) {
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, RM, 0xf, BC);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(x >> 32), CTRL, RM, 0xf, BC);
+  return (static_cast<unsigned long long>(static_cast<unsigned int>(hi)) << 32) | static_cast<unsigned int>(lo);
+}
+
+// Inclusive scan of a 64-bit integer over the wave (lane pattern of
+// wave_incl_scan_dpp).
+__device__ __forceinline__ unsigned long long wave_incl_scan_dpp(unsigned long long x) {
+  x += dpp_u64<0x111, 0xf, true>(x);
+  x += dpp_u64<0x112, 0xf, true>(x);
+  x += dpp_u64<0x114, 0xf, true>(x);
+  x += dpp_u64<0x118, 0xf, true>(x);
+  x += dpp_u64<0x142, 0xa, false>(x);
+  x += dpp_u64<0x143, 0xc, false>(x);
+  return x;
+}
+
+// Exclusive block scan of an integer (int or 64-bit) for an lds array that no
+// thread of the block has read since the last barrier: one barrier; *total is
+// the block sum.  lds: WAVES entries.
+template <typename T>
+__device__ __forceinline__ T block_excl_scan_dpp(T x, T* lds, T* total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const T inc = wave_incl_scan_dpp(x);
+  if (lane == 63) lds[wid] = inc;
+  __syncthreads();
+  T off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    const T t = lds[w];
+    off += w < wid ? t : T(0);
+    tot += t;
+  }
+  *total = tot;
+  return inc - x + off;
+}
+
 // Exclusive block scan of an int for an lds array that no thread of the block
 // has read since the last barrier: one barrier, no LDS round trips inside the
 // waves.  lds: WAVES entries.
@@ -425,6 +493,39 @@ __device__ __forceinline__ void bitonic_stage(float& v, int& i) {
 }
 
 // Bitonic sort of one entry per lane, best (v desc, i asc) in lane 0.
+// Bitonic sort of (index, weight) pairs by ascending index (no equal indices
+// but INT_MAX, whose weight is 0).
+template <int J>
+__device__ __forceinline__ void cx_idx(int& i, double& w, bool asc) {
+  const int lane = threadIdx.x & 63;
+  const int oi = xshf<J>(i);
+  const double ow = xshf<J>(w);
+  const bool first = (lane & J) == 0;
+  const bool ob = oi < i;
+  if ((first == asc) ? ob : !ob) {
+    i = oi;
+    w = ow;
+  }
+}
+template <int K>
+__device__ __forceinline__ void bitonic_stage_idx(int& i, double& w) {
+  const bool asc = ((threadIdx.x & 63) & K) == 0;
+  if constexpr (K >= 64) cx_idx<32>(i, w, asc);
+  if constexpr (K >= 32) cx_idx<16>(i, w, asc);
+  if constexpr (K >= 16) cx_idx<8>(i, w, asc);
+  if constexpr (K >= 8) cx_idx<4>(i, w, asc);
+  if constexpr (K >= 4) cx_idx<2>(i, w, asc);
+  cx_idx<1>(i, w, asc);
+}
+__device__ __forceinline__ void wave_sort_idx(int& i, double& w) {
+  bitonic_stage_idx<2>(i, w);
+  bitonic_stage_idx<4>(i, w);
+  bitonic_stage_idx<8>(i, w);
+  bitonic_stage_idx<16>(i, w);
+  bitonic_stage_idx<32>(i, w);
+  bitonic_stage_idx<64>(i, w);
+}
+
 __device__ __forceinline__ void wave_sort(float& v, int& i) {
   bitonic_stage<2>(v, i);
   bitonic_stage<4>(v, i);

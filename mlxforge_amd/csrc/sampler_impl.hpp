@@ -643,6 +643,8 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
 
 struct D1Lds {
   unsigned long long lst[MAX_S * LIST];  // (the per-slice lists; dead once merged)
+  unsigned long long sv[MAX_S * LIST];   // list entries at or above theta
+  int nsv;
   TopEnt lists[WAVES * LIST];
   TopEnt mlist[LIST];
   float szmax[MAX_S];
@@ -684,30 +686,28 @@ __device__ __forceinline__ bool klist_resolve(const Mode& md, float Mp, const To
   const bool k1 = si != INT_MAX;
   const float nc = -(Mp * LOG2E);
   const bool minf = !__builtin_isfinite(Mp);
-  const unsigned long long w = k1 ? q40(wfun(sv, Mp, nc, minf)) : 0ull;
-  const unsigned long long incl = wave_incl_scan(w);
-  const unsigned long long Wk = rdl(incl, 63);
+  // masses in 2^-40 units: each below 2^41, so every sum of 64 is an exact double
+  const double w = k1 ? static_cast<double>(q40(wfun(sv, Mp, nc, minf))) : 0.0;
+  const double incl = wave_incl_scan_dpp(w);
+  const double Wk = rdl(incl, 63);
   bool keep = k1;
   if (md.topp) {
-    const unsigned long long PW =
-        static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
+    const double PW = ceil(static_cast<double>(md.pr) * Wk);
     keep = k1 && (incl - w) < PW;
   }
-  const unsigned long long wf = keep ? w : 0ull;
-  const unsigned long long Wf = wave_sum(wf);
-  unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(Wf));
-  if (Wf == 0)
+  const double wf = keep ? w : 0.0;
+  const double Wf = wave_sum(wf);
+  unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * Wf);
+  if (Wf == 0.0)
     Tu = 0;
-  else if (Tu >= Wf)
-    Tu = Wf - 1;
-  // kept mass at or before my index, in vocabulary order
-  unsigned long long cum = 0;
-  for (int q = 0; q < 64; ++q) {
-    const unsigned long long wq = rdl(wf, q);
-    const int iq = __builtin_amdgcn_readlane(si, q);
-    if (iq <= si) cum += wq;
-  }
-  const int cand = wave_min((keep && (Wf == 0 || (wf > 0 && cum > Tu))) ? si : INT_MAX);
+  else if (static_cast<double>(Tu) >= Wf)
+    Tu = static_cast<unsigned long long>(Wf) - 1;
+  // the kept entries in vocabulary order and their running mass
+  int ki = keep ? si : INT_MAX;
+  double kw = wf;
+  wave_sort_idx(ki, kw);
+  const double cum = wave_incl_scan_dpp(kw);
+  const int cand = wave_min((ki != INT_MAX && (Wf == 0.0 || (kw > 0.0 && cum > static_cast<double>(Tu)))) ? ki : INT_MAX);
   *id_out = cand == INT_MAX ? rdl(si, 0) : cand;
   return true;
 }
@@ -743,6 +743,10 @@ struct RLds {
   unsigned long long selu[8];
   unsigned int kmin, kmax, ncand;
   int found;
+  float wz[64];                      // the draw's run of elements (walk)
+  unsigned long long wex;
+  unsigned int wrk;
+  int wbase;
 };
 
 // ---- one slice of one stage: the histogram, the gathered elements or the kept
@@ -862,53 +866,76 @@ __device__ __forceinline__ int walk(const Args& a, int r, int s, float Mp, unsig
   const bool fast = !md.tslow && (sfl & SL_FAST);
   const float nc = -(Mp * LOG2E);
   const bool minf = !__builtin_isfinite(Mp);
-  // thread t owns EPT consecutive elements, held as z' keys
-  unsigned int kz[EPT];
+  // z' values are never -0 (zdiv), so the key of -0 keeps every z' >= +0: as a
+  // value threshold that is +0 with every tie kept
+  float tauf = kval<DT>(tau);
+  unsigned int lim = tie_lim;
+  if (tau == (1u << (keybits<DT>() - 1)) - 1u) {
+    tauf = 0.0f;
+    lim = 0xffffffffu;
+  }
+  // thread t owns EPT consecutive elements, held as z' values
+  float zp[EPT];
 #pragma unroll
   for (int it = 0; it < EPT / VEC; ++it) {
     float z[VEC];
     load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) kz[it * VEC + j] = zkey<DT>(zdiv<DT>(z[j], md.Tr, md.y, fast));
+    for (int j = 0; j < VEC; ++j) zp[it * VEC + j] = zdiv<DT>(z[j], md.Tr, md.y, fast);
   }
-  unsigned int nt = 0;
+  // rank of my first tie at tau among the slice's ties (all ties kept: none)
+  const bool all_ties = lim == 0xffffffffu;
+  int tex = 0;
+  if (!all_ties) {
+    int nt = 0;
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) nt += (my0 + e < e0 && kz[e] == tau) ? 1u : 0u;
-  unsigned int tex, tin, ttot;
-  block_scan<unsigned int>(nt, sh.sl.rv, &tex, &tin, &ttot);
-  auto qof = [&](int e, unsigned int& rk) -> unsigned long long {
-    const bool valid = my0 + e < e0;
-    const bool tie = valid && kz[e] == tau;
-    const bool kept = valid && (kz[e] > tau || (tie && rk < tie_lim));
-    rk += tie ? 1u : 0u;
-    return kept ? q40(wfun(kval<DT>(kz[e]), Mp, nc, minf)) : 0ull;
-  };
+    for (int e = 0; e < EPT; ++e) nt += (my0 + e < e0 && zp[e] == tauf) ? 1 : 0;
+    int ttot;
+    tex = block_excl_scan_dpp<int>(nt, sh.ri, &ttot);
+  }
   unsigned long long qs = 0;
   int last = -1;
   {
-    unsigned int rk = tex;
+    unsigned int rk = static_cast<unsigned int>(tex);
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-      const unsigned long long q = qof(e, rk);
+      const bool valid = my0 + e < e0;
+      const bool tie = valid && zp[e] == tauf;
+      const bool kept = valid && (zp[e] > tauf || (tie && rk < lim));
+      rk += tie ? 1u : 0u;
+      const unsigned long long q = kept ? q40(wfun(zp[e], Mp, nc, minf)) : 0ull;
       qs += q;
       if (q > 0) last = my0 + e;
     }
   }
-  unsigned long long ex, in, tot;
-  block_scan<unsigned long long>(qs, sh.sl.ru, &ex, &in, &tot);
   if (tid == 0) sh.found = -1;
-  __syncthreads();
-  if (ex <= rem && rem < in) {
-    unsigned long long c = ex;
-    unsigned int rk = tex;
-    int pick = -1;
+  unsigned long long tot;
+  const unsigned long long ex = block_excl_scan_dpp<unsigned long long>(qs, sh.sl.ru, &tot);
+  if (ex <= rem && rem < ex + qs) {
+    // the one thread whose run holds the draw hands its elements to wave 0
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const unsigned long long q = qof(e, rk);
-      c += q;
-      if (pick < 0 && q > 0 && c > rem) pick = my0 + e;
-    }
-    sh.found = pick;
+    for (int e = 0; e < EPT; ++e) sh.wz[e] = zp[e];
+    sh.wex = ex;
+    sh.wrk = static_cast<unsigned int>(tex);
+    sh.wbase = my0;
+    sh.found = -2;
+  }
+  __syncthreads();
+  if (tid < 64 && sh.found == -2) {
+    // one element per lane: running kept mass in index order, first past rem
+    const int lane = tid;
+    const int idx = sh.wbase + lane;
+    const bool valid = lane < EPT && idx < e0;
+    const float z = lane < EPT ? sh.wz[lane] : -INFINITY;
+    const bool tie = valid && z == tauf;
+    const unsigned long long tb = __ballot(tie);
+    const unsigned int rk = sh.wrk + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(tb >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(tb), 0u));
+    const bool kept = valid && (z > tauf || (tie && rk < lim));
+    const unsigned long long q = kept ? q40(wfun(z, Mp, nc, minf)) : 0ull;
+    const unsigned long long c = sh.wex + wave_incl_scan_dpp(q);
+    const int pk = wave_min((q > 0 && c > rem) ? idx : INT_MAX);
+    if (lane == 0) sh.found = pk == INT_MAX ? -1 : pk;
   }
   __syncthreads();
   int id = sh.found;
@@ -935,32 +962,32 @@ __device__ __forceinline__ int draw(const Args& a, int r, const Mode& md, float 
                     RLds& sh) {
   const int tid = threadIdx.x;
   const int S = a.S;
-  if (tid == 0) {
-    unsigned long long W = 0;
-    for (int t = 0; t < S; ++t) W += sh.kept[t];
+  if (tid < 64) {
+    // lane t: slice t's kept mass and the running sum up to it (S <= 64)
+    const int lane = tid;
+    const unsigned long long kt = lane < S ? sh.kept[lane] : 0ull;
+    const unsigned long long inc = wave_incl_scan_dpp(kt);
+    const unsigned long long W = rdl(inc, 63);
     unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(W));
     if (W == 0)
       Tu = 0;
     else if (Tu >= W)
       Tu = W - 1;
-    unsigned long long cum = 0;
-    int st = -1;
+    // the first slice with kept mass whose running sum passes Tu (else the last
+    // slice with kept mass, else slice 0)
+    int st = wave_min(kt > 0 && inc > Tu ? lane : 64);
+    if (st == 64) st = wave_max(kt > 0 ? lane : -1);
     unsigned long long rem = 0;
-    for (int t = 0; t < S; ++t) {
-      if (sh.kept[t] > 0) {
-        st = t;
-        rem = Tu - cum;
-        if (cum + sh.kept[t] > Tu) break;
-      }
-      cum += sh.kept[t];
-    }
     if (st < 0) {
       st = 0;
-      rem = 0;
+    } else {
+      rem = Tu - (rdl(inc, st) - rdl(kt, st));
     }
-    sh.sel[0] = st;
-    sh.selu[0] = rem;
-    sh.sel[1] = static_cast<int>(all_ties ? 0xffffffffu : sh.tcnt[st]);
+    if (lane == 0) {
+      sh.sel[0] = st;
+      sh.selu[0] = rem;
+      sh.sel[1] = static_cast<int>(all_ties ? 0xffffffffu : sh.tcnt[st]);
+    }
   }
   __syncthreads();
   const int st = sh.sel[0];
@@ -1527,16 +1554,64 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
   if (md.need_list) {
     const unsigned long long* src = a.list + static_cast<size_t>(r) * S * LIST;
     for (int i = tid; i < S * LIST; i += THREADS) sh.lst[i] = src[i];
+    if (tid == 0) sh.nsv = 0;
   }
   __syncthreads();
   if (md.need_list) {
+    // theta: the best of the slices' 64th entries.  Each slice holds 64 entries
+    // at or above its own 64th, so the row's 64th best is at least theta, and an
+    // entry of the row's best 64 is in its slice's list: the entries at or above
+    // theta hold the row's best 64.
+    float th = -INFINITY;
+#pragma unroll
+    for (int w2 = 0; w2 < MAX_S / LIST + 1; ++w2) {
+      const int t = w2 * LIST + lane;
+      if (t < S) th = fmaxf(th, __uint_as_float(static_cast<unsigned int>(sh.lst[t * LIST + LIST - 1])));
+    }
+    th = wave_max(th);
+    if (th > -INFINITY) {
+      for (int t = wid; t < S; t += WAVES) {
+        const unsigned long long w = sh.lst[t * LIST + lane];
+        const bool in = __uint_as_float(static_cast<unsigned int>(w)) >= th;
+        const unsigned long long bal = __ballot(in);
+        if (bal) {
+          int base = 0;
+          if (lane == 0) base = atomicAdd(&sh.nsv, __popcll(bal));
+          base = __builtin_amdgcn_readfirstlane(base);
+          const int at = base + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(bal >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(bal), 0u));
+          if (in && at < MAX_S * LIST) sh.sv[at] = w;
+        }
+      }
+    }
+    __syncthreads();
+    const int nsv = sh.nsv;
     float lv = -INFINITY;
     int li = INT_MAX;
-    for (int t = wid; t < S; t += WAVES) {
-      const unsigned long long w = sh.lst[t * LIST + lane];
-      wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
+    if (th > -INFINITY && nsv <= THREADS) {
+      // the survivors (in any order) sorted: 64-entry chunks by the waves, merged
+      const int nch = (nsv + LIST - 1) / LIST;
+      if (wid < nch) {
+        const int c = wid * LIST + lane;
+        float cv = -INFINITY;
+        int ci = INT_MAX;
+        if (c < nsv) {
+          const unsigned long long w = sh.sv[c];
+          cv = __uint_as_float(static_cast<unsigned int>(w));
+          ci = static_cast<int>(w >> 32);
+        }
+        wave_sort(cv, ci);
+        lv = cv;
+        li = ci;
+      }
+      if (nch > 1) tree_merge(lv, li, sh.lists, nch);
+    } else {
+      for (int t = wid; t < S; t += WAVES) {
+        const unsigned long long w = sh.lst[t * LIST + lane];
+        wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
+      }
+      tree_merge(lv, li, sh.lists, S < WAVES ? S : WAVES);
     }
-    tree_merge(lv, li, sh.lists, S < WAVES ? S : WAVES);
     if (wid == 0) {
       sh.mlist[lane].v = lv;
       sh.mlist[lane].i = li;
