@@ -471,16 +471,18 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
     }
   }
   if (md.need_list) {
-    // theta: each wave's 16th largest thread-maximum key, by bisection on the
-    // key bits with ballots; the smallest of the four is reached by at least 64
-    // elements (16 thread maxima per wave), so the slice's best 64 all reach it.
-    // (A thread with no element in the slice counts as key 0, below every key;
-    // its first element, at beg + tid * VEC, is its lowest index.)
+    // theta: each wave's 16th largest thread-maximum key, rounded down to its
+    // top 16 bits, by bisection with ballots; the smallest of the four is
+    // reached by at least 64 elements (16 thread maxima per wave), so the
+    // slice's best 64 all reach it.  (A thread with no element in the slice
+    // counts as key 0, below every key; its first element, at beg + tid * VEC,
+    // is its lowest index.)
     const unsigned int kt = beg + tid * VEC < end ? f2key(tmax) : 0u;
     unsigned int tw = 0u;
-    for (int b = 31; b >= 0; --b) {
+#pragma unroll
+    for (int b = 31; b >= 16; --b) {
       const unsigned int c = tw | (1u << b);
-      if (__popcll(__ballot(kt >= c)) >= LIST / WAVES) tw = c;
+      if (__builtin_popcountll(__builtin_amdgcn_ballot_w64(kt >= c)) >= LIST / WAVES) tw = c;
     }
     if (lane == 0) sh.rth[wid] = tw;
   }
