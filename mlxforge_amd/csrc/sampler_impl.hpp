@@ -783,20 +783,28 @@ __device__ __forceinline__ void slice_stage(const Args& a, int r, int s, const P
       sh.hm[b] = 0ull;
     }
     __syncthreads();
+    auto add = [&](float z) {
+      const float zp = zdiv<DT>(z, md.Tr, md.y, fast);
+      const float x = wlog2(zp, nc);
+      unsigned long long q = 0;
+      if (mass) q = q40(minf ? (zp == Mp ? 1.0f : 0.0f) : __builtin_amdgcn_exp2f(x));
+      if (!mass || q) {
+        const int bin = vgrid ? vbin_x(x, pl.R2)
+                              : max(0, NB - 1 - static_cast<int>(min((zkey<DT>(zp) - pl.kb) >> pl.sh, 255u)));
+        atomicAdd(&sh.hc[bin], 1u);
+        if (mass) atomicAdd(&sh.hm[bin], q);
+      }
+    };
+    // the first level brackets every key; entries past the row end read as
+    // -inf, which weigh nothing (MASS) -- so no per-element test is needed
+    if (zlo <= KEY_NEG_INF && zhi >= KEY_POS_INF && (mass || end - beg == a.L)) {
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const unsigned int zk = f2key(v[e]);
-      if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) {
-        const float zp = zdiv<DT>(v[e], md.Tr, md.y, fast);
-        const float x = wlog2(zp, nc);
-        unsigned long long q = 0;
-        if (mass) q = q40(minf ? (zp == Mp ? 1.0f : 0.0f) : __builtin_amdgcn_exp2f(x));
-        if (!mass || q) {
-          const int bin = vgrid ? vbin_x(x, pl.R2)
-                                : max(0, NB - 1 - static_cast<int>(min((zkey<DT>(zp) - pl.kb) >> pl.sh, 255u)));
-          atomicAdd(&sh.hc[bin], 1u);
-          if (mass) atomicAdd(&sh.hm[bin], q);
-        }
+      for (int e = 0; e < EPT; ++e) add(v[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const unsigned int zk = f2key(v[e]);
+        if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) add(v[e]);
       }
     }
     __syncthreads();
@@ -1387,7 +1395,21 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
     }
     __syncthreads();
     const int n = static_cast<int>(sh.ncand);
-    for (int c = tid; c < n; c += THREADS) sh.cand[c] = LDP(a.cand + static_cast<size_t>(r) * CAP + c);
+    {
+      // every load issued before the first store: one memory round trip
+      unsigned long long cv[CAP / THREADS];
+      const unsigned long long* src = a.cand + static_cast<size_t>(r) * CAP;
+#pragma unroll
+      for (int k = 0; k < CAP / THREADS; ++k) {
+        const int c = tid + k * THREADS;
+        cv[k] = c < n ? src[c] : 0ull;
+      }
+#pragma unroll
+      for (int k = 0; k < CAP / THREADS; ++k) {
+        const int c = tid + k * THREADS;
+        if (c < n) sh.cand[c] = cv[k];
+      }
+    }
     __syncthreads();
     unsigned long long bef;
     unsigned int g;
@@ -1555,7 +1577,18 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
   }
   if (md.need_list) {
     const unsigned long long* src = a.list + static_cast<size_t>(r) * S * LIST;
-    for (int i = tid; i < S * LIST; i += THREADS) sh.lst[i] = src[i];
+    // every load issued before the first store: one memory round trip
+    unsigned long long lw[MAX_S * LIST / THREADS];
+#pragma unroll
+    for (int k = 0; k < MAX_S * LIST / THREADS; ++k) {
+      const int i = tid + k * THREADS;
+      lw[k] = i < S * LIST ? src[i] : 0ull;
+    }
+#pragma unroll
+    for (int k = 0; k < MAX_S * LIST / THREADS; ++k) {
+      const int i = tid + k * THREADS;
+      if (i < S * LIST) sh.lst[i] = lw[k];
+    }
     if (tid == 0) sh.nsv = 0;
   }
   __syncthreads();
