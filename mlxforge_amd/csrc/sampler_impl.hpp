@@ -1389,26 +1389,24 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
     id = draw<DT, EPT, VECOK>(a, r, md, Mp, pl.fkey, true, sh);
     done = true;
   } else if (ph == PH_GATHER) {
+    // every candidate slot is requested at once, together with the count
+    // (unused slots hold stale words that are never stored)
+    unsigned long long cv[CAP / THREADS];
+    {
+      const unsigned long long* src = a.cand + static_cast<size_t>(r) * CAP;
+#pragma unroll
+      for (int k = 0; k < CAP / THREADS; ++k) cv[k] = src[tid + k * THREADS];
+    }
     if (tid == 0) {
       sh.ncand = ng < CAP ? ng : CAP;
       a.ncand[r] = 0u;
     }
     __syncthreads();
     const int n = static_cast<int>(sh.ncand);
-    {
-      // every load issued before the first store: one memory round trip
-      unsigned long long cv[CAP / THREADS];
-      const unsigned long long* src = a.cand + static_cast<size_t>(r) * CAP;
 #pragma unroll
-      for (int k = 0; k < CAP / THREADS; ++k) {
-        const int c = tid + k * THREADS;
-        cv[k] = c < n ? src[c] : 0ull;
-      }
-#pragma unroll
-      for (int k = 0; k < CAP / THREADS; ++k) {
-        const int c = tid + k * THREADS;
-        if (c < n) sh.cand[c] = cv[k];
-      }
+    for (int k = 0; k < CAP / THREADS; ++k) {
+      const int c = tid + k * THREADS;
+      if (c < n) sh.cand[c] = cv[k];
     }
     __syncthreads();
     unsigned long long bef;
