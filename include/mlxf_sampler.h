@@ -125,6 +125,22 @@ int mlxf_sample_staged(const void* d_logits, int dtype, int B, int V, int64_t ro
                        int K_max, void* d_workspace, size_t workspace_bytes, int refine_stages,
                        void* stream, char** err);
 
+/* mlxf_sample_staged with per-row min_p as well (src/sample/sampler.h:19,
+ * applied after top-p as in src/sample/sampler.cpp:163 and :87-93):
+ *   d_min_p   [B] fp32 or NULL (NULL: every row off).  Active when
+ *             0 < min_p <= 1, else off (src/capi/mlxforge.cpp:58); rounded to
+ *             the logits dtype; keeps the tokens whose exp(z' - max z')
+ *             reaches it.
+ * The stage hint of mlxf_sampler_refine_stages holds unchanged (a row whose
+ * min_p cuts deeper than its top-k / top-p takes one more pass, which the last
+ * launched stage runs itself when no stage is left). */
+int mlxf_sample_ex(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                   const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                   const float* d_min_p, const int32_t* d_top_logprobs, const float* d_uniforms,
+                   int32_t* d_out_ids, float* d_out_logprobs, int32_t* d_out_top_ids,
+                   float* d_out_top_logprobs, int K_max, void* d_workspace, size_t workspace_bytes,
+                   int refine_stages, void* stream, char** err);
+
 /* Refine stages a call needs, from HOST copies of the per-row temperature,
  * top_k and top_p (NULL = the sentinel: greedy / off / off), with the same
  * sanitisation as mlxf_sample (src/sample/sampler.h:16-29,

@@ -22,6 +22,7 @@ SYMBOLS = (
     "mlxf_sampler_workspace_size",
     "mlxf_sample",
     "mlxf_sample_staged",
+    "mlxf_sample_ex",
     "mlxf_sampler_refine_stages",
     "mlxf_sampler_first_pass",
     "mlxf_greedy",
@@ -56,6 +57,8 @@ def load() -> ctypes.CDLL:
     L.mlxf_sample.restype = I
     L.mlxf_sample_staged.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, I, P, SZ, I, P, PP]
     L.mlxf_sample_staged.restype = I
+    L.mlxf_sample_ex.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, P, I, P, SZ, I, P, PP]
+    L.mlxf_sample_ex.restype = I
     L.mlxf_sampler_first_pass.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, I, P, SZ, P, PP]
     L.mlxf_sampler_first_pass.restype = I
     L.mlxf_sampler_refine_stages.argtypes = [I, I, I, P, P, P]

@@ -149,7 +149,7 @@ int host_refine_stages(int B, int V, int dtype, const float* T, const int32_t* k
 }
 
 int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
-               const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+               const float* d_temperature, const int32_t* d_top_k, const float* d_top_p, const float* d_min_p,
                const int32_t* d_top_logprobs, const float* d_uniforms, int32_t* d_out_ids,
                float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
                int K_max, void* d_workspace, size_t workspace_bytes, void* stream, int nst, char** err) {
@@ -201,6 +201,7 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
     a.T = d_temperature;
     a.k = d_top_k;
     a.p = d_top_p;
+    a.minp = d_min_p;
     a.tlp = d_top_logprobs;
     a.u = d_uniforms;
     a.out_ids = d_out_ids;
@@ -296,7 +297,7 @@ int mlxf_sample(const void* d_logits, int dtype, int B, int V, int64_t row_strid
                 const int32_t* d_top_logprobs, const float* d_uniforms, int32_t* d_out_ids,
                 float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
                 int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err) {
-  return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p,
+  return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p, nullptr,
                     d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
                     d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, mlxf::NSTAGE, err);
 }
@@ -311,7 +312,22 @@ int mlxf_sample_staged(const void* d_logits, int dtype, int B, int V, int64_t ro
     set_err(err, "mlxf: refine_stages must be in [0, 3]");
     return MLXF_EINVAL;
   }
-  return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p,
+  return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p, nullptr,
+                    d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
+                    d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, refine_stages, err);
+}
+
+int mlxf_sample_ex(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                   const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                   const float* d_min_p, const int32_t* d_top_logprobs, const float* d_uniforms,
+                   int32_t* d_out_ids, float* d_out_logprobs, int32_t* d_out_top_ids,
+                   float* d_out_top_logprobs, int K_max, void* d_workspace, size_t workspace_bytes,
+                   int refine_stages, void* stream, char** err) {
+  if (refine_stages < 0) {
+    set_err(err, "mlxf: refine_stages must be in [0, 3]");
+    return MLXF_EINVAL;
+  }
+  return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p, d_min_p,
                     d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
                     d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, refine_stages, err);
 }
@@ -321,7 +337,7 @@ int mlxf_sampler_first_pass(const void* d_logits, int dtype, int B, int V, int64
                             const int32_t* d_top_logprobs, const float* d_uniforms, int32_t* d_out_ids,
                             float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
                             int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err) {
-  return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p,
+  return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p, nullptr,
                     d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
                     d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, -1, err);
 }
@@ -334,7 +350,7 @@ int mlxf_sampler_refine_stages(int B, int V, int dtype, const float* h_temperatu
 int mlxf_greedy(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
                 int32_t* d_out_ids, void* d_workspace, size_t workspace_bytes, void* stream,
                 char** err) {
-  return run_sample(d_logits, dtype, B, V, row_stride, nullptr, nullptr, nullptr, nullptr, nullptr,
+  return run_sample(d_logits, dtype, B, V, row_stride, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                     d_out_ids, nullptr, nullptr, nullptr, 0, d_workspace, workspace_bytes, stream, 0,
                     err);
 }

@@ -81,6 +81,7 @@ struct Args {
   const float* T;
   const int* k;
   const float* p;
+  const float* minp;           // [B] or null: min_p
   const int* tlp;
   const float* u;
   int* out_ids;
@@ -111,7 +112,7 @@ namespace {
 
 struct Mode {
   int sampling, kk, topp, K, need_lse, want_lp, kind, need_list, tslow;
-  float Tr, pr, u, y;
+  float Tr, pr, u, y, mr;
 };
 
 // Per-row parameters with the reference's sentinels and the C ABI's
@@ -129,6 +130,10 @@ __device__ __forceinline__ Mode decode(const Args& a, int r) {
   const float p = a.p ? a.p[r] : 1.0f;
   m.topp = (m.sampling && p > 0.0f && p < 1.0f) ? 1 : 0;
   m.pr = round_dt<DT>(p);
+  // min_p in (0, 1], else off (src/capi/mlxforge.cpp:58), rounded to the
+  // logits dtype (src/sample/sampler.cpp:91 multiplies by array(min_p, dtype))
+  const float mp = a.minp ? a.minp[r] : 0.0f;
+  m.mr = (m.sampling && mp > 0.0f && mp <= 1.0f) ? round_dt<DT>(mp) : 0.0f;
   const int tlp = a.tlp ? a.tlp[r] : -1;
   int K = tlp > 0 ? tlp : 0;
   K = K < a.K_max ? K : a.K_max;
@@ -312,6 +317,16 @@ __device__ __forceinline__ unsigned int ld_dev32(const unsigned int* p) {
 }
 __device__ __forceinline__ void st_dev32(unsigned int* p, unsigned int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// min_p (src/sample/sampler.cpp:87-93, after top-p): an element is kept when
+// its weight exp(z' - max z') reaches mr; weights are non-decreasing in z', so
+// that is every z' key from the smallest one whose weight reaches mr.  Whole
+// wave.
+template <int DT>
+__device__ __forceinline__ unsigned int minp_key(float mr, float Mp, float nc, bool minf) {
+  return wave_search(key_lo<DT>(), key_hi<DT>(),
+                     [&](unsigned int k) { return wfun(kval<DT>(k), Mp, nc, minf) >= mr; });
 }
 
 // Sampled id (and its logprob) of row r.
@@ -689,7 +704,8 @@ __device__ __forceinline__ bool klist_resolve(const Mode& md, float Mp, const To
   const float nc = -(Mp * LOG2E);
   const bool minf = !__builtin_isfinite(Mp);
   // masses in 2^-40 units: each below 2^41, so every sum of 64 is an exact double
-  const double w = k1 ? static_cast<double>(q40(wfun(sv, Mp, nc, minf))) : 0.0;
+  const float wv = k1 ? wfun(sv, Mp, nc, minf) : 0.0f;
+  const double w = static_cast<double>(q40(wv));
   const double incl = wave_incl_scan_dpp(w);
   const double Wk = rdl(incl, 63);
   bool keep = k1;
@@ -697,6 +713,7 @@ __device__ __forceinline__ bool klist_resolve(const Mode& md, float Mp, const To
     const double PW = ceil(static_cast<double>(md.pr) * Wk);
     keep = k1 && (incl - w) < PW;
   }
+  if (md.mr > 0.0f) keep = keep && wv >= md.mr;  // min_p, after top-p
   const double wf = keep ? w : 0.0;
   const double Wf = wave_sum(wf);
   unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * Wf);
@@ -846,13 +863,16 @@ __device__ __forceinline__ void slice_stage(const Args& a, int r, int s, const P
       }
     }
   } else if (pl.phase == PH_DRAWSUM) {
+    // kept: z' keys from fkey (the bracket holds them; a min_p threshold can
+    // fall inside the bracket's edge values)
     unsigned long long t = 0;
+    const bool fk = pl.fkey > key_lo<DT>();
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       const unsigned int zk = f2key(v[e]);
       if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) {
         const float zp = zdiv<DT>(v[e], md.Tr, md.y, fast);
-        t += q40(wfun(zp, Mp, nc, minf));
+        if (!fk || zkey<DT>(zp) >= pl.fkey) t += q40(wfun(zp, Mp, nc, minf));
       }
     }
     t = block_sum<unsigned long long>(t, sh.ru);
@@ -1190,6 +1210,30 @@ __device__ __forceinline__ void set_digits(Plan& pl, unsigned int klo, unsigned 
   pl.sh = static_cast<unsigned int>(bl > 8 ? bl - 8 : 0);
 }
 
+// minp_key for the whole workgroup (wave 0 searches; uniform control flow).
+template <int DT>
+__device__ __forceinline__ unsigned int minp_key_block(float mr, float Mp, float nc, bool minf, RLds& sh) {
+  if (threadIdx.x < 64) {
+    const unsigned int t = minp_key<DT>(mr, Mp, nc, minf);
+    if (threadIdx.x == 0) sh.sel[5] = static_cast<int>(t);
+  }
+  __syncthreads();
+  const unsigned int t = static_cast<unsigned int>(sh.sel[5]);
+  __syncthreads();
+  return t;
+}
+
+// A row whose min_p keeps less than its top-k / top-p set keeps every z' key
+// from tm: its per-slice kept masses are summed by a DRAWSUM pass.
+template <int DT>
+__device__ __forceinline__ void plan_minp_drawsum(Plan& pl, unsigned int tm, float Tr, RLds& sh) {
+  pl.phase = PH_DRAWSUM;
+  pl.fkey = tm;
+  pl.target = 0;
+  pl.cabove = 0u;
+  set_bracket<DT>(pl, tm, key_hi<DT>(), Tr, sh);
+}
+
 // ---- the deciding step of a stage for row r (whole workgroup): reads the
 // slices' results, then either writes the sampled id or leaves the next plan in
 // sh.sl.pw and in the row's plan words.
@@ -1348,6 +1392,10 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
           for (int t = tid; t < S; t += THREADS) a.above[static_cast<size_t>(r) * S + t] = 0ull;
         } else {
           pl.phase = PH_DRAWSUM;
+          if (md.mr > 0.0f) {
+            const unsigned int tm = minp_key_block<DT>(md.mr, Mp, nc, minf, sh);
+            if (tm > pl.fkey) pl.fkey = tm;
+          }
         }
       } else {
         set_digits(pl, klo, khi);
@@ -1356,7 +1404,10 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
         set_bracket<DT>(pl, klo, khi, md.Tr, sh);
       }
     } else {
-      if (exact) {
+      const unsigned int tm = (exact && md.mr > 0.0f) ? minp_key_block<DT>(md.mr, Mp, nc, minf, sh) : 0u;
+      if (exact && tm > klo) {
+        plan_minp_drawsum<DT>(pl, tm, md.Tr, sh);
+      } else if (exact) {
         // cutoff value klo: its first t ties (lowest indices) are kept
         const unsigned long long wt = q40(wfun(kval<DT>(klo), Mp, nc, minf));
         const unsigned int t = ties_kept(rest, wt, cstar);
@@ -1432,9 +1483,12 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
           cut = cselect<DT, false, false>(n, eq, Mp, t, false, sh, &bef, &g);
         }
       }
-      auto kept = [tau, cut](unsigned long long e) {
+      // min_p keeps z' keys from tm (every candidate at or above the bracket's
+      // low edge is here, so it applies to them directly)
+      const unsigned int tm = md.mr > 0.0f ? minp_key_block<DT>(md.mr, Mp, nc, minf, sh) : 0u;
+      auto kept = [tau, cut, tm](unsigned long long e) {
         const unsigned int k = static_cast<unsigned int>(e);
-        return k > tau || (k == tau && static_cast<unsigned int>(e >> 32) <= cut);
+        return k >= tm && (k > tau || (k == tau && static_cast<unsigned int>(e >> 32) <= cut));
       };
       const unsigned long long Wf = cmass<DT>(n, kept, Mp, sh);
       unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(Wf));
@@ -1456,25 +1510,30 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
         auto eq = [tau](unsigned long long e) { return static_cast<unsigned int>(e) == tau; };
         cut = cselect<DT, false, false>(n, eq, Mp, t, false, sh, &bef, &g);
       }
-      // per-slice kept mass: above the bin, plus the kept candidates
-      for (int t2 = tid; t2 < S; t2 += THREADS) {
-        sh.kept[t2] = LDP(a.above + static_cast<size_t>(r) * S + t2);
-        sh.tcnt[t2] = 0u;
-      }
-      __syncthreads();
-      for (int c = tid; c < n; c += THREADS) {
-        const unsigned long long e = sh.cand[c];
-        const unsigned int k = static_cast<unsigned int>(e);
-        const unsigned int i = static_cast<unsigned int>(e >> 32);
-        const int st = static_cast<int>(i) / a.L;
-        if (k > tau || (k == tau && i <= cut)) {
-          atomicAdd(&sh.kept[st], q40(wfun(kval<DT>(k), Mp, nc, minf)));
-          if (k == tau) atomicAdd(&sh.tcnt[st], 1u);
+      const unsigned int tm = md.mr > 0.0f ? minp_key_block<DT>(md.mr, Mp, nc, minf, sh) : 0u;
+      if (tm > tau) {
+        plan_minp_drawsum<DT>(pl, tm, md.Tr, sh);
+      } else {
+        // per-slice kept mass: above the bin, plus the kept candidates
+        for (int t2 = tid; t2 < S; t2 += THREADS) {
+          sh.kept[t2] = LDP(a.above + static_cast<size_t>(r) * S + t2);
+          sh.tcnt[t2] = 0u;
         }
+        __syncthreads();
+        for (int c = tid; c < n; c += THREADS) {
+          const unsigned long long e = sh.cand[c];
+          const unsigned int k = static_cast<unsigned int>(e);
+          const unsigned int i = static_cast<unsigned int>(e >> 32);
+          const int st = static_cast<int>(i) / a.L;
+          if (k > tau || (k == tau && i <= cut)) {
+            atomicAdd(&sh.kept[st], q40(wfun(kval<DT>(k), Mp, nc, minf)));
+            if (k == tau) atomicAdd(&sh.tcnt[st], 1u);
+          }
+        }
+        __syncthreads();
+        id = draw<DT, EPT, VECOK>(a, r, md, Mp, tau, false, sh);
+        done = true;
       }
-      __syncthreads();
-      id = draw<DT, EPT, VECOK>(a, r, md, Mp, tau, false, sh);
-      done = true;
     }
   }
   if (done) pl.phase = PH_DONE;
@@ -1733,6 +1792,15 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
     for (int t = tid; t < S; t += THREADS) a.above[static_cast<size_t>(r) * S + t] = 0ull;
   } else {
     pl.phase = PH_DRAWSUM;
+    if (md.mr > 0.0f) {
+      // min_p: the kept set is every z' key from tm
+      if (wid == 0) {
+        const unsigned int tm = minp_key<DT>(md.mr, Mp, nc, !__builtin_isfinite(Mp));
+        if (lane == 0) sh.sel[2] = static_cast<int>(tm);
+      }
+      __syncthreads();
+      pl.fkey = static_cast<unsigned int>(sh.sel[2]);
+    }
   }
   if (tid == 0) plan_store(a, r, pl);
   if (nstage > 0) {

@@ -12,8 +12,10 @@
 //     src/sample/sampler.cpp:165);
 //   * results are copied back to host vectors (what the reference's worker
 //     does right after its async_eval, src/runtime/worker.cpp:498-512);
-//   * min_p and the penalties are not on the GPU path: sample() reports them
-//     as an error instead of ignoring them.
+//   * the penalties are applied to the logits beforehand (apply_penalties on
+//     a mutable view; the reference builds a penalized copy, `adj`,
+//     src/sample/sampler.cpp:144): sample() reports penalties left in its
+//     params as an error instead of ignoring them.
 // Header-only; needs the HIP runtime for device buffers and copies.  The
 // sampler library itself never allocates: this wrapper owns the workspace.
 #pragma once
@@ -34,7 +36,7 @@ struct SamplingParams {
   float temperature = 1.0f;  // <= 0 => greedy (argmax)
   int top_k = 0;             // <= 0 => disabled
   float top_p = 1.0f;        // >= 1 => disabled
-  float min_p = 0.0f;        // <= 0 => disabled (not on the GPU path)
+  float min_p = 0.0f;        // <= 0 => disabled; applied after top-p
   float repetition_penalty = 1.0f;
   float frequency_penalty = 0.0f;
   float presence_penalty = 0.0f;
@@ -117,23 +119,24 @@ class Sampler {
     const int B = logits.B;
     if (static_cast<int>(params.size()) != B || static_cast<int>(uniforms.size()) != B)
       throw SamplerError(MLXF_EINVAL, "mlxf: params and uniforms need one entry per row");
-    std::vector<float> T(B), p(B);
+    std::vector<float> T(B), p(B), mp(B);
     std::vector<int32_t> k(B), tlp(B);
     int K_max = 0;
     for (int r = 0; r < B; ++r) {
       const SamplingParams& sp = params[r];
-      if (sp.min_p > 0.0f || sp.has_penalties())
-        throw SamplerError(MLXF_EINVAL, "mlxf: min_p and penalties are not on the GPU path");
+      if (sp.has_penalties())
+        throw SamplerError(MLXF_EINVAL, "mlxf: penalties must be applied to the logits first");
       T[r] = sp.temperature;
       k[r] = sp.top_k;
       p[r] = sp.top_p;
+      mp[r] = sp.min_p;
       tlp[r] = sp.top_logprobs;
       if (sp.top_logprobs > K_max) K_max = sp.top_logprobs;
     }
     if (K_max > logits.V) K_max = logits.V;
     if (K_max > MLXF_MAX_TOP_LOGPROBS)
       throw SamplerError(MLXF_EINVAL, "mlxf: top_logprobs above MLXF_MAX_TOP_LOGPROBS");
-    return run(logits, T.data(), k.data(), p.data(), tlp.data(), uniforms.data(), K_max);
+    return run(logits, T.data(), k.data(), p.data(), mp.data(), tlp.data(), uniforms.data(), K_max);
   }
 
   // Sampler::sample(logits, params, key) (src/sample/sampler.h:51-52) with one
@@ -186,7 +189,7 @@ class Sampler {
   }
 
   SampleResult run(const DeviceLogits& logits, const float* T, const int32_t* k, const float* p,
-                   const int32_t* tlp, const float* u, int K_max) {
+                   const float* mp, const int32_t* tlp, const float* u, int K_max) {
     const int B = logits.B, V = logits.V;
     const int64_t stride = logits.row_stride ? logits.row_stride : V;
     char* err = nullptr;
@@ -196,6 +199,7 @@ class Sampler {
     upload(T_, T, B);
     upload(k_, k, B);
     upload(p_, p, B);
+    upload(mp_, mp, B);
     upload(tlp_, tlp, B);
     upload(u_, u, B);
     ids_.reserve(B > 0 ? B : 1);
@@ -207,10 +211,10 @@ class Sampler {
     // can need are launched
     const int stages = mlxf_sampler_refine_stages(B, V, logits.dtype, T, k, p);
     err = nullptr;
-    detail::check(mlxf_sample_staged(logits.data, logits.dtype, B, V, stride, T_.p, k_.p, p_.p, tlp_.p,
-                                     u_.p, ids_.p, lp_.p, K_max ? top_ids_.p : nullptr,
-                                     K_max ? top_lp_.p : nullptr, K_max, ws_.p, ws_bytes_, stages,
-                                     stream_, &err),
+    detail::check(mlxf_sample_ex(logits.data, logits.dtype, B, V, stride, T_.p, k_.p, p_.p, mp_.p,
+                                 tlp_.p, u_.p, ids_.p, lp_.p, K_max ? top_ids_.p : nullptr,
+                                 K_max ? top_lp_.p : nullptr, K_max, ws_.p, ws_bytes_, stages, stream_,
+                                 &err),
                   err);
     SampleResult res;
     res.K = K_max;
@@ -239,7 +243,7 @@ class Sampler {
   hipStream_t stream_;
   detail::DeviceBuf<unsigned char> ws_;
   size_t ws_bytes_ = 0;
-  detail::DeviceBuf<float> T_, p_, u_, lp_, top_lp_;
+  detail::DeviceBuf<float> T_, p_, mp_, u_, lp_, top_lp_;
   detail::DeviceBuf<int32_t> k_, tlp_, ids_, top_ids_;
 };
 

@@ -30,7 +30,7 @@ class SamplingParams:
     temperature: float = 1.0   # <= 0 => greedy
     top_k: int = 0             # <= 0 => disabled
     top_p: float = 1.0         # >= 1 => disabled
-    min_p: float = 0.0         # <= 0 => disabled (not on the GPU path yet)
+    min_p: float = 0.0         # <= 0 => disabled; applied after top-p
     repetition_penalty: float = 1.0
     frequency_penalty: float = 0.0
     presence_penalty: float = 0.0
@@ -99,12 +99,13 @@ def _host_view(x, B):
 
 def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
                 top_logprobs=None, uniforms=None, K_max: int = 0, V: int | None = None,
-                workspace: Workspace | None = None, refine_stages: int | None = None) -> SampleResult:
+                workspace: Workspace | None = None, refine_stages: int | None = None,
+                min_p=None) -> SampleResult:
     """Sample one token per row of a [B, row_stride] logits view.
 
     Per-row parameters are device tensors of length B (or Python scalars /
     host sequences, which are copied); None disables the knob (temperature
-    None = all greedy).  refine_stages: refine stages to launch (0..3); by
+    None = all greedy; min_p None = off).  refine_stages: refine stages to launch (0..3); by
     default derived from the parameters when they are all known on the host
     (mlxf_sampler_refine_stages), else 3.
     """
@@ -126,6 +127,7 @@ def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
     T = _param(temperature, B, torch.float32, dev)
     k = _param(top_k, B, torch.int32, dev)
     p = _param(top_p, B, torch.float32, dev)
+    mp = _param(min_p, B, torch.float32, dev)
     tlp = _param(top_logprobs, B, torch.int32, dev)
     u = _param(uniforms, B, torch.float32, dev)
     ids = torch.empty(B, dtype=torch.int32, device=dev)
@@ -137,8 +139,9 @@ def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
     ws = workspace.get(B, V, K_max, code)
     stream = torch.cuda.current_stream(dev).cuda_stream
     err = ctypes.c_void_p()
-    rc = _lib.load().mlxf_sample_staged(
-        _ptr(logits), code, B, V, logits.stride(0), _ptr(T), _ptr(k), _ptr(p), _ptr(tlp), _ptr(u),
+    rc = _lib.load().mlxf_sample_ex(
+        _ptr(logits), code, B, V, logits.stride(0), _ptr(T), _ptr(k), _ptr(p), _ptr(mp), _ptr(tlp),
+        _ptr(u),
         _ptr(ids), _ptr(lp), _ptr(top_ids) if K_max else None, _ptr(top_lp) if K_max else None,
         K_max, _ptr(ws), ws.numel(), int(refine_stages), ctypes.c_void_p(stream), ctypes.byref(err))
     _lib.check(rc, err)
@@ -169,14 +172,14 @@ class Sampler:
 
     @staticmethod
     def sample(logits: torch.Tensor, params: SamplingParams, uniforms) -> SampleResult:
-        if params.min_p > 0.0 or params.has_penalties():
-            raise NotImplementedError("min_p and penalties are not on the GPU path yet")
+        if params.has_penalties():
+            raise NotImplementedError("penalties: call apply_penalties on the logits first")
         B, V = logits.shape
         K = min(max(params.top_logprobs, 0), V)
         # Sampler::sample always returns the chosen-token logprob (sampler.cpp:151-154).
         res = sample_rows(logits, temperature=params.temperature, top_k=params.top_k,
                           top_p=params.top_p, top_logprobs=max(params.top_logprobs, 0),
-                          uniforms=uniforms, K_max=K)
+                          uniforms=uniforms, K_max=K, min_p=params.min_p)
         return res
 
     @staticmethod

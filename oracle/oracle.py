@@ -19,7 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, BF16, F16 = 0, 1, 2
-FLAG_GREEDY, FLAG_TOPP_AMBIG, FLAG_DRAW_AMBIG = 1, 2, 4
+FLAG_GREEDY, FLAG_TOPP_AMBIG, FLAG_DRAW_AMBIG, FLAG_MINP_AMBIG = 1, 2, 4, 8
 
 _lib = None
 
@@ -41,6 +41,9 @@ def lib():
         L.orc_sample.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_long,
                                  P, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, ctypes.c_int]
         L.orc_sample.restype = ctypes.c_int
+        L.orc_sample_ex.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_long,
+                                    P, P, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, ctypes.c_int]
+        L.orc_sample_ex.restype = ctypes.c_int
         L.orc_filter_row.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                      ctypes.c_int, ctypes.c_float, ctypes.c_float, P]
         L.orc_filter_row.restype = ctypes.c_int
@@ -73,7 +76,8 @@ def dtype_code(arr: np.ndarray, dtype: int | None = None) -> int:
 
 
 def sample(logits: np.ndarray, T=None, k=None, p=None, tlp=None, u=None, K_max: int = 0,
-           dtype: int | None = None, V: int | None = None, nthreads: int | None = None):
+           dtype: int | None = None, V: int | None = None, nthreads: int | None = None,
+           min_p=None):
     """Run the oracle over a [B, row_stride] host array.
 
     For bf16, pass the raw uint16 bit patterns with dtype=BF16.
@@ -84,7 +88,7 @@ def sample(logits: np.ndarray, T=None, k=None, p=None, tlp=None, u=None, K_max: 
     V = stride if V is None else V
     code = dtype_code(logits, dtype)
     f = lambda a, t: None if a is None else np.ascontiguousarray(np.asarray(a, dtype=t).reshape(B))
-    T, p, u = f(T, np.float32), f(p, np.float32), f(u, np.float32)
+    T, p, u, mp = f(T, np.float32), f(p, np.float32), f(u, np.float32), f(min_p, np.float32)
     k, tlp = f(k, np.int32), f(tlp, np.int32)
     ids = np.zeros(B, np.int32)
     lp = np.zeros(B, np.float32)
@@ -94,9 +98,9 @@ def sample(logits: np.ndarray, T=None, k=None, p=None, tlp=None, u=None, K_max: 
     margins = np.zeros((B, 2), np.float64)
     if nthreads is None:
         nthreads = min(os.cpu_count() or 1, 16)
-    rc = lib().orc_sample(_ptr(logits), code, B, V, stride, _ptr(T), _ptr(k), _ptr(p), _ptr(tlp),
-                          _ptr(u), _ptr(ids), _ptr(lp), _ptr(top_ids), _ptr(top_lp), K_max,
-                          _ptr(flags), _ptr(margins), nthreads)
+    rc = lib().orc_sample_ex(_ptr(logits), code, B, V, stride, _ptr(T), _ptr(k), _ptr(p), _ptr(mp),
+                             _ptr(tlp), _ptr(u), _ptr(ids), _ptr(lp), _ptr(top_ids), _ptr(top_lp),
+                             K_max, _ptr(flags), _ptr(margins), nthreads)
     if rc != 0:
         raise ValueError("orc_sample rejected its arguments")
     return dict(ids=ids, lp=lp, top_ids=top_ids[:, :K_max], top_lp=top_lp[:, :K_max],

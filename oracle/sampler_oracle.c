@@ -41,10 +41,15 @@
  *       (so +inf and all -inf rows stay finite and well defined).
  *   D8  top_logprobs alternatives are ordered by (z desc, index asc), the exact
  *       order of log_softmax(z).
+ *   D9  min_p in (0, 1] (else off, src/capi/mlxforge.cpp:58) is rounded to the
+ *       logits dtype like p (sampler.cpp:91 multiplies by array(min_p,
+ *       probs.dtype())) and applied after top-p: keep exp(z' - max z') >= min_p.
  *
  * Ambiguity flags (the north-star exclusion rule): a row whose top-p cutoff or
  * draw boundary lies within 1e-6 of the compared quantity is reported with
- * ORC_FLAG_TOPP_AMBIG / ORC_FLAG_DRAW_AMBIG; bit-exact id comparison excludes it.
+ * ORC_FLAG_TOPP_AMBIG / ORC_FLAG_DRAW_AMBIG; a kept weight within 1e-6
+ * (relative) of min_p is ORC_FLAG_MINP_AMBIG.  Bit-exact id comparison excludes
+ * such rows.
  */
 #include <math.h>
 #include <pthread.h>
@@ -59,6 +64,7 @@
 #define ORC_FLAG_GREEDY 1
 #define ORC_FLAG_TOPP_AMBIG 2
 #define ORC_FLAG_DRAW_AMBIG 4
+#define ORC_FLAG_MINP_AMBIG 8
 
 #define ORC_AMBIG_EPS 1e-6
 
@@ -257,18 +263,30 @@ int orc_apply_top_p(float* zs, int V, float pc, double* margin) {
   return mg < ORC_AMBIG_EPS ? ORC_FLAG_TOPP_AMBIG : 0;
 }
 
-/* In place: keep prob >= min_p * max prob (src/sample/sampler.cpp:87-93). */
-void orc_apply_min_p(float* zs, int V, float min_p) {
-  if (!(min_p > 0.0f)) return;
-  float m = zs[0];
-  for (int i = 1; i < V; ++i)
-    if (zs[i] > m) m = zs[i];
-  double W = 0.0;
-  for (int i = 0; i < V; ++i) W += wexp(zs[i], m);
-  const double thr = (1.0 / W) * (double)min_p; /* peak prob = 1/W */
-  for (int i = 0; i < V; ++i)
-    if (wexp(zs[i], m) / W < thr) zs[i] = -INFINITY;
+/* In place: keep prob >= min_p * max prob (src/sample/sampler.cpp:87-93).
+ * *margin (if given) gets the smallest |w_i / min_p - 1| over the finite
+ * entries, w_i = exp(z'_i - max z'). */
+static int apply_min_p_m(float* zs, int V, float min_p, double* margin) {
+  double mg = INFINITY;
+  if (min_p > 0.0f) {
+    float m = zs[0];
+    for (int i = 1; i < V; ++i)
+      if (zs[i] > m) m = zs[i];
+    double W = 0.0;
+    for (int i = 0; i < V; ++i) W += wexp(zs[i], m);
+    const double thr = (1.0 / W) * (double)min_p; /* peak prob = 1/W */
+    for (int i = 0; i < V; ++i) {
+      if (zs[i] == -INFINITY) continue;
+      const double w = wexp(zs[i], m);
+      const double d = fabs(w / (double)min_p - 1.0);
+      if (d < mg) mg = d;
+      if (w / W < thr) zs[i] = -INFINITY;
+    }
+  }
+  if (margin) *margin = mg;
+  return mg < ORC_AMBIG_EPS ? ORC_FLAG_MINP_AMBIG : 0;
 }
+void orc_apply_min_p(float* zs, int V, float min_p) { apply_min_p_m(zs, V, min_p, NULL); }
 
 /* D4: inverse-CDF draw over the finite (kept) entries of zs, ascending index.
  * Replaces mx::random::categorical (src/sample/sampler.cpp:165). */
@@ -314,7 +332,7 @@ typedef struct {
 } orc_ctx;
 
 static void sample_one_row(const void* row, const orc_ctx* c, int V, float T, int k, float p,
-                           int tlp, float u, int32_t* id_out, float* lp_out, int32_t* top_ids,
+                           float mp, int tlp, float u, int32_t* id_out, float* lp_out, int32_t* top_ids,
                            float* top_lp, int32_t* flags_out, double* margins) {
   float* z = (float*)malloc(sizeof(float) * (size_t)V);
   for (int i = 0; i < V; ++i) z[i] = load_logit(row, c->dtype, (size_t)i);
@@ -335,6 +353,8 @@ static void sample_one_row(const void* row, const orc_ctx* c, int V, float T, in
     if (p > 0.0f && p < 1.0f) {                                            /* :162 */
       flags |= orc_apply_top_p(zs, V, round_dtype(p, c->dtype), &mg_p);    /* D6 */
     }
+    if (mp > 0.0f && mp <= 1.0f)                                           /* :163, D9 */
+      flags |= apply_min_p_m(zs, V, round_dtype(mp, c->dtype), NULL);
     id = orc_draw_row(zs, V, u, &mg_d); /* :165, D4 */
     if (mg_d < ORC_AMBIG_EPS) flags |= ORC_FLAG_DRAW_AMBIG;
     free(zs);
@@ -386,7 +406,7 @@ typedef struct {
   const orc_ctx* c;
   int B, V;
   long row_stride;
-  const float *T, *p, *u;
+  const float *T, *p, *mp, *u;
   const int *k, *tlp;
   int32_t* ids;
   float* lp;
@@ -409,7 +429,8 @@ static void* worker(void* arg) {
     const char* row = (const char*)j->logits + (size_t)r * (size_t)j->row_stride * esz;
     const int K_max = j->c->K_max;
     sample_one_row(row, j->c, j->V, j->T ? j->T[r] : 0.0f, j->k ? j->k[r] : 0,
-                   j->p ? j->p[r] : 1.0f, j->tlp ? j->tlp[r] : -1, j->u ? j->u[r] : 0.0f,
+                   j->p ? j->p[r] : 1.0f, j->mp ? j->mp[r] : 0.0f, j->tlp ? j->tlp[r] : -1,
+                   j->u ? j->u[r] : 0.0f,
                    &j->ids[r], j->lp ? &j->lp[r] : NULL,
                    (j->top_ids && K_max > 0) ? &j->top_ids[(size_t)r * K_max] : NULL,
                    (j->top_lp && K_max > 0) ? &j->top_lp[(size_t)r * K_max] : NULL,
@@ -418,12 +439,13 @@ static void* worker(void* arg) {
   return NULL;
 }
 
-/* Batched oracle with the same argument meaning as the product's mlxf_sample
- * (host pointers).  Returns 0 on success, -1 on bad arguments. */
-int orc_sample(const void* logits, int dtype, int B, int V, long row_stride, const float* T,
-               const int* k, const float* p, const int* tlp, const float* u, int32_t* ids,
-               float* lp, int32_t* top_ids, float* top_lp, int K_max, int32_t* flags,
-               double* margins, int nthreads) {
+/* Batched oracle with the same argument meaning as the product's mlxf_sample_ex
+ * (host pointers; min_p may be NULL).  Returns 0 on success, -1 on bad
+ * arguments. */
+int orc_sample_ex(const void* logits, int dtype, int B, int V, long row_stride, const float* T,
+                  const int* k, const float* p, const float* min_p, const int* tlp, const float* u,
+                  int32_t* ids, float* lp, int32_t* top_ids, float* top_lp, int K_max,
+                  int32_t* flags, double* margins, int nthreads) {
   if (!logits || !ids || B < 0 || V <= 0 || row_stride < V || K_max < 0) return -1;
   if (dtype != ORC_F32 && dtype != ORC_BF16 && dtype != ORC_F16) return -1;
   orc_ctx c = {dtype, K_max};
@@ -436,6 +458,7 @@ int orc_sample(const void* logits, int dtype, int B, int V, long row_stride, con
   j.T = T;
   j.k = k;
   j.p = p;
+  j.mp = min_p;
   j.u = u;
   j.tlp = tlp;
   j.ids = ids;
@@ -454,6 +477,15 @@ int orc_sample(const void* logits, int dtype, int B, int V, long row_stride, con
   for (int t = 1; t < nthreads; ++t) pthread_join(th[t], NULL);
   pthread_mutex_destroy(&j.mu);
   return 0;
+}
+
+/* orc_sample_ex without min_p: the product's mlxf_sample. */
+int orc_sample(const void* logits, int dtype, int B, int V, long row_stride, const float* T,
+               const int* k, const float* p, const int* tlp, const float* u, int32_t* ids,
+               float* lp, int32_t* top_ids, float* top_lp, int K_max, int32_t* flags,
+               double* margins, int nthreads) {
+  return orc_sample_ex(logits, dtype, B, V, row_stride, T, k, p, NULL, tlp, u, ids, lp, top_ids,
+                       top_lp, K_max, flags, margins, nthreads);
 }
 
 /* Filter stage only (for the reference's filter known-answer tests):

@@ -201,14 +201,22 @@ void case_top_logprobs_pre_temperature(Sampler& s) {  // :194-203
   KAT_CHECK((r.top_tokens == std::vector<int32_t>{1, 3}));
 }
 
-void case_off_path_parameters_refused(Sampler& s) {  // :76-124 are not on the GPU path
+void case_min_p(Sampler& s) {  // :76-87
+  // probs [0.5, 0.3, 0.15, 0.05]; min_p 0.4 keeps prob >= 0.2, i.e. {0, 1}
+  Logits lg({log_of({0.5f, 0.3f, 0.15f, 0.05f})});
+  SamplingParams p;
+  p.min_p = 0.4f;
+  std::set<int> kept = kept_by_sweep(s, lg, p, 64);
+  KAT_CHECK((kept == std::set<int>{0, 1}));
+}
+
+void case_penalties_refused(Sampler& s) {  // :89-124 need apply_penalties first
   Logits lg({{2.0f, 1.0f, 0.5f}});
-  for (int which = 0; which < 4; ++which) {
+  for (int which = 0; which < 3; ++which) {
     SamplingParams p;
-    if (which == 0) p.min_p = 0.4f;
-    if (which == 1) p.repetition_penalty = 4.0f;
-    if (which == 2) p.frequency_penalty = 0.5f;
-    if (which == 3) p.presence_penalty = 0.7f;
+    if (which == 0) p.repetition_penalty = 4.0f;
+    if (which == 1) p.frequency_penalty = 0.5f;
+    if (which == 2) p.presence_penalty = 0.7f;
     bool threw = false;
     try {
       s.sample(lg.view(), p, {0.5f});
@@ -265,7 +273,8 @@ int main() {
       {"top_logprobs > 0 ranks ids by descending logprob", case_top_logprobs_ranked},
       {"a full top-k recovers a normalised distribution", case_full_top_k_normalised},
       {"top_logprobs come from the pre-temperature logits", case_top_logprobs_pre_temperature},
-      {"min_p and penalties are refused", case_off_path_parameters_refused},
+      {"min-p keeps tokens with prob >= min_p * max_prob", case_min_p},
+      {"penalties left in the parameters are refused", case_penalties_refused},
       {"row_stride samples B rows of a padded buffer", case_row_stride},
       {"errors carry a code and a message", case_error_reporting},
   };

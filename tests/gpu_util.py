@@ -2,7 +2,8 @@
 and compare it with the CPU oracle under the north-star rules.
 
   * token ids bit-exact, except rows the oracle flags as ambiguous (top-p
-    cutoff or draw boundary within 1e-6 of the compared mass); those are
+    cutoff, min_p threshold or draw boundary within 1e-6 of the compared
+    quantity); those are
     reported, and how many of them still matched;
   * logprobs within 1e-5 (fp32 logits) or 2e-3 (bf16 / fp16 logits);
   * top_logprobs ids bit-exact, values within the same tolerance.
@@ -30,27 +31,30 @@ def to_device(host: np.ndarray, dtype: str, device="cuda:0") -> torch.Tensor:
 
 
 def gpu_sample(logits_dev, T=None, k=None, p=None, tlp=None, u=None, K_max=0, V=None,
-               stages=None):
+               stages=None, min_p=None):
     """stages: refine stages to launch (None: all three, the generic path)."""
     dev = logits_dev.device
     f = lambda a, t: None if a is None else torch.as_tensor(np.asarray(a), dtype=t).to(dev)
     res = sampler.sample_rows(logits_dev, temperature=f(T, torch.float32), top_k=f(k, torch.int32),
                               top_p=f(p, torch.float32), top_logprobs=f(tlp, torch.int32),
                               uniforms=f(u, torch.float32), K_max=K_max, V=V,
-                              refine_stages=3 if stages is None else stages)
+                              refine_stages=3 if stages is None else stages,
+                              min_p=f(min_p, torch.float32))
     torch.cuda.synchronize()
     return dict(ids=res.tokens.cpu().numpy(), lp=res.logprobs.cpu().numpy(),
                 top_ids=res.top_tokens.cpu().numpy(), top_lp=res.top_logprobs.cpu().numpy())
 
 
-def oracle_sample(host, dtype, T=None, k=None, p=None, tlp=None, u=None, K_max=0, V=None):
-    return orc.sample(host, T=T, k=k, p=p, tlp=tlp, u=u, K_max=K_max, dtype=DT[dtype][1], V=V)
+def oracle_sample(host, dtype, T=None, k=None, p=None, tlp=None, u=None, K_max=0, V=None,
+                  min_p=None):
+    return orc.sample(host, T=T, k=k, p=p, tlp=tlp, u=u, K_max=K_max, dtype=DT[dtype][1], V=V,
+                      min_p=min_p)
 
 
 def compare(g, o, dtype, tlp=None, label=""):
     """Assert parity; returns a small report dict."""
     B = o["ids"].shape[0]
-    amb = (o["flags"] & (orc.FLAG_TOPP_AMBIG | orc.FLAG_DRAW_AMBIG)) != 0
+    amb = (o["flags"] & (orc.FLAG_TOPP_AMBIG | orc.FLAG_DRAW_AMBIG | orc.FLAG_MINP_AMBIG)) != 0
     same = g["ids"] == o["ids"]
     bad = np.nonzero(~same & ~amb)[0]
     assert bad.size == 0, (f"{label}: {bad.size} non-excluded rows differ, first rows "

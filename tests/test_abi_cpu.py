@@ -84,6 +84,25 @@ def test_sample_argument_errors_need_no_gpu():
                          0, None, 0, None, None) == 0
 
 
+def test_sample_ex_argument_errors_need_no_gpu():
+    L = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    # negative stage count
+    err = ctypes.c_void_p()
+    rc = L.mlxf_sample_ex(fake, 0, 1, 10, 10, None, None, None, None, None, None, fake, None, None,
+                          None, 0, fake, 1 << 20, -1, None, ctypes.byref(err))
+    assert rc == _lib.EINVAL and err.value
+    L.mlxf_string_free(err)
+    # min_p without temperature is fine (greedy rows ignore it); NULL logits is not
+    err = ctypes.c_void_p()
+    rc = L.mlxf_sample_ex(None, 0, 1, 10, 10, None, None, None, fake, None, None, fake, None, None,
+                          None, 0, fake, 1 << 20, 3, None, ctypes.byref(err))
+    assert rc == _lib.EINVAL
+    L.mlxf_string_free(err)
+    assert L.mlxf_sample_ex(None, 0, 0, 10, 10, None, None, None, None, None, None, None, None, None,
+                            None, 0, None, 0, 0, None, None) == 0
+
+
 def test_refine_stage_hint_from_host_parameters():
     """Host-side stage count: greedy and top-k <= 63 rows need none, temperature-
     only rows one (the kept-mass pass), anything else all three."""

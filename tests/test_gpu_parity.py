@@ -273,3 +273,45 @@ def test_stage_counts_agree(dtype):
             g = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=3, stages=st)
             assert np.array_equal(g["ids"], ref["ids"]), (st, g["ids"], ref["ids"])
             assert np.array_equal(g["lp"].view(np.uint32), ref["lp"].view(np.uint32))
+
+
+def _minp_case(rng, B, V, dtype, kind):
+    """Rows where min_p binds or not, behind each earlier filter: temperature
+    only, top-k <= 63, top-k > 63, top-p, and top-k > 63 with top-p."""
+    z = rng.standard_normal((B, V)).astype(np.float32) * np.float32(rng.uniform(0.5, 3.0))
+    for r in range(B):
+        hot = rng.choice(V, size=min(V, 12), replace=False)
+        z[r, hot] += rng.uniform(2.0, 6.0, hot.size).astype(np.float32)
+    host = z if dtype == "f32" else (workloads.to_bf16_bits(z) if dtype == "bf16" else z.astype(np.float16))
+    T = rng.uniform(0.4, 1.3, B).astype(np.float32)
+    k = np.zeros(B, np.int32)
+    p = np.ones(B, np.float32)
+    if kind in ("klist",):
+        k[:] = rng.integers(1, 60, B)
+    if kind in ("khist", "khist_topp"):
+        k[:] = rng.integers(100, 3000, B)
+    if kind in ("topp", "khist_topp"):
+        p[:] = rng.uniform(0.5, 0.99, B)
+    mp = rng.choice(np.array([0.0, 0.001, 0.02, 0.1, 0.3, 0.7, 1.0], np.float32), B)
+    tlp = rng.integers(-1, 3, B).astype(np.int32)
+    u = rng.random(B).astype(np.float32)
+    return host, T, k, p, mp, tlp, u
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("kind", ["temp", "klist", "khist", "topp", "khist_topp"])
+def test_min_p_parity(dtype, kind):
+    """min_p (src/sample/sampler.cpp:87-93, after top-p) against the oracle,
+    behind every earlier filter, at every refine stage count."""
+    rng = np.random.default_rng(500 + len(kind) * 13 + len(dtype))
+    for V in (4000, 30000):
+        B = 8
+        host, T, k, p, mp, tlp, u = _minp_case(rng, B, V, dtype, kind)
+        say(f"[parity] min_p {kind} dtype={dtype} V={V}")
+        dev = gu.to_device(host, dtype)
+        o = gu.oracle_sample(host, dtype, T=T, k=k, p=p, tlp=tlp, u=u, K_max=2, min_p=mp)
+        ref = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=2, min_p=mp, stages=3)
+        gu.compare(ref, o, dtype, tlp=tlp, label=f"min_p {kind} {dtype} V={V}")
+        for st in (0, 1):
+            g = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=2, min_p=mp, stages=st)
+            assert np.array_equal(g["ids"], ref["ids"]), (kind, st, g["ids"], ref["ids"])

@@ -288,3 +288,29 @@ def test_workloads_are_deterministic(orc):
     assert np.array_equal(a.logits, b.logits) and a.B == 1 and a.V == 128256
     assert a.algorithmic_bytes() == 513048
     assert workloads.make(3).algorithmic_bytes() == 19448576
+
+
+def test_min_p_in_the_batched_oracle(orc):
+    """The batched oracle's min_p (after top-p) equals filtering the row with
+    the filter stage and drawing from what is left, and keeps exactly the
+    weights exp(z' - max z') >= min_p (brute force)."""
+    rng = np.random.default_rng(31)
+    B, V = 24, 300
+    z = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    T = rng.uniform(0.5, 1.5, B).astype(np.float32)
+    k = rng.choice([0, 5, 40], B).astype(np.int32)
+    p = rng.choice([1.0, 0.9, 0.6], B).astype(np.float32)
+    mp = rng.choice([0.0, 0.01, 0.1, 0.5, 1.0], B).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    r = orc.sample(z, T=T, k=k, p=p, min_p=mp, u=u, tlp=np.full(B, -1, np.int32))
+    for i in range(B):
+        f = orc.filter_row(z[i], T=float(T[i]), k=int(k[i]), p=float(p[i]), min_p=float(mp[i]))
+        # brute force of the min_p step alone on the top-k / top-p survivors
+        g = orc.filter_row(z[i], T=float(T[i]), k=int(k[i]), p=float(p[i]))
+        fin = np.isfinite(g)
+        w = np.exp(g[fin].astype(np.float64) - g[fin].max())
+        keep = np.zeros(V, bool)
+        keep[np.nonzero(fin)[0]] = w >= float(mp[i]) if mp[i] > 0 else True
+        assert np.array_equal(np.isfinite(f), keep), i
+        if not (r["flags"][i] & (orc.FLAG_DRAW_AMBIG | orc.FLAG_MINP_AMBIG | orc.FLAG_TOPP_AMBIG)):
+            assert r["ids"][i] == orc.draw_row(f, float(u[i]))[0], i
