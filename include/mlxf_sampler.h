@@ -159,6 +159,36 @@ int mlxf_sampler_first_pass(const void* d_logits, int dtype, int B, int V, int64
                             float* d_out_logprobs, int32_t* d_out_top_ids, float* d_out_top_logprobs,
                             int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err);
 
+/* Bytes of device workspace mlxf_apply_penalties needs: one 32-bit counter per
+ * (row, vocabulary id).  Zero it once before first use; every call leaves it
+ * zero.  No reference counterpart (MLX allocates the counts per call). */
+int mlxf_penalties_workspace_size(int B, int V, size_t* bytes, char** err);
+
+/* Repetition / frequency / presence penalties applied to the logits IN PLACE,
+ * before mlxf_sample / mlxf_greedy on the same logits: the penalized `adj` of
+ * Sampler::sample (src/sample/sampler.cpp:122-133, used at :144; the worker
+ * passes the history only to rows with penalties, src/runtime/worker.cpp:469).
+ * Only the logits at history ids change:
+ *   repetition  z > 0 ? z / pen : z * pen         (sampler.cpp:95-105)
+ *   then        z - count * frequency - presence  (sampler.cpp:107-120)
+ * each step rounded to the logits dtype, with pen, frequency, presence and the
+ * id's count in the history as values of that dtype.  NaN logits are left
+ * as they are.
+ *   d_logits      [B, row_stride] of `dtype`, modified in place.
+ *   d_history     [B, hist_stride] int32 token ids; row r uses its first
+ *                 d_hist_len[r] entries (d_hist_len NULL: all hist_stride).
+ *                 Ids outside [0, V) are ignored.
+ *   d_repetition  [B] fp32 or NULL (1 = off; not finite and positive: off).
+ *   d_frequency, d_presence
+ *                 [B] fp32 or NULL (0 = off; not finite: off)
+ *                 (src/capi/mlxforge.cpp:59-64).
+ *   d_workspace   >= mlxf_penalties_workspace_size(B, V) bytes, zeroed once.
+ * Two kernels on `stream`; no allocation. */
+int mlxf_apply_penalties(void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                         const int32_t* d_history, int64_t hist_stride, const int32_t* d_hist_len,
+                         const float* d_repetition, const float* d_frequency, const float* d_presence,
+                         void* d_workspace, size_t workspace_bytes, void* stream, char** err);
+
 /* argmax over each row, lowest index on ties: Sampler::greedy
  * (src/sample/sampler.h:61, src/sample/sampler.cpp:59-61). */
 int mlxf_greedy(const void* d_logits, int dtype, int B, int V, int64_t row_stride,

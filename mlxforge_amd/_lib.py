@@ -23,6 +23,8 @@ SYMBOLS = (
     "mlxf_sample",
     "mlxf_sample_staged",
     "mlxf_sample_ex",
+    "mlxf_penalties_workspace_size",
+    "mlxf_apply_penalties",
     "mlxf_sampler_refine_stages",
     "mlxf_sampler_first_pass",
     "mlxf_greedy",
@@ -59,6 +61,10 @@ def load() -> ctypes.CDLL:
     L.mlxf_sample_staged.restype = I
     L.mlxf_sample_ex.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, P, I, P, SZ, I, P, PP]
     L.mlxf_sample_ex.restype = I
+    L.mlxf_penalties_workspace_size.argtypes = [I, I, ctypes.POINTER(SZ), PP]
+    L.mlxf_penalties_workspace_size.restype = I
+    L.mlxf_apply_penalties.argtypes = [P, I, I, I, I64, P, I64, P, P, P, P, P, SZ, P, PP]
+    L.mlxf_apply_penalties.restype = I
     L.mlxf_sampler_first_pass.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, I, P, SZ, P, PP]
     L.mlxf_sampler_first_pass.restype = I
     L.mlxf_sampler_refine_stages.argtypes = [I, I, I, P, P, P]

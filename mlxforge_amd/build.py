@@ -1,8 +1,9 @@
 """Build recipe for the HIP sampler library (gfx950).
 
 Produces ``mlxforge_amd/libmlxf_sampler.so`` in-tree from
-``mlxforge_amd/csrc/sampler.hip`` (host side) and ``sampler_{f32,bf16,f16}.hip``
-(one logits dtype's kernels each, compiled in parallel) with hipcc, and the C++
+``mlxforge_amd/csrc/sampler.hip`` (host side), ``sampler_{f32,bf16,f16}.hip``
+(one logits dtype's kernels each) and ``penalties.hip``, compiled in parallel
+with hipcc, and the C++
 known-answer test
 driver ``mlxforge_amd/sampler_kat`` (tests/cpp/sampler_kat.cpp) that exercises
 the C++ host wrapper (mlxforge_amd/include/mlxforge_amd/sampler.hpp).
@@ -25,7 +26,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
-SRCS = [os.path.join(CSRC, f) for f in ("sampler.hip", "sampler_f32.hip", "sampler_bf16.hip", "sampler_f16.hip")]
+SRCS = [os.path.join(CSRC, f) for f in ("sampler.hip", "sampler_f32.hip", "sampler_bf16.hip", "sampler_f16.hip",
+                                         "penalties.hip")]
 LIB = os.path.join(HERE, "libmlxf_sampler.so")
 KAT_SRC = os.path.join(ROOT, "tests", "cpp", "sampler_kat.cpp")
 KAT_BIN = os.path.join(HERE, "sampler_kat")

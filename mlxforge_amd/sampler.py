@@ -6,6 +6,8 @@
   sequence over all rows with per-row parameter arrays.
 * ``Sampler.sample`` / ``Sampler.greedy`` mirror the per-call static API
   (src/sample/sampler.h:51-61) with one parameter set for every row.
+* ``apply_penalties`` penalizes the logits in place (the reference's `adj`,
+  src/sample/sampler.cpp:122-144) before they are sampled.
 
 PyTorch provides device memory and the current stream only; every result is
 computed by libmlxf_sampler.so.  The MLX PRNG key of the reference is replaced
@@ -148,6 +150,56 @@ def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
     return SampleResult(ids, lp, top_ids, top_lp)
 
 
+class PenaltyWorkspace:
+    """Caller-owned counter array of mlxf_apply_penalties (zeroed once, left zero)."""
+
+    def __init__(self, device=None):
+        self.device = torch.device(device) if device is not None else torch.device("cuda")
+        self.buf = None
+
+    def get(self, B: int, V: int) -> torch.Tensor:
+        n = ctypes.c_size_t()
+        err = ctypes.c_void_p()
+        _lib.check(_lib.load().mlxf_penalties_workspace_size(B, V, ctypes.byref(n), ctypes.byref(err)), err)
+        if self.buf is None or self.buf.numel() < n.value:
+            self.buf = torch.zeros(n.value, dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+_default_pen_ws: dict = {}
+
+
+def apply_penalties(logits: torch.Tensor, history: torch.Tensor, hist_len=None, repetition=None,
+                    frequency=None, presence=None, V: int | None = None,
+                    workspace: PenaltyWorkspace | None = None) -> torch.Tensor:
+    """Repetition / frequency / presence penalties on a [B, row_stride] logits
+    view, in place (src/sample/sampler.cpp:95-133): the `adj` the sampler then
+    reads.  history: [B, N] int32 device tensor; hist_len: per-row used length
+    (None: N).  Per-row knobs as in sample_rows (None: off).  Returns logits."""
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be a [B, V] view with unit stride along V")
+    if history.dim() != 2 or history.dtype != torch.int32 or history.stride(1) != 1:
+        raise ValueError("history must be a [B, N] int32 tensor with unit stride along N")
+    dev = logits.device
+    B = logits.shape[0]
+    V = logits.shape[1] if V is None else V
+    code = _DTYPES[logits.dtype]
+    hl = _param(hist_len, B, torch.int32, dev)
+    rep = _param(repetition, B, torch.float32, dev)
+    fq = _param(frequency, B, torch.float32, dev)
+    ps = _param(presence, B, torch.float32, dev)
+    if workspace is None:
+        workspace = _default_pen_ws.setdefault(dev, PenaltyWorkspace(dev))
+    ws = workspace.get(B, V)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    err = ctypes.c_void_p()
+    rc = _lib.load().mlxf_apply_penalties(
+        _ptr(logits), code, B, V, logits.stride(0), _ptr(history), history.stride(0), _ptr(hl),
+        _ptr(rep), _ptr(fq), _ptr(ps), _ptr(ws), ws.numel(), ctypes.c_void_p(stream), ctypes.byref(err))
+    _lib.check(rc, err)
+    return logits
+
+
 def greedy(logits: torch.Tensor, workspace: Workspace | None = None) -> torch.Tensor:
     """argmax per row, lowest index on ties (src/sample/sampler.cpp:59-61)."""
     if logits.dim() != 2 or logits.stride(1) != 1:
@@ -171,9 +223,12 @@ class Sampler:
     """Per-call API of src/sample/sampler.h:47-79, one parameter set for all rows."""
 
     @staticmethod
-    def sample(logits: torch.Tensor, params: SamplingParams, uniforms) -> SampleResult:
-        if params.has_penalties():
-            raise NotImplementedError("penalties: call apply_penalties on the logits first")
+    def sample(logits: torch.Tensor, params: SamplingParams, uniforms, history=None) -> SampleResult:
+        """history: [B, N] int32 device tensor; with penalties in params the
+        logits are penalized in place first (src/sample/sampler.cpp:144)."""
+        if params.has_penalties() and history is not None and history.shape[1] > 0:
+            apply_penalties(logits, history, repetition=params.repetition_penalty,
+                            frequency=params.frequency_penalty, presence=params.presence_penalty)
         B, V = logits.shape
         K = min(max(params.top_logprobs, 0), V)
         # Sampler::sample always returns the chosen-token logprob (sampler.cpp:151-154).

@@ -57,6 +57,9 @@ def lib():
         L.orc_lse_row.restype = ctypes.c_double
         L.orc_draw_row.argtypes = [P, ctypes.c_int, ctypes.c_float, P]
         L.orc_draw_row.restype = ctypes.c_int
+        L.orc_apply_penalties.argtypes = [P, ctypes.c_int, ctypes.c_int, P, ctypes.c_int,
+                                          ctypes.c_float, ctypes.c_float, ctypes.c_float]
+        L.orc_apply_penalties.restype = None
         _lib = L
     return _lib
 
@@ -114,6 +117,14 @@ def filter_row(z, T=0.0, k=0, p=1.0, min_p=0.0, dtype: int = F32) -> np.ndarray:
     rc = lib().orc_filter_row(_ptr(z), z.size, dtype, T, k, p, min_p, _ptr(out))
     assert rc == 0
     return out
+
+
+def apply_penalties(z, hist, rep=1.0, freq=0.0, pres=0.0, dtype: int = F32) -> np.ndarray:
+    """Penalized copy of one row (float32 values of the logits dtype)."""
+    z = np.array(z, np.float32)
+    h = np.ascontiguousarray(np.asarray(hist, np.int32))
+    lib().orc_apply_penalties(_ptr(z), z.size, dtype, _ptr(h), h.size, rep, freq, pres)
+    return z
 
 
 def greedy_row(z) -> int:

@@ -13,6 +13,7 @@
  *   apply_top_k       src/sample/sampler.cpp:63-68   (clamp k to V: :159-161)
  *   apply_top_p       src/sample/sampler.cpp:70-85
  *   apply_min_p       src/sample/sampler.cpp:87-93
+ *   penalties         src/sample/sampler.cpp:95-133
  *   log_probs / gather_logprob / top_k_logprobs   src/sample/sampler.cpp:15-38
  *   per-row application in the decode step        src/runtime/worker.cpp:448-486
  *   parameter sanitisation                        src/capi/mlxforge.cpp:43-70
@@ -44,6 +45,9 @@
  *   D9  min_p in (0, 1] (else off, src/capi/mlxforge.cpp:58) is rounded to the
  *       logits dtype like p (sampler.cpp:91 multiplies by array(min_p,
  *       probs.dtype())) and applied after top-p: keep exp(z' - max z') >= min_p.
+ *   D10 a history id's count for the frequency penalty is its exact number of
+ *       occurrences rounded once to the logits dtype (sampler.cpp:113 sums
+ *       ones in the logits dtype; below 257 every order of summation agrees).
  *
  * Ambiguity flags (the north-star exclusion rule): a row whose top-p cutoff or
  * draw boundary lies within 1e-6 of the compared quantity is reported with
@@ -477,6 +481,38 @@ int orc_sample_ex(const void* logits, int dtype, int B, int V, long row_stride, 
   for (int t = 1; t < nthreads; ++t) pthread_join(th[t], NULL);
   pthread_mutex_destroy(&j.mu);
   return 0;
+}
+
+/* Penalties on one row in place (z holds values of the logits dtype):
+ *   apply_repetition_penalty  src/sample/sampler.cpp:95-105
+ *   apply_frequency_presence  src/sample/sampler.cpp:107-120
+ *   penalize (order, when)    src/sample/sampler.cpp:122-133
+ * with the C ABI's sanitisation (src/capi/mlxforge.cpp:59-64).  Every graph
+ * op rounds to the logits dtype; the count of an id is its exact number of
+ * occurrences, as a value of the dtype (D10).  Ids outside [0, V) are
+ * ignored; NaN logits are left as they are. */
+void orc_apply_penalties(float* z, int V, int dtype, const int* hist, int n, float rep, float freq,
+                         float pres) {
+  if (!(isfinite(rep) && rep > 0.0f)) rep = 1.0f;
+  if (!isfinite(freq)) freq = 0.0f;
+  if (!isfinite(pres)) pres = 0.0f;
+  if (rep == 1.0f && freq == 0.0f && pres == 0.0f) return;
+  unsigned* cnt = (unsigned*)calloc((size_t)V, sizeof(unsigned));
+  for (int j = 0; j < n; ++j)
+    if (hist[j] >= 0 && hist[j] < V) cnt[hist[j]]++;
+  const float pen = round_dtype(rep, dtype), fq = round_dtype(freq, dtype), ps = round_dtype(pres, dtype);
+  for (int i = 0; i < V; ++i) {
+    if (!cnt[i] || isnan(z[i])) continue;
+    float x = z[i];
+    if (rep != 1.0f) x = x > 0.0f ? round_dtype(x / pen, dtype) : round_dtype(x * pen, dtype);
+    if (freq != 0.0f || pres != 0.0f) {
+      const float cd = round_dtype((float)cnt[i], dtype);
+      x = round_dtype(x - round_dtype(cd * fq, dtype), dtype);
+      x = round_dtype(x - ps, dtype);
+    }
+    z[i] = x;
+  }
+  free(cnt);
 }
 
 /* orc_sample_ex without min_p: the product's mlxf_sample. */

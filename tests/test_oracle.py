@@ -314,3 +314,47 @@ def test_min_p_in_the_batched_oracle(orc):
         assert np.array_equal(np.isfinite(f), keep), i
         if not (r["flags"][i] & (orc.FLAG_DRAW_AMBIG | orc.FLAG_MINP_AMBIG | orc.FLAG_TOPP_AMBIG)):
             assert r["ids"][i] == orc.draw_row(f, float(u[i]))[0], i
+
+
+def test_repetition_penalty(orc):  # tests/sample/sampler_test.cpp:89-98
+    f = orc.apply_penalties([2.0, 1.0, 0.5], [0], rep=4.0)
+    assert f.tolist() == [0.5, 1.0, 0.5]
+    # a negative seen logit is multiplied (pushed further down)
+    assert orc.apply_penalties([-2.0, 1.0], [0], rep=4.0).tolist() == [-8.0, 1.0]
+
+
+def test_frequency_and_presence_penalties(orc):  # :100-115
+    hist = [1, 1, 2]
+    assert orc.apply_penalties([0.0] * 4, hist, freq=0.5).tolist() == [0.0, -1.0, -0.5, 0.0]
+    assert np.allclose(orc.apply_penalties([0.0] * 4, hist, pres=0.7), [0.0, -0.7, -0.7, 0.0])
+
+
+def test_repetition_penalty_moves_greedy(orc):  # :117-124
+    f = orc.apply_penalties([2.0, 1.0, 0.5], [0], rep=4.0)
+    assert orc.greedy_row(f) == 1
+
+
+def test_penalty_sanitisation_and_rounding(orc):
+    # off: rep 1 / non-finite / non-positive, freq and pres 0 / non-finite
+    for kw in (dict(rep=1.0), dict(rep=float("nan")), dict(rep=-2.0), dict(freq=float("inf")),
+               dict(pres=float("nan"))):
+        assert orc.apply_penalties([2.0, 1.0], [0, 1], **kw).tolist() == [2.0, 1.0]
+    # ids outside [0, V) are ignored
+    assert orc.apply_penalties([2.0, 1.0], [-1, 7], rep=2.0).tolist() == [2.0, 1.0]
+    # bf16: every step rounds to bf16 (0.3 -> 0.30078125, 1/3 of 1 -> 0.333984375)
+    b = orc.apply_penalties([1.0, 0.0], [0, 0, 0], rep=3.0, freq=0.3, dtype=orc.BF16)
+    x = orc.round_bf16(1.0 / orc.round_bf16(3.0))
+    x = orc.round_bf16(x - orc.round_bf16(3.0 * orc.round_bf16(0.3)))
+    assert b[0] == x and b[1] == 0.0
+    # against a float64 restatement with rounding after every op (fp32 rows)
+    rng = np.random.default_rng(4)
+    z = (rng.standard_normal(50) * 3).astype(np.float32)
+    h = rng.integers(0, 50, 80)
+    got = orc.apply_penalties(z, h, rep=1.7, freq=0.25, pres=0.4)
+    exp = z.copy()
+    for i, c in zip(*np.unique(h, return_counts=True)):
+        x = np.float32(z[i])
+        x = np.float32(x / np.float32(1.7)) if x > 0 else np.float32(x * np.float32(1.7))
+        x = np.float32(x - np.float32(np.float32(c) * np.float32(0.25)))
+        exp[i] = np.float32(x - np.float32(0.4))
+    assert np.array_equal(got, exp)
