@@ -189,6 +189,16 @@ int mlxf_apply_penalties(void* d_logits, int dtype, int B, int V, int64_t row_st
                          const float* d_repetition, const float* d_frequency, const float* d_presence,
                          void* d_workspace, size_t workspace_bytes, void* stream, char** err);
 
+/* Per-row draw uniforms on the device: u[r] = Philox4x32-10 keyed by
+ * d_seed[r] at counter (step_r, 0), first word's top 24 bits times 2^-24, in
+ * [0, 1).  step_r = d_step[r], or `step` when d_step is NULL.  Replaces the
+ * per-row MLX key derived from the request seed and split every step
+ * (src/runtime/worker.cpp:416,465-466): the same (seed, step) gives the same
+ * uniform, so a seed replays its tokens (tests/sample/sampler_test.cpp:126-134).
+ * One small kernel on `stream`; feed d_uniforms to mlxf_sample*. */
+int mlxf_uniforms(int B, const uint64_t* d_seed, const uint64_t* d_step, uint64_t step,
+                  float* d_uniforms, void* stream, char** err);
+
 /* argmax over each row, lowest index on ties: Sampler::greedy
  * (src/sample/sampler.h:61, src/sample/sampler.cpp:59-61). */
 int mlxf_greedy(const void* d_logits, int dtype, int B, int V, int64_t row_stride,

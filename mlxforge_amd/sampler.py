@@ -200,6 +200,30 @@ def apply_penalties(logits: torch.Tensor, history: torch.Tensor, hist_len=None, 
     return logits
 
 
+def uniforms(seed: torch.Tensor, step, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-row draw uniforms from (seed, step) on the device (Philox4x32-10,
+    mlxf_uniforms): the replacement of the reference's per-row MLX key split
+    each step (src/runtime/worker.cpp:416,465-466).  seed: (B,) int64 device
+    tensor (bit pattern of the uint64 seed); step: int (same for every row) or
+    a (B,) int64 device tensor."""
+    if seed.dim() != 1 or seed.dtype != torch.int64 or not seed.is_contiguous():
+        raise ValueError("seed must be a contiguous (B,) int64 tensor")
+    dev = seed.device
+    B = seed.shape[0]
+    if out is None:
+        out = torch.empty(B, dtype=torch.float32, device=dev)
+    st_t = step if torch.is_tensor(step) else None
+    if st_t is not None and (st_t.dtype != torch.int64 or st_t.numel() != B or not st_t.is_contiguous()):
+        raise ValueError("step must be an int or a contiguous (B,) int64 tensor")
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    err = ctypes.c_void_p()
+    rc = _lib.load().mlxf_uniforms(B, _ptr(seed), _ptr(st_t) if st_t is not None else None,
+                                   0 if st_t is not None else int(step) & (2**64 - 1),
+                                   _ptr(out), ctypes.c_void_p(stream), ctypes.byref(err))
+    _lib.check(rc, err)
+    return out
+
+
 def greedy(logits: torch.Tensor, workspace: Workspace | None = None) -> torch.Tensor:
     """argmax per row, lowest index on ties (src/sample/sampler.cpp:59-61)."""
     if logits.dim() != 2 or logits.stride(1) != 1:

@@ -60,6 +60,10 @@ def lib():
         L.orc_apply_penalties.argtypes = [P, ctypes.c_int, ctypes.c_int, P, ctypes.c_int,
                                           ctypes.c_float, ctypes.c_float, ctypes.c_float]
         L.orc_apply_penalties.restype = None
+        L.orc_philox4x32_10.argtypes = [P, P, P]
+        L.orc_philox4x32_10.restype = None
+        L.orc_uniforms.argtypes = [ctypes.c_int, P, P, P]
+        L.orc_uniforms.restype = None
         _lib = L
     return _lib
 
@@ -125,6 +129,22 @@ def apply_penalties(z, hist, rep=1.0, freq=0.0, pres=0.0, dtype: int = F32) -> n
     h = np.ascontiguousarray(np.asarray(hist, np.int32))
     lib().orc_apply_penalties(_ptr(z), z.size, dtype, _ptr(h), h.size, rep, freq, pres)
     return z
+
+
+def philox4x32_10(ctr, key) -> list:
+    c = np.ascontiguousarray(np.asarray(ctr, np.uint32))
+    k = np.ascontiguousarray(np.asarray(key, np.uint32))
+    o = np.zeros(4, np.uint32)
+    lib().orc_philox4x32_10(_ptr(c), _ptr(k), _ptr(o))
+    return [int(x) for x in o]
+
+
+def uniforms(seed, step) -> np.ndarray:
+    seed = np.ascontiguousarray(np.asarray(seed, np.uint64))
+    step = np.ascontiguousarray(np.broadcast_to(np.asarray(step, np.uint64), seed.shape))
+    u = np.zeros(seed.size, np.float32)
+    lib().orc_uniforms(seed.size, _ptr(seed), _ptr(step), _ptr(u))
+    return u
 
 
 def greedy_row(z) -> int:

@@ -515,6 +515,40 @@ void orc_apply_penalties(float* z, int V, int dtype, const int* hist, int n, flo
   free(cnt);
 }
 
+/* Philox4x32-10 (J. Salmon et al., "Parallel random numbers: as easy as 1,
+ * 2, 3", SC'11): ten rounds of two 32x32->64 multiplies with the published
+ * multipliers and Weyl key increments.  The draw uniform of a row is
+ * (first word >> 8) * 2^-24 at key = seed, counter = (step, 0) -- the
+ * product's replacement for the MLX key split per step
+ * (src/runtime/worker.cpp:416,465-466). */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+  uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+    c0 = n0;
+    c1 = (uint32_t)p1;
+    c2 = n2;
+    c3 = (uint32_t)p0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  out[0] = c0;
+  out[1] = c1;
+  out[2] = c2;
+  out[3] = c3;
+}
+
+void orc_uniforms(int B, const uint64_t* seed, const uint64_t* step, float* u) {
+  for (int r = 0; r < B; ++r) {
+    const uint32_t ctr[4] = {(uint32_t)step[r], (uint32_t)(step[r] >> 32), 0u, 0u};
+    const uint32_t key[2] = {(uint32_t)seed[r], (uint32_t)(seed[r] >> 32)};
+    uint32_t o[4];
+    orc_philox4x32_10(ctr, key, o);
+    u[r] = (float)(o[0] >> 8) * 0x1p-24f;
+  }
+}
+
 /* orc_sample_ex without min_p: the product's mlxf_sample. */
 int orc_sample(const void* logits, int dtype, int B, int V, long row_stride, const float* T,
                const int* k, const float* p, const int* tlp, const float* u, int32_t* ids,

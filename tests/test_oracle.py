@@ -358,3 +358,27 @@ def test_penalty_sanitisation_and_rounding(orc):
         x = np.float32(x - np.float32(np.float32(c) * np.float32(0.25)))
         exp[i] = np.float32(x - np.float32(0.4))
     assert np.array_equal(got, exp)
+
+
+def test_philox_known_answers(orc):
+    """Philox4x32-10 against the published known-answer vectors of its authors'
+    Random123 library (counter, key -> output)."""
+    assert orc.philox4x32_10([0, 0, 0, 0], [0, 0]) == [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]
+    f = 0xFFFFFFFF
+    assert orc.philox4x32_10([f, f, f, f], [f, f]) == [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]
+    assert orc.philox4x32_10([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344],
+                             [0xA4093822, 0x299F31D0]) == [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]
+
+
+def test_uniforms_are_a_function_of_seed_and_step(orc):
+    seeds = np.array([0, 1, 2**63 + 5, 42], np.uint64)
+    a = orc.uniforms(seeds, 7)
+    assert np.array_equal(a, orc.uniforms(seeds, 7))          # same seed, same step: replay
+    assert not np.array_equal(a, orc.uniforms(seeds, 8))      # next step draws anew
+    assert ((a >= 0) & (a < 1)).all()
+    # u is the top 24 bits of the first output word
+    w = orc.philox4x32_10([7, 0, 0, 0], [42, 0])[0]
+    assert a[3] == np.float32((w >> 8) * 2.0 ** -24)
+    # roughly uniform over many steps
+    u = orc.uniforms(np.full(20000, 9, np.uint64), np.arange(20000, dtype=np.uint64))
+    assert abs(float(u.mean()) - 0.5) < 0.01 and abs(float((u < 0.1).mean()) - 0.1) < 0.01
