@@ -199,6 +199,19 @@ int mlxf_apply_penalties(void* d_logits, int dtype, int B, int V, int64_t row_st
 int mlxf_uniforms(int B, const uint64_t* d_seed, const uint64_t* d_step, uint64_t step,
                   float* d_uniforms, void* stream, char** err);
 
+/* The grammar-constrained rows of a step: row + an additive fp32 mask of
+ * 0 / -inf, which MLX evaluates as an fp32 row (src/runtime/worker.cpp:455-459;
+ * the mask, :142-179).  The mask is given as one bit per token, 1 = allowed:
+ *   d_allowed_bits  [B, bits_stride] uint32 words, bit (i & 31) of word i >> 5.
+ * Writes d_out [B, out_stride] fp32: the logit where allowed, -inf elsewhere.
+ * A row with no allowed token is copied unmasked (the reference never builds
+ * an all -inf mask, :175-177).  Sample d_out with dtype MLXF_DTYPE_F32, as the
+ * reference samples the promoted row.  No reference counterpart for the bit
+ * packing (the reference uploads the fp32 array). */
+int mlxf_apply_mask(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                    const uint32_t* d_allowed_bits, int64_t bits_stride, float* d_out,
+                    int64_t out_stride, void* stream, char** err);
+
 /* argmax over each row, lowest index on ties: Sampler::greedy
  * (src/sample/sampler.h:61, src/sample/sampler.cpp:59-61). */
 int mlxf_greedy(const void* d_logits, int dtype, int B, int V, int64_t row_stride,

@@ -26,6 +26,7 @@ SYMBOLS = (
     "mlxf_penalties_workspace_size",
     "mlxf_apply_penalties",
     "mlxf_uniforms",
+    "mlxf_apply_mask",
     "mlxf_sampler_refine_stages",
     "mlxf_sampler_first_pass",
     "mlxf_greedy",
@@ -68,6 +69,8 @@ def load() -> ctypes.CDLL:
     L.mlxf_apply_penalties.restype = I
     L.mlxf_uniforms.argtypes = [I, P, P, ctypes.c_uint64, P, P, PP]
     L.mlxf_uniforms.restype = I
+    L.mlxf_apply_mask.argtypes = [P, I, I, I, I64, P, I64, P, I64, P, PP]
+    L.mlxf_apply_mask.restype = I
     L.mlxf_sampler_first_pass.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, I, P, SZ, P, PP]
     L.mlxf_sampler_first_pass.restype = I
     L.mlxf_sampler_refine_stages.argtypes = [I, I, I, P, P, P]

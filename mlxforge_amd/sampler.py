@@ -224,6 +224,31 @@ def uniforms(seed: torch.Tensor, step, out: torch.Tensor | None = None) -> torch
     return out
 
 
+def apply_mask(logits: torch.Tensor, allowed_bits: torch.Tensor, V: int | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Grammar-constrained rows (src/runtime/worker.cpp:455-459): an fp32
+    [B, V] copy with -inf where the bit mask (int32 [B, ceil(V/32)], bit 1 =
+    allowed) forbids a token; rows with no allowed token are left unmasked.
+    Sample the result as fp32 logits, as the reference samples the promoted
+    row."""
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be a [B, V] view with unit stride along V")
+    if allowed_bits.dim() != 2 or allowed_bits.dtype != torch.int32 or allowed_bits.stride(1) != 1:
+        raise ValueError("allowed_bits must be a [B, W] int32 tensor with unit stride along W")
+    dev = logits.device
+    B = logits.shape[0]
+    V = logits.shape[1] if V is None else V
+    if out is None:
+        out = torch.empty((B, V), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    err = ctypes.c_void_p()
+    rc = _lib.load().mlxf_apply_mask(_ptr(logits), _DTYPES[logits.dtype], B, V, logits.stride(0),
+                                     _ptr(allowed_bits), allowed_bits.stride(0), _ptr(out), out.stride(0),
+                                     ctypes.c_void_p(stream), ctypes.byref(err))
+    _lib.check(rc, err)
+    return out
+
+
 def greedy(logits: torch.Tensor, workspace: Workspace | None = None) -> torch.Tensor:
     """argmax per row, lowest index on ties (src/sample/sampler.cpp:59-61)."""
     if logits.dim() != 2 or logits.stride(1) != 1:

@@ -147,6 +147,30 @@ def uniforms(seed, step) -> np.ndarray:
     return u
 
 
+def apply_mask(z, allowed) -> np.ndarray:
+    """row + the grammar's additive fp32 mask (0 allowed, -inf not), as MLX
+    evaluates it: an fp32 row (src/runtime/worker.cpp:455-459).  A row with no
+    allowed token gets the zero mask (:175-177).  z: float32 values of the
+    logits dtype; allowed: bool per token."""
+    z = np.asarray(z, np.float32)
+    allowed = np.asarray(allowed, bool)
+    if not allowed.any():
+        allowed = np.ones_like(allowed)
+    mask = np.where(allowed, np.float32(0.0), np.float32(-np.inf)).astype(np.float32)
+    return (z + mask).astype(np.float32)
+
+
+def pack_bits(allowed) -> np.ndarray:
+    """bool [B, V] -> uint32 [B, ceil(V / 32)], bit (i & 31) of word i >> 5."""
+    allowed = np.asarray(allowed, bool)
+    B, V = allowed.shape
+    W = (V + 31) // 32
+    padded = np.zeros((B, W * 32), bool)
+    padded[:, :V] = allowed
+    bits = padded.reshape(B, W, 32).astype(np.uint64) << np.arange(32, dtype=np.uint64)
+    return bits.sum(axis=2).astype(np.uint32)
+
+
 def greedy_row(z) -> int:
     z = np.ascontiguousarray(np.asarray(z, np.float32))
     return lib().orc_greedy_row(_ptr(z), z.size)

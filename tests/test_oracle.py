@@ -382,3 +382,16 @@ def test_uniforms_are_a_function_of_seed_and_step(orc):
     # roughly uniform over many steps
     u = orc.uniforms(np.full(20000, 9, np.uint64), np.arange(20000, dtype=np.uint64))
     assert abs(float(u.mean()) - 0.5) < 0.01 and abs(float((u < 0.1).mean()) - 0.1) < 0.01
+
+
+def test_grammar_mask(orc):
+    """row + fp32 mask (src/runtime/worker.cpp:142-179,455-459): allowed
+    entries keep their value, the rest are -inf; an all-disallowed row is left
+    as is; bits pack little-endian within each word."""
+    z = np.array([1.5, -2.0, 0.25, 7.0], np.float32)
+    m = orc.apply_mask(z, [True, False, True, False])
+    assert m.tolist() == [1.5, -np.inf, 0.25, -np.inf]
+    assert orc.apply_mask(z, [False] * 4).tolist() == z.tolist()
+    # token 33 is bit 1 of word 1
+    assert orc.pack_bits([[True, False, True] + [False] * 30 + [True]]).tolist() == [[0b101, 0b10]]
+    assert orc.greedy_row(orc.apply_mask(z, [True, False, True, False])) == 0
