@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -149,6 +150,51 @@ class Sampler {
     return sample_rows(logits, rows, uniforms);
   }
 
+  // The penalized `adj` of Sampler::sample (src/sample/sampler.cpp:95-133,144),
+  // written over the logits in place: row r of `history` holds its token ids
+  // (prompt and generated so far, src/runtime/worker.cpp:415,437,549); each
+  // row's penalties come from its SamplingParams.  Call before sample_rows on
+  // the same logits; sample_rows then needs the penalties cleared from params.
+  void apply_penalties(void* logits, int dtype, int B, int V, int64_t row_stride,
+                       const std::vector<std::vector<int32_t>>& history,
+                       const std::vector<SamplingParams>& params) {
+    if (static_cast<int>(history.size()) != B || static_cast<int>(params.size()) != B)
+      throw SamplerError(MLXF_EINVAL, "mlxf: history and params need one entry per row");
+    size_t N = 0;
+    for (const auto& h : history) N = h.size() > N ? h.size() : N;
+    if (B == 0 || N == 0) return;
+    std::vector<int32_t> flat(static_cast<size_t>(B) * N, 0), len(B);
+    std::vector<float> rep(B), fq(B), ps(B);
+    for (int r = 0; r < B; ++r) {
+      std::copy(history[r].begin(), history[r].end(), flat.begin() + static_cast<size_t>(r) * N);
+      len[r] = static_cast<int32_t>(history[r].size());
+      rep[r] = params[r].repetition_penalty;
+      fq[r] = params[r].frequency_penalty;
+      ps[r] = params[r].presence_penalty;
+    }
+    char* err = nullptr;
+    size_t pw = 0;
+    detail::check(mlxf_penalties_workspace_size(B, V, &pw, &err), err);
+    if (pw > pen_ws_bytes_) {
+      pen_ws_.reserve(pw);
+      pen_ws_bytes_ = pw;
+      // once per growth, outside any steady-state step: the counters start at
+      // zero and every call leaves them there
+      detail::hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+      detail::hip_check(hipMemset(pen_ws_.p, 0, pw), "hipMemset");
+    }
+    upload(hist_, flat.data(), static_cast<int>(flat.size()));
+    upload(hlen_, len.data(), B);
+    upload(rep_, rep.data(), B);
+    upload(fq_, fq.data(), B);
+    upload(ps_, ps.data(), B);
+    err = nullptr;
+    detail::check(mlxf_apply_penalties(logits, dtype, B, V, row_stride ? row_stride : V, hist_.p,
+                                       static_cast<int64_t>(N), hlen_.p, rep_.p, fq_.p, ps_.p, pen_ws_.p,
+                                       pen_ws_bytes_, stream_, &err),
+                  err);
+  }
+
   // Sampler::greedy (src/sample/sampler.h:61): argmax, lowest index on ties.
   std::vector<int32_t> greedy(const DeviceLogits& logits) {
     const int B = logits.B, V = logits.V;
@@ -243,8 +289,10 @@ class Sampler {
   hipStream_t stream_;
   detail::DeviceBuf<unsigned char> ws_;
   size_t ws_bytes_ = 0;
-  detail::DeviceBuf<float> T_, p_, mp_, u_, lp_, top_lp_;
-  detail::DeviceBuf<int32_t> k_, tlp_, ids_, top_ids_;
+  detail::DeviceBuf<float> T_, p_, mp_, u_, lp_, top_lp_, rep_, fq_, ps_;
+  detail::DeviceBuf<int32_t> k_, tlp_, ids_, top_ids_, hist_, hlen_;
+  detail::DeviceBuf<unsigned char> pen_ws_;
+  size_t pen_ws_bytes_ = 0;
 };
 
 }  // namespace mlxforge_amd

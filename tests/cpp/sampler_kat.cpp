@@ -227,6 +227,47 @@ void case_penalties_refused(Sampler& s) {  // :89-124 need apply_penalties first
   }
 }
 
+std::vector<float> penalized(Sampler& s, const std::vector<float>& z, const std::vector<int32_t>& hist,
+                             const SamplingParams& p) {
+  Logits lg({z});
+  s.apply_penalties(lg.d, MLXF_DTYPE_F32, 1, static_cast<int>(z.size()), 0, {hist}, {p});
+  std::vector<float> out(z.size());
+  (void)hipMemcpy(out.data(), lg.d, z.size() * sizeof(float), hipMemcpyDeviceToHost);
+  return out;
+}
+
+void case_repetition_penalty(Sampler& s) {  // :89-98
+  SamplingParams p;
+  p.repetition_penalty = 4.0f;
+  std::vector<float> f = penalized(s, {2.0f, 1.0f, 0.5f}, {0}, p);
+  KAT_CHECK(f[0] == 0.5f);  // 2.0 / 4.0
+  KAT_CHECK(f[1] == 1.0f);  // untouched
+  KAT_CHECK(f[0] < f[1]);
+}
+
+void case_frequency_presence(Sampler& s) {  // :100-115
+  SamplingParams pf;
+  pf.frequency_penalty = 0.5f;
+  std::vector<float> f = penalized(s, {0.0f, 0.0f, 0.0f, 0.0f}, {1, 1, 2}, pf);
+  KAT_CHECK((f == std::vector<float>{0.0f, -1.0f, -0.5f, 0.0f}));
+  SamplingParams pp;
+  pp.presence_penalty = 0.7f;
+  std::vector<float> g = penalized(s, {0.0f, 0.0f, 0.0f, 0.0f}, {1, 1, 2}, pp);
+  KAT_CHECK(g[0] == 0.0f && g[3] == 0.0f);
+  KAT_CHECK(g[1] == -0.7f && g[2] == -0.7f);
+}
+
+void case_penalty_moves_greedy(Sampler& s) {  // :117-124
+  Logits lg({{2.0f, 1.0f, 0.5f}});
+  SamplingParams p;
+  p.temperature = 0.0f;
+  p.repetition_penalty = 4.0f;
+  s.apply_penalties(lg.d, MLXF_DTYPE_F32, 1, 3, 0, {{0}}, {p});
+  p.repetition_penalty = 1.0f;  // applied
+  SampleResult r = s.sample(lg.view(), p, {0.5f});
+  KAT_CHECK((r.tokens == std::vector<int32_t>{1}));
+}
+
 void case_row_stride(Sampler& s) {  // the (bucket, 1, V) view with B rows sampled
   // Rows of 5 logits inside rows of 8; the padding holds a value that would win.
   Logits lg({{0.0f, 1.0f, 3.0f, 2.0f, 0.5f, 99.0f, 99.0f, 99.0f},
@@ -275,6 +316,9 @@ int main() {
       {"top_logprobs come from the pre-temperature logits", case_top_logprobs_pre_temperature},
       {"min-p keeps tokens with prob >= min_p * max_prob", case_min_p},
       {"penalties left in the parameters are refused", case_penalties_refused},
+      {"repetition penalty pushes a seen token below an unseen one", case_repetition_penalty},
+      {"frequency penalty scales with count, presence is flat", case_frequency_presence},
+      {"repetition penalty changes greedy choice", case_penalty_moves_greedy},
       {"row_stride samples B rows of a padded buffer", case_row_stride},
       {"errors carry a code and a message", case_error_reporting},
   };
