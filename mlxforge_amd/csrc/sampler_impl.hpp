@@ -1623,6 +1623,17 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int r = static_cast<int>(blockIdx.x);
   const int S = a.S;
+  // the slices' lists are requested before the row's parameters say whether
+  // they are needed: one memory round trip for everything this kernel reads
+  unsigned long long lw[MAX_S * LIST / THREADS];
+  {
+    const unsigned long long* src = a.list + static_cast<size_t>(r) * S * LIST;
+#pragma unroll
+    for (int k = 0; k < MAX_S * LIST / THREADS; ++k) {
+      const int i = tid + k * THREADS;
+      lw[k] = i < S * LIST ? src[i] : 0ull;
+    }
+  }
   const Mode md = decode<DT>(a, r);
   if (tid < S) {
     const unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + tid) * 4;
@@ -1633,14 +1644,6 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
     sh.slse[tid] = __longlong_as_double(static_cast<long long>(w2));
   }
   if (md.need_list) {
-    const unsigned long long* src = a.list + static_cast<size_t>(r) * S * LIST;
-    // every load issued before the first store: one memory round trip
-    unsigned long long lw[MAX_S * LIST / THREADS];
-#pragma unroll
-    for (int k = 0; k < MAX_S * LIST / THREADS; ++k) {
-      const int i = tid + k * THREADS;
-      lw[k] = i < S * LIST ? src[i] : 0ull;
-    }
 #pragma unroll
     for (int k = 0; k < MAX_S * LIST / THREADS; ++k) {
       const int i = tid + k * THREADS;
