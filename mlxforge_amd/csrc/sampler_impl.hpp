@@ -422,7 +422,6 @@ struct S1Lds {
   float rmin[WAVES];
   int ri[WAVES];
   unsigned int ramin[WAVES];
-  int ramax[WAVES];
   double rd[WAVES];
   unsigned int rth[WAVES];
   int rsc[WAVES + 1];
@@ -448,7 +447,6 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
   // rows that reach the refine stages: the division range of the slice, and
   // (top-k rows) its minimum
   const bool refine = md.kind == KIND_TEMP || md.kind == KIND_TOPP || md.kind == KIND_KHIST;
-  const bool want_min = md.kind == KIND_KHIST || md.kind == KIND_TOPP;
 
   float v[EPT];
 #pragma unroll
@@ -463,25 +461,24 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
     if (lane == 0) sh.rf[wid] = wm;
   }
   if (refine) {
-    // smallest nonzero |z| (as bits - 1, so zeros wrap past every value) and
-    // largest finite |z| (as bits + 2^23: infinities wrap negative)
+    // smallest nonzero |z| (as bits - 1, so zeros wrap past every value; the
+    // -inf read past the row end is never the smallest) and the slice minimum
+    // (with the maximum: the largest finite |z| when neither is infinite)
     unsigned int amin = 0xffffffffu;
-    int amax = 0;
     float tmin = INFINITY;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const bool ok = MLXF_IDX(e) < end;
-      const unsigned int az = __float_as_uint(v[e]) & 0x7fffffffu;
-      amin = min(amin, ok ? az - 1u : 0xffffffffu);
-      amax = max(amax, ok ? static_cast<int>(az + 0x00800000u) : 0);
-      if (want_min) tmin = fminf(tmin, ok ? v[e] : INFINITY);
+    for (int e = 0; e < EPT; ++e) amin = min(amin, (__float_as_uint(v[e]) & 0x7fffffffu) - 1u);
+    if (end - beg == a.L) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) tmin = fminf(tmin, v[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) tmin = fminf(tmin, MLXF_IDX(e) < end ? v[e] : INFINITY);
     }
     amin = wave_min(amin);
-    amax = wave_max(amax);
-    if (want_min) tmin = wave_min(tmin);
+    tmin = wave_min(tmin);
     if (lane == 0) {
       sh.ramin[wid] = amin;
-      sh.ramax[wid] = amax;
       sh.rmin[wid] = tmin;
     }
   }
@@ -612,17 +609,19 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
   unsigned int sfl = 0u;
   if (refine) {
     unsigned int amin = sh.ramin[0];
-    int amax = sh.ramax[0];
     zmin = sh.rmin[0];
 #pragma unroll
     for (int w2 = 1; w2 < WAVES; ++w2) {
       amin = min(amin, sh.ramin[w2]);
-      amax = max(amax, sh.ramax[w2]);
       zmin = fminf(zmin, sh.rmin[w2]);
     }
     // the FMA-corrected division is exact when every nonzero |z| >= 2^-96 and
-    // every finite |z| < 2^100
-    sfl = (amin >= 0x0f7fffffu && amax < static_cast<int>(0x71800000u + 0x00800000u)) ? static_cast<unsigned int>(SL_FAST) : 0u;
+    // every finite |z| < 2^100: here, when the slice's maximum and minimum are
+    // both below 2^100 in magnitude (a slice holding an infinity divides
+    // exactly)
+    sfl = (amin >= 0x0f7fffffu && fabsf(zmax) < 0x1p100f && fabsf(zmin) < 0x1p100f)
+              ? static_cast<unsigned int>(SL_FAST)
+              : 0u;
   }
   if (md.need_list) {
     // the survivors sorted: 64-entry chunks sorted by the waves and merged
