@@ -827,13 +827,13 @@ __device__ __forceinline__ void slice_stage(const Args& a, int r, int s, const P
     // cumulative from the top bin down: the deciding step reads a bin's total
     // and everything above it in one word
     const size_t o = (static_cast<size_t>(r) * a.S + s) * NB;
-    unsigned int cex, cin, ctot;
-    block_scan<unsigned int>(sh.hc[tid], sh.rv, &cex, &cin, &ctot);
-    a.hcnt[o + tid] = cin;
+    const int ci = static_cast<int>(sh.hc[tid]);
+    int ctot;
+    a.hcnt[o + tid] = static_cast<unsigned int>(block_excl_scan_dpp<int>(ci, reinterpret_cast<int*>(sh.rv), &ctot) + ci);
     if (mass) {
-      unsigned long long mex, min_, mtot;
-      block_scan<unsigned long long>(sh.hm[tid], sh.ru, &mex, &min_, &mtot);
-      a.hmass[o + tid] = min_;
+      const unsigned long long mi = sh.hm[tid];
+      unsigned long long mtot;
+      a.hmass[o + tid] = block_excl_scan_dpp<unsigned long long>(mi, sh.ru, &mtot) + mi;
     }
   } else if (pl.phase == PH_GATHER) {
     // the slice's elements in the bracket: one reservation per workgroup
@@ -843,12 +843,14 @@ __device__ __forceinline__ void slice_stage(const Args& a, int r, int s, const P
       const unsigned int zk = f2key(v[e]);
       mine += (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) ? 1u : 0u;
     }
-    unsigned int total;
-    unsigned int pos = block_excl_scan<unsigned int>(mine, sh.rv, &total);
+    int total;
+    int pos = block_excl_scan_dpp<int>(static_cast<int>(mine), reinterpret_cast<int*>(sh.rv), &total);
     if (tid == 0)
-      sh.ncand = total ? __hip_atomic_fetch_add(a.ncand + r, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+      sh.ncand = total ? __hip_atomic_fetch_add(a.ncand + r, static_cast<unsigned int>(total), __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                       : 0u;
     __syncthreads();
-    pos += sh.ncand;
+    pos += static_cast<int>(sh.ncand);
     unsigned long long* dst = a.cand + static_cast<size_t>(r) * CAP;
     if (mine) {
 #pragma unroll
