@@ -754,6 +754,7 @@ struct SLds {
 struct RLds {
   SLds sl;
   unsigned long long cand[CAP];      // gathered candidates (z' key | index << 32)
+  unsigned long long cmq[CAP];       // ... and their fixed-point masses
   unsigned long long kept[MAX_S];    // per-slice kept mass
   unsigned int tcnt[MAX_S];          // per-slice ties / counts
   int ri[WAVES + 1];
@@ -1041,19 +1042,15 @@ template <int DT, bool BY_KEY, bool MASSM, typename PRED>
 __device__ __forceinline__ unsigned int cselect(int n, PRED pred, float Mp, unsigned long long target, bool strict, RLds& sh,
                                 unsigned long long* before_out, unsigned int* gcount) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const float nc = -(Mp * LOG2E);
-  const bool minf = !__builtin_isfinite(Mp);
+  (void)Mp;
   auto field = [](unsigned long long c) {
     return BY_KEY ? static_cast<unsigned int>(c) : static_cast<unsigned int>(c >> 32);
   };
-  auto meas = [&](unsigned long long c) -> unsigned long long {
-    if (!MASSM) return 1ull;
-    return q40(wfun(kval<DT>(static_cast<unsigned int>(c)), Mp, nc, minf));
-  };
+  auto meas = [&](int c) -> unsigned long long { return MASSM ? sh.cmq[c] : 1ull; };
   unsigned int lo = 0xffffffffu, hi = 0u;
   for (int c = tid; c < n; c += THREADS) {
     const unsigned long long e = sh.cand[c];
-    if (pred(e) && meas(e) > 0) {
+    if (pred(e) && meas(c) > 0) {
       lo = min(lo, field(e));
       hi = max(hi, field(e));
     }
@@ -1094,7 +1091,7 @@ __device__ __forceinline__ unsigned int cselect(int n, PRED pred, float Mp, unsi
       const unsigned long long e = sh.cand[c];
       const unsigned int f = field(e);
       if (pred(e) && (f & mask) == prefix) {
-        const unsigned long long m = meas(e);
+        const unsigned long long m = meas(c);
         if (m > 0) {
           const int d = static_cast<int>((f >> shift) & 255u);
           const int pos = BY_KEY ? NB - 1 - d : d;
@@ -1114,7 +1111,7 @@ __device__ __forceinline__ unsigned int cselect(int n, PRED pred, float Mp, unsi
         val[q] = MASSM ? sh.sl.hm[4 * lane + q] : static_cast<unsigned long long>(cnt[q]);
         sum += val[q];
       }
-      const unsigned long long inc = wave_incl_scan(sum);
+      const unsigned long long inc = wave_incl_scan_dpp(sum);
       unsigned long long run = before + inc - sum;
       int found = NB, lastne = -1;
       unsigned long long bef = 0, bef_last = 0;
@@ -1163,13 +1160,10 @@ __device__ __forceinline__ unsigned int cselect(int n, PRED pred, float Mp, unsi
 // Block sum of the fixed-point masses of the candidates with pred.
 template <int DT, typename PRED>
 __device__ __forceinline__ unsigned long long cmass(int n, PRED pred, float Mp, RLds& sh) {
-  const float nc = -(Mp * LOG2E);
-  const bool minf = !__builtin_isfinite(Mp);
+  (void)Mp;
   unsigned long long t = 0;
-  for (int c = threadIdx.x; c < n; c += THREADS) {
-    const unsigned long long e = sh.cand[c];
-    if (pred(e)) t += q40(wfun(kval<DT>(static_cast<unsigned int>(e)), Mp, nc, minf));
-  }
+  for (int c = threadIdx.x; c < n; c += THREADS)
+    if (pred(sh.cand[c])) t += sh.cmq[c];
   return block_sum<unsigned long long>(t, sh.sl.ru);
 }
 
@@ -1458,7 +1452,10 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
 #pragma unroll
     for (int k = 0; k < CAP / THREADS; ++k) {
       const int c = tid + k * THREADS;
-      if (c < n) sh.cand[c] = cv[k];
+      if (c < n) {
+        sh.cand[c] = cv[k];
+        sh.cmq[c] = q40(wfun(kval<DT>(static_cast<unsigned int>(cv[k])), Mp, nc, minf));
+      }
     }
     __syncthreads();
     unsigned long long bef;
@@ -1527,7 +1524,7 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
           const unsigned int i = static_cast<unsigned int>(e >> 32);
           const int st = static_cast<int>(i) / a.L;
           if (k > tau || (k == tau && i <= cut)) {
-            atomicAdd(&sh.kept[st], q40(wfun(kval<DT>(k), Mp, nc, minf)));
+            atomicAdd(&sh.kept[st], sh.cmq[c]);
             if (k == tau) atomicAdd(&sh.tcnt[st], 1u);
           }
         }
