@@ -1,6 +1,6 @@
 // device_common.hpp -- device helpers of the gfx950 sampler: monotone float
-// keys, dtype rounding, raw vector loads, the weight function, device-coherent
-// accesses, wave/block scans and the best-64 list sort / merge.
+// keys, dtype rounding, raw vector loads, the weight function, lane exchanges,
+// DPP wave / block scans and the best-64 list sort / merge.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -18,7 +18,6 @@ constexpr int WAVES = THREADS / 64;
 constexpr int VEC = 8;                  // elements per 16-byte (bf16/f16) or 32-byte (f32) load
 constexpr int CHUNK = THREADS * VEC;    // elements one load instruction covers across the block
 constexpr int MAX_S = 64;               // slices per row (<= 64: one wave combines them)
-constexpr int NBIN = 2048;              // digit / histogram width (11 bits)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr unsigned int KEY_NEG_INF = 0x007fffffu;  // key of -inf; smaller keys are NaNs
 constexpr unsigned int KEY_POS_INF = 0xff800000u;
@@ -177,36 +176,8 @@ __device__ __forceinline__ double wexp_d(float x, float m) {
   return x == m ? 1.0 : exp(static_cast<double>(x) - static_cast<double>(m));
 }
 
-// floor(w * 2^42) for w in [0, 1]: fixed-point mass, exact and order-free to sum.
-__device__ __forceinline__ unsigned long long quant(float w) {
-  const float t = w * 1024.0f;
-  const float h = floorf(t);
-  const float fr = t - h;
-  const unsigned int lo = static_cast<unsigned int>(fr * 4294967296.0f);
-  const unsigned int hi = static_cast<unsigned int>(h);
-  return (static_cast<unsigned long long>(hi) << 32) | lo;
-}
-constexpr double QUNIT = 1.0 / 4398046511104.0;  // 2^-42
-
-// Device-coherent 64-bit accesses (relaxed, agent scope).  Data one workgroup
-// hands to another goes through these: they compile to sc1 loads / stores that
-// are coherent across the XCDs' L2 caches without an L2-wide write-back or
-// invalidate, which a release/acquire fence would cost per workgroup.
-__device__ __forceinline__ void st_dev(void* p, unsigned long long v) {
-  __hip_atomic_store(static_cast<unsigned long long*>(p), v, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long ld_dev(const void* p) {
-  return __hip_atomic_load(static_cast<unsigned long long*>(const_cast<void*>(p)), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ unsigned long long pack2(unsigned int lo, unsigned int hi) {
   return (static_cast<unsigned long long>(hi) << 32) | lo;
-}
-__device__ __forceinline__ void st_dev(uint2* p, uint2 v) { st_dev(static_cast<void*>(p), pack2(v.x, v.y)); }
-__device__ __forceinline__ uint2 ld_dev2(const uint2* p) {
-  const unsigned long long w = ld_dev(static_cast<const void*>(p));
-  return make_uint2(static_cast<unsigned int>(w), static_cast<unsigned int>(w >> 32));
 }
 
 // (av, ai) before (bv, bi) in (value desc, index asc) order.  Bitwise, not
@@ -316,49 +287,6 @@ __device__ __forceinline__ T wave_min(T x) {
   return x;
 }
 
-template <typename T>
-__device__ __forceinline__ T wave_incl_scan(T x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const T y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
-
-// Scan over the block (WAVES waves): *excl / *incl are this thread's exclusive
-// and inclusive prefix, *total the block sum.  incl is defined as the next
-// thread's excl, so for floating T the ranges [excl, incl) of consecutive
-// threads meet bit for bit.  lds: WAVES entries.  Contains barriers: call from
-// uniform control flow.
-template <typename T>
-__device__ __forceinline__ void block_scan(T x, T* lds, T* excl, T* incl, T* total) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const T inc = wave_incl_scan(x);
-  __syncthreads();  // lds may still be read by a previous call
-  if (lane == 63) lds[wid] = inc;
-  __syncthreads();
-  const T wt = lane < WAVES ? lds[lane] : T(0);
-  const T wsc = wave_incl_scan(wt);  // every wave derives the same wave offsets
-  const T off = wid == 0 ? T(0) : __shfl(wsc, wid - 1, 64);
-  const T off_next = __shfl(wsc, wid, 64);
-  T exw = __shfl_up(inc, 1, 64);
-  if (lane == 0) exw = T(0);
-  const T ex = exw + off;
-  const T nx = __shfl_down(ex, 1, 64);
-  *excl = ex;
-  *incl = lane == 63 ? off_next : nx;
-  *total = __shfl(wsc, WAVES - 1, 64);
-}
-
-template <typename T>
-__device__ __forceinline__ T block_excl_scan(T x, T* lds, T* total) {
-  T ex, in;
-  block_scan<T>(x, lds, &ex, &in, total);
-  return ex;
-}
-
 // Inclusive scan of an int over the wave on the VALU: shifts within each row
 // of 16 lanes, then the rows' last lanes broadcast forward (row_bcast:15 into
 // rows 1 and 3, row_bcast:31 into rows 2 and 3).  Whole wave active.
@@ -428,25 +356,6 @@ __device__ __forceinline__ T block_excl_scan_dpp(T x, T* lds, T* total) {
   for (int w = 0; w < WAVES; ++w) {
     const T t = lds[w];
     off += w < wid ? t : T(0);
-    tot += t;
-  }
-  *total = tot;
-  return inc - x + off;
-}
-
-// Exclusive block scan of an int for an lds array that no thread of the block
-// has read since the last barrier: one barrier, no LDS round trips inside the
-// waves.  lds: WAVES entries.
-__device__ __forceinline__ int block_excl_scan_fresh(int x, int* lds, int* total) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int inc = wave_incl_scan_dpp(x);
-  if (lane == 63) lds[wid] = inc;
-  __syncthreads();
-  int off = 0, tot = 0;
-#pragma unroll
-  for (int w = 0; w < WAVES; ++w) {
-    const int t = lds[w];
-    off += w < wid ? t : 0;
     tot += t;
   }
   *total = tot;

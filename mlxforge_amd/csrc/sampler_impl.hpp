@@ -310,15 +310,6 @@ __device__ __forceinline__ unsigned long long pack_ent(float v, int i) {
   return pack2(__float_as_uint(v), static_cast<unsigned int>(i));
 }
 
-__device__ __forceinline__ unsigned long long LDP(const unsigned long long* p) { return *p; }
-
-__device__ __forceinline__ unsigned int ld_dev32(const unsigned int* p) {
-  return __hip_atomic_load(const_cast<unsigned int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev32(unsigned int* p, unsigned int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // min_p (src/sample/sampler.cpp:87-93, after top-p): an element is kept when
 // its weight exp(z' - max z') reaches mr; weights are non-decreasing in z', so
 // that is every z' key from the smallest one whose weight reaches mr.  Whole
@@ -547,7 +538,7 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && v[e] >= thf) ? 1 : 0;
     }
-    int pos = block_excl_scan_fresh(mine, sh.rsc, &nsurv);
+    int pos = block_excl_scan_dpp<int>(mine, sh.rsc, &nsurv);
     if (nsurv <= SURV) {
       if (mine) {
 #pragma unroll
@@ -583,7 +574,7 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
       mine = 0;
 #pragma unroll
       for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && !better(tv, ti, v[e], MLXF_IDX(e))) ? 1 : 0;
-      pos = block_excl_scan_fresh(mine, sh.rsc, &nsurv);
+      pos = block_excl_scan_dpp<int>(mine, sh.rsc, &nsurv);
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
         const int i = MLXF_IDX(e);
@@ -1514,7 +1505,7 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
       } else {
         // per-slice kept mass: above the bin, plus the kept candidates
         for (int t2 = tid; t2 < S; t2 += THREADS) {
-          sh.kept[t2] = LDP(a.above + static_cast<size_t>(r) * S + t2);
+          sh.kept[t2] = a.above[static_cast<size_t>(r) * S + t2];
           sh.tcnt[t2] = 0u;
         }
         __syncthreads();
