@@ -10,8 +10,10 @@
 //   * apply_top_k / apply_top_p are not separate entry points: their kept sets
 //     are observed through the draw (a uniform sweep only ever returns kept
 //     ids, and reaches every one of them).
-// The reference's penalty and min_p cases (sampler_test.cpp:76-124) are not on
-// the GPU path; the wrapper must refuse them, which is checked instead.
+// The reference's min_p and penalty cases (sampler_test.cpp:76-124) run through
+// the wrapper's min_p parameter and apply_penalties; penalties left in the
+// parameters of a sampling call must be refused.  The C ABI's seeded uniforms
+// and grammar mask are checked on their own known answers.
 //
 // Prints one line per case and exits non-zero on the first failure set.
 #include <hip/hip_runtime.h>
@@ -268,6 +270,63 @@ void case_penalty_moves_greedy(Sampler& s) {  // :117-124
   KAT_CHECK((r.tokens == std::vector<int32_t>{1}));
 }
 
+void case_seeded_uniforms(Sampler&) {  // :126-134 with a seed instead of a key
+  // u = Philox4x32-10(key = seed, counter = (step, 0)) word 0 >> 8, * 2^-24:
+  // the published vector for key 0, counter 0 starts 0x6627e8d5
+  std::vector<uint64_t> seed = {0, 0, 42};
+  std::vector<uint64_t> step = {0, 1, 0};
+  uint64_t *ds = nullptr, *dt = nullptr;
+  float* du = nullptr;
+  (void)hipMalloc(reinterpret_cast<void**>(&ds), 3 * sizeof(uint64_t));
+  (void)hipMalloc(reinterpret_cast<void**>(&dt), 3 * sizeof(uint64_t));
+  (void)hipMalloc(reinterpret_cast<void**>(&du), 3 * sizeof(float));
+  (void)hipMemcpy(ds, seed.data(), 3 * sizeof(uint64_t), hipMemcpyHostToDevice);
+  (void)hipMemcpy(dt, step.data(), 3 * sizeof(uint64_t), hipMemcpyHostToDevice);
+  char* err = nullptr;
+  KAT_CHECK(mlxf_uniforms(3, ds, dt, 0, du, nullptr, &err) == MLXF_OK);
+  std::vector<float> u(3), u2(3);
+  (void)hipMemcpy(u.data(), du, 3 * sizeof(float), hipMemcpyDeviceToHost);
+  KAT_CHECK(u[0] == static_cast<float>(0x6627e8d5u >> 8) * 0x1p-24f);
+  KAT_CHECK(u[1] != u[0] && u[2] != u[0]);  // another step, another seed
+  KAT_CHECK(mlxf_uniforms(3, ds, dt, 0, du, nullptr, &err) == MLXF_OK);
+  (void)hipMemcpy(u2.data(), du, 3 * sizeof(float), hipMemcpyDeviceToHost);
+  KAT_CHECK(u == u2);  // same seed and step: same uniform
+  (void)hipFree(ds);
+  (void)hipFree(dt);
+  (void)hipFree(du);
+}
+
+void case_grammar_mask(Sampler& s) {  // src/runtime/worker.cpp:142-179,455-459
+  // only tokens 1 and 3 allowed: greedy picks the best allowed one, and no
+  // draw ever returns a forbidden token
+  Logits lg({{5.0f, 1.0f, 4.0f, 2.0f, 3.0f}});
+  uint32_t bits = (1u << 1) | (1u << 3);
+  uint32_t* db = nullptr;
+  float* dout = nullptr;
+  (void)hipMalloc(reinterpret_cast<void**>(&db), sizeof(uint32_t));
+  (void)hipMalloc(reinterpret_cast<void**>(&dout), 5 * sizeof(float));
+  (void)hipMemcpy(db, &bits, sizeof(uint32_t), hipMemcpyHostToDevice);
+  char* err = nullptr;
+  KAT_CHECK(mlxf_apply_mask(lg.d, MLXF_DTYPE_F32, 1, 5, 5, db, 1, dout, 5, nullptr, &err) == MLXF_OK);
+  std::vector<float> m(5);
+  (void)hipMemcpy(m.data(), dout, 5 * sizeof(float), hipMemcpyDeviceToHost);
+  KAT_CHECK(m[1] == 1.0f && m[3] == 2.0f);
+  KAT_CHECK(std::isinf(m[0]) && m[0] < 0 && std::isinf(m[2]) && std::isinf(m[4]));
+  DeviceLogits v{dout, MLXF_DTYPE_F32, 1, 5, 0};
+  KAT_CHECK((s.greedy(v) == std::vector<int32_t>{3}));
+  SamplingParams p;
+  std::set<int> seen;
+  for (int i = 0; i < 32; ++i) seen.insert(s.sample_rows(v, {p}, {(i + 0.5f) / 32.0f}).tokens[0]);
+  KAT_CHECK((seen == std::set<int>{1, 3}));
+  // nothing allowed: the row is left as it is (the reference adds zeros)
+  bits = 0u;
+  (void)hipMemcpy(db, &bits, sizeof(uint32_t), hipMemcpyHostToDevice);
+  KAT_CHECK(mlxf_apply_mask(lg.d, MLXF_DTYPE_F32, 1, 5, 5, db, 1, dout, 5, nullptr, &err) == MLXF_OK);
+  KAT_CHECK((s.greedy(v) == std::vector<int32_t>{0}));
+  (void)hipFree(db);
+  (void)hipFree(dout);
+}
+
 void case_row_stride(Sampler& s) {  // the (bucket, 1, V) view with B rows sampled
   // Rows of 5 logits inside rows of 8; the padding holds a value that would win.
   Logits lg({{0.0f, 1.0f, 3.0f, 2.0f, 0.5f, 99.0f, 99.0f, 99.0f},
@@ -319,6 +378,8 @@ int main() {
       {"repetition penalty pushes a seen token below an unseen one", case_repetition_penalty},
       {"frequency penalty scales with count, presence is flat", case_frequency_presence},
       {"repetition penalty changes greedy choice", case_penalty_moves_greedy},
+      {"same seed and step give the same uniform (device Philox)", case_seeded_uniforms},
+      {"the grammar mask only lets allowed tokens through", case_grammar_mask},
       {"row_stride samples B rows of a padded buffer", case_row_stride},
       {"errors carry a code and a message", case_error_reporting},
   };
