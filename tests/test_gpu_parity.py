@@ -315,3 +315,53 @@ def test_min_p_parity(dtype, kind):
         for st in (0, 1):
             g = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=2, min_p=mp, stages=st)
             assert np.array_equal(g["ids"], ref["ids"]), (kind, st, g["ids"], ref["ids"])
+
+
+def _mixed_rows(rng, B, V, dtype):
+    """Rows of every kind at once: flat, peaked, heavy ties, -inf runs."""
+    z = np.empty((B, V), np.float32)
+    for r in range(B):
+        kind = r % 4
+        if kind == 0:    # flat: few distinct 16-bit values, many ties
+            z[r] = np.round(rng.standard_normal(V) * 0.1, 2)
+        elif kind == 1:  # peaked
+            z[r] = rng.standard_normal(V) * 3
+            z[r, rng.integers(0, V, 5)] += 12
+        elif kind == 2:  # ties at the top
+            z[r] = rng.standard_normal(V)
+            z[r, rng.integers(0, V, 200)] = z[r].max() + 1
+        else:            # masked-out runs
+            z[r] = rng.standard_normal(V) * 2
+            z[r, : V // 3] = -np.inf
+    if dtype == "f32":
+        host = z
+    elif dtype == "bf16":
+        host = workloads.to_bf16_bits(np.nan_to_num(z, neginf=-3e38))
+        host[np.isneginf(z)] = 0xFF80
+    else:
+        host = z.astype(np.float16)
+    T = rng.choice(np.array([0.0, 0.5, 1.0, 1.7], np.float32), B)
+    k = rng.choice(np.array([0, 0, 1, 10, 63, 64, 500, 5000], np.int32), B)
+    p = rng.choice(np.array([1.0, 1.0, 0.3, 0.9, 0.999], np.float32), B)
+    mp = rng.choice(np.array([0.0, 0.0, 0.01, 0.2, 0.9], np.float32), B)
+    tlp = rng.integers(-1, 4, B).astype(np.int32)
+    u = rng.random(B).astype(np.float32)
+    return host, T, k, p, mp, tlp, u
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_mixed_rows_every_path(seed):
+    """Every row kind and parameter combination in one call, all three dtypes,
+    at the generic and the hinted stage count."""
+    rng = np.random.default_rng(7000 + seed)
+    dtype = ("f32", "bf16", "f16")[seed % 3]
+    V = int(rng.integers(1000, 70000))
+    B = 16
+    host, T, k, p, mp, tlp, u = _mixed_rows(rng, B, V, dtype)
+    say(f"[parity] mixed rows seed={seed} dtype={dtype} V={V}")
+    dev = gu.to_device(host, dtype)
+    o = gu.oracle_sample(host, dtype, T=T, k=k, p=p, tlp=tlp, u=u, K_max=3, min_p=mp)
+    g = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=3, min_p=mp)
+    gu.compare(g, o, dtype, tlp=tlp, label=f"mixed seed={seed}")
+    gh = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=3, min_p=mp, stages=1)
+    assert np.array_equal(gh["ids"], g["ids"])
