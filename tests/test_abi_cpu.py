@@ -121,3 +121,49 @@ def test_refine_stage_hint_from_host_parameters():
     assert rs(np.ones(4, np.float32), np.full(4, 20, np.int32), np.full(4, 0.9, np.float32)) == 0
     # bf16: a temperature that rounds to 0 is greedy
     assert rs(np.full(4, 1e-45, np.float32), dt=_lib.DTYPE_BF16) == 0
+
+
+def test_pre_sampling_entry_points_argument_errors_need_no_gpu():
+    L = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    n = ctypes.c_size_t()
+    # penalties: workspace size is B * V counters, 256-byte aligned
+    assert L.mlxf_penalties_workspace_size(3, 1000, ctypes.byref(n), None) == 0
+    assert n.value >= 3 * 1000 * 4 and n.value % 256 == 0
+    assert L.mlxf_penalties_workspace_size(-1, 1000, ctypes.byref(n), None) == _lib.EINVAL
+    # penalties: bad dtype / shape, missing history, small workspace; nothing to do is a success
+    err = ctypes.c_void_p()
+    assert L.mlxf_apply_penalties(fake, 9, 1, 10, 10, fake, 4, None, fake, None, None, fake, 1 << 20,
+                                  None, ctypes.byref(err)) == _lib.EINVAL
+    L.mlxf_string_free(err)
+    err = ctypes.c_void_p()
+    assert L.mlxf_apply_penalties(fake, 0, 1, 10, 9, fake, 4, None, fake, None, None, fake, 1 << 20,
+                                  None, ctypes.byref(err)) == _lib.EINVAL
+    L.mlxf_string_free(err)
+    err = ctypes.c_void_p()
+    assert L.mlxf_apply_penalties(fake, 0, 1, 10, 10, None, 4, None, fake, None, None, fake, 1 << 20,
+                                  None, ctypes.byref(err)) == _lib.EINVAL
+    L.mlxf_string_free(err)
+    err = ctypes.c_void_p()
+    assert L.mlxf_apply_penalties(fake, 0, 2, 10, 10, fake, 4, None, fake, None, None, fake, 16,
+                                  None, ctypes.byref(err)) == _lib.EWORKSPACE
+    L.mlxf_string_free(err)
+    assert L.mlxf_apply_penalties(fake, 0, 2, 10, 10, fake, 4, None, None, None, None, None, 0,
+                                  None, None) == 0  # no penalty array: nothing to do
+    assert L.mlxf_apply_penalties(fake, 0, 2, 10, 10, fake, 0, None, fake, None, None, None, 0,
+                                  None, None) == 0  # empty history
+    # uniforms
+    err = ctypes.c_void_p()
+    assert L.mlxf_uniforms(-1, fake, None, 0, fake, None, ctypes.byref(err)) == _lib.EINVAL
+    L.mlxf_string_free(err)
+    err = ctypes.c_void_p()
+    assert L.mlxf_uniforms(4, None, None, 0, fake, None, ctypes.byref(err)) == _lib.EINVAL
+    L.mlxf_string_free(err)
+    assert L.mlxf_uniforms(0, None, None, 0, None, None, None) == 0
+    # mask: bad dtype, bits_stride too small, missing output
+    for args in ((fake, 7, 1, 100, 100, fake, 4, fake, 100), (fake, 0, 1, 100, 100, fake, 3, fake, 100),
+                 (fake, 0, 1, 100, 100, fake, 4, None, 100), (fake, 0, 1, 100, 100, fake, 4, fake, 99)):
+        err = ctypes.c_void_p()
+        assert L.mlxf_apply_mask(*args, None, ctypes.byref(err)) == _lib.EINVAL and err.value
+        L.mlxf_string_free(err)
+    assert L.mlxf_apply_mask(None, 0, 0, 100, 100, None, 4, None, 100, None, None) == 0
