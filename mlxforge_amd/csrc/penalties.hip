@@ -159,9 +159,9 @@ int mlxf_apply_penalties(void* d_logits, int dtype, int B, int V, int64_t row_st
     set_err(err, "mlxf: dtype must be MLXF_DTYPE_F32, MLXF_DTYPE_BF16 or MLXF_DTYPE_F16");
     return MLXF_EINVAL;
   }
-  if (B < 0 || V < 1 || V > MLXF_MAX_VOCAB || row_stride < V || hist_stride < 0 ||
+  if (B < 0 || B > 65535 || V < 1 || V > MLXF_MAX_VOCAB || row_stride < V || hist_stride < 0 ||
       hist_stride > (int64_t{1} << 30)) {
-    set_err(err, "mlxf: bad shape (B >= 0, V in [1, MLXF_MAX_VOCAB], row_stride >= V, "
+    set_err(err, "mlxf: bad shape (B in [0, 65535], V in [1, MLXF_MAX_VOCAB], row_stride >= V, "
                  "0 <= hist_stride <= 2^30)");
     return MLXF_EINVAL;
   }
