@@ -132,9 +132,9 @@ __device__ __forceinline__ void load_raw(const void* row, int i0, int end, Raw8<
   }
 }
 
-// Raw -> fp32 values; NaN reads as -inf.
+// Raw -> fp32 values, NaN kept.
 template <int DT>
-__device__ __forceinline__ void decode8(const Raw8<DT>& r, float* v) {
+__device__ __forceinline__ void decode8_nan(const Raw8<DT>& r, float* v) {
   if constexpr (DT == MLXF_DTYPE_F32) {
     const unsigned int w[8] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[0].w,
                                r.q[1].x, r.q[1].y, r.q[1].z, r.q[1].w};
@@ -156,8 +156,52 @@ __device__ __forceinline__ void decode8(const Raw8<DT>& r, float* v) {
       }
     }
   }
+}
+
+// Raw -> fp32 values; NaN reads as -inf.
+template <int DT>
+__device__ __forceinline__ void decode8(const Raw8<DT>& r, float* v) {
+  decode8_nan<DT>(r, v);
 #pragma unroll
   for (int j = 0; j < VEC; ++j) v[j] = v[j] != v[j] ? -INFINITY : v[j];
+}
+
+// Three-operand maximum / minimum / minimum of magnitudes.  The inputs must not
+// be NaN (callers clear NaNs first): then the instruction is the exact
+// maximum or minimum, and asm keeps the compiler from adding the quieting
+// instructions it puts before a max of values it cannot prove NaN-free.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ float vmin3(float a, float b, float c) {
+  float d;
+  asm("v_min3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ float vmin3_abs(float a, float b, float c) {  // min(a, |b|, |c|)
+  float d;
+  asm("v_min3_f32 %0, %1, |%2|, |%3|" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
+// n values, NaN read as -inf.  A NaN is found from two maxima of the bit
+// patterns (unsigned: a negative NaN lies above -inf; signed: a positive NaN
+// above +inf), and only a wave holding one rewrites its values.
+template <int N>
+__device__ __forceinline__ void clear_nans(float (&v)[N]) {
+  unsigned int hu = 0u;
+  int hs = INT_MIN;
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    hu = max(hu, __float_as_uint(v[e]));
+    hs = max(hs, static_cast<int>(__float_as_uint(v[e])));
+  }
+  if (__builtin_amdgcn_ballot_w64(hu > 0xff800000u || hs > 0x7f800000)) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) v[e] = v[e] != v[e] ? -INFINITY : v[e];
+  }
 }
 
 template <int DT, bool VECOK>
@@ -165,6 +209,12 @@ __device__ __forceinline__ void load8(const void* row, int i0, int end, float* v
   Raw8<DT> r;
   load_raw<DT, VECOK>(row, i0, end, r);
   decode8<DT>(r, v);
+}
+template <int DT, bool VECOK>
+__device__ __forceinline__ void load8_nan(const void* row, int i0, int end, float* v) {
+  Raw8<DT> r;
+  load_raw<DT, VECOK>(row, i0, end, r);
+  decode8_nan<DT>(r, v);
 }
 
 // exp(x - m) with exp(m - m) = 1 also for infinite m.

@@ -412,7 +412,7 @@ struct S1Lds {
   float rf[WAVES];
   float rmin[WAVES];
   int ri[WAVES];
-  unsigned int ramin[WAVES];
+  float ramin[WAVES];
   double rd[WAVES];
   unsigned int rth[WAVES];
   int rsc[WAVES + 1];
@@ -441,27 +441,30 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
 
   float v[EPT];
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
+  for (int it = 0; it < NIT; ++it) load8_nan<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
+  clear_nans(v);
 #define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
 
+  static_assert(EPT % 2 == 0, "pairs of elements");
   float tmax = v[0];
 #pragma unroll
-  for (int e = 1; e < EPT; ++e) tmax = fmaxf(tmax, v[e]);
+  for (int e = 1; e < EPT - 1; e += 2) tmax = vmax3(tmax, v[e], v[e + 1]);
+  tmax = vmax3(tmax, v[EPT - 1], v[EPT - 1]);
   {
     const float wm = wave_max(tmax);
     if (lane == 0) sh.rf[wid] = wm;
   }
   if (refine) {
-    // smallest nonzero |z| (as bits - 1, so zeros wrap past every value; the
-    // -inf read past the row end is never the smallest) and the slice minimum
-    // (with the maximum: the largest finite |z| when neither is infinite)
-    unsigned int amin = 0xffffffffu;
-    float tmin = INFINITY;
+    // smallest |z| (the -inf read past the row end is never the smallest) and
+    // the slice minimum (with the maximum: the largest finite |z| when neither
+    // is infinite)
+    float amin = INFINITY;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) amin = min(amin, (__float_as_uint(v[e]) & 0x7fffffffu) - 1u);
+    for (int e = 0; e < EPT; e += 2) amin = vmin3_abs(amin, v[e], v[e + 1]);
+    float tmin = INFINITY;
     if (end - beg == a.L) {
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) tmin = fminf(tmin, v[e]);
+      for (int e = 0; e < EPT; e += 2) tmin = vmin3(tmin, v[e], v[e + 1]);
     } else {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) tmin = fminf(tmin, MLXF_IDX(e) < end ? v[e] : INFINITY);
@@ -599,18 +602,18 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
   float zmin = 0.0f;
   unsigned int sfl = 0u;
   if (refine) {
-    unsigned int amin = sh.ramin[0];
+    float amin = sh.ramin[0];
     zmin = sh.rmin[0];
 #pragma unroll
     for (int w2 = 1; w2 < WAVES; ++w2) {
-      amin = min(amin, sh.ramin[w2]);
+      amin = fminf(amin, sh.ramin[w2]);
       zmin = fminf(zmin, sh.rmin[w2]);
     }
     // the FMA-corrected division is exact when every nonzero |z| >= 2^-96 and
-    // every finite |z| < 2^100: here, when the slice's maximum and minimum are
-    // both below 2^100 in magnitude (a slice holding an infinity divides
-    // exactly)
-    sfl = (amin >= 0x0f7fffffu && fabsf(zmax) < 0x1p100f && fabsf(zmin) < 0x1p100f)
+    // every finite |z| < 2^100: here, when every |z| >= 2^-96 and the slice's
+    // maximum and minimum are both below 2^100 in magnitude (a slice holding a
+    // zero or an infinity divides exactly)
+    sfl = (amin >= 0x1p-96f && fabsf(zmax) < 0x1p100f && fabsf(zmin) < 0x1p100f)
               ? static_cast<unsigned int>(SL_FAST)
               : 0u;
   }
