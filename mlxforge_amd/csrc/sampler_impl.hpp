@@ -654,7 +654,8 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
 struct D1Lds {
   unsigned long long lst[MAX_S * LIST];  // (the per-slice lists; dead once merged)
   unsigned long long sv[MAX_S * LIST];   // list entries at or above theta
-  int nsv;
+  int ncnt[MAX_S];                       // ... per slice
+  unsigned int thk[WAVES];
   TopEnt lists[WAVES * LIST];
   TopEnt mlist[LIST];
   float szmax[MAX_S];
@@ -1641,38 +1642,67 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
       const int i = tid + k * THREADS;
       if (i < S * LIST) sh.lst[i] = lw[k];
     }
-    if (tid == 0) sh.nsv = 0;
   }
   __syncthreads();
   if (md.need_list) {
-    // theta: the best of the slices' 64th entries.  Each slice holds 64 entries
-    // at or above its own 64th, so the row's 64th best is at least theta, and an
-    // entry of the row's best 64 is in its slice's list: the entries at or above
-    // theta hold the row's best 64.
-    float th = -INFINITY;
+    // theta, a value the row's 64th best reaches: slice t's j-th entry e_t has
+    // j entries of the slice at or above it, so a value c that 64 / j of the
+    // e_t reach is reached by 64 entries of the row.  Wave w takes j = 64 >> w
+    // (64, 32, 16, 8) and finds the (64 / j)-th largest e_t by a bisection over
+    // keys, rounded down to their top 16 bits (ballot and popcount); theta is
+    // the largest of the four.  An entry of the row's best 64 is in its slice's
+    // list, so the entries at or above theta hold the row's best 64.  (With
+    // slices alike, the 8th entries give a theta near the row's 64th best; the
+    // 64th entries alone would let most of every list through.)
+    {
+      const int j = LIST >> wid;
+      const unsigned int kt =
+          lane < S ? f2key(__uint_as_float(static_cast<unsigned int>(sh.lst[lane * LIST + j - 1]))) : 0u;
+      unsigned int c = 0u;
 #pragma unroll
-    for (int w2 = 0; w2 < MAX_S / LIST + 1; ++w2) {
-      const int t = w2 * LIST + lane;
-      if (t < S) th = fmaxf(th, __uint_as_float(static_cast<unsigned int>(sh.lst[t * LIST + LIST - 1])));
+      for (int b = 31; b >= 16; --b) {
+        const unsigned int t = c | (1u << b);
+        if (__builtin_popcountll(__builtin_amdgcn_ballot_w64(kt >= t)) >= (1 << wid)) c = t;
+      }
+      if (lane == 0) sh.thk[wid] = c;
     }
-    th = wave_max(th);
+    __syncthreads();
+    unsigned int ck = sh.thk[0];
+#pragma unroll
+    for (int w2 = 1; w2 < WAVES; ++w2) ck = max(ck, sh.thk[w2]);
+    const float th = ck <= KEY_NEG_INF ? -INFINITY : key2f(ck);
+    int nsv = 0;
     if (th > -INFINITY) {
-      for (int t = wid; t < S; t += WAVES) {
-        const unsigned long long w = sh.lst[t * LIST + lane];
-        const bool in = __uint_as_float(static_cast<unsigned int>(w)) >= th;
-        const unsigned long long bal = __ballot(in);
-        if (bal) {
-          int base = 0;
-          if (lane == 0) base = atomicAdd(&sh.nsv, __popcll(bal));
-          base = __builtin_amdgcn_readfirstlane(base);
-          const int at = base + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(bal >> 32),
-                                                          __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(bal), 0u));
-          if (in && at < MAX_S * LIST) sh.sv[at] = w;
+      // the entries at or above theta are a prefix of each (sorted) list: its
+      // length by a ballot, the prefixes' places by a scan over the slices
+      constexpr int SPW = MAX_S / WAVES;  // slices per wave
+      unsigned long long w[SPW];
+      int cnt[SPW];
+#pragma unroll
+      for (int q = 0; q < SPW; ++q) {
+        const int t = wid + q * WAVES;
+        w[q] = 0ull;
+        cnt[q] = 0;
+        if (t < S) {
+          w[q] = sh.lst[t * LIST + lane];
+          cnt[q] = __builtin_popcountll(
+              __builtin_amdgcn_ballot_w64(__uint_as_float(static_cast<unsigned int>(w[q])) >= th));
+          if (lane == 0) sh.ncnt[t] = cnt[q];
+        }
+      }
+      __syncthreads();
+      const int incl = wave_incl_scan_dpp(lane < S ? sh.ncnt[lane] : 0);
+      nsv = __builtin_amdgcn_readlane(incl, S - 1);
+#pragma unroll
+      for (int q = 0; q < SPW; ++q) {
+        const int t = wid + q * WAVES;
+        if (t < S) {
+          const int off = __builtin_amdgcn_readlane(incl, t) - cnt[q];
+          if (lane < cnt[q]) sh.sv[off + lane] = w[q];
         }
       }
     }
     __syncthreads();
-    const int nsv = sh.nsv;
     float lv = -INFINITY;
     int li = INT_MAX;
     if (th > -INFINITY && nsv <= THREADS) {

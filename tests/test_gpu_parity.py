@@ -187,6 +187,42 @@ def test_degenerate_rows():
     assert g["ids"][4] == 1234
 
 
+# quiet and signalling NaNs of both signs, as bit patterns of each dtype
+NAN_BITS = {"f32": [0x7fc00000, 0xffc00000, 0x7f800001, 0xff800001],
+            "bf16": [0x7fc0, 0xffc0, 0x7f81, 0xff81],
+            "f16": [0x7e00, 0xfe00, 0x7c01, 0xfc01]}
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_nan_patterns_every_path(dtype):
+    """Every NaN bit pattern reads as -inf on every row kind: scattered NaNs,
+    a NaN where the row maximum was, and a whole slice of NaNs."""
+    rng = np.random.default_rng(31)
+    B, V = 8, 20000
+    z = rng.standard_normal((B, V)).astype(np.float32) * np.float32(2.0)
+    if dtype == "f32":
+        bits = z.view(np.uint32).copy()
+    elif dtype == "bf16":
+        bits = workloads.to_bf16_bits(z)
+    else:
+        bits = z.astype(np.float16).view(np.uint16).copy()
+    nb = np.array(NAN_BITS[dtype], dtype=bits.dtype)
+    for r in range(B):
+        pos = rng.choice(V, 40, replace=False)
+        bits[r, pos] = nb[np.arange(40) % 4]
+    bits[0, int(np.argmax(z[0]))] = nb[1]
+    bits[7, 8192:16384] = nb[2]
+    host = bits.view(np.float32) if dtype == "f32" else (bits.view(np.float16) if dtype == "f16" else bits)
+    T = np.array([0.0, 1.0, 0.7, 1.0, 0.9, 1.0, 1.2, 1.0], np.float32)
+    k = np.array([0, 5, 0, 200, 0, 40, 0, 0], np.int32)
+    p = np.array([1.0, 1.0, 0.9, 0.95, 1.0, 0.8, 1.0, 0.9], np.float32)
+    tlp = np.array([2, 0, 3, -1, 1, 5, 0, 2], np.int32)
+    u = rng.random(B).astype(np.float32)
+    g = gu.gpu_sample(gu.to_device(host, dtype), T=T, k=k, p=p, tlp=tlp, u=u, K_max=5)
+    o = gu.oracle_sample(host, dtype, T=T, k=k, p=p, tlp=tlp, u=u, K_max=5)
+    gu.compare(g, o, dtype, tlp=tlp, label=f"NaN patterns {dtype}")
+
+
 def test_parameter_sanitisation():
     rng = np.random.default_rng(9)
     V = 4000
