@@ -145,7 +145,9 @@ int mlxf_sample_ex(const void* d_logits, int dtype, int B, int V, int64_t row_st
  * top_k and top_p (NULL = the sentinel: greedy / off / off), with the same
  * sanitisation as mlxf_sample (src/sample/sampler.h:16-29,
  * src/capi/mlxforge.cpp:43-70): 0 when every row is greedy or has a top-k of
- * at most 63, 1 when every other row is temperature-only, else 3. */
+ * at most 63, 1 when every other row is temperature-only, else 2 (a row still
+ * open after the second stage is finished by its deciding kernel, which
+ * measured faster than a third stage). */
 int mlxf_sampler_refine_stages(int B, int V, int dtype, const float* h_temperature,
                                const int32_t* h_top_k, const float* h_top_p);
 

@@ -109,7 +109,7 @@ def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
     host sequences, which are copied); None disables the knob (temperature
     None = all greedy; min_p None = off).  refine_stages: refine stages to launch (0..3); by
     default derived from the parameters when they are all known on the host
-    (mlxf_sampler_refine_stages), else 3.
+    (mlxf_sampler_refine_stages: 0, 1 or 2), else 3 (mlxf_sample's count).
     """
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be a [B, V] view with unit stride along V")

@@ -105,7 +105,7 @@ def test_sample_ex_argument_errors_need_no_gpu():
 
 def test_refine_stage_hint_from_host_parameters():
     """Host-side stage count: greedy and top-k <= 63 rows need none, temperature-
-    only rows one (the kept-mass pass), anything else all three."""
+    only rows one (the kept-mass pass), anything else two."""
     import numpy as np
     rs = lambda T, k=None, p=None, B=4, V=1000, dt=_lib.DTYPE_F32: _lib.refine_stages(B, V, dt, T, k, p)
     z = np.zeros(4, np.float32)
@@ -113,11 +113,11 @@ def test_refine_stage_hint_from_host_parameters():
     assert rs(z) == 0                                            # all greedy
     assert rs(np.full(4, np.nan, np.float32)) == 0               # non-finite T is greedy
     assert rs(np.ones(4, np.float32), np.full(4, 63, np.int32)) == 0
-    assert rs(np.ones(4, np.float32), np.full(4, 64, np.int32)) == 3
+    assert rs(np.ones(4, np.float32), np.full(4, 64, np.int32)) == 2
     assert rs(np.ones(4, np.float32), np.full(4, 5000, np.int32), V=50) == 0  # k clamped to V
     assert rs(np.ones(4, np.float32)) == 1                      # temperature only
     assert rs(np.ones(4, np.float32), None, np.full(4, 1.0, np.float32)) == 1  # p >= 1 is off
-    assert rs(np.ones(4, np.float32), None, np.full(4, 0.9, np.float32)) == 3
+    assert rs(np.ones(4, np.float32), None, np.full(4, 0.9, np.float32)) == 2
     assert rs(np.ones(4, np.float32), np.full(4, 20, np.int32), np.full(4, 0.9, np.float32)) == 0
     # bf16: a temperature that rounds to 0 is greedy
     assert rs(np.full(4, 1e-45, np.float32), dt=_lib.DTYPE_BF16) == 0

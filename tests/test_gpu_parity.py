@@ -187,6 +187,46 @@ def test_degenerate_rows():
     assert g["ids"][4] == 1234
 
 
+# (B, V) shapes that select each first-pass slice layout: 32, 16 and 8 logits
+# per thread of a 256-thread slice
+LAYOUT_SHAPES = [(32, 151936), (8, 151936), (1, 128256)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("B,V", LAYOUT_SHAPES)
+def test_degenerate_rows_each_layout(B, V, dtype):
+    """Constant rows (the heavy-tie fallback of the per-slice best-64 list),
+    all -inf, NaN stripes, two +inf, duplicate maxima, each with a list-using
+    parameter set, in every slice layout."""
+    rng = np.random.default_rng(77 + B)
+    z = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    kinds = B if B < 6 else 6
+    for r in range(B):
+        c = r % 6 if kinds == 6 else 3
+        if c == 0:
+            z[r] = -np.inf
+        elif c == 1:
+            z[r, ::5] = np.nan
+        elif c == 2:
+            z[r, 7] = np.inf
+            z[r, V - 3] = np.inf
+        elif c == 3:
+            z[r] = 0.5
+        elif c == 4:
+            z[r, 100] = 30.0
+            z[r, V - 100] = 30.0
+    host = z if dtype == "f32" else workloads.to_bf16_bits(z)
+    T = rng.choice(np.array([0.0, 0.8, 1.0], np.float32), B).astype(np.float32)
+    k = rng.choice(np.array([0, 1, 5, 40], np.int32), B).astype(np.int32)
+    p = rng.choice(np.array([1.0, 0.9], np.float32), B).astype(np.float32)
+    tlp = rng.choice(np.array([0, 3, 5], np.int32), B).astype(np.int32)
+    u = rng.random(B).astype(np.float32)
+    say(f"[parity] degenerate layout B={B} V={V} {dtype}")
+    g = gu.gpu_sample(gu.to_device(host, dtype), T=T, k=k, p=p, tlp=tlp, u=u, K_max=5)
+    o = gu.oracle_sample(host, dtype, T=T, k=k, p=p, tlp=tlp, u=u, K_max=5)
+    gu.compare(g, o, dtype, tlp=tlp, label=f"degenerate layout B={B} V={V} {dtype}")
+
+
 # quiet and signalling NaNs of both signs, as bit patterns of each dtype
 NAN_BITS = {"f32": [0x7fc00000, 0xffc00000, 0x7f800001, 0xff800001],
             "bf16": [0x7fc0, 0xffc0, 0x7f81, 0xff81],
