@@ -739,8 +739,8 @@ __device__ __forceinline__ void enlist(const Args& a, int stage, int r, unsigned
 // of the streaming kernels).
 struct SLds {
   unsigned long long pw[RS_WORDS];   // the row plan as read
-  unsigned int hc[NB];               // slice histogram: counts
-  unsigned long long hm[NB];         // slice histogram: masses
+  unsigned int hc[NB + 64];          // slice histogram: counts (+ one unread slot per lane)
+  unsigned long long hm[NB + 64];    // slice histogram: masses (+ one unread slot per lane)
   unsigned long long ru[WAVES + 1];
   unsigned int rv[WAVES + 1];
   unsigned int ncand;
@@ -762,6 +762,59 @@ struct RLds {
   unsigned int wrk;
   int wbase;
 };
+
+// ---- a slice's histogram in the common case (the FMA-corrected division, a
+// finite row max) as straight-line code, so the elements' exps, conversions and
+// LDS atomics overlap: the flags that are uniform over the slice -- MASS, the
+// value grid VG, and FULL (no bracket or row-end test needed) -- are template
+// parameters, and an element that adds nothing (outside the bracket or the row,
+// or of zero mass in the MASS phase) goes to its lane's own slot past the NB
+// bins, which nothing reads.  Bins and masses are those of the generic path.
+template <int DT, int EPT, bool MASS, bool VG, bool FULL>
+__device__ __forceinline__ void hist_fast(const float (&v)[EPT], const Mode& md, const Plan& pl, float nc, int beg,
+                                          int end, SLds& sh) {
+  const int tid = threadIdx.x, lane = tid & 63;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const float zp = zdiv<DT>(v[e], md.Tr, md.y, true);
+    const float x = wlog2(zp, nc);
+    bool ok = true;
+    if constexpr (!FULL) {
+      const unsigned int zk = f2key(v[e]);
+      const int i = beg + (e / VEC) * CHUNK + tid * VEC + (e % VEC);
+      ok = i < end && zk >= pl.zlo && zk <= pl.zhi;
+    }
+    unsigned long long q = 0;
+    if constexpr (MASS) {
+      q = q40(__builtin_amdgcn_exp2f(x));
+      ok = ok && q != 0ull;
+    }
+    int bin;
+    if constexpr (VG)
+      bin = vbin_x(x, pl.R2);
+    else
+      bin = max(0, NB - 1 - static_cast<int>(min((zkey<DT>(zp) - pl.kb) >> pl.sh, 255u)));
+    bin = ok ? bin : NB + lane;
+    atomicAdd(&sh.hc[bin], 1u);
+    if constexpr (MASS) atomicAdd(&sh.hm[bin], q);
+  }
+}
+
+template <int DT, int EPT, bool MASS>
+__device__ __forceinline__ void hist_fast_any(bool vg, bool full, const float (&v)[EPT], const Mode& md,
+                                              const Plan& pl, float nc, int beg, int end, SLds& sh) {
+  if (vg) {
+    if (full)
+      hist_fast<DT, EPT, MASS, true, true>(v, md, pl, nc, beg, end, sh);
+    else
+      hist_fast<DT, EPT, MASS, true, false>(v, md, pl, nc, beg, end, sh);
+  } else {
+    if (full)
+      hist_fast<DT, EPT, MASS, false, true>(v, md, pl, nc, beg, end, sh);
+    else
+      hist_fast<DT, EPT, MASS, false, false>(v, md, pl, nc, beg, end, sh);
+  }
+}
 
 // ---- one slice of one stage: the histogram, the gathered elements or the kept
 // mass of slice s of row r under the plan in sh.pw.  Results go to the
@@ -809,7 +862,13 @@ __device__ __forceinline__ void slice_stage(const Args& a, int r, int s, const P
     };
     // the first level brackets every key; entries past the row end read as
     // -inf, which weigh nothing (MASS) -- so no per-element test is needed
-    if (zlo <= KEY_NEG_INF && zhi >= KEY_POS_INF && (mass || end - beg == a.L)) {
+    const bool full = zlo <= KEY_NEG_INF && zhi >= KEY_POS_INF && (mass || end - beg == a.L);
+    if (fast && !minf) {
+      if (mass)
+        hist_fast_any<DT, EPT, true>(vgrid, full, v, md, pl, nc, beg, end, sh);
+      else
+        hist_fast_any<DT, EPT, false>(vgrid, full, v, md, pl, nc, beg, end, sh);
+    } else if (full) {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) add(v[e]);
     } else {
