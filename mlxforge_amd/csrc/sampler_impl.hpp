@@ -838,7 +838,8 @@ __device__ __forceinline__ void slice_stage(const Args& a, int r, int s, const P
 
   float v[EPT];
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) load8<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
+  for (int it = 0; it < NIT; ++it) load8_nan<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
+  clear_nans(v);  // NaN reads as -inf
 #define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
 
   if (pl.phase == PH_COUNT || pl.phase == PH_MASS) {
@@ -923,12 +924,26 @@ __device__ __forceinline__ void slice_stage(const Args& a, int r, int s, const P
     // fall inside the bracket's edge values)
     unsigned long long t = 0;
     const bool fk = pl.fkey > key_lo<DT>();
+    if (fast && !minf) {
+      // straight-line: every element's mass computed, the kept ones summed
+      // (with no threshold, key >= 0 keeps all)
+      const unsigned int fke = fk ? pl.fkey : 0u;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const unsigned int zk = f2key(v[e]);
-      if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) {
-        const float zp = zdiv<DT>(v[e], md.Tr, md.y, fast);
-        if (!fk || zkey<DT>(zp) >= pl.fkey) t += q40(wfun(zp, Mp, nc, minf));
+      for (int e = 0; e < EPT; ++e) {
+        const unsigned int zk = f2key(v[e]);
+        const float zp = zdiv<DT>(v[e], md.Tr, md.y, true);
+        const unsigned long long q = q40(__builtin_amdgcn_exp2f(wlog2(zp, nc)));
+        const bool keep = MLXF_IDX(e) < end && zk >= zlo && zk <= zhi && zkey<DT>(zp) >= fke;
+        t += keep ? q : 0ull;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const unsigned int zk = f2key(v[e]);
+        if (MLXF_IDX(e) < end && zk >= zlo && zk <= zhi) {
+          const float zp = zdiv<DT>(v[e], md.Tr, md.y, fast);
+          if (!fk || zkey<DT>(zp) >= pl.fkey) t += q40(wfun(zp, Mp, nc, minf));
+        }
       }
     }
     t = block_sum<unsigned long long>(t, sh.ru);
@@ -963,11 +978,14 @@ __device__ __forceinline__ int walk(const Args& a, int r, int s, float Mp, unsig
   // thread t owns EPT consecutive elements, held as z' values
   float zp[EPT];
 #pragma unroll
-  for (int it = 0; it < EPT / VEC; ++it) {
-    float z[VEC];
-    load8<DT, VECOK>(row, my0 + it * VEC, e0, z);
+  for (int it = 0; it < EPT / VEC; ++it) load8<DT, VECOK>(row, my0 + it * VEC, e0, &zp[it * VEC]);
+  // the division form chosen once for the run, so each loop is straight-line
+  if (fast) {
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) zp[it * VEC + j] = zdiv<DT>(z[j], md.Tr, md.y, fast);
+    for (int e = 0; e < EPT; ++e) zp[e] = zdiv<DT>(zp[e], md.Tr, md.y, true);
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) zp[e] = zdiv<DT>(zp[e], md.Tr, md.y, false);
   }
   // rank of my first tie at tau among the slice's ties (all ties kept: none)
   const bool all_ties = lim == 0xffffffffu;
