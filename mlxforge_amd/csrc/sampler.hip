@@ -119,9 +119,9 @@ int check_shape(int B, int V, int K_max, int dtype, char** err) {
 //
 // HINT_STAGES is 2, not NSTAGE: results are the same for every count, and the
 // rows still open after a second stage are fewer than a third launch costs.
-// Measured per step on MI355X, 2 vs 3 stages: B=8 V=151936 bf16 top-p 53.2 vs
-// 55.8 us; B=64 V=151936 fp32 top-p 98.0 vs 101.0 us; B=256 V=262144 bf16
-// mixed 171.4 vs 176.1 us (one stage: 125, 207 and 331 us).
+// Measured per step on MI355X, 2 vs 3 stages: B=8 V=151936 bf16 top-p 49.9 vs
+// 52.6 us; B=64 V=151936 fp32 top-p 91.0 vs 94.2 us; B=256 V=262144 bf16
+// mixed 161.8 vs 166.4 us (one stage: 122, 185 and 314 us).
 constexpr int HINT_STAGES = 2;
 int host_refine_stages(int B, int V, int dtype, const float* T, const int32_t* k, const float* p) {
   if (!T) return 0;

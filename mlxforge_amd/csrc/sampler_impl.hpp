@@ -1594,7 +1594,8 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
           const unsigned long long e = sh.cand[c];
           const unsigned int k = static_cast<unsigned int>(e);
           const unsigned int i = static_cast<unsigned int>(e >> 32);
-          const int st = static_cast<int>(i) / a.L;
+          // the slice length is THREADS * EPT, a power of two: a shift
+          const int st = static_cast<int>(i / static_cast<unsigned int>(THREADS * EPT));
           if (k > tau || (k == tau && i <= cut)) {
             atomicAdd(&sh.kept[st], sh.cmq[c]);
             if (k == tau) atomicAdd(&sh.tcnt[st], 1u);
