@@ -1722,6 +1722,25 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
     }
   }
   __syncthreads();
+  // the row's max, lowest argmax, minimum and log-sum-exp from the slice
+  // records, by one wave (the last: it has no survivor chunk to sort when they
+  // fill fewer than WAVES chunks, so the work overlaps the sort)
+  auto row_stats = [&]() {
+    const float zm = lane < S ? sh.szmax[lane] : -INFINITY;
+    const int za = lane < S ? sh.szarg[lane] : INT_MAX;
+    float rm = zm;
+    int ra = za;
+    wave_best(rm, ra);
+    double part = (lane < S && md.need_lse) ? sh.slse[lane] * wexp_d(zm, rm) : 0.0;
+    part = wave_sum(part);
+    const float mn = wave_min(lane < S ? sh.szmin[lane] : INFINITY);
+    if (lane == 0) {
+      sh.zmax = rm;
+      sh.zarg = ra;
+      sh.zmin = mn;
+      sh.lse = md.need_lse ? static_cast<double>(rm) + log(part) : static_cast<double>(NAN);
+    }
+  };
   if (md.need_list) {
     // theta, a value the row's 64th best reaches: slice t's j-th entry e_t has
     // j entries of the slice at or above it, so a value c that 64 / j of the
@@ -1799,34 +1818,22 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
         lv = cv;
         li = ci;
       }
+      if (wid == WAVES - 1) row_stats();  // idle here when nch < WAVES
       if (nch > 1) tree_merge(lv, li, sh.lists, nch);
     } else {
       for (int t = wid; t < S; t += WAVES) {
         const unsigned long long w = sh.lst[t * LIST + lane];
         wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
       }
+      if (wid == WAVES - 1) row_stats();
       tree_merge(lv, li, sh.lists, S < WAVES ? S : WAVES);
     }
     if (wid == 0) {
       sh.mlist[lane].v = lv;
       sh.mlist[lane].i = li;
     }
-  }
-  if (wid == 0) {
-    const float zm = lane < S ? sh.szmax[lane] : -INFINITY;
-    const int za = lane < S ? sh.szarg[lane] : INT_MAX;
-    float rm = zm;
-    int ra = za;
-    wave_best(rm, ra);
-    double part = (lane < S && md.need_lse) ? sh.slse[lane] * wexp_d(zm, rm) : 0.0;
-    part = wave_sum(part);
-    const float mn = wave_min(lane < S ? sh.szmin[lane] : INFINITY);
-    if (lane == 0) {
-      sh.zmax = rm;
-      sh.zarg = ra;
-      sh.zmin = mn;
-      sh.lse = md.need_lse ? static_cast<double>(rm) + log(part) : static_cast<double>(NAN);
-    }
+  } else if (wid == WAVES - 1) {
+    row_stats();
   }
   __syncthreads();
   const double lse = sh.lse;
