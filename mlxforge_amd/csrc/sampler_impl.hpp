@@ -230,8 +230,9 @@ __device__ __forceinline__ unsigned int key_hi() {  // key of +inf
 }
 
 // log2 of the weight: (z' - Mp) * log2(e) as one FMA with nc = -RN(Mp * log2 e).
-// The rounding of nc scales every weight of the row by the same factor, which
-// cancels in every mass ratio.
+// The rounding of nc scales every weight of the row by the same factor (within
+// an ulp of 1), which cancels in every mass ratio; min_p, an absolute
+// comparison, scales its threshold by the max's own weight (minp_thr).
 __device__ __forceinline__ float wlog2(float zp, float nc) { return __builtin_fmaf(zp, LOG2E, nc); }
 
 // w = exp(z' - Mp); for an infinite row max the limit (1 where z' == Mp, else 0).
@@ -311,13 +312,22 @@ __device__ __forceinline__ unsigned long long pack_ent(float v, int i) {
 }
 
 // min_p (src/sample/sampler.cpp:87-93, after top-p): an element is kept when
-// its weight exp(z' - max z') reaches mr; weights are non-decreasing in z', so
-// that is every z' key from the smallest one whose weight reaches mr.  Whole
-// wave.
+// its probability reaches mr times the largest one, i.e. when its weight
+// reaches mr times the weight of the row max.  The weight of the max is
+// exp2(fma(Mp, log2 e, -RN(Mp * log2 e))), within an ulp of 1 but not 1, so
+// the threshold is scaled by it: min_p = 1 then keeps exactly the elements
+// whose weight equals the max's, the max among them.
+__device__ __forceinline__ float minp_thr(float mr, float Mp, float nc, bool minf) {
+  return mr * wfun(Mp, Mp, nc, minf);
+}
+
+// Weights are non-decreasing in z', so the kept set is every z' key from the
+// smallest one whose weight reaches the threshold.  Whole wave.
 template <int DT>
 __device__ __forceinline__ unsigned int minp_key(float mr, float Mp, float nc, bool minf) {
+  const float thr = minp_thr(mr, Mp, nc, minf);
   return wave_search(key_lo<DT>(), key_hi<DT>(),
-                     [&](unsigned int k) { return wfun(kval<DT>(k), Mp, nc, minf) >= mr; });
+                     [&](unsigned int k) { return wfun(kval<DT>(k), Mp, nc, minf) >= thr; });
 }
 
 // Sampled id (and its logprob) of row r.
@@ -330,12 +340,6 @@ __device__ __forceinline__ void write_out(const Args& a, int r, int id, double l
   }
 }
 
-// Uniform draw over the whole vocabulary: what the reference's categorical
-// does when every logit left is -inf (all -inf rows, or a top-p of 0).
-__device__ __forceinline__ int uniform_id(float u, int V) {
-  const double x = floor(static_cast<double>(u) * static_cast<double>(V));
-  return x < V - 1 ? static_cast<int>(x) : V - 1;
-}
 
 // ----------------------------------------------------------- row plans --
 
@@ -707,7 +711,7 @@ __device__ __forceinline__ bool klist_resolve(const Mode& md, float Mp, const To
     const double PW = ceil(static_cast<double>(md.pr) * Wk);
     keep = k1 && (incl - w) < PW;
   }
-  if (md.mr > 0.0f) keep = keep && wv >= md.mr;  // min_p, after top-p
+  if (md.mr > 0.0f) keep = keep && wv >= minp_thr(md.mr, Mp, nc, minf);  // min_p, after top-p
   const double wf = keep ? w : 0.0;
   const double Wf = wave_sum(wf);
   unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * Wf);
@@ -1640,7 +1644,11 @@ __global__ __launch_bounds__(THREADS) void k_scan(Args a, int stage) {
 
 // Finish row r here: run the remaining levels over the row's slices in this
 // workgroup (the row plan is in sh.sl.pw).  Each level narrows the bracket or
-// advances the phase, so the loop ends; its bound is a guard.
+// advances the phase: a selection takes a value-grid level and at most four
+// 8-bit key-digit levels (a digit level whose bin is one key is exact), and
+// the phases only move forward (COUNT, MASS, GATHER / DRAWSUM), so a row needs
+// far fewer than SERIAL_MAX levels.  Should the bound ever be reached, the row
+// still gets a defined id: its argmax.
 template <int DT, int EPT, bool VECOK>
 __device__ __forceinline__ void serial_finish(const Args& a, int r, RLds& sh) {
   for (int it = 0; it < SERIAL_MAX && static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) != PH_DONE; ++it) {
@@ -1655,6 +1663,20 @@ __device__ __forceinline__ void serial_finish(const Args& a, int r, RLds& sh) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     finish_stage<DT, EPT, VECOK>(a, r, pl.phase, sh.sl.pw, sh);
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  if (static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) != PH_DONE && threadIdx.x == 0) {
+    float bm = -INFINITY;
+    int bi = 0;
+    for (int s2 = 0; s2 < a.S; ++s2) {
+      const unsigned long long w0 = a.rec[(static_cast<size_t>(r) * a.S + s2) * 4];
+      const float m = __uint_as_float(static_cast<unsigned int>(w0));
+      if (m > bm) {
+        bm = m;
+        bi = static_cast<int>(w0 >> 32);
+      }
+    }
+    const Plan pl = plan_unpack(sh.sl.pw);
+    write_out<DT>(a, r, bi, pl.lse, decode<DT>(a, r).want_lp);
   }
 }
 
@@ -1868,8 +1890,10 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
   const float Mp = zdiv<DT>(M, md.Tr, md.y, false);  // max z' = z'(max z)
   pl.Mp = Mp;
   if (M == -INFINITY || (md.topp && !(md.pr > 0.0f))) {
-    // every logit left is -inf: the reference's draw is uniform
-    if (tid == 0) write_out<DT>(a, r, uniform_id(md.u, a.V), lse, md.want_lp);
+    // nothing left to draw (every logit -inf, or a top-p that rounds to 0):
+    // the reference's categorical is the argmax of the logits plus Gumbel
+    // noise, -inf everywhere, whose first index is 0
+    if (tid == 0) write_out<DT>(a, r, 0, lse, md.want_lp);
     return;
   }
   if (md.kind == KIND_KLIST) {

@@ -36,36 +36,51 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             build()
-        L = ctypes.CDLL(LIB_PATH)
-        P = ctypes.c_void_p
-        L.orc_sample.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_long,
-                                 P, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, ctypes.c_int]
-        L.orc_sample.restype = ctypes.c_int
-        L.orc_sample_ex.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_long,
-                                    P, P, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, ctypes.c_int]
-        L.orc_sample_ex.restype = ctypes.c_int
-        L.orc_filter_row.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_float,
-                                     ctypes.c_int, ctypes.c_float, ctypes.c_float, P]
-        L.orc_filter_row.restype = ctypes.c_int
-        L.orc_round_bf16.argtypes = [ctypes.c_float]
-        L.orc_round_bf16.restype = ctypes.c_float
-        L.orc_round_f16.argtypes = [ctypes.c_float]
-        L.orc_round_f16.restype = ctypes.c_float
-        L.orc_greedy_row.argtypes = [P, ctypes.c_int]
-        L.orc_greedy_row.restype = ctypes.c_int
-        L.orc_lse_row.argtypes = [P, ctypes.c_int]
-        L.orc_lse_row.restype = ctypes.c_double
-        L.orc_draw_row.argtypes = [P, ctypes.c_int, ctypes.c_float, P]
-        L.orc_draw_row.restype = ctypes.c_int
-        L.orc_apply_penalties.argtypes = [P, ctypes.c_int, ctypes.c_int, P, ctypes.c_int,
-                                          ctypes.c_float, ctypes.c_float, ctypes.c_float]
-        L.orc_apply_penalties.restype = None
-        L.orc_philox4x32_10.argtypes = [P, P, P]
-        L.orc_philox4x32_10.restype = None
-        L.orc_uniforms.argtypes = [ctypes.c_int, P, P, P]
-        L.orc_uniforms.restype = None
-        _lib = L
+        _lib = _configure(ctypes.CDLL(LIB_PATH))
     return _lib
+
+
+def native_lib(out_dir: str):
+    """The CPU baseline's build of the same source (-O3 -march=native), compiled
+    on the machine that times it into out_dir (make -C oracle native)."""
+    subprocess.run(["make", "-s", "-C", HERE, "native", f"OUT={out_dir}"], check=True)
+    return _configure(ctypes.CDLL(os.path.join(out_dir, "liboracle_native.so")))
+
+
+def _configure(L):
+    """Argument and result types of every exported function."""
+    P = ctypes.c_void_p
+    L.orc_sample.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_long,
+                             P, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, ctypes.c_int]
+    L.orc_sample.restype = ctypes.c_int
+    L.orc_sample_ex.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_long,
+                                P, P, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, ctypes.c_int]
+    L.orc_sample_ex.restype = ctypes.c_int
+    L.orc_filter_row.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                 ctypes.c_int, ctypes.c_float, ctypes.c_float, P]
+    L.orc_filter_row.restype = ctypes.c_int
+    L.orc_round_bf16.argtypes = [ctypes.c_float]
+    L.orc_round_bf16.restype = ctypes.c_float
+    L.orc_round_f16.argtypes = [ctypes.c_float]
+    L.orc_round_f16.restype = ctypes.c_float
+    L.orc_greedy_row.argtypes = [P, ctypes.c_int]
+    L.orc_greedy_row.restype = ctypes.c_int
+    L.orc_lse_row.argtypes = [P, ctypes.c_int]
+    L.orc_lse_row.restype = ctypes.c_double
+    L.orc_draw_row.argtypes = [P, ctypes.c_int, ctypes.c_float, P]
+    L.orc_draw_row.restype = ctypes.c_int
+    L.orc_apply_penalties.argtypes = [P, ctypes.c_int, ctypes.c_int, P, ctypes.c_int,
+                                      ctypes.c_float, ctypes.c_float, ctypes.c_float]
+    L.orc_apply_penalties.restype = None
+    L.orc_philox4x32_10.argtypes = [P, P, P]
+    L.orc_philox4x32_10.restype = None
+    L.orc_uniforms.argtypes = [ctypes.c_int, P, P, P]
+    L.orc_uniforms.restype = None
+    L.orc_admissible.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int,
+                                 ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_double,
+                                 P, ctypes.c_int]
+    L.orc_admissible.restype = ctypes.c_int
+    return L
 
 
 def _ptr(a):
@@ -84,10 +99,11 @@ def dtype_code(arr: np.ndarray, dtype: int | None = None) -> int:
 
 def sample(logits: np.ndarray, T=None, k=None, p=None, tlp=None, u=None, K_max: int = 0,
            dtype: int | None = None, V: int | None = None, nthreads: int | None = None,
-           min_p=None):
+           min_p=None, L=None):
     """Run the oracle over a [B, row_stride] host array.
 
-    For bf16, pass the raw uint16 bit patterns with dtype=BF16.
+    For bf16, pass the raw uint16 bit patterns with dtype=BF16.  L: a library
+    from native_lib() instead of the default build.
     Returns dict(ids, lp, top_ids, top_lp, flags, margins).
     """
     logits = np.ascontiguousarray(logits)
@@ -105,13 +121,66 @@ def sample(logits: np.ndarray, T=None, k=None, p=None, tlp=None, u=None, K_max: 
     margins = np.zeros((B, 2), np.float64)
     if nthreads is None:
         nthreads = min(os.cpu_count() or 1, 16)
-    rc = lib().orc_sample_ex(_ptr(logits), code, B, V, stride, _ptr(T), _ptr(k), _ptr(p), _ptr(mp),
+    rc = (L or lib()).orc_sample_ex(_ptr(logits), code, B, V, stride, _ptr(T), _ptr(k), _ptr(p), _ptr(mp),
                              _ptr(tlp), _ptr(u), _ptr(ids), _ptr(lp), _ptr(top_ids), _ptr(top_lp),
                              K_max, _ptr(flags), _ptr(margins), nthreads)
     if rc != 0:
         raise ValueError("orc_sample rejected its arguments")
     return dict(ids=ids, lp=lp, top_ids=top_ids[:, :K_max], top_lp=top_lp[:, :K_max],
                 flags=flags, margins=margins)
+
+
+AMBIG_EPS = 1e-6
+AMBIG = FLAG_TOPP_AMBIG | FLAG_DRAW_AMBIG | FLAG_MINP_AMBIG
+
+
+def admissible(row: np.ndarray, dtype: int, T=0.0, k=0, p=1.0, min_p=0.0, u=0.0,
+               eps: float = AMBIG_EPS, cap: int = 4096):
+    """Every id one row can produce when p, u and min_p each move by up to eps
+    (the checker of rows the ambiguity rule excludes from the bit-exact
+    comparison).  row: the row's host elements (float32, float16, or bf16 bit
+    patterns with dtype=BF16).  Returns a sorted list, or None when the row has
+    more variants than cap."""
+    row = np.ascontiguousarray(row)
+    out = np.zeros(cap, np.int32)
+    n = lib().orc_admissible(_ptr(row), dtype, row.size, float(T), int(k), float(p), float(min_p),
+                             float(u), eps, _ptr(out), cap)
+    if n == -2:
+        raise ValueError("orc_admissible rejected its arguments")
+    return None if n < 0 else sorted(out[:n].tolist())
+
+
+def check_rows(ids, ref: dict, logits: np.ndarray, dtype: int, T=None, k=None, p=None, min_p=None,
+               u=None, V: int | None = None) -> dict:
+    """Ids of one call (ids) against an oracle result (ref, from sample() on the
+    same inputs): every row must be the oracle's id, or -- for a row the oracle
+    flags as ambiguous -- one of its admissible ids.  Returns the counts
+    rows / excluded (flagged) / excluded_matching (flagged, same id as the
+    oracle) / excluded_admissible (flagged, an admissible id) and the rows that
+    fail ("bad": neither)."""
+    ids = np.asarray(ids)
+    B = ids.shape[0]
+    V = logits.shape[1] if V is None else V
+    g = lambda a, d: d if a is None else a[r]
+    amb = (ref["flags"] & AMBIG) != 0
+    same = ids == ref["ids"]
+    bad, adm_ok = [], 0
+    for r in range(B):
+        if same[r]:
+            if amb[r]:
+                adm_ok += 1
+            continue
+        if not amb[r]:
+            bad.append(r)
+            continue
+        a = admissible(logits[r, :V], dtype, T=g(T, 0.0), k=g(k, 0), p=g(p, 1.0), min_p=g(min_p, 0.0),
+                       u=g(u, 0.0))
+        if a is not None and int(ids[r]) in a:
+            adm_ok += 1
+        else:
+            bad.append(r)
+    return dict(rows=int(B), excluded=int(amb.sum()), excluded_matching=int((amb & same).sum()),
+                excluded_admissible=int(adm_ok), bad=bad)
 
 
 def filter_row(z, T=0.0, k=0, p=1.0, min_p=0.0, dtype: int = F32) -> np.ndarray:

@@ -39,7 +39,10 @@
  *   D6  for bf16/f16 logits p is rounded to the logits dtype
  *       (sampler.cpp:79 compares against array(p, probs.dtype())).
  *   D7  NaN logits are read as -inf; exp(x - max) is taken as 1 where x == max
- *       (so +inf and all -inf rows stay finite and well defined).
+ *       (so rows with +inf entries stay finite and well defined: their mass is
+ *       split evenly over the +inf entries).  A row with nothing left to draw
+ *       (all -inf, or a top-p that rounds to 0) returns index 0, the argmax of
+ *       an all -inf row that MLX's Gumbel-max categorical takes.
  *   D8  top_logprobs alternatives are ordered by (z desc, index asc), the exact
  *       order of log_softmax(z).
  *   D9  min_p in (0, 1] (else off, src/capi/mlxforge.cpp:58) is rounded to the
@@ -51,9 +54,11 @@
  *
  * Ambiguity flags (the north-star exclusion rule): a row whose top-p cutoff or
  * draw boundary lies within 1e-6 of the compared quantity is reported with
- * ORC_FLAG_TOPP_AMBIG / ORC_FLAG_DRAW_AMBIG; a kept weight within 1e-6
- * (relative) of min_p is ORC_FLAG_MINP_AMBIG.  Bit-exact id comparison excludes
- * such rows.
+ * ORC_FLAG_TOPP_AMBIG / ORC_FLAG_DRAW_AMBIG; a weight other than the max's
+ * within 1e-6 (relative) of min_p is ORC_FLAG_MINP_AMBIG.  Such a row is not
+ * compared bit-exactly; orc_admissible() gives every id the row can produce
+ * when p, u and min_p each move by up to 1e-6, and the GPU's id must be one
+ * of them.
  */
 #include <math.h>
 #include <pthread.h>
@@ -282,8 +287,11 @@ static int apply_min_p_m(float* zs, int V, float min_p, double* margin) {
     for (int i = 0; i < V; ++i) {
       if (zs[i] == -INFINITY) continue;
       const double w = wexp(zs[i], m);
-      const double d = fabs(w / (double)min_p - 1.0);
-      if (d < mg) mg = d;
+      /* the max itself (w = 1) is kept for every min_p <= 1: no margin */
+      if (zs[i] != m) {
+        const double d = fabs(w / (double)min_p - 1.0);
+        if (d < mg) mg = d;
+      }
       if (w / W < thr) zs[i] = -INFINITY;
     }
   }
@@ -298,16 +306,23 @@ int orc_draw_row(const float* zs, int V, float u, double* margin) {
   float m = -INFINITY;
   for (int i = 0; i < V; ++i)
     if (zs[i] > m) m = zs[i];
+  if (m == -INFINITY) {
+    /* nothing left to draw (an all -inf row, or a top-p that rounds to 0):
+     * MLX's categorical is the argmax of the logits plus Gumbel noise, -inf
+     * everywhere, whose first index is 0 (D7) */
+    if (margin) *margin = INFINITY;
+    return 0;
+  }
   double W = 0.0;
   for (int i = 0; i < V; ++i)
-    if (zs[i] != -INFINITY || m == -INFINITY) W += wexp(zs[i], m);
+    if (zs[i] != -INFINITY) W += wexp(zs[i], m);
   if (!(u >= 0.0f)) u = 0.0f;
   if (u >= 1.0f) u = 0x1.fffffep-1f;
   const double target = (double)u * W;
   double cum = 0.0, prev = 0.0;
   int id = -1, last_pos = -1;
   for (int i = 0; i < V; ++i) {
-    if (zs[i] == -INFINITY && m != -INFINITY) continue;
+    if (zs[i] == -INFINITY) continue;
     const double w = wexp(zs[i], m);
     if (w > 0.0) last_pos = i;
     prev = cum;
@@ -547,6 +562,149 @@ void orc_uniforms(int B, const uint64_t* seed, const uint64_t* step, float* u) {
     orc_philox4x32_10(ctr, key, o);
     u[r] = (float)(o[0] >> 8) * 0x1p-24f;
   }
+}
+
+/* ---- admissible ids of an ambiguous row ---------------------------------- */
+
+typedef struct {
+  int32_t* out;
+  int n, cap;
+} idset;
+
+static int idset_add(idset* s, int id) {
+  for (int j = 0; j < s->n; ++j)
+    if (s->out[j] == id) return 0;
+  if (s->n >= s->cap) return -1;
+  s->out[s->n++] = id;
+  return 0;
+}
+
+/* Every id one row of Sampler::sample (src/sample/sampler.cpp:141-166, with
+ * the decisions D1-D9) can return when the top-p threshold p, the draw
+ * uniform u and the min_p threshold each move by up to eps (absolute for p and
+ * u, relative for min_p): the checker for rows the ambiguity rule excludes
+ * from the bit-exact comparison.
+ *
+ * After top-k (whose threshold is a comparison and never ambiguous), top-p and
+ * min_p both keep a prefix of the (z' desc, index asc) order, so the kept set
+ * is a prefix whose length L ranges over [L_lo, L_hi]; for each L the draw
+ * (D4, ascending index) can return every kept element whose cumulative-mass
+ * interval meets [(u - eps) W_L, (u + eps) W_L].  Writes the ids to out
+ * (unordered) and returns their number; returns -1 when the range of L or of
+ * the ids exceeds cap (the row cannot be checked), -2 on bad arguments. */
+int orc_admissible(const void* row, int dtype, int V, float T, int k, float p, float mp, float u,
+                   double eps, int32_t* out, int cap) {
+  if (!row || !out || V <= 0 || cap <= 0) return -2;
+  idset set = {out, 0, cap};
+  float* z = (float*)malloc(sizeof(float) * (size_t)V);
+  for (int i = 0; i < V; ++i) z[i] = load_logit(row, dtype, (size_t)i);
+  const int sampling = isfinite(T) && T > 0.0f && round_dtype(T, dtype) > 0.0f;
+  if (!sampling) {
+    out[0] = orc_greedy_row(z, V);
+    free(z);
+    return 1;
+  }
+  const float Tr = round_dtype(T, dtype);
+  float* zs = (float*)malloc(sizeof(float) * (size_t)V);
+  for (int i = 0; i < V; ++i) zs[i] = round_dtype(z[i] / Tr, dtype);
+  free(z);
+  if (k > 0) orc_apply_top_k(zs, V, k < V ? k : V);
+  vi_t* ord = (vi_t*)malloc(sizeof(vi_t) * (size_t)V);
+  int N = 0;
+  for (int i = 0; i < V; ++i)
+    if (zs[i] != -INFINITY) {
+      ord[N].v = zs[i];
+      ord[N].i = i;
+      ++N;
+    }
+  int rc = 0;
+  if (N == 0) { /* nothing to draw: index 0 (D7) */
+    idset_add(&set, 0);
+    rc = 1;
+    goto done;
+  }
+  qsort(ord, (size_t)N, sizeof(vi_t), cmp_desc_idx);
+  {
+    const float m = ord[0].v;
+    double* w = (double*)malloc(sizeof(double) * (size_t)N);
+    double* prior = (double*)malloc(sizeof(double) * (size_t)N);
+    double W = 0.0;
+    for (int j = 0; j < N; ++j) {
+      w[j] = wexp(ord[j].v, m);
+      prior[j] = W;
+      W += w[j];
+    }
+    int n_lo = N, n_hi = N;
+    if (p > 0.0f && p < 1.0f) {
+      const double pc = (double)round_dtype(p, dtype);
+      n_lo = n_hi = 0;
+      for (int j = 0; j < N; ++j) {
+        if (prior[j] < (pc - eps) * W) n_lo = j + 1;
+        if (prior[j] < (pc + eps) * W) n_hi = j + 1;
+      }
+      if (pc > 0.0 && n_lo < 1) n_lo = 1;
+      if (pc > 0.0 && n_hi < 1) n_hi = 1;
+    }
+    int m_lo = N, m_hi = N;
+    if (mp > 0.0f && mp <= 1.0f) {
+      const double mr = (double)round_dtype(mp, dtype);
+      int ties = 0;
+      m_lo = m_hi = 0;
+      for (int j = 0; j < N; ++j) {
+        if (w[j] >= mr * (1.0 + eps)) m_lo = j + 1;
+        if (w[j] >= mr * (1.0 - eps)) m_hi = j + 1;
+        if (ord[j].v == m) ties = j + 1;
+      }
+      if (m_lo < ties) m_lo = ties; /* the max's ties are always kept */
+      if (m_hi < ties) m_hi = ties;
+    }
+    const int L_lo = n_lo < m_lo ? n_lo : m_lo;
+    const int L_hi = n_hi < m_hi ? n_hi : m_hi;
+    if (L_hi - L_lo > cap) {
+      rc = -1;
+    } else if (L_hi == 0) {
+      idset_add(&set, 0); /* top-p rounded to 0: nothing kept */
+      rc = 1;
+    } else {
+      int* rank = (int*)malloc(sizeof(int) * (size_t)V);
+      for (int i = 0; i < V; ++i) rank[i] = -1;
+      for (int j = 0; j < N; ++j) rank[ord[j].i] = j;
+      float uc = u;
+      if (!(uc >= 0.0f)) uc = 0.0f;
+      if (uc >= 1.0f) uc = 0x1.fffffep-1f;
+      for (int L = L_lo < 1 ? 1 : L_lo; L <= L_hi && rc >= 0; ++L) {
+        double WL = 0.0;
+        int last_pos = -1;
+        for (int i = 0; i < V; ++i)
+          if (rank[i] >= 0 && rank[i] < L) {
+            WL += w[rank[i]];
+            if (w[rank[i]] > 0.0) last_pos = i;
+          }
+        const double lo_t = ((double)uc - eps) * WL, hi_t = ((double)uc + eps) * WL;
+        double C = 0.0;
+        for (int i = 0; i < V && rc >= 0; ++i) {
+          if (rank[i] < 0 || rank[i] >= L) continue;
+          const double wi = w[rank[i]];
+          if (wi <= 0.0) continue;
+          const double prev = C;
+          if (prev > hi_t) break;
+          C += wi;
+          if (C > lo_t && idset_add(&set, i)) rc = -1;
+        }
+        /* rounding can leave the target at or past the total: the last
+         * positive-weight entry (orc_draw_row's fallback) */
+        if (rc >= 0 && hi_t >= WL && last_pos >= 0 && idset_add(&set, last_pos)) rc = -1;
+      }
+      free(rank);
+      if (rc >= 0) rc = set.n;
+    }
+    free(w);
+    free(prior);
+  }
+done:
+  free(ord);
+  free(zs);
+  return rc;
 }
 
 /* orc_sample_ex without min_p: the product's mlxf_sample. */

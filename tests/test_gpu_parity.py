@@ -44,7 +44,9 @@ def test_config_parity(cfg):
     code = {"f32": _lib.DTYPE_F32, "bf16": _lib.DTYPE_BF16, "f16": _lib.DTYPE_F16}[wl.dtype]
     st = _lib.refine_stages(wl.B, wl.V, code, wl.T, wl.k, wl.p)
     gh = gu.gpu_sample(dev, T=wl.T, k=wl.k, p=wl.p, tlp=wl.tlp, u=wl.u, K_max=wl.K_max, stages=st)
-    assert np.array_equal(g["ids"], gh["ids"]), f"C{cfg}: {st} stages differ from 3"
+    for key in ("ids", "lp", "top_ids", "top_lp"):
+        assert np.array_equal(g[key].view(np.uint32), gh[key].view(np.uint32)), \
+            f"C{cfg}: {key} with {st} stages differs from 3"
     # determinism: a second run is bit-identical
     g2 = gu.gpu_sample(dev, T=wl.T, k=wl.k, p=wl.p, tlp=wl.tlp, u=wl.u, K_max=wl.K_max)
     assert np.array_equal(g["ids"], g2["ids"])
@@ -391,6 +393,40 @@ def test_min_p_parity(dtype, kind):
         for st in (0, 1):
             g = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=2, min_p=mp, stages=st)
             assert np.array_equal(g["ids"], ref["ids"]), (kind, st, g["ids"], ref["ids"])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_min_p_one_draws_the_max(dtype):
+    """min_p = 1 keeps only the row max and its ties, behind every earlier
+    filter: the id is the argmax (one max) or one of the tied maxima, whatever
+    the uniform -- checked directly, not through the oracle."""
+    rng = np.random.default_rng(1234 + len(dtype))
+    B, V = 16, 30000
+    z = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    ties = {}
+    for r in range(B):
+        top = float(np.float32(z[r].max() + 3.0))
+        if r % 2:
+            pos = rng.choice(V, size=int(rng.integers(2, 6)), replace=False)
+        else:
+            pos = rng.choice(V, size=1)
+        z[r, pos] = top
+        ties[r] = set(int(i) for i in pos)
+    host = z if dtype == "f32" else (workloads.to_bf16_bits(z) if dtype == "bf16" else z.astype(np.float16))
+    vals = gu.host_values(host, dtype)
+    for r in range(B):  # the tie set in the dtype's own values
+        ties[r] = set(np.nonzero(vals[r] == vals[r].max())[0].tolist())
+    T = rng.uniform(0.5, 1.5, B).astype(np.float32)
+    k = np.array([0, 0, 5, 5, 200, 200, 0, 0] * 2, np.int32)
+    p = np.array([1.0, 1.0, 1.0, 1.0, 1.0, 1.0, 0.9, 0.9] * 2, np.float32)
+    mp = np.ones(B, np.float32)
+    dev = gu.to_device(host, dtype)
+    for u in (0.0, 0.3, 0.7, 0.9999):
+        uu = np.full(B, u, np.float32)
+        for st in (0, 3):
+            g = gu.gpu_sample(dev, T=T, k=k, p=p, u=uu, min_p=mp, stages=st)
+            for r in range(B):
+                assert int(g["ids"][r]) in ties[r], (dtype, u, st, r, g["ids"][r], sorted(ties[r]))
 
 
 def _mixed_rows(rng, B, V, dtype):

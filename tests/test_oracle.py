@@ -252,7 +252,8 @@ def test_nan_reads_as_neg_inf_and_degenerate_rows(orc):
     assert orc.sample(z)["ids"].tolist() == [1]
     allneg = np.full((1, 5), -np.inf, np.float32)
     r = orc.sample(allneg, T=[1.0], u=[0.99], tlp=[0])
-    assert r["ids"].tolist() == [4] and np.isnan(r["lp"][0])  # uniform over the row
+    # nothing to draw: index 0, the argmax MLX's Gumbel-max categorical takes
+    assert r["ids"].tolist() == [0] and np.isnan(r["lp"][0])
     assert orc.sample(allneg)["ids"].tolist() == [0]
     inf = np.array([[1.0, np.inf, 3.0, np.inf]], np.float32)
     r = orc.sample(inf, T=[1.0], u=[0.75])
@@ -280,6 +281,72 @@ def test_ambiguity_flags(orc):
     # draw boundary: u at the cumulative mass of the first kept token
     r = orc.sample(z, T=[1.0], u=[0.5])
     assert r["flags"][0] & orc.FLAG_DRAW_AMBIG
+
+
+def test_min_p_one_keeps_the_max_and_is_not_ambiguous(orc):
+    """min_p = 1 keeps exactly the row max (and its ties); the max's own
+    weight is 1, so it gives no ambiguity margin."""
+    z = np.array([[0.5, 2.0, 1.0, 2.0, -1.0], [0.5, 3.0, 1.0, 2.0, -1.0]], np.float32)
+    for u in (0.0, 0.3, 0.6, 0.99):
+        r = orc.sample(z, T=[1.0, 1.0], min_p=[1.0, 1.0], u=[u, u])
+        assert r["ids"][0] in (1, 3) and r["ids"][1] == 1
+        assert not (r["flags"] & orc.FLAG_MINP_AMBIG).any()
+    r = orc.sample(z[:1], T=[1.0], min_p=[1.0], u=[0.3])
+    assert r["ids"].tolist() == [1]
+    r = orc.sample(z[:1], T=[1.0], min_p=[1.0], u=[0.6])
+    assert r["ids"].tolist() == [3]
+
+
+def test_admissible_ids(orc):
+    """The checker of ambiguous rows: the ids a row can produce when p, u and
+    min_p move by up to 1e-6."""
+    z = np.array([0.0, 0.0, -30.0], np.float32)
+    # top-p cutoff exactly at p = 0.5: {0} or {0, 1} kept
+    assert orc.admissible(z, orc.F32, T=1.0, p=0.5, u=0.3) == [0]
+    assert orc.admissible(z, orc.F32, T=1.0, p=0.5, u=0.7) == [0, 1]
+    # draw boundary at u = 0.5: either side
+    assert orc.admissible(z, orc.F32, T=1.0, u=0.5) == [0, 1]
+    # an unambiguous row admits only the oracle's id
+    assert orc.admissible(z, orc.F32, T=1.0, u=0.25) == [0]
+    assert orc.admissible(z, orc.F32, T=0.0) == [0]
+    # min_p at a kept weight: e^-1 at min_p = e^-1 (rounded to fp32)
+    zz = np.array([1.0, 0.0, -5.0], np.float32)
+    mp = float(np.float32(np.exp(-1.0)))
+    a = orc.admissible(zz, orc.F32, T=1.0, min_p=mp, u=0.9)
+    assert a == [0, 1], a
+    # nothing to draw: index 0
+    assert orc.admissible(np.full(4, -np.inf, np.float32), orc.F32, T=1.0, u=0.7) == [0]
+
+
+def test_admissible_covers_perturbed_oracle(orc):
+    """Brute force: the oracle's own ids with p, u and min_p moved anywhere in
+    [-1e-6, 1e-6] all lie in the admissible set, and a row the oracle does not
+    flag admits only its id."""
+    rng = np.random.default_rng(404)
+    eps = 1e-6
+    for trial in range(40):
+        V = int(rng.integers(2, 40))
+        z = rng.integers(-4, 5, V).astype(np.float32) * np.float32(0.5)  # ties and round masses
+        T = float(rng.choice([0.5, 1.0]))
+        k = int(rng.choice([0, 0, 3]))
+        p = float(rng.choice([1.0, 0.5, 0.75, 0.9]))
+        mp = float(rng.choice([0.0, 0.0, 0.25, 1.0]))
+        u = float(rng.choice([0.0, 0.25, 0.5, 0.75, float(rng.random())]))
+        a = orc.admissible(z, orc.F32, T=T, k=k, p=p, min_p=mp, u=u)
+        assert a is not None
+        base = orc.sample(z[None], T=[T], k=[k], p=[p], min_p=[mp], u=[u])
+        assert base["ids"][0] in a
+        if not (base["flags"][0] & orc.AMBIG):
+            assert a == [int(base["ids"][0])], (trial, a, base)
+        for d in np.linspace(-eps, eps, 9):
+            for which in ("p", "u", "mp"):
+                pp = p + d if which == "p" and p < 1.0 else p
+                uu = min(max(u + d, 0.0), 0.9999999) if which == "u" else u
+                mm = mp * (1 + d) if which == "mp" and mp > 0 else mp
+                mm = min(mm, 1.0)
+                r = orc.sample(z[None], T=[T], k=[k], p=[np.float32(pp)], min_p=[np.float32(mm)],
+                               u=[np.float32(uu)])
+                assert r["ids"][0] in a, (trial, which, d, r["ids"][0], a)
 
 
 def test_workloads_are_deterministic(orc):
