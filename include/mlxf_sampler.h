@@ -17,9 +17,8 @@
  *     mlxf_string_free();
  *   - no exception ever crosses the boundary;
  *   - the library allocates nothing in mlxf_sample / mlxf_greedy: scratch is the
- *     caller-provided workspace (size from mlxf_sampler_workspace_size), zeroed
- *     once before first use (mlxf_sampler_workspace_init, or any zero fill);
- *     every call leaves it ready for the next;
+ *     caller-provided workspace (size from mlxf_sampler_workspace_size); it
+ *     needs no initialisation (each call clears what it counts in);
  *   - calls are reentrant per stream; two calls that share a workspace must be
  *     ordered on one stream.
  */
@@ -62,10 +61,10 @@ int mlxf_sampler_abi_version(void);
  * (src/sample/sampler.cpp:141-166); the caller owns and reuses the buffer. */
 int mlxf_sampler_workspace_size(int B, int V, int K_max, int dtype, size_t* bytes, char** err);
 
-/* Prepare a freshly allocated workspace for its first call (zeroes the per-row
- * counters at its start with a fill kernel on `stream`; no hipMemset, so it may
- * be captured in a graph).  A workspace that came from a zero fill needs no
- * call.  No reference counterpart: the reference's MLX temporaries need none. */
+/* Zero the per-row counters at the start of a workspace with a fill kernel on
+ * `stream` (no hipMemset, so it may be captured in a graph).  Kept for
+ * callers of ABI version 1; no call needs it any more (each call clears its
+ * counters itself).  No reference counterpart. */
 int mlxf_sampler_workspace_init(void* d_workspace, size_t workspace_bytes, void* stream,
                                 char** err);
 
@@ -140,6 +139,31 @@ int mlxf_sample_ex(const void* d_logits, int dtype, int B, int V, int64_t row_st
                    int32_t* d_out_ids, float* d_out_logprobs, int32_t* d_out_top_ids,
                    float* d_out_top_logprobs, int K_max, void* d_workspace, size_t workspace_bytes,
                    int refine_stages, void* stream, char** err);
+
+/* Bytes of the fixed scratch mlxf_sample_noalloc holds on each GPU it runs on
+ * (from that GPU's first call until the process ends). */
+#define MLXF_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* mlxf_sample_ex without a workspace argument: the call allocates nothing and
+ * takes no caller memory besides its inputs and outputs, for callers that
+ * cannot allocate device memory or hold a workspace (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference (its MLX temporaries are allocated per call).
+ *
+ * Scratch is a fixed MLXF_NOALLOC_SCRATCH_BYTES array in device memory, one
+ * per GPU, shared by every call on that GPU and kept between calls: calls that
+ * may overlap on one GPU (on different streams, or from different threads)
+ * race and must be ordered by the caller.  Its device address is looked up on
+ * the stream's GPU at that GPU's first call.  Shapes whose workspace
+ * (mlxf_sampler_workspace_size) exceeds the scratch are refused with
+ * MLXF_EWORKSPACE; B = 256 rows of V = 262144 fit.  Arguments and results are
+ * those of mlxf_sample_ex. */
+int mlxf_sample_noalloc(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                        const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                        const float* d_min_p, const int32_t* d_top_logprobs, const float* d_uniforms,
+                        int32_t* d_out_ids, float* d_out_logprobs, int32_t* d_out_top_ids,
+                        float* d_out_top_logprobs, int K_max, int refine_stages, void* stream,
+                        char** err);
 
 /* Refine stages a call needs, from HOST copies of the per-row temperature,
  * top_k and top_p (NULL = the sentinel: greedy / off / off), with the same

@@ -32,7 +32,9 @@ SYMBOLS = (
     "mlxf_greedy",
     "mlxf_string_free",
     "mlxf_sampler_workspace_init",
+    "mlxf_sample_noalloc",
 )
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _lib = None
 
@@ -77,6 +79,8 @@ def load() -> ctypes.CDLL:
     L.mlxf_sampler_refine_stages.restype = I
     L.mlxf_greedy.argtypes = [P, I, I, I, I64, P, P, SZ, P, PP]
     L.mlxf_greedy.restype = I
+    L.mlxf_sample_noalloc.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, P, I, I, P, PP]
+    L.mlxf_sample_noalloc.restype = I
     L.mlxf_sampler_workspace_init.argtypes = [P, SZ, P, PP]
     L.mlxf_sampler_workspace_init.restype = I
     L.mlxf_string_free.argtypes = [P]

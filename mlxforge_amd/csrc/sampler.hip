@@ -2,7 +2,15 @@
 // behind the C ABI in include/mlxf_sampler.h: workspace layout, argument
 // checks, the stage count, and the launch of one dtype's kernel sequence
 // (sampler_impl.hpp, instantiated per dtype in sampler_<dtype>.hip).
+#include <mutex>
+
 #include "sampler_impl.hpp"
+
+// Scratch of the allocation-free entry point, mlxf_sample_noalloc: one copy per
+// GPU, held from the library's first use on that GPU until the process ends.
+// In host code `scratch` only names the symbol; the device address of each
+// GPU's copy comes from hipGetSymbolAddress (noalloc_scratch below).
+static __device__ __align__(256) unsigned char scratch[MLXF_NOALLOC_SCRATCH_BYTES];
 
 namespace mlxf {
 namespace {
@@ -21,11 +29,11 @@ struct Layout {
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-// The zero-initialised head of the workspace, at offsets that do not depend on
-// the shape (so one workspace serves calls of every shape): per-row gathered-
-// candidate counters (65536 32-bit words) and the stage-list counts.  A
-// decide kernel clears the candidate counters it read; the first kernel of a
-// call clears the stage-list counts.
+// The head of the workspace, at offsets that do not depend on the shape: per-row
+// gathered-candidate counters (65536 32-bit words) and the stage-list counts.
+// The first kernel of every call clears the stage-list counts and the counters
+// of its rows, so a workspace needs no initialisation and a call never depends
+// on what an earlier (possibly failed) call left behind.
 constexpr size_t ROWS_MAX = 65536;
 constexpr size_t CTR_BYTES_MAX = ROWS_MAX * sizeof(unsigned int) + 256;
 
@@ -250,6 +258,44 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
   }
 }
 
+// Device address of `scratch` on the GPU that runs `stream` (the current
+// device for the null stream), looked up once per GPU with that GPU current.
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+int noalloc_scratch(void* stream, void** out, char** err) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  int dev = cur;
+  if (e == hipSuccess && stream) e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev);
+  if (e != hipSuccess) {
+    set_err(err, std::string("mlxf: cannot find the stream's device: ") + hipGetErrorString(e));
+    return MLXF_EHIP;
+  }
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+    set_err(err, "mlxf: device index beyond the allocation-free entry point's table");
+    return MLXF_EINVAL;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) {
+      set_err(err, std::string("mlxf: hipSetDevice failed: ") + hipGetErrorString(e));
+      return MLXF_EHIP;
+    }
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p) {
+      set_err(err, std::string("mlxf: hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+      return MLXF_EHIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MLXF_OK;
+}
+
 }  // namespace
 }  // namespace mlxf
 
@@ -337,6 +383,41 @@ int mlxf_sample_ex(const void* d_logits, int dtype, int B, int V, int64_t row_st
   return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p, d_min_p,
                     d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
                     d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, refine_stages, err);
+}
+
+int mlxf_sample_noalloc(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                        const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                        const float* d_min_p, const int32_t* d_top_logprobs, const float* d_uniforms,
+                        int32_t* d_out_ids, float* d_out_logprobs, int32_t* d_out_top_ids,
+                        float* d_out_top_logprobs, int K_max, int refine_stages, void* stream,
+                        char** err) {
+  try {
+    if (refine_stages < 0) {
+      set_err(err, "mlxf: refine_stages must be in [0, 3]");
+      return MLXF_EINVAL;
+    }
+    int rc = check_shape(B, V, K_max, dtype, err);
+    if (rc) return rc;
+    const size_t need = make_layout(B, V, K_max).total;
+    if (need > MLXF_NOALLOC_SCRATCH_BYTES) {
+      set_err(err, "mlxf: mlxf_sample_noalloc: this shape needs " + std::to_string(need) +
+                       " bytes of scratch, more than its fixed " +
+                       std::to_string(static_cast<size_t>(MLXF_NOALLOC_SCRATCH_BYTES)) +
+                       "; use mlxf_sample_ex with a workspace");
+      return MLXF_EWORKSPACE;
+    }
+    if (B == 0) return MLXF_OK;
+    void* ws = nullptr;
+    rc = mlxf::noalloc_scratch(stream, &ws, err);
+    if (rc) return rc;
+    return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p, d_min_p,
+                      d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
+                      d_out_top_logprobs, K_max, ws, MLXF_NOALLOC_SCRATCH_BYTES, stream, refine_stages,
+                      err);
+  } catch (...) {
+    set_err(err, "mlxf: unexpected exception");
+    return MLXF_EINVAL;
+  }
 }
 
 int mlxf_sampler_first_pass(const void* d_logits, int dtype, int B, int V, int64_t row_stride,

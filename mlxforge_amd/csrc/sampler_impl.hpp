@@ -432,8 +432,11 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
   const int S = a.S;
   const int r = bid / S, s = bid - r * S;
   // a new call: the stage lists of the previous call (whatever number of stages
-  // it launched) are spent
+  // it launched) are spent, and the row's gathered-candidate counter starts
+  // at zero (it is first used by a later kernel), so the workspace needs no
+  // initialisation and no call depends on what the previous one left
   if (bid == 0 && tid < NSTAGE) a.actcnt[tid] = 0u;
+  if (tid == 0 && s == 0) a.ncand[r] = 0u;
   const Mode md = decode<DT>(a, r);
   const void* row = row_ptr<DT>(a, r);
   const int beg = s * a.L;
