@@ -1,0 +1,781 @@
+#pragma once
+// rowhist.hpp -- the row-histogram path for bf16 logits: one 1024-thread
+// workgroup per row reads the row once and counts it into exact per-value
+// histograms in LDS, from which every selection of Sampler::sample
+// (src/sample/sampler.cpp:141-166) follows without touching the logits
+// again; only the draw re-reads one quarter of the row.
+//
+// Why it is exact: for bf16 logits, z' = round_bf16(z / T), the weight
+// w = exp2(fma(z', log2 e, -RN(max z' log2 e))) and its fixed-point mass
+// floor(w 2^40) are functions of the 16-bit value alone.  So the count of
+// each distinct value is all the top-k count, the nucleus mass and min_p need:
+// a bin's mass is count x mass(value), an exact integer, and every cutoff is
+// found on the bins with the same integers the per-element path sums.
+//
+// Bins.  A bin is one bf16 value with magnitude in [2^-28, 2^8) (36 binades of
+// 128 values per sign), plus three merged bins: |z| < 2^-28 ("tiny", which
+// holds +-0), z <= -256 (with -inf and negative NaNs) and z >= 256 (with +inf
+// and positive NaNs).  A merged bin has one weight only when its elements'
+// z' cannot be told apart by the weight function: the tiny bin when |z' log2 e|
+// stays below half an ulp of the weight's offset, the low bin when its weight
+// rounds to a zero mass.  The row is split into four contiguous chunks with a
+// histogram each (4 x 9220 32-bit counters, 144 KB of LDS), so per-chunk kept
+// masses locate the draw to one chunk, which the walk then reads.
+//
+// Rows the bins cannot decide exactly -- the maximum in a merged bin (a
+// logit >= 256, +inf, a positive NaN, or a row of values all within 2^-28 of
+// zero or below -256), a cutoff that falls in or next to a merged bin, or a
+// merged bin whose elements' weights differ -- are flagged, and k_rowfb runs
+// the per-slice path for them.
+//
+// Memory per row: one read of the row (V * 2 bytes) in pass 1, a quarter row
+// in the draw.  No MFMA: nothing here is a dense contraction.
+
+namespace mlxf {
+
+// Per-call constants of the row-histogram path.
+struct RhArgs {
+  int ipc;                   // pass-1 iterations per chunk (chunk length ipc * 8192 logits)
+  int nfull;                 // iterations wholly inside the row
+  unsigned int* rowflag;     // [B] 1 = the fallback kernel finishes the row
+};
+
+// One bf16 call on the row-histogram path (defined in sampler_bf16.hip).
+hipError_t launch_row16_bf16(const Args& a, int ept, const RhArgs& x, hipStream_t st);
+
+// Per-phase timestamps for a profiling harness that defines MLXF_RH_STAMPS
+// (and the array it writes); no effect otherwise.
+#ifdef MLXF_RH_STAMPS
+#define MLXF_RH_STAMP(i) \
+  if (threadIdx.x == 0) mlxf_rh_stamps[blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime()
+#else
+#define MLXF_RH_STAMP(i)
+#endif
+
+namespace {
+namespace rh {
+
+constexpr int NT = 1024;             // threads per workgroup (16 waves, 4 per SIMD)
+constexpr int NWV = NT / 64;
+constexpr int NWIN = 4608;           // bf16 magnitudes in [2^-28, 2^8): 36 binades x 128
+constexpr int LOMAG = 0x3180;        // bf16 bit pattern of 2^-28
+constexpr int NBIN = 2 * NWIN + 3;   // window bins of both signs + three merged bins
+constexpr int B_NEGHUGE = 0;         // z <= -256, -inf, negative NaN
+constexpr int B_TINY = NWIN + 1;     // |z| < 2^-28, +-0
+constexpr int B_POSHUGE = 2 * NWIN + 2;  // z >= 256, +inf, positive NaN
+constexpr int B_TRASH = NBIN;        // elements past the row end
+constexpr int CHW = NBIN + 1;        // counters per chunk histogram
+constexpr int CHB = CHW * 4;         // bytes per chunk histogram (36880)
+constexpr int NCH = 4;               // chunks per row
+constexpr int ITER = NT * 8;         // elements one pass-1 iteration covers
+constexpr int BPT = 10;              // bins per thread in the deciding step (10 * 1024 >= NBIN)
+// LDS: chunk c's histogram at byte c * CHB.  Pass 1 addresses a counter as
+// page + immediate + 4 * bin with 16-bit packed bin offsets: chunks 0 and 1 on
+// page 0 (immediates 0 and CHB), chunks 2 and 3 on page 65536 with the
+// offsets raised by 2 * CHB - 65536.
+constexpr unsigned PAGE1 = 65536u;
+constexpr unsigned PAGE1_ADD = 2u * CHB - PAGE1;
+constexpr size_t HIST_BYTES = static_cast<size_t>(NCH) * CHB;
+
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+struct Scratch {
+  unsigned long long u64r[NWV][NCH];
+  double dr[NWV];
+  int ir[NWV][2];
+  unsigned int ur[NWV][NCH];
+  unsigned long long sel64[8];
+  int sel[16];
+};
+constexpr size_t LDS_BYTES = HIST_BYTES + sizeof(Scratch);
+static_assert(LDS_BYTES <= 160 * 1024, "row-histogram LDS exceeds a CU's 160 KB");
+
+// Bins of the two bf16 values of a 32-bit word, packed: b = NWIN - t for a
+// negative value and NWIN + 2 + t for a positive one, t = clamp(magnitude bits
+// - LOMAG, -1, NWIN) (t = -1: tiny, t = NWIN: beyond the window).  Monotone
+// non-decreasing in the value.
+__device__ __forceinline__ unsigned int bins2(unsigned int w) {
+  s16x2 t = __builtin_bit_cast(s16x2, w & 0x7fff7fffu) - (s16x2){static_cast<short>(LOMAG), static_cast<short>(LOMAG)};
+  t = __builtin_elementwise_max(t, (s16x2){-1, -1});
+  t = __builtin_elementwise_min(t, (s16x2){static_cast<short>(NWIN), static_cast<short>(NWIN)});
+  const s16x2 sg = __builtin_bit_cast(s16x2, w) >> (s16x2){15, 15};
+  const s16x2 b = (t ^ sg) + sg + (s16x2){static_cast<short>(NWIN + 2), static_cast<short>(NWIN + 2)};
+  return __builtin_bit_cast(unsigned int, b);
+}
+
+__device__ __forceinline__ unsigned int pkmax_u16(unsigned int a, unsigned int b) {
+  return __builtin_bit_cast(unsigned int,
+                            __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+
+// The bf16 value of a window bin (merged bins: a representative).
+__device__ __forceinline__ float bin_value(int b) {
+  if (b >= 1 && b <= NWIN) return __uint_as_float((0x8000u | static_cast<unsigned>(LOMAG + NWIN - b)) << 16);
+  if (b >= NWIN + 2 && b <= 2 * NWIN + 1) return __uint_as_float(static_cast<unsigned>(LOMAG + b - (NWIN + 2)) << 16);
+  if (b == B_TINY) return 0.0f;
+  return b == B_POSHUGE ? INFINITY : -INFINITY;
+}
+
+// Bin owned by thread tid at slot j of the deciding step: bins in descending
+// order from the top, BPT per thread; negative = none.
+__device__ __forceinline__ int own_bin(int tid, int j) { return NBIN - 1 - (tid * BPT + j); }
+
+// ---- block primitives for NT threads (16 waves)
+template <typename T>
+__device__ __forceinline__ T bsum(T x, T* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  x = wave_sum(x);
+  __syncthreads();
+  if (lane == 0) red[wid] = x;
+  __syncthreads();
+  T t = red[0];
+#pragma unroll
+  for (int w = 1; w < NWV; ++w) t += red[w];
+  return t;
+}
+__device__ __forceinline__ int bmin_i(int x, int* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  x = wave_min(x);
+  __syncthreads();
+  if (lane == 0) red[wid] = x;
+  __syncthreads();
+  int t = red[0];
+#pragma unroll
+  for (int w = 1; w < NWV; ++w) t = min(t, red[w]);
+  return t;
+}
+__device__ __forceinline__ int bmax_i(int x, int* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  x = wave_max(x);
+  __syncthreads();
+  if (lane == 0) red[wid] = x;
+  __syncthreads();
+  int t = red[0];
+#pragma unroll
+  for (int w = 1; w < NWV; ++w) t = max(t, red[w]);
+  return t;
+}
+// Exclusive scan over threads in index order; *total = the block sum.
+template <typename T>
+__device__ __forceinline__ T bscan(T x, T* red, T* total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const T inc = wave_incl_scan_dpp(x);
+  __syncthreads();
+  if (lane == 63) red[wid] = inc;
+  __syncthreads();
+  T off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NWV; ++w) {
+    const T t = red[w];
+    off += w < wid ? t : T(0);
+    tot += t;
+  }
+  *total = tot;
+  return inc - x + off;
+}
+
+// ---- pass 1: one word (two values) into chunk histogram (PAGE, ADD, IMM)
+template <unsigned PAGE, unsigned ADD, unsigned IMM>
+__device__ __forceinline__ void count_word(unsigned char* lds, unsigned int b2) {
+  const u16x2 o = __builtin_bit_cast(u16x2, b2) * (u16x2){4, 4} +
+                  (u16x2){static_cast<unsigned short>(ADD), static_cast<unsigned short>(ADD)};
+  const unsigned int o2 = __builtin_bit_cast(unsigned int, o);
+  const unsigned int a0 = (o2 & 0xffffu) | PAGE;
+  const unsigned int a1 = PAGE ? __builtin_amdgcn_alignbit(PAGE >> 16, o2, 16) : (o2 >> 16);
+  atomicAdd(reinterpret_cast<unsigned int*>(lds + IMM + a0), 1u);
+  atomicAdd(reinterpret_cast<unsigned int*>(lds + IMM + a1), 1u);
+}
+
+template <unsigned PAGE, unsigned ADD, unsigned IMM>
+__device__ __forceinline__ void count_iter(unsigned char* lds, const uint4& q, int it, unsigned int& best,
+                                           int& bestit) {
+  const unsigned int w[4] = {q.x, q.y, q.z, q.w};
+  unsigned int m = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const unsigned int b2 = bins2(w[k]);
+    m = pkmax_u16(m, b2);
+    count_word<PAGE, ADD, IMM>(lds, b2);
+  }
+  const unsigned int mf = max(m & 0xffffu, m >> 16);
+  if (mf > best) {
+    best = mf;
+    bestit = it;
+  }
+}
+
+// One iteration into the histogram of chunk c (wave-uniform).
+__device__ __forceinline__ void count_iter_c(unsigned char* lds, const uint4& q, int it, int c, unsigned int& best,
+                                             int& bestit) {
+  if (c == 0)
+    count_iter<0u, 0u, 0u>(lds, q, it, best, bestit);
+  else if (c == 1)
+    count_iter<0u, 0u, static_cast<unsigned>(CHB)>(lds, q, it, best, bestit);
+  else if (c == 2)
+    count_iter<PAGE1, PAGE1_ADD, 0u>(lds, q, it, best, bestit);
+  else
+    count_iter<PAGE1, PAGE1_ADD, static_cast<unsigned>(CHB)>(lds, q, it, best, bestit);
+}
+
+// The iteration the row ends in (ITER * it < V < ITER * (it + 1)): elements
+// past the end count in the trash slot and not towards the maximum.
+__device__ __forceinline__ void count_tail(unsigned char* lds, const unsigned short* row, int V, int it, int c,
+                                           unsigned int& best, int& bestit) {
+  const int p0 = it * ITER + static_cast<int>(threadIdx.x) * 8;
+  unsigned int w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const unsigned int lo = p0 + 2 * k < V ? row[p0 + 2 * k] : 0u;
+    const unsigned int hi = p0 + 2 * k + 1 < V ? row[p0 + 2 * k + 1] : 0u;
+    w[k] = lo | (hi << 16);
+  }
+  unsigned int m = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    unsigned int b2 = bins2(w[k]);
+    const bool vlo = p0 + 2 * k < V, vhi = p0 + 2 * k + 1 < V;
+    m = pkmax_u16(m, (vlo ? (b2 & 0xffffu) : 0u) | (vhi ? (b2 & 0xffff0000u) : 0u));
+    b2 = (vlo ? (b2 & 0xffffu) : static_cast<unsigned>(B_TRASH)) |
+         (vhi ? (b2 & 0xffff0000u) : (static_cast<unsigned>(B_TRASH) << 16));
+    if (c == 0)
+      count_word<0u, 0u, 0u>(lds, b2);
+    else if (c == 1)
+      count_word<0u, 0u, static_cast<unsigned>(CHB)>(lds, b2);
+    else if (c == 2)
+      count_word<PAGE1, PAGE1_ADD, 0u>(lds, b2);
+    else
+      count_word<PAGE1, PAGE1_ADD, static_cast<unsigned>(CHB)>(lds, b2);
+  }
+  const unsigned int mf = max(m & 0xffffu, m >> 16);
+  if (mf > best && p0 < V) {
+    best = mf;
+    bestit = it;
+  }
+}
+
+// Pass 1 over the whole row: D iterations' loads in flight (a register ring;
+// the first D are issued before the histograms are cleared, so the clear
+// overlaps them), chunk c = it / ipc.
+template <int D>
+__device__ __forceinline__ void count_row(unsigned char* lds, const unsigned short* row, int V, int ipc, int nfull,
+                                          unsigned int& best, int& bestit) {
+  const int tid = threadIdx.x;
+  const uint4* rv = reinterpret_cast<const uint4*>(row);
+  uint4 buf[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j)
+    if (j < nfull) buf[j] = rv[static_cast<size_t>(j) * NT + tid];
+  {
+    uint4* h4 = reinterpret_cast<uint4*>(lds);
+    for (int i = tid; i < NCH * CHW / 4; i += NT) h4[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  __syncthreads();
+  for (int it = 0; it < nfull; it += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int i = it + j;
+      if (i < nfull) {
+        const uint4 q = buf[j];
+        if (i + D < nfull) buf[j] = rv[static_cast<size_t>(i + D) * NT + tid];
+        const int c = (i >= ipc) + (i >= 2 * ipc) + (i >= 3 * ipc);
+        count_iter_c(lds, q, i, c, best, bestit);
+      }
+    }
+  }
+  if (nfull * ITER < V) {
+    const int c = (nfull >= ipc) + (nfull >= 2 * ipc) + (nfull >= 3 * ipc);
+    count_tail(lds, row, V, nfull, c, best, bestit);
+  }
+}
+
+__device__ __forceinline__ unsigned int hcount(const unsigned int* hist, int c, int b) {
+  return hist[c * CHW + b];
+}
+
+// The row's kept set after top-k, top-p and min_p, on the bins: every bin
+// >= kb whole, plus (when t > 0) the first t elements in index order of the
+// tie group [glo, ghi] (one z' value) below it.
+struct Kept {
+  int kb, glo, ghi;
+  unsigned int t;
+  unsigned long long wt;
+};
+
+}  // namespace rh
+
+constexpr int RH_DEPTH = 6;  // pass-1 iterations in flight per thread (96 KB per workgroup)
+
+template <int DT>
+__global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
+  using namespace rh;
+  extern __shared__ __align__(16) unsigned char lds[];
+  unsigned int* hist = reinterpret_cast<unsigned int*>(lds);
+  Scratch& sc = *reinterpret_cast<Scratch*>(lds + HIST_BYTES);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int r = static_cast<int>(blockIdx.x);
+  const int V = a.V;
+  const Mode md = decode<DT>(a, r);
+  const unsigned short* row = static_cast<const unsigned short*>(row_ptr<DT>(a, r));
+
+  MLXF_RH_STAMP(0);
+  // ---- pass 1: every element counted once
+  unsigned int best = 0u;
+  int bestit = -1;
+  count_row<RH_DEPTH>(lds, row, V, x.ipc, x.nfull, best, bestit);
+  __syncthreads();
+  MLXF_RH_STAMP(1);
+
+  // ---- the row maximum (its bin); its lowest index only for greedy rows
+  const int bmax = bmax_i(static_cast<int>(best), &sc.ir[0][0]);
+  bool fb = bmax == B_POSHUGE || bmax == B_TINY || bmax == B_NEGHUGE;
+  const float M = bin_value(bmax);
+  int id = -1;
+  if (!md.sampling) {
+    int myarg = INT_MAX;
+    if (static_cast<int>(best) == bmax && bestit >= 0) {
+      const int p0 = bestit * ITER + tid * 8;
+      for (int j = 0; j < 8 && myarg == INT_MAX; j += 2) {
+        const unsigned int lo = p0 + j < V ? row[p0 + j] : 0u;
+        const unsigned int hi = p0 + j + 1 < V ? row[p0 + j + 1] : 0u;
+        const unsigned int b2 = bins2(lo | (hi << 16));
+        if (p0 + j < V && static_cast<int>(b2 & 0xffffu) == bmax)
+          myarg = p0 + j;
+        else if (p0 + j + 1 < V && static_cast<int>(b2 >> 16) == bmax)
+          myarg = p0 + j + 1;
+      }
+    }
+    id = bmin_i(myarg, &sc.ir[0][0]);
+    fb = fb || id == INT_MAX;
+  }
+
+  // the thread's bins (descending from the top) and their counts
+  int cnt[BPT];
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    const int b = own_bin(tid, j);
+    cnt[j] = b >= 0 ? static_cast<int>(hcount(hist, 0, b) + hcount(hist, 1, b) + hcount(hist, 2, b) +
+                                        hcount(hist, 3, b))
+                    : 0;
+  }
+
+  // ---- log-sum-exp of the unscaled row from the counts
+  double lse = static_cast<double>(NAN);
+  if (md.need_lse && !fb) {
+    double part = 0.0;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const int b = own_bin(tid, j);
+      if (cnt[j] > 0 && b > B_NEGHUGE) part += static_cast<double>(cnt[j]) * static_cast<double>(wexp(bin_value(b), M));
+    }
+    lse = static_cast<double>(M) + log(bsum(part, sc.dr));
+  }
+  MLXF_RH_STAMP(2);
+
+  if (md.sampling && !fb) {
+    const float Mp = zdiv<DT>(M, md.Tr, md.y, false);
+    const float nc = -(Mp * LOG2E);
+    // every window value is in the fast division's range (2^-96 <= |z| < 2^100)
+    const bool fast = !md.tslow;
+    // z' of a bin: -inf for the low bin (its mass is zero, checked below), 0
+    // for the tiny bin (its elements' weights are equal, checked below)
+    auto zp_of = [&](int b) -> float {
+      if (b <= B_NEGHUGE || b >= B_POSHUGE) return -INFINITY;
+      return b == B_TINY ? 0.0f : zdiv<DT>(bin_value(b), md.Tr, md.y, fast);
+    };
+    auto q_of = [&](float z) -> unsigned long long { return z == -INFINITY ? 0ull : q40(wfun(z, Mp, nc, false)); };
+    if (tid == 0) {
+      bool bad = !__builtin_isfinite(Mp);
+      if (!bad && hcount(hist, 0, B_TINY) + hcount(hist, 1, B_TINY) + hcount(hist, 2, B_TINY) +
+                          hcount(hist, 3, B_TINY) > 0u) {
+        // |z'| of a tiny value is below 2^-28 / T (rounded up by the bf16
+        // rounding); the weight's log2 offset nc must absorb it
+        const float zb = 0x1p-28f / md.Tr * 1.0078125f;
+        const int e = nc == 0.0f ? -1000 : ilogbf(nc);
+        bad = !(zb * LOG2E * 1.0001f < ldexpf(1.0f, e - 24));
+      }
+      if (!bad && hcount(hist, 0, B_NEGHUGE) + hcount(hist, 1, B_NEGHUGE) + hcount(hist, 2, B_NEGHUGE) +
+                          hcount(hist, 3, B_NEGHUGE) > 0u) {
+        // the largest value of the low bin, -256, must carry no mass
+        bad = q40(wfun(zdiv<DT>(-256.0f, md.Tr, md.y, false), Mp, nc, false)) != 0ull;
+      }
+      sc.sel[0] = bad ? 1 : 0;
+      sc.sel[3] = -1;
+      sc.sel[4] = -1;
+      sc.sel[5] = 0;
+      sc.sel[6] = INT_MAX;
+    }
+    __syncthreads();
+    fb = sc.sel[0] != 0;
+    MLXF_RH_STAMP(3);
+
+    // The tie group of bin bb: the run of adjacent bins with z' == z'(bb) (z'
+    // is monotone in z).  Every wave finds it by itself, 64 bins per step.
+    auto group_of = [&](int bb, int* glo, int* ghi) {
+      const float zb = zp_of(bb);
+      int lo = bb, hi = bb;
+      for (;;) {
+        const int b = lo - 1 - lane;
+        const unsigned long long m = __ballot(b >= 0 && zp_of(b) == zb);
+        const int run = m == ~0ull ? 64 : __ffsll(static_cast<long long>(~m)) - 1;
+        lo -= run;
+        if (run < 64) break;
+      }
+      for (;;) {
+        const int b = hi + 1 + lane;
+        const unsigned long long m = __ballot(b < NBIN && zp_of(b) == zb);
+        const int run = m == ~0ull ? 64 : __ffsll(static_cast<long long>(~m)) - 1;
+        hi += run;
+        if (run < 64) break;
+      }
+      *glo = lo;
+      *ghi = hi;
+    };
+    // a group at or next to a merged bin cannot be ordered exactly
+    auto near_merged = [](int glo, int ghi) {
+      return glo <= B_NEGHUGE + 1 || (glo <= B_TINY + 1 && ghi >= B_TINY - 1) || ghi >= B_POSHUGE - 1;
+    };
+
+    Kept kp;
+    kp.kb = 0;
+    kp.glo = 0;
+    kp.ghi = -1;
+    kp.t = 0u;
+    kp.wt = 0ull;
+    // top-k: the k'-th largest z' counting multiplicity; its ties are kept
+    int klo = 0;
+    if (!fb && md.kk > 0) {
+      int csum = 0;
+#pragma unroll
+      for (int j = 0; j < BPT; ++j) csum += cnt[j];
+      int ctot;
+      int run = bscan(csum, &sc.ir[0][0], &ctot);
+#pragma unroll
+      for (int j = 0; j < BPT; ++j) {
+        if (cnt[j] > 0 && run < md.kk && run + cnt[j] >= md.kk) sc.sel[3] = own_bin(tid, j);
+        run += cnt[j];
+      }
+      __syncthreads();
+      const int bk = sc.sel[3];
+      int glo = 0, ghi = 0;
+      if (bk >= 0) group_of(bk, &glo, &ghi);
+      fb = bk < 0 || near_merged(glo, ghi);
+      klo = glo;
+      kp.kb = glo;
+    }
+    MLXF_RH_STAMP(4);
+    // top-p over the top-k survivors: keep while the mass before an element
+    // (in z' desc, index asc order) is below ceil(p * W)
+    if (!fb && md.topp) {
+      // mass of the thread's slot j (recomputed where needed: registers are
+      // scarce at 1024 threads)
+      auto mass = [&](int j) -> unsigned long long {
+        const int b = own_bin(tid, j);
+        return (b >= klo && cnt[j] > 0) ? static_cast<unsigned long long>(cnt[j]) * q_of(zp_of(b)) : 0ull;
+      };
+      unsigned long long msum = 0ull;
+#pragma unroll
+      for (int j = 0; j < BPT; ++j) msum += mass(j);
+      unsigned long long Wk;
+      const unsigned long long run = bscan(msum, &sc.u64r[0][0], &Wk);
+      unsigned long long PW = static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
+      if (PW < 1ull) PW = 1ull;
+      {
+        unsigned long long rr = run;
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) {
+          const unsigned long long mj = mass(j);
+          if (mj > 0ull && rr < PW && rr + mj >= PW) sc.sel[4] = own_bin(tid, j);
+          rr += mj;
+        }
+      }
+      __syncthreads();
+      const int bp = sc.sel[4];
+      int glo = 0, ghi = 0;
+      if (bp >= 0) group_of(bp, &glo, &ghi);
+      fb = bp < 0 || near_merged(glo, ghi);
+      if (!fb) {
+        // the mass above the group (from the owner of its top bin) and the
+        // group's elements
+        unsigned long long rr = run;
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) {
+          const int b = own_bin(tid, j);
+          if (b == ghi) sc.sel64[2] = rr;
+          if (b >= glo && b <= ghi && cnt[j] > 0) atomicAdd(&sc.sel[5], cnt[j]);
+          rr += mass(j);
+        }
+        __syncthreads();
+        const unsigned long long above = sc.sel64[2];
+        const unsigned int gcnt = static_cast<unsigned int>(sc.sel[5]);
+        const unsigned long long wt = q_of(zp_of(bp));
+        const unsigned int t = ties_kept(PW > above ? PW - above : 0ull, wt, gcnt);
+        if (t >= gcnt) {
+          kp.kb = glo;  // the whole group is kept
+        } else {
+          kp.kb = ghi + 1;
+          kp.glo = glo;
+          kp.ghi = ghi;
+          kp.t = t;
+          kp.wt = wt;
+        }
+      }
+    }
+    MLXF_RH_STAMP(5);
+    // min_p, after top-p: the weights that reach min_p times the max's
+    if (!fb && md.mr > 0.0f) {
+      const float thr = minp_thr(md.mr, Mp, nc, false);
+      int lo = INT_MAX;
+#pragma unroll
+      for (int j = 0; j < BPT; ++j) {
+        const int b = own_bin(tid, j);
+        const float z = zp_of(b);
+        if (z != -INFINITY && wfun(z, Mp, nc, false) >= thr) lo = min(lo, b);
+      }
+      lo = wave_min(lo);
+      if (lane == 0 && lo != INT_MAX) atomicMin(&sc.sel[6], lo);
+      __syncthreads();
+      const int bm = sc.sel[6];
+      const int low_kept = kp.t > 0u ? kp.glo : kp.kb;  // lowest bin with a kept element
+      if (bm > low_kept) {
+        kp.kb = max(kp.kb, bm);
+        kp.t = 0u;
+      }
+    }
+    MLXF_RH_STAMP(6);
+
+    if (!fb) {
+      // ---- per-chunk kept masses and the chunk holding u * W
+      unsigned long long kc[NCH];
+      unsigned int gc[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        kc[c] = 0ull;
+        gc[c] = 0u;
+      }
+#pragma unroll
+      for (int j = 0; j < BPT; ++j) {
+        const int b = own_bin(tid, j);
+        if (b < 0 || cnt[j] == 0) continue;
+        if (b >= kp.kb) {
+          const unsigned long long qq = q_of(zp_of(b));
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) kc[c] += static_cast<unsigned long long>(hcount(hist, c, b)) * qq;
+        } else if (kp.t > 0u && b >= kp.glo && b <= kp.ghi) {
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) gc[c] += hcount(hist, c, b);
+        }
+      }
+      const int wid = tid >> 6;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        kc[c] = wave_sum(kc[c]);
+        gc[c] = static_cast<unsigned int>(wave_sum(static_cast<int>(gc[c])));
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          sc.u64r[wid][c] = kc[c];
+          sc.ur[wid][c] = gc[c];
+        }
+      }
+      __syncthreads();
+      if (wid == 0) {
+        // lane c < NCH: chunk c's kept mass; the first t ties in index order
+        // are spread over the chunks in order
+        unsigned long long K = 0ull;
+        int G = 0;
+        if (lane < NCH) {
+#pragma unroll
+          for (int w2 = 0; w2 < NWV; ++w2) {
+            K += sc.u64r[w2][lane];
+            G += static_cast<int>(sc.ur[w2][lane]);
+          }
+        }
+        const int before = wave_incl_scan_dpp(G) - G;
+        const unsigned int want = kp.t > static_cast<unsigned>(before) ? kp.t - static_cast<unsigned>(before) : 0u;
+        const unsigned int tk = want < static_cast<unsigned>(G) ? want : static_cast<unsigned>(G);
+        K += static_cast<unsigned long long>(tk) * kp.wt;
+        const unsigned long long cumi = wave_incl_scan_dpp(K);
+        const unsigned long long W = rdl(cumi, 63);
+        unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(W));
+        if (W == 0ull)
+          Tu = 0ull;
+        else if (Tu >= W)
+          Tu = W - 1ull;
+        const unsigned long long hit = __ballot(lane < NCH && K > 0ull && cumi > Tu);
+        const int cs = hit ? __ffsll(static_cast<long long>(hit)) - 1 : -1;
+        if (lane == 0) {
+          sc.sel[1] = cs;
+          sc.sel[2] = cs >= 0 ? static_cast<int>(rdl(tk, cs)) : 0;
+          sc.sel64[0] = cs >= 0 ? Tu - (rdl(cumi, cs) - rdl(K, cs)) : 0ull;
+        }
+      }
+      __syncthreads();
+      const int cs = sc.sel[1];
+      const unsigned int tkc = static_cast<unsigned int>(sc.sel[2]);
+      const unsigned long long rem = sc.sel64[0];
+      fb = cs < 0;
+      MLXF_RH_STAMP(7);
+      if (!fb) {
+        // ---- the walk over chunk cs: thread t holds its EPTW consecutive
+        // elements; their loads are issued before the weight table is built
+        const int CL = x.ipc * ITER;
+        const int EPTW = x.ipc * 8;
+        const int c0 = cs * CL + tid * EPTW;
+        const bool partial = kp.t > 0u;
+        const unsigned int span = static_cast<unsigned>(kp.ghi - kp.glo);
+        constexpr int WG = 4;  // 16-byte loads in flight per thread
+        unsigned long long km = 0ull;
+        int gt = 0;
+        bool table = false;
+        for (int g0 = 0; g0 < EPTW; g0 += 8 * WG) {
+          uint4 wq[WG];
+#pragma unroll
+          for (int k = 0; k < WG; ++k) {
+            const int p = c0 + g0 + 8 * k;
+            if (g0 + 8 * k < EPTW && p + 8 <= V) {
+              wq[k] = *reinterpret_cast<const uint4*>(row + p);
+            } else {
+              unsigned int w4[4];
+#pragma unroll
+              for (int h = 0; h < 4; ++h) {
+                const bool in0 = g0 + 8 * k < EPTW && p + 2 * h < V, in1 = g0 + 8 * k < EPTW && p + 2 * h + 1 < V;
+                w4[h] = (in0 ? static_cast<unsigned int>(row[p + 2 * h]) : 0u) |
+                        ((in1 ? static_cast<unsigned int>(row[p + 2 * h + 1]) : 0u) << 16);
+              }
+              wq[k] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+            }
+          }
+          if (!table) {
+            // the weight table over the dead histograms: each wholly kept
+            // bin's mass (low and high 32-bit halves), 0 for every other bin
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < BPT; ++j) {
+              const int b = own_bin(tid, j);
+              if (b < 0) continue;
+              const unsigned long long mq = b >= kp.kb ? q_of(zp_of(b)) : 0ull;
+              hist[b] = static_cast<unsigned int>(mq);
+              hist[CHW + b] = static_cast<unsigned int>(mq >> 32);
+            }
+            if (tid == 0) {
+              hist[B_TRASH] = 0u;
+              hist[CHW + B_TRASH] = 0u;
+            }
+            __syncthreads();
+            table = true;
+          }
+#pragma unroll
+          for (int k = 0; k < WG; ++k) {
+            const int p = c0 + g0 + 8 * k;
+            const unsigned int w4[4] = {wq[k].x, wq[k].y, wq[k].z, wq[k].w};
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+              unsigned int b2 = bins2(w4[h]);
+              if (!(g0 + 8 * k < EPTW && p + 2 * h < V)) b2 = (b2 & 0xffff0000u) | static_cast<unsigned>(B_TRASH);
+              if (!(g0 + 8 * k < EPTW && p + 2 * h + 1 < V))
+                b2 = (b2 & 0xffffu) | (static_cast<unsigned>(B_TRASH) << 16);
+              const unsigned int o0 = (b2 & 0xffffu) * 4u, o1 = (b2 >> 16) * 4u;
+              km += (static_cast<unsigned long long>(*reinterpret_cast<const unsigned int*>(lds + CHB + o0)) << 32 |
+                     *reinterpret_cast<const unsigned int*>(lds + o0)) +
+                    (static_cast<unsigned long long>(*reinterpret_cast<const unsigned int*>(lds + CHB + o1)) << 32 |
+                     *reinterpret_cast<const unsigned int*>(lds + o1));
+              if (partial)
+                gt += ((b2 & 0xffffu) - static_cast<unsigned>(kp.glo) <= span ? 1 : 0) +
+                      ((b2 >> 16) - static_cast<unsigned>(kp.glo) <= span ? 1 : 0);
+            }
+          }
+        }
+        MLXF_RH_STAMP(8);
+        int gex = 0;
+        if (partial) {
+          int gtot;
+          gex = bscan(gt, &sc.ir[0][0], &gtot);
+          const unsigned int kt = tkc > static_cast<unsigned>(gex)
+                                      ? min(tkc - static_cast<unsigned>(gex), static_cast<unsigned>(gt))
+                                      : 0u;
+          km += static_cast<unsigned long long>(kt) * kp.wt;
+        }
+        if (tid == 0) sc.sel[7] = -1;
+        unsigned long long ktot;
+        const unsigned long long kex = bscan(km, &sc.u64r[0][0], &ktot);
+        if (km > 0ull && kex <= rem && rem < kex + km) {
+          sc.sel[7] = tid;
+          sc.sel[8] = gex;
+          sc.sel64[1] = rem - kex;
+        }
+        __syncthreads();
+        MLXF_RH_STAMP(9);
+        const int holder = sc.sel[7];
+        if (holder >= 0 && tid < 64) {
+          // wave 0 walks the holder's elements, one per lane per round
+          const int hbase = cs * CL + holder * EPTW;
+          const unsigned long long hrem = sc.sel64[1];
+          unsigned int tie_rank = static_cast<unsigned int>(sc.sel[8]);
+          unsigned long long carry = 0ull;
+          int found = -1;
+          for (int e0 = 0; e0 < EPTW && found < 0; e0 += 64) {
+            const int p = hbase + e0 + lane;
+            const bool valid = e0 + lane < EPTW && p < V;
+            const unsigned int bits = valid ? row[p] : 0u;
+            const int b = valid ? static_cast<int>(bins2(bits) & 0xffffu) : B_TRASH;
+            unsigned long long mm = static_cast<unsigned long long>(hist[b]) |
+                                    (static_cast<unsigned long long>(hist[CHW + b]) << 32);
+            if (partial) {
+              const bool tie = valid && b >= kp.glo && b <= kp.ghi;
+              const unsigned long long tb = __ballot(tie);
+              const unsigned int rk = tie_rank + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(tb >> 32),
+                                                                          __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(tb), 0u));
+              if (tie && rk < tkc) mm = kp.wt;
+              tie_rank += static_cast<unsigned int>(__builtin_popcountll(tb));
+            }
+            const unsigned long long c = carry + wave_incl_scan_dpp(mm);
+            const int pk = wave_min((mm > 0ull && c > hrem) ? p : INT_MAX);
+            if (pk != INT_MAX) found = pk;
+            carry = rdl(c, 63);
+          }
+          if (lane == 0) sc.sel[9] = found;
+        }
+        __syncthreads();
+        id = holder >= 0 ? sc.sel[9] : -1;
+        fb = id < 0;
+      }
+    }
+  }
+  MLXF_RH_STAMP(10);
+  if (tid == 0) {
+    x.rowflag[r] = fb ? 1u : 0u;
+    if (!fb) write_out<DT>(a, r, id, lse, md.want_lp);
+  }
+}
+
+// One call on the row-histogram path: k_row16 over every row, then the
+// per-slice path (first pass and deciding step in one workgroup) for the rows
+// it flagged.
+template <int DT, int EPT>
+hipError_t launch_row16(const Args& a, const RhArgs& x, hipStream_t st) {
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_row16<DT>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     static_cast<int>(rh::LDS_BYTES));
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((k_row16<DT>), dim3(static_cast<unsigned int>(a.B)), dim3(rh::NT), rh::LDS_BYTES, st, a, x);
+  hipLaunchKernelGGL((k_rowfb<DT, EPT, true>), dim3(static_cast<unsigned int>(a.B < 64 ? a.B : 64)), dim3(THREADS), 0, st, a,
+                     static_cast<const unsigned int*>(x.rowflag));
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_row16_dt(const Args& a, int ept, const RhArgs& x, hipStream_t st) {
+  switch (ept) {
+    case 8:
+      return launch_row16<DT, 8>(a, x, st);
+    case 16:
+      return launch_row16<DT, 16>(a, x, st);
+    default:
+      return launch_row16<DT, 32>(a, x, st);
+  }
+}
+
+}  // namespace
+}  // namespace mlxf

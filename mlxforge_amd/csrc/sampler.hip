@@ -24,7 +24,7 @@ __global__ void k_zero(unsigned int* p, size_t n) {
 struct Layout {
   int S, L, EPT;
   size_t off_ncand, off_actcnt, off_actlist, off_rec, off_list, off_rowst, off_hcnt, off_hmass, off_above,
-      off_dsum, off_cand, total;
+      off_dsum, off_cand, off_rowflag, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -87,6 +87,8 @@ Layout make_layout(int B, int V, int K_max) {
   o = align256(o + sizeof(unsigned long long) * BS);
   l.off_cand = o;
   o = align256(o + sizeof(unsigned long long) * nb * CAP);
+  l.off_rowflag = o;
+  o = align256(o + sizeof(unsigned int) * nb);
   l.total = o;
   return l;
 }
@@ -161,6 +163,17 @@ int host_refine_stages(int B, int V, int dtype, const float* T, const int32_t* k
     return HINT_STAGES;
   }
   return need;
+}
+
+// bf16 rows with no top_logprobs take the row-histogram path (rowhist.hpp):
+// one workgroup per row counts the row into exact per-value histograms and
+// decides everything from them.  It serves every stage count alike (it has
+// no refine stages), but not the first-pass-only timing call (nst < 0).
+constexpr int ROW_ITER_LOGITS = 1024 * 8;              // logits per pass-1 iteration
+constexpr int ROW_CHUNK_LOGITS = 4 * ROW_ITER_LOGITS;  // logits per chunk iteration count
+constexpr int ROW_MIN_V = 32768;
+bool use_row_path(int dtype, int V, int K_max, bool vecok, int nst) {
+  return dtype == MLXF_DTYPE_BF16 && K_max == 0 && vecok && nst >= 0 && V >= ROW_MIN_V;
 }
 
 int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
@@ -241,7 +254,13 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
     if (!d_temperature && nst > 0) nst = 0;  // every row greedy
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e;
-    if (dtype == MLXF_DTYPE_F32)
+    if (use_row_path(dtype, V, K_max, vecok, nst)) {
+      RhArgs x;
+      x.ipc = (V + ROW_CHUNK_LOGITS - 1) / ROW_CHUNK_LOGITS;
+      x.nfull = V / ROW_ITER_LOGITS;
+      x.rowflag = reinterpret_cast<unsigned int*>(ws + l.off_rowflag);
+      e = launch_row16_bf16(a, l.EPT, x, st);
+    } else if (dtype == MLXF_DTYPE_F32)
       e = launch_f32(a, l.EPT, vecok, nst, st);
     else if (dtype == MLXF_DTYPE_BF16)
       e = launch_bf16(a, l.EPT, vecok, nst, st);

@@ -424,18 +424,15 @@ struct S1Lds {
   int thi;
 };
 
+// Slice s of row r (whole workgroup of THREADS threads).  Also called slice
+// after slice by the fallback kernel of the row-histogram path.
 template <int DT, int EPT, bool VECOK>
-__global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
-  __shared__ S1Lds sh;
+__device__ __forceinline__ void scan1_slice(const Args& a, int r, int s, S1Lds& sh) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int bid = static_cast<int>(blockIdx.x);
   const int S = a.S;
-  const int r = bid / S, s = bid - r * S;
-  // a new call: the stage lists of the previous call (whatever number of stages
-  // it launched) are spent, and the row's gathered-candidate counter starts
-  // at zero (it is first used by a later kernel), so the workspace needs no
-  // initialisation and no call depends on what the previous one left
-  if (bid == 0 && tid < NSTAGE) a.actcnt[tid] = 0u;
+  // the row's gathered-candidate counter starts at zero (it is first used by a
+  // later kernel), so the workspace needs no initialisation and no call
+  // depends on what the previous one left
   if (tid == 0 && s == 0) a.ncand[r] = 0u;
   const Mode md = decode<DT>(a, r);
   const void* row = row_ptr<DT>(a, r);
@@ -651,6 +648,17 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
     rp[1] = pack2(__float_as_uint(zmin), sfl);
     rp[2] = static_cast<unsigned long long>(__double_as_longlong(lse_s));
   }
+}
+
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
+  __shared__ S1Lds sh;
+  const int bid = static_cast<int>(blockIdx.x);
+  const int r = bid / a.S, s = bid - r * a.S;
+  // a new call: the stage lists of the previous call (whatever number of
+  // stages it launched) are spent
+  if (bid == 0 && threadIdx.x < NSTAGE) a.actcnt[threadIdx.x] = 0u;
+  scan1_slice<DT, EPT, VECOK>(a, r, s, sh);
 }
 
 // ============================================================== k_decide1 ==
@@ -1712,12 +1720,13 @@ union D1Shared {
   RLds r;
 };
 
+// Row r after its slices' first pass (whole workgroup): argmax, log-sum-exp,
+// top_logprobs, top-k <= 63, and a plan for every other sampling row, which
+// goes on the first refine stage's list (nstage > 0) or is finished here.
 template <int DT, int EPT, bool VECOK>
-__global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
-  __shared__ D1Shared shu;
+__device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1Shared& shu) {
   D1Lds& sh = shu.d;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int r = static_cast<int>(blockIdx.x);
   const int S = a.S;
   // the slices' lists are requested before the row's parameters say whether
   // they are needed: one memory round trip for everything this kernel reads
@@ -1962,6 +1971,42 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
   serial_finish<DT, EPT, VECOK>(a, r, shu.r);
 }
 
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
+  __shared__ D1Shared shu;
+  decide1_row<DT, EPT, VECOK>(a, static_cast<int>(blockIdx.x), nstage, shu);
+}
+
+// Fallback of the row-histogram path: rows it flagged (rowflag[r] != 0) run
+// the first pass over their slices and the deciding step here, one
+// workgroup per row, finishing every refine level in this workgroup.
+union FbShared {
+  S1Lds s1;
+  D1Shared d1;
+};
+
+// Fallback rows are rare: a small grid strides over the rows, so a call with
+// none costs one short launch.
+template <int DT, int EPT, bool VECOK>
+__global__ __launch_bounds__(THREADS, 1) void k_rowfb(Args a, const unsigned int* rowflag) {
+  __shared__ FbShared sh;
+  for (int r = static_cast<int>(blockIdx.x); r < a.B; r += static_cast<int>(gridDim.x)) {
+    if (rowflag[r] == 0u) continue;
+    for (int s = 0; s < a.S; ++s) {
+      scan1_slice<DT, EPT, VECOK>(a, r, s, sh.s1);
+      __syncthreads();
+    }
+    // this workgroup's slice records and lists are complete; drop stale L1
+    // lines before reading them back
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    decide1_row<DT, EPT, VECOK>(a, r, 0, sh.d1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+}
+
 
 
 // ================================================================ host side ==
@@ -1996,3 +2041,5 @@ hipError_t launch_dt(const Args& a, int ept, bool vecok, int nst, hipStream_t st
 
 }  // namespace
 }  // namespace mlxf
+
+#include "rowhist.hpp"
