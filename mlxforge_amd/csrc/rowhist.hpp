@@ -68,7 +68,8 @@ constexpr int CHW = NBIN + 1;        // counters per chunk histogram
 constexpr int CHB = CHW * 4;         // bytes per chunk histogram (36880)
 constexpr int NCH = 4;               // chunks per row
 constexpr int ITER = NT * 8;         // elements one pass-1 iteration covers
-constexpr int BPT = 10;              // bins per thread in the deciding step (10 * 1024 >= NBIN)
+constexpr int BPT = 11;              // bins per thread in the deciding step (11 * 1024 >= NBIN;
+                                     // an odd stride keeps a wave's LDS accesses on distinct banks)
 // LDS: chunk c's histogram at byte c * CHB.  Pass 1 addresses a counter as
 // page + immediate + 4 * bin with 16-bit packed bin offsets: chunks 0 and 1 on
 // page 0 (immediates 0 and CHB), chunks 2 and 3 on page 65536 with the
@@ -91,17 +92,25 @@ struct Scratch {
 constexpr size_t LDS_BYTES = HIST_BYTES + sizeof(Scratch);
 static_assert(LDS_BYTES <= 160 * 1024, "row-histogram LDS exceeds a CU's 160 KB");
 
-// Bins of the two bf16 values of a 32-bit word, packed: b = NWIN - t for a
-// negative value and NWIN + 2 + t for a positive one, t = clamp(magnitude bits
-// - LOMAG, -1, NWIN) (t = -1: tiny, t = NWIN: beyond the window).  Monotone
-// non-decreasing in the value.
-__device__ __forceinline__ unsigned int bins2(unsigned int w) {
-  s16x2 t = __builtin_bit_cast(s16x2, w & 0x7fff7fffu) - (s16x2){static_cast<short>(LOMAG), static_cast<short>(LOMAG)};
-  t = __builtin_elementwise_max(t, (s16x2){-1, -1});
-  t = __builtin_elementwise_min(t, (s16x2){static_cast<short>(NWIN), static_cast<short>(NWIN)});
+// Bin offsets of the two bf16 values of a 32-bit word, packed signed 16-bit:
+// x = t for a positive value and -t for a negative one, t = clamp(magnitude
+// bits - LOMAG + 1, 0, NWIN + 1) (t = 0: tiny, t = NWIN + 1: beyond the
+// window); the bin is NWIN + 1 + x.  Monotone non-decreasing in the value.
+__device__ __forceinline__ unsigned int binx2(unsigned int w) {
+  u16x2 t = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, w & 0x7fff7fffu),
+                                          (u16x2){static_cast<unsigned short>(LOMAG - 1), static_cast<unsigned short>(LOMAG - 1)});
+  t = __builtin_elementwise_min(t, (u16x2){static_cast<unsigned short>(NWIN + 1), static_cast<unsigned short>(NWIN + 1)});
   const s16x2 sg = __builtin_bit_cast(s16x2, w) >> (s16x2){15, 15};
-  const s16x2 b = (t ^ sg) + sg + (s16x2){static_cast<short>(NWIN + 2), static_cast<short>(NWIN + 2)};
-  return __builtin_bit_cast(unsigned int, b);
+  return __builtin_bit_cast(unsigned int, (__builtin_bit_cast(s16x2, t) ^ sg) - sg);
+}
+// The bins themselves, packed.
+__device__ __forceinline__ unsigned int bins2(unsigned int w) {
+  return __builtin_bit_cast(unsigned int, __builtin_bit_cast(s16x2, binx2(w)) +
+                                              (s16x2){static_cast<short>(NWIN + 1), static_cast<short>(NWIN + 1)});
+}
+__device__ __forceinline__ unsigned int pkmax_i16(unsigned int a, unsigned int b) {
+  return __builtin_bit_cast(unsigned int,
+                            __builtin_elementwise_max(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b)));
 }
 
 __device__ __forceinline__ unsigned int pkmax_u16(unsigned int a, unsigned int b) {
@@ -175,30 +184,34 @@ __device__ __forceinline__ T bscan(T x, T* red, T* total) {
   return inc - x + off;
 }
 
-// ---- pass 1: one word (two values) into chunk histogram (PAGE, ADD, IMM)
+// ---- pass 1: one word (two values, as bin offsets x2) into chunk histogram
+// (PAGE, ADD, IMM)
 template <unsigned PAGE, unsigned ADD, unsigned IMM>
-__device__ __forceinline__ void count_word(unsigned char* lds, unsigned int b2) {
-  const u16x2 o = __builtin_bit_cast(u16x2, b2) * (u16x2){4, 4} +
-                  (u16x2){static_cast<unsigned short>(ADD), static_cast<unsigned short>(ADD)};
+__device__ __forceinline__ void count_word(unsigned char* lds, unsigned int x2) {
+  constexpr unsigned short K = static_cast<unsigned short>(4u * (NWIN + 1) + ADD);
+  const u16x2 o = __builtin_bit_cast(u16x2, x2) * (u16x2){4, 4} + (u16x2){K, K};
   const unsigned int o2 = __builtin_bit_cast(unsigned int, o);
-  const unsigned int a0 = (o2 & 0xffffu) | PAGE;
+  // page 1: the low half's address takes its top bytes from PAGE by a byte
+  // permute (one operation, and IMM stays in the instruction's offset field)
+  const unsigned int a0 = PAGE ? __builtin_amdgcn_perm(PAGE, o2, 0x07060100u) : (o2 & 0xffffu);
   const unsigned int a1 = PAGE ? __builtin_amdgcn_alignbit(PAGE >> 16, o2, 16) : (o2 >> 16);
   atomicAdd(reinterpret_cast<unsigned int*>(lds + IMM + a0), 1u);
   atomicAdd(reinterpret_cast<unsigned int*>(lds + IMM + a1), 1u);
 }
 
+// One iteration (8 values) into a chunk histogram; best / bestit track the
+// largest bin offset and the first iteration holding it.
 template <unsigned PAGE, unsigned ADD, unsigned IMM>
-__device__ __forceinline__ void count_iter(unsigned char* lds, const uint4& q, int it, unsigned int& best,
-                                           int& bestit) {
+__device__ __forceinline__ void count_iter(unsigned char* lds, const uint4& q, int it, int& best, int& bestit) {
   const unsigned int w[4] = {q.x, q.y, q.z, q.w};
-  unsigned int m = 0;
+  unsigned int m = 0x80008000u;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const unsigned int b2 = bins2(w[k]);
-    m = pkmax_u16(m, b2);
-    count_word<PAGE, ADD, IMM>(lds, b2);
+    const unsigned int x2 = binx2(w[k]);
+    m = pkmax_i16(m, x2);
+    count_word<PAGE, ADD, IMM>(lds, x2);
   }
-  const unsigned int mf = max(m & 0xffffu, m >> 16);
+  const int mf = max(static_cast<int>(static_cast<short>(m & 0xffffu)), static_cast<int>(static_cast<short>(m >> 16)));
   if (mf > best) {
     best = mf;
     bestit = it;
@@ -206,7 +219,7 @@ __device__ __forceinline__ void count_iter(unsigned char* lds, const uint4& q, i
 }
 
 // One iteration into the histogram of chunk c (wave-uniform).
-__device__ __forceinline__ void count_iter_c(unsigned char* lds, const uint4& q, int it, int c, unsigned int& best,
+__device__ __forceinline__ void count_iter_c(unsigned char* lds, const uint4& q, int it, int c, int& best,
                                              int& bestit) {
   if (c == 0)
     count_iter<0u, 0u, 0u>(lds, q, it, best, bestit);
@@ -221,7 +234,7 @@ __device__ __forceinline__ void count_iter_c(unsigned char* lds, const uint4& q,
 // The iteration the row ends in (ITER * it < V < ITER * (it + 1)): elements
 // past the end count in the trash slot and not towards the maximum.
 __device__ __forceinline__ void count_tail(unsigned char* lds, const unsigned short* row, int V, int it, int c,
-                                           unsigned int& best, int& bestit) {
+                                           int& best, int& bestit) {
   const int p0 = it * ITER + static_cast<int>(threadIdx.x) * 8;
   unsigned int w[4];
 #pragma unroll
@@ -230,24 +243,24 @@ __device__ __forceinline__ void count_tail(unsigned char* lds, const unsigned sh
     const unsigned int hi = p0 + 2 * k + 1 < V ? row[p0 + 2 * k + 1] : 0u;
     w[k] = lo | (hi << 16);
   }
-  unsigned int m = 0;
+  constexpr unsigned int XT = static_cast<unsigned>(B_TRASH - (NWIN + 1));
+  int mf = -32768;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    unsigned int b2 = bins2(w[k]);
+    unsigned int x2 = binx2(w[k]);
     const bool vlo = p0 + 2 * k < V, vhi = p0 + 2 * k + 1 < V;
-    m = pkmax_u16(m, (vlo ? (b2 & 0xffffu) : 0u) | (vhi ? (b2 & 0xffff0000u) : 0u));
-    b2 = (vlo ? (b2 & 0xffffu) : static_cast<unsigned>(B_TRASH)) |
-         (vhi ? (b2 & 0xffff0000u) : (static_cast<unsigned>(B_TRASH) << 16));
+    if (vlo) mf = max(mf, static_cast<int>(static_cast<short>(x2 & 0xffffu)));
+    if (vhi) mf = max(mf, static_cast<int>(static_cast<short>(x2 >> 16)));
+    x2 = (vlo ? (x2 & 0xffffu) : XT) | (vhi ? (x2 & 0xffff0000u) : (XT << 16));
     if (c == 0)
-      count_word<0u, 0u, 0u>(lds, b2);
+      count_word<0u, 0u, 0u>(lds, x2);
     else if (c == 1)
-      count_word<0u, 0u, static_cast<unsigned>(CHB)>(lds, b2);
+      count_word<0u, 0u, static_cast<unsigned>(CHB)>(lds, x2);
     else if (c == 2)
-      count_word<PAGE1, PAGE1_ADD, 0u>(lds, b2);
+      count_word<PAGE1, PAGE1_ADD, 0u>(lds, x2);
     else
-      count_word<PAGE1, PAGE1_ADD, static_cast<unsigned>(CHB)>(lds, b2);
+      count_word<PAGE1, PAGE1_ADD, static_cast<unsigned>(CHB)>(lds, x2);
   }
-  const unsigned int mf = max(m & 0xffffu, m >> 16);
   if (mf > best && p0 < V) {
     best = mf;
     bestit = it;
@@ -259,7 +272,7 @@ __device__ __forceinline__ void count_tail(unsigned char* lds, const unsigned sh
 // overlaps them), chunk c = it / ipc.
 template <int D>
 __device__ __forceinline__ void count_row(unsigned char* lds, const unsigned short* row, int V, int ipc, int nfull,
-                                          unsigned int& best, int& bestit) {
+                                          int& best, int& bestit) {
   const int tid = threadIdx.x;
   const uint4* rv = reinterpret_cast<const uint4*>(row);
   uint4 buf[D];
@@ -302,6 +315,66 @@ struct Kept {
   unsigned long long wt;
 };
 
+// The walk's per-thread sum over its EPTW consecutive elements from c0: the
+// kept mass from the weight table (low 56 bits; masses stay far below 2^56:
+// at most 128 elements of at most 2^41 each), and with PARTIAL the count
+// of the partial tie group's elements (top 8 bits; at most 128 per thread).
+// The first WG 16-byte words come preloaded (requested before the weight
+// table was built).
+template <bool PARTIAL, int WG>
+__device__ __forceinline__ unsigned long long walk_sum(const unsigned short* row, int V, int c0, int EPTW,
+                                                       const unsigned long long* tab, const Kept& kp,
+                                                       const uint4 (&wq0)[WG], bool whole) {
+  unsigned long long km = 0ull;
+  int gt = 0;
+  const unsigned int span = static_cast<unsigned>(kp.ghi - kp.glo);
+  auto add_word = [&](unsigned int b2) {
+    const unsigned int b0 = b2 & 0xffffu, b1 = b2 >> 16;
+    km += tab[b0] + tab[b1];
+    if (PARTIAL) gt += (b0 - static_cast<unsigned>(kp.glo) <= span ? 1 : 0) + (b1 - static_cast<unsigned>(kp.glo) <= span ? 1 : 0);
+  };
+  if (whole) {
+    // the first WG words came preloaded; the rest (long rows) in groups
+    const uint4* rv = reinterpret_cast<const uint4*>(row + c0);
+#pragma unroll
+    for (int k = 0; k < WG; ++k) {
+      if (k < EPTW / 8) {
+        add_word(bins2(wq0[k].x));
+        add_word(bins2(wq0[k].y));
+        add_word(bins2(wq0[k].z));
+        add_word(bins2(wq0[k].w));
+      }
+    }
+    for (int g0 = WG; g0 < EPTW / 8; g0 += WG) {
+      uint4 wq[WG];
+#pragma unroll
+      for (int k = 0; k < WG; ++k)
+        if (g0 + k < EPTW / 8) wq[k] = rv[g0 + k];
+#pragma unroll
+      for (int k = 0; k < WG; ++k) {
+        if (g0 + k < EPTW / 8) {
+          add_word(bins2(wq[k].x));
+          add_word(bins2(wq[k].y));
+          add_word(bins2(wq[k].z));
+          add_word(bins2(wq[k].w));
+        }
+      }
+    }
+  } else {
+    // the row ends in this thread's range: element by element
+    for (int e = 0; e < EPTW; e += 2) {
+      const int p = c0 + e;
+      const unsigned int lo = p < V ? row[p] : 0u;
+      const unsigned int hi = p + 1 < V ? row[p + 1] : 0u;
+      unsigned int b2 = bins2(lo | (hi << 16));
+      if (p >= V) b2 = (b2 & 0xffff0000u) | static_cast<unsigned>(B_TRASH);
+      if (p + 1 >= V) b2 = (b2 & 0xffffu) | (static_cast<unsigned>(B_TRASH) << 16);
+      add_word(b2);
+    }
+  }
+  return km | (static_cast<unsigned long long>(gt) << 56);
+}
+
 }  // namespace rh
 
 constexpr int RH_DEPTH = 6;  // pass-1 iterations in flight per thread (96 KB per workgroup)
@@ -309,7 +382,7 @@ constexpr int RH_DEPTH = 6;  // pass-1 iterations in flight per thread (96 KB pe
 template <int DT>
 __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
   using namespace rh;
-  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ __align__(16) unsigned char lds[LDS_BYTES];
   unsigned int* hist = reinterpret_cast<unsigned int*>(lds);
   Scratch& sc = *reinterpret_cast<Scratch*>(lds + HIST_BYTES);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -320,20 +393,20 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
 
   MLXF_RH_STAMP(0);
   // ---- pass 1: every element counted once
-  unsigned int best = 0u;
+  int best = -(NWIN + 1) - 1;  // (bin offset; below every bin)
   int bestit = -1;
   count_row<RH_DEPTH>(lds, row, V, x.ipc, x.nfull, best, bestit);
   __syncthreads();
   MLXF_RH_STAMP(1);
 
   // ---- the row maximum (its bin); its lowest index only for greedy rows
-  const int bmax = bmax_i(static_cast<int>(best), &sc.ir[0][0]);
+  const int bmax = bmax_i(best, &sc.ir[0][0]) + NWIN + 1;
   bool fb = bmax == B_POSHUGE || bmax == B_TINY || bmax == B_NEGHUGE;
   const float M = bin_value(bmax);
   int id = -1;
   if (!md.sampling) {
     int myarg = INT_MAX;
-    if (static_cast<int>(best) == bmax && bestit >= 0) {
+    if (best + NWIN + 1 == bmax && bestit >= 0) {
       const int p0 = bestit * ITER + tid * 8;
       for (int j = 0; j < 8 && myarg == INT_MAX; j += 2) {
         const unsigned int lo = p0 + j < V ? row[p0 + j] : 0u;
@@ -383,7 +456,16 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
       if (b <= B_NEGHUGE || b >= B_POSHUGE) return -INFINITY;
       return b == B_TINY ? 0.0f : zdiv<DT>(bin_value(b), md.Tr, md.y, fast);
     };
-    auto q_of = [&](float z) -> unsigned long long { return z == -INFINITY ? 0ull : q40(wfun(z, Mp, nc, false)); };
+    // the weight of each of the thread's bins, 0 for an empty one (a bin's
+    // fixed-point mass is q40 of it)
+    float w[BPT];
+    unsigned long long q[BPT];
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const float z = cnt[j] > 0 ? zp_of(own_bin(tid, j)) : -INFINITY;
+      w[j] = z == -INFINITY ? 0.0f : wfun(z, Mp, nc, false);
+      q[j] = q40(w[j]);
+    }
     if (tid == 0) {
       bool bad = !__builtin_isfinite(Mp);
       if (!bad && hcount(hist, 0, B_TINY) + hcount(hist, 1, B_TINY) + hcount(hist, 2, B_TINY) +
@@ -410,7 +492,8 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
     MLXF_RH_STAMP(3);
 
     // The tie group of bin bb: the run of adjacent bins with z' == z'(bb) (z'
-    // is monotone in z).  Every wave finds it by itself, 64 bins per step.
+    // is monotone in z), found by one wave 64 bins per step.  A group at or
+    // next to a merged bin cannot be ordered exactly (the fallback).
     auto group_of = [&](int bb, int* glo, int* ghi) {
       const float zb = zp_of(bb);
       int lo = bb, hi = bb;
@@ -431,11 +514,20 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
       *glo = lo;
       *ghi = hi;
     };
-    // a group at or next to a merged bin cannot be ordered exactly
     auto near_merged = [](int glo, int ghi) {
       return glo <= B_NEGHUGE + 1 || (glo <= B_TINY + 1 && ghi >= B_TINY - 1) || ghi >= B_POSHUGE - 1;
     };
+    // (whole wave) count of row elements in bins [lo, hi], from the histograms
+    auto count_range = [&](int lo, int hi) -> int {
+      int c = 0;
+      for (int b = lo + lane; b <= hi; b += 64)
+        c += static_cast<int>(hcount(hist, 0, b) + hcount(hist, 1, b) + hcount(hist, 2, b) + hcount(hist, 3, b));
+      return wave_sum(c);
+    };
+    const int wid = tid >> 6;
 
+    // the kept set so far, as published by wave 0 in sc: kb (sel[10]), the
+    // partial group glo, ghi, t (sel[11..13]) and its mass (sel64[3])
     Kept kp;
     kp.kb = 0;
     kp.glo = 0;
@@ -443,109 +535,135 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
     kp.t = 0u;
     kp.wt = 0ull;
     // top-k: the k'-th largest z' counting multiplicity; its ties are kept
-    int klo = 0;
     if (!fb && md.kk > 0) {
       int csum = 0;
 #pragma unroll
       for (int j = 0; j < BPT; ++j) csum += cnt[j];
       int ctot;
-      int run = bscan(csum, &sc.ir[0][0], &ctot);
+      const int run = bscan(csum, &sc.ir[0][0], &ctot);
+      if (run < md.kk && md.kk <= run + csum) {  // the one thread holding the k'-th
+        int rr = run;
 #pragma unroll
-      for (int j = 0; j < BPT; ++j) {
-        if (cnt[j] > 0 && run < md.kk && run + cnt[j] >= md.kk) sc.sel[3] = own_bin(tid, j);
-        run += cnt[j];
+        for (int j = 0; j < BPT; ++j) {
+          if (cnt[j] > 0 && rr < md.kk && rr + cnt[j] >= md.kk) sc.sel[3] = own_bin(tid, j);
+          rr += cnt[j];
+        }
       }
       __syncthreads();
-      const int bk = sc.sel[3];
-      int glo = 0, ghi = 0;
-      if (bk >= 0) group_of(bk, &glo, &ghi);
-      fb = bk < 0 || near_merged(glo, ghi);
-      klo = glo;
-      kp.kb = glo;
+      if (wid == 0) {
+        const int bk = sc.sel[3];
+        int glo = 0, ghi = 0;
+        if (bk >= 0) group_of(bk, &glo, &ghi);
+        if (lane == 0) {
+          sc.sel[10] = glo;
+          sc.sel[0] = (bk < 0 || near_merged(glo, ghi)) ? 1 : 0;
+        }
+      }
+      __syncthreads();
+      kp.kb = sc.sel[10];
+      fb = sc.sel[0] != 0;
     }
+    const int klo = kp.kb;
     MLXF_RH_STAMP(4);
-    // top-p over the top-k survivors: keep while the mass before an element
-    // (in z' desc, index asc order) is below ceil(p * W)
-    if (!fb && md.topp) {
-      // mass of the thread's slot j (recomputed where needed: registers are
-      // scarce at 1024 threads)
-      auto mass = [&](int j) -> unsigned long long {
-        const int b = own_bin(tid, j);
-        return (b >= klo && cnt[j] > 0) ? static_cast<unsigned long long>(cnt[j]) * q_of(zp_of(b)) : 0ull;
-      };
-      unsigned long long msum = 0ull;
+    // top-p over the top-k survivors (keep while the mass before an element,
+    // in z' desc / index asc order, is below ceil(p * W)), and min_p after it
+    // (the weights that reach min_p times the max's; the lowest such occupied
+    // bin, empty bins below it changing nothing); both from one pass over the
+    // bins
+    if (!fb && (md.topp || md.mr > 0.0f)) {
+      const float thr = md.mr > 0.0f ? minp_thr(md.mr, Mp, nc, false) : 0.0f;
+      if (md.mr > 0.0f) {
+        int lo = INT_MAX;
 #pragma unroll
-      for (int j = 0; j < BPT; ++j) msum += mass(j);
-      unsigned long long Wk;
-      const unsigned long long run = bscan(msum, &sc.u64r[0][0], &Wk);
-      unsigned long long PW = static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
-      if (PW < 1ull) PW = 1ull;
-      {
-        unsigned long long rr = run;
+        for (int j = 0; j < BPT; ++j)
+          if (w[j] >= thr && cnt[j] > 0) lo = min(lo, own_bin(tid, j));
+        lo = wave_min(lo);
+        if (lane == 0 && lo != INT_MAX) atomicMin(&sc.sel[6], lo);
+      }
+      unsigned long long PW = 0ull;
+      if (md.topp) {
+        auto mass = [&](int j) -> unsigned long long {
+          return own_bin(tid, j) >= klo ? static_cast<unsigned long long>(cnt[j]) * q[j] : 0ull;
+        };
+        unsigned long long msum = 0ull;
 #pragma unroll
-        for (int j = 0; j < BPT; ++j) {
-          const unsigned long long mj = mass(j);
-          if (mj > 0ull && rr < PW && rr + mj >= PW) sc.sel[4] = own_bin(tid, j);
-          rr += mj;
+        for (int j = 0; j < BPT; ++j) msum += mass(j);
+        unsigned long long Wk;
+        const unsigned long long run = bscan(msum, &sc.u64r[0][0], &Wk);
+        PW = static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
+        if (PW < 1ull) PW = 1ull;
+        if (run < PW && PW <= run + msum) {  // the one thread holding the cutoff
+          unsigned long long rr = run;
+#pragma unroll
+          for (int j = 0; j < BPT; ++j) {
+            const unsigned long long mj = mass(j);
+            if (mj > 0ull && rr < PW && rr + mj >= PW) {
+              sc.sel[4] = own_bin(tid, j);
+              sc.sel64[2] = rr;  // mass of the bins above it
+            }
+            rr += mj;
+          }
         }
       }
       __syncthreads();
-      const int bp = sc.sel[4];
-      int glo = 0, ghi = 0;
-      if (bp >= 0) group_of(bp, &glo, &ghi);
-      fb = bp < 0 || near_merged(glo, ghi);
-      if (!fb) {
-        // the mass above the group (from the owner of its top bin) and the
-        // group's elements
-        unsigned long long rr = run;
-#pragma unroll
-        for (int j = 0; j < BPT; ++j) {
-          const int b = own_bin(tid, j);
-          if (b == ghi) sc.sel64[2] = rr;
-          if (b >= glo && b <= ghi && cnt[j] > 0) atomicAdd(&sc.sel[5], cnt[j]);
-          rr += mass(j);
+      if (wid == 0) {
+        int kb = klo, glo = 0, ghi = -1;
+        unsigned int t = 0u;
+        unsigned long long wt = 0ull;
+        bool bad = false;
+        if (md.topp) {
+          const int bp = sc.sel[4];
+          if (bp >= 0) group_of(bp, &glo, &ghi);
+          bad = bp < 0 || near_merged(glo, ghi);
+          if (!bad) {
+            // the group's bins share one weight: its elements, and the mass
+            // above the group = the mass above bp less the group's bins above bp
+            wt = q40(wfun(zp_of(bp), Mp, nc, false));
+            const unsigned int gcnt = static_cast<unsigned int>(count_range(glo, ghi));
+            const unsigned long long above =
+                sc.sel64[2] - static_cast<unsigned long long>(count_range(bp + 1, ghi)) * wt;
+            t = ties_kept(PW > above ? PW - above : 0ull, wt, gcnt);
+            if (t >= gcnt) {
+              kb = glo;  // the whole group is kept
+              t = 0u;
+            } else {
+              kb = ghi + 1;
+            }
+          }
         }
-        __syncthreads();
-        const unsigned long long above = sc.sel64[2];
-        const unsigned int gcnt = static_cast<unsigned int>(sc.sel[5]);
-        const unsigned long long wt = q_of(zp_of(bp));
-        const unsigned int t = ties_kept(PW > above ? PW - above : 0ull, wt, gcnt);
-        if (t >= gcnt) {
-          kp.kb = glo;  // the whole group is kept
-        } else {
-          kp.kb = ghi + 1;
-          kp.glo = glo;
-          kp.ghi = ghi;
-          kp.t = t;
-          kp.wt = wt;
+        if (!bad && md.mr > 0.0f) {
+          const int bm = sc.sel[6];
+          const int low_kept = t > 0u ? glo : kb;  // lowest bin with a kept element
+          if (bm > low_kept) {
+            kb = max(kb, bm);
+            t = 0u;
+          }
         }
+        if (lane == 0) {
+          sc.sel[0] = bad ? 1 : 0;
+          sc.sel[10] = kb;
+          sc.sel[11] = glo;
+          sc.sel[12] = ghi;
+          sc.sel[13] = static_cast<int>(t);
+          sc.sel64[3] = wt;
+        }
+      }
+      __syncthreads();
+      fb = sc.sel[0] != 0;
+      kp.kb = sc.sel[10];
+      kp.t = static_cast<unsigned int>(sc.sel[13]);
+      if (kp.t > 0u) {
+        kp.glo = sc.sel[11];
+        kp.ghi = sc.sel[12];
+        kp.wt = sc.sel64[3];
       }
     }
     MLXF_RH_STAMP(5);
-    // min_p, after top-p: the weights that reach min_p times the max's
-    if (!fb && md.mr > 0.0f) {
-      const float thr = minp_thr(md.mr, Mp, nc, false);
-      int lo = INT_MAX;
-#pragma unroll
-      for (int j = 0; j < BPT; ++j) {
-        const int b = own_bin(tid, j);
-        const float z = zp_of(b);
-        if (z != -INFINITY && wfun(z, Mp, nc, false) >= thr) lo = min(lo, b);
-      }
-      lo = wave_min(lo);
-      if (lane == 0 && lo != INT_MAX) atomicMin(&sc.sel[6], lo);
-      __syncthreads();
-      const int bm = sc.sel[6];
-      const int low_kept = kp.t > 0u ? kp.glo : kp.kb;  // lowest bin with a kept element
-      if (bm > low_kept) {
-        kp.kb = max(kp.kb, bm);
-        kp.t = 0u;
-      }
-    }
     MLXF_RH_STAMP(6);
 
     if (!fb) {
       // ---- per-chunk kept masses and the chunk holding u * W
+      const int need_lo = kp.t > 0u ? kp.glo : kp.kb;
       unsigned long long kc[NCH];
       unsigned int gc[NCH];
 #pragma unroll
@@ -553,20 +671,21 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         kc[c] = 0ull;
         gc[c] = 0u;
       }
+      if (own_bin(tid, 0) >= need_lo) {
 #pragma unroll
-      for (int j = 0; j < BPT; ++j) {
-        const int b = own_bin(tid, j);
-        if (b < 0 || cnt[j] == 0) continue;
-        if (b >= kp.kb) {
-          const unsigned long long qq = q_of(zp_of(b));
+        for (int j = 0; j < BPT; ++j) {
+          const int b = own_bin(tid, j);
+          if (b < 0 || cnt[j] == 0) continue;
+          if (b >= kp.kb) {
+            const unsigned long long qq = q[j];
 #pragma unroll
-          for (int c = 0; c < NCH; ++c) kc[c] += static_cast<unsigned long long>(hcount(hist, c, b)) * qq;
-        } else if (kp.t > 0u && b >= kp.glo && b <= kp.ghi) {
+            for (int c = 0; c < NCH; ++c) kc[c] += static_cast<unsigned long long>(hcount(hist, c, b)) * qq;
+          } else if (kp.t > 0u && b >= kp.glo && b <= kp.ghi) {
 #pragma unroll
-          for (int c = 0; c < NCH; ++c) gc[c] += hcount(hist, c, b);
+            for (int c = 0; c < NCH; ++c) gc[c] += hcount(hist, c, b);
+          }
         }
       }
-      const int wid = tid >> 6;
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         kc[c] = wave_sum(kc[c]);
@@ -618,78 +737,37 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
       fb = cs < 0;
       MLXF_RH_STAMP(7);
       if (!fb) {
-        // ---- the walk over chunk cs: thread t holds its EPTW consecutive
-        // elements; their loads are issued before the weight table is built
-        const int CL = x.ipc * ITER;
         const int EPTW = x.ipc * 8;
-        const int c0 = cs * CL + tid * EPTW;
-        const bool partial = kp.t > 0u;
-        const unsigned int span = static_cast<unsigned>(kp.ghi - kp.glo);
-        constexpr int WG = 4;  // 16-byte loads in flight per thread
-        unsigned long long km = 0ull;
-        int gt = 0;
-        bool table = false;
-        for (int g0 = 0; g0 < EPTW; g0 += 8 * WG) {
-          uint4 wq[WG];
+        const int c0 = cs * x.ipc * ITER + tid * EPTW;
+        // the thread's first 16-byte words of the walk requested before the
+        // weight table is built (the table needs the histograms to be dead)
+        constexpr int WG = 8;
+        uint4 wq[WG];
+        const bool whole = c0 + EPTW <= V;
+        if (whole) {
+          const uint4* rv = reinterpret_cast<const uint4*>(row + c0);
 #pragma unroll
-          for (int k = 0; k < WG; ++k) {
-            const int p = c0 + g0 + 8 * k;
-            if (g0 + 8 * k < EPTW && p + 8 <= V) {
-              wq[k] = *reinterpret_cast<const uint4*>(row + p);
-            } else {
-              unsigned int w4[4];
-#pragma unroll
-              for (int h = 0; h < 4; ++h) {
-                const bool in0 = g0 + 8 * k < EPTW && p + 2 * h < V, in1 = g0 + 8 * k < EPTW && p + 2 * h + 1 < V;
-                w4[h] = (in0 ? static_cast<unsigned int>(row[p + 2 * h]) : 0u) |
-                        ((in1 ? static_cast<unsigned int>(row[p + 2 * h + 1]) : 0u) << 16);
-              }
-              wq[k] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-            }
-          }
-          if (!table) {
-            // the weight table over the dead histograms: each wholly kept
-            // bin's mass (low and high 32-bit halves), 0 for every other bin
-            __syncthreads();
-#pragma unroll
-            for (int j = 0; j < BPT; ++j) {
-              const int b = own_bin(tid, j);
-              if (b < 0) continue;
-              const unsigned long long mq = b >= kp.kb ? q_of(zp_of(b)) : 0ull;
-              hist[b] = static_cast<unsigned int>(mq);
-              hist[CHW + b] = static_cast<unsigned int>(mq >> 32);
-            }
-            if (tid == 0) {
-              hist[B_TRASH] = 0u;
-              hist[CHW + B_TRASH] = 0u;
-            }
-            __syncthreads();
-            table = true;
-          }
-#pragma unroll
-          for (int k = 0; k < WG; ++k) {
-            const int p = c0 + g0 + 8 * k;
-            const unsigned int w4[4] = {wq[k].x, wq[k].y, wq[k].z, wq[k].w};
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-              unsigned int b2 = bins2(w4[h]);
-              if (!(g0 + 8 * k < EPTW && p + 2 * h < V)) b2 = (b2 & 0xffff0000u) | static_cast<unsigned>(B_TRASH);
-              if (!(g0 + 8 * k < EPTW && p + 2 * h + 1 < V))
-                b2 = (b2 & 0xffffu) | (static_cast<unsigned>(B_TRASH) << 16);
-              const unsigned int o0 = (b2 & 0xffffu) * 4u, o1 = (b2 >> 16) * 4u;
-              km += (static_cast<unsigned long long>(*reinterpret_cast<const unsigned int*>(lds + CHB + o0)) << 32 |
-                     *reinterpret_cast<const unsigned int*>(lds + o0)) +
-                    (static_cast<unsigned long long>(*reinterpret_cast<const unsigned int*>(lds + CHB + o1)) << 32 |
-                     *reinterpret_cast<const unsigned int*>(lds + o1));
-              if (partial)
-                gt += ((b2 & 0xffffu) - static_cast<unsigned>(kp.glo) <= span ? 1 : 0) +
-                      ((b2 >> 16) - static_cast<unsigned>(kp.glo) <= span ? 1 : 0);
-            }
-          }
+          for (int k = 0; k < WG; ++k)
+            if (k < EPTW / 8) wq[k] = rv[k];
         }
+        // the weight table over the dead histograms: each wholly kept bin's
+        // mass at byte 8 * bin, 0 for every other bin
+        unsigned long long* tab = reinterpret_cast<unsigned long long*>(lds);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) {
+          const int b = own_bin(tid, j);
+          if (b >= 0) tab[b] = (b >= kp.kb && cnt[j] > 0) ? q[j] : 0ull;
+        }
+        if (tid == 0) tab[B_TRASH] = 0ull;
+        __syncthreads();
+        const unsigned long long km0 = kp.t > 0u ? walk_sum<true, WG>(row, V, c0, EPTW, tab, kp, wq, whole)
+                                                 : walk_sum<false, WG>(row, V, c0, EPTW, tab, kp, wq, whole);
+        unsigned long long km = km0 & 0x00ffffffffffffffull;  // (mass; tie count in the top byte, see walk_sum)
+        const int gt = static_cast<int>(km0 >> 56);
         MLXF_RH_STAMP(8);
         int gex = 0;
-        if (partial) {
+        if (kp.t > 0u) {
           int gtot;
           gex = bscan(gt, &sc.ir[0][0], &gtot);
           const unsigned int kt = tkc > static_cast<unsigned>(gex)
@@ -710,7 +788,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         const int holder = sc.sel[7];
         if (holder >= 0 && tid < 64) {
           // wave 0 walks the holder's elements, one per lane per round
-          const int hbase = cs * CL + holder * EPTW;
+          const int hbase = cs * x.ipc * ITER + holder * EPTW;
           const unsigned long long hrem = sc.sel64[1];
           unsigned int tie_rank = static_cast<unsigned int>(sc.sel[8]);
           unsigned long long carry = 0ull;
@@ -720,9 +798,8 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
             const bool valid = e0 + lane < EPTW && p < V;
             const unsigned int bits = valid ? row[p] : 0u;
             const int b = valid ? static_cast<int>(bins2(bits) & 0xffffu) : B_TRASH;
-            unsigned long long mm = static_cast<unsigned long long>(hist[b]) |
-                                    (static_cast<unsigned long long>(hist[CHW + b]) << 32);
-            if (partial) {
+            unsigned long long mm = tab[b];
+            if (kp.t > 0u) {
               const bool tie = valid && b >= kp.glo && b <= kp.ghi;
               const unsigned long long tb = __ballot(tie);
               const unsigned int rk = tie_rank + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(tb >> 32),
@@ -755,11 +832,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
 // it flagged.
 template <int DT, int EPT>
 hipError_t launch_row16(const Args& a, const RhArgs& x, hipStream_t st) {
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_row16<DT>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     static_cast<int>(rh::LDS_BYTES));
-  if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((k_row16<DT>), dim3(static_cast<unsigned int>(a.B)), dim3(rh::NT), rh::LDS_BYTES, st, a, x);
+  hipLaunchKernelGGL((k_row16<DT>), dim3(static_cast<unsigned int>(a.B)), dim3(rh::NT), 0, st, a, x);
   hipLaunchKernelGGL((k_rowfb<DT, EPT, true>), dim3(static_cast<unsigned int>(a.B < 64 ? a.B : 64)), dim3(THREADS), 0, st, a,
                      static_cast<const unsigned int*>(x.rowflag));
   return hipGetLastError();

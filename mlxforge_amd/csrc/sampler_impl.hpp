@@ -1990,6 +1990,11 @@ union FbShared {
 template <int DT, int EPT, bool VECOK>
 __global__ __launch_bounds__(THREADS, 1) void k_rowfb(Args a, const unsigned int* rowflag) {
   __shared__ FbShared sh;
+  // a workgroup with no flagged row leaves before any of the slice path's
+  // set-up (its code is large; the common call flags nothing)
+  unsigned int any = 0u;
+  for (int r = static_cast<int>(blockIdx.x); r < a.B; r += static_cast<int>(gridDim.x)) any |= rowflag[r];
+  if (any == 0u) return;
   for (int r = static_cast<int>(blockIdx.x); r < a.B; r += static_cast<int>(gridDim.x)) {
     if (rowflag[r] == 0u) continue;
     for (int s = 0; s < a.S; ++s) {
