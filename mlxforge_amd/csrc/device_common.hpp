@@ -512,6 +512,44 @@ __device__ __forceinline__ void wave_list_merge(float& lv, int& li, float nv, in
   cx<1>(lv, li, true);
 }
 
+// Unsigned keys, one per lane, sorted descending across the wave (largest in
+// lane 0); the same bitonic network on bare keys.
+template <int J>
+__device__ __forceinline__ void cxk(unsigned int& k, bool asc) {
+  const unsigned int o = xshf<J>(k);
+  const bool first = ((threadIdx.x & 63) & J) == 0;
+  k = (first == asc) ? max(k, o) : min(k, o);
+}
+template <int K>
+__device__ __forceinline__ void bitonic_stage_k(unsigned int& k) {
+  const bool asc = ((threadIdx.x & 63) & K) == 0;
+  if constexpr (K >= 64) cxk<32>(k, asc);
+  if constexpr (K >= 32) cxk<16>(k, asc);
+  if constexpr (K >= 16) cxk<8>(k, asc);
+  if constexpr (K >= 8) cxk<4>(k, asc);
+  if constexpr (K >= 4) cxk<2>(k, asc);
+  cxk<1>(k, asc);
+}
+__device__ __forceinline__ void wave_sort_keys(unsigned int& k) {
+  bitonic_stage_k<2>(k);
+  bitonic_stage_k<4>(k);
+  bitonic_stage_k<8>(k);
+  bitonic_stage_k<16>(k);
+  bitonic_stage_k<32>(k);
+  bitonic_stage_k<64>(k);
+}
+// The 64 largest of two descending lane lists, descending (the incoming list
+// reversed, the larger of each pair kept, one half-cleaning pass).
+__device__ __forceinline__ void wave_merge_keys(unsigned int& l, unsigned int n) {
+  l = max(l, xshf<32>(xshf<16>(xshf<15>(n))));
+  cxk<32>(l, true);
+  cxk<16>(l, true);
+  cxk<8>(l, true);
+  cxk<4>(l, true);
+  cxk<2>(l, true);
+  cxk<1>(l, true);
+}
+
 // Best (v desc, i asc) over the wave, in every lane.
 __device__ __forceinline__ void wave_best(float& v, int& i) {
 #define MLXF_BEST_STEP(M)                  \

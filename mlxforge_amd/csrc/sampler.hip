@@ -72,9 +72,9 @@ Layout make_layout(int B, int V, int K_max) {
   l.off_actlist = o;
   o = align256(o + sizeof(unsigned int) * NSTAGE * nb);
   l.off_rec = o;
-  o = align256(o + 4 * sizeof(unsigned long long) * BS);
+  o = align256(o + REC * sizeof(unsigned long long) * BS);
   l.off_list = o;
-  o = align256(o + sizeof(unsigned long long) * BS * LIST);
+  o = align256(o + sizeof(unsigned long long) * BS * SCAP);
   l.off_rowst = o;
   o = align256(o + sizeof(unsigned long long) * RS_WORDS * nb);
   l.off_hcnt = o;

@@ -51,6 +51,22 @@
 #include "device_common.hpp"
 #include "mlxf_sampler.h"
 
+// Per-phase timestamps of the first pass (one record per slice) and the
+// deciding kernel (one per row) for a profiling harness that defines
+// MLXF_S1_STAMPS (and the arrays they write); no effect otherwise.
+#ifdef MLXF_S1_STAMPS
+#define MLXF_S1_STAMP(arr, i) \
+  if (threadIdx.x == 0) arr[stamp_id * 16 + (i)] = __builtin_amdgcn_s_memrealtime()
+#define MLXF_S1_VAL(arr, i, val) \
+  if (threadIdx.x == 0) arr[stamp_id * 16 + (i)] = (val)
+#define MLXF_S1_STAMP_T(arr, i, t) \
+  if (threadIdx.x == (t)) arr[stamp_id * 16 + (i)] = __builtin_amdgcn_s_memrealtime()
+#else
+#define MLXF_S1_STAMP_T(arr, i, t)
+#define MLXF_S1_STAMP(arr, i)
+#define MLXF_S1_VAL(arr, i, val)
+#endif
+
 namespace mlxf {
 
 enum { KIND_GREEDY = 0, KIND_TEMP = 1, KIND_KLIST = 2, KIND_KHIST = 3, KIND_TOPP = 4 };
@@ -69,6 +85,10 @@ constexpr int CAP = 4096;            // gathered candidates per row (LDS)
 constexpr int NSTAGE = 3;            // refine launches per call
 constexpr int SERIAL_MAX = 40;       // bound on the levels the last stage runs itself
 constexpr int SURV = 64 * 32;        // best-64 survivors of a slice (<= 64 * EPT)
+constexpr int SCAP = 128;            // unsorted candidates a slice hands on (else its best 64)
+constexpr int SCAP_LOG2 = 7;
+constexpr int REC = 8;               // 64-bit words per slice record
+constexpr int CBUF = 4096;           // row candidates the deciding workgroup sorts in LDS
 constexpr float MASS_LOG2_SPAN = 40.0f;  // weights below 2^-40 quantise to zero
 
 
@@ -91,8 +111,8 @@ struct Args {
   unsigned int* actcnt;        // [4] rows on each stage's list (zero between calls, see below)
   unsigned int* ncand;         // [B] gathered-candidate counters, zero between calls
   unsigned int* actlist;       // [NSTAGE][B] rows still open before each refine stage
-  unsigned long long* rec;     // [B*S][4] slice records
-  unsigned long long* list;    // [B*S][64] (z bits, index)
+  unsigned long long* rec;     // [B*S][REC] slice records
+  unsigned long long* list;    // [B*S][SCAP] candidates (z bits, index)
   unsigned long long* rowst;   // [B][8] row plans
   unsigned int* hcnt;          // [B*S][256] histogram counts, cumulative from bin 0 (the top)
   unsigned long long* hmass;   // [B*S][256] histogram masses, cumulative from bin 0
@@ -311,6 +331,18 @@ __device__ __forceinline__ unsigned long long pack_ent(float v, int i) {
   return pack2(__float_as_uint(v), static_cast<unsigned int>(i));
 }
 
+// (value desc, index asc) as one unsigned order on an entry: the larger key is
+// the better entry.  -0 and +0 are equal values, so both take the key of +0
+// (and read back as +0).
+__device__ __forceinline__ unsigned long long order_key(unsigned long long ent) {
+  const float v = __uint_as_float(static_cast<unsigned int>(ent));
+  return pack2(0xffffffffu - static_cast<unsigned int>(ent >> 32), f2key(v == 0.0f ? 0.0f : v));
+}
+__device__ __forceinline__ float order_key_v(unsigned long long k) { return key2f(static_cast<unsigned int>(k >> 32)); }
+__device__ __forceinline__ int order_key_i(unsigned long long k) {
+  return static_cast<int>(0xffffffffu - static_cast<unsigned int>(k));
+}
+
 // min_p (src/sample/sampler.cpp:87-93, after top-p): an element is kept when
 // its probability reaches mr times the largest one, i.e. when its weight
 // reaches mr times the weight of the row max.  The weight of the max is
@@ -410,32 +442,73 @@ __device__ __forceinline__ void plan_level1(Plan& p, float span2) {
 //
 // Stage 0, one workgroup per slice: the one HBM read of every logit.
 
-struct S1Lds {
-  TopEnt surv[SURV];
+struct alignas(16) S1Lds {
+  union alignas(16) {
+    TopEnt surv[SURV];         // survivors of a heavy slice
+    float stg[THREADS * 32];   // the slice's values, in index order (candidate writes)
+  };
   TopEnt lists[WAVES * LIST];  // bitonic fallback for many survivors
+  unsigned int klst[WAVES * 64];  // each wave's thread-maximum keys, descending
   float rf[WAVES];
   float rmin[WAVES];
   int ri[WAVES];
   float ramin[WAVES];
   double rd[WAVES];
-  unsigned int rth[WAVES];
   int rsc[WAVES + 1];
+  int ncnt;  // survivors counted so far
   float thv;
   int thi;
 };
 
-// Slice s of row r (whole workgroup of THREADS threads).  Also called slice
-// after slice by the fallback kernel of the row-histogram path.
+// Slice s of row r (whole workgroup of THREADS threads), from its loaded bits.
+//
+// For rows that need their best 64 entries (top_logprobs, top-k <= 63) the
+// slice hands on candidates: t_j, the j-th largest thread maximum (j = 64, 32,
+// 16, 8, 4, 2, 1), is reached by at least j elements of the slice, so its best
+// 64 are all at or above t_64.  Those elements go to the slice's SCAP slots
+// unsorted when they fit (the common case: about 73 of 8192 on random rows);
+// otherwise (heavy ties) the slice's best 64, sorted.  The t_j go into the
+// slice record, where the deciding kernel combines them into a row bound.
+// A slice's logits as loaded (raw bits, 8 per 16- or 32-byte load).
+template <int DT, int EPT>
+struct SliceRaw {
+  Raw8<DT> c[EPT / VEC];
+};
+
+// (A slice wholly inside the row takes plain vector loads, one per register
+// group: no per-lane fallback path whose loads the compiler would wait for
+// before reusing the registers.)
 template <int DT, int EPT, bool VECOK>
-__device__ __forceinline__ void scan1_slice(const Args& a, int r, int s, S1Lds& sh) {
+__device__ __forceinline__ void scan1_load(const Args& a, int r, int s, SliceRaw<DT, EPT>& raw) {
+  const void* row = row_ptr<DT>(a, r);
+  const int beg = s * a.L;
+  const int end = min(a.V, beg + a.L);
+  const int t8 = static_cast<int>(threadIdx.x) * VEC;
+  if (VECOK && end - beg == a.L) {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const char*>(row) +
+                                                    static_cast<size_t>(beg + t8) * elem_size<DT>());
+    constexpr int QPC = CHUNK * Raw8<DT>::NQ / VEC;  // uint4 per CHUNK elements
+#pragma unroll
+    for (int it = 0; it < EPT / VEC; ++it)
+#pragma unroll
+      for (int q = 0; q < Raw8<DT>::NQ; ++q) raw.c[it].q[q] = p[it * QPC + q];
+  } else {
+#pragma unroll
+    for (int it = 0; it < EPT / VEC; ++it) load_raw<DT, VECOK>(row, beg + it * CHUNK + t8, end, raw.c[it]);
+  }
+}
+
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ void scan1_body(const Args& a, int r, int s, const SliceRaw<DT, EPT>& raw, S1Lds& sh) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int S = a.S;
+  [[maybe_unused]] const int stamp_id = r * S + s;
   // the row's gathered-candidate counter starts at zero (it is first used by a
   // later kernel), so the workspace needs no initialisation and no call
   // depends on what the previous one left
   if (tid == 0 && s == 0) a.ncand[r] = 0u;
   const Mode md = decode<DT>(a, r);
-  const void* row = row_ptr<DT>(a, r);
+  MLXF_S1_STAMP(mlxf_s1_stamps, 0);
   const int beg = s * a.L;
   const int end = min(a.V, beg + a.L);
   constexpr int NIT = EPT / VEC;
@@ -445,9 +518,19 @@ __device__ __forceinline__ void scan1_slice(const Args& a, int r, int s, S1Lds& 
 
   float v[EPT];
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) load8_nan<DT, VECOK>(row, beg + it * CHUNK + tid * VEC, end, &v[it * VEC]);
+  for (int it = 0; it < NIT; ++it) decode8_nan<DT>(raw.c[it], &v[it * VEC]);
   clear_nans(v);
 #define MLXF_IDX(e) (beg + ((e) / VEC) * CHUNK + tid * VEC + ((e) % VEC))
+  if (md.need_list) {
+    // a copy of the values in LDS, where a thread finds its candidates by
+    // position (registers cannot be indexed by a lane-varying position)
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      float4* d = reinterpret_cast<float4*>(&sh.stg[it * CHUNK + tid * VEC]);
+      d[0] = make_float4(v[it * VEC + 0], v[it * VEC + 1], v[it * VEC + 2], v[it * VEC + 3]);
+      d[1] = make_float4(v[it * VEC + 4], v[it * VEC + 5], v[it * VEC + 6], v[it * VEC + 7]);
+    }
+  }
 
   static_assert(EPT % 2 == 0, "pairs of elements");
   float tmax = v[0];
@@ -458,6 +541,7 @@ __device__ __forceinline__ void scan1_slice(const Args& a, int r, int s, S1Lds& 
     const float wm = wave_max(tmax);
     if (lane == 0) sh.rf[wid] = wm;
   }
+  MLXF_S1_STAMP(mlxf_s1_stamps, 1);
   if (refine) {
     // smallest |z| (the -inf read past the row end is never the smallest) and
     // the slice minimum (with the maximum: the largest finite |z| when neither
@@ -481,22 +565,16 @@ __device__ __forceinline__ void scan1_slice(const Args& a, int r, int s, S1Lds& 
     }
   }
   if (md.need_list) {
-    // theta: each wave's 16th largest thread-maximum key, rounded down to its
-    // top 16 bits, by bisection with ballots; the smallest of the four is
-    // reached by at least 64 elements (16 thread maxima per wave), so the
-    // slice's best 64 all reach it.  (A thread with no element in the slice
-    // counts as key 0, below every key; its first element, at beg + tid * VEC,
-    // is its lowest index.)
-    const unsigned int kt = beg + tid * VEC < end ? f2key(tmax) : 0u;
-    unsigned int tw = 0u;
-#pragma unroll
-    for (int b = 31; b >= 16; --b) {
-      const unsigned int c = tw | (1u << b);
-      if (__builtin_popcountll(__builtin_amdgcn_ballot_w64(kt >= c)) >= LIST / WAVES) tw = c;
-    }
-    if (lane == 0) sh.rth[wid] = tw;
+    // each wave's thread-maximum keys, sorted (a thread with no element in the
+    // slice counts as key 0, below every key; its first element, at
+    // beg + tid * VEC, is its lowest index)
+    unsigned int kt = beg + tid * VEC < end ? f2key(tmax) : 0u;
+    wave_sort_keys(kt);
+    sh.klst[wid * 64 + lane] = kt;
+    if (tid == 0) sh.ncnt = 0;
   }
   __syncthreads();
+  MLXF_S1_STAMP(mlxf_s1_stamps, 2);
   float zmax = sh.rf[0];
 #pragma unroll
   for (int w2 = 1; w2 < WAVES; ++w2) zmax = fmaxf(zmax, sh.rf[w2]);
@@ -525,75 +603,68 @@ __device__ __forceinline__ void scan1_slice(const Args& a, int r, int s, S1Lds& 
     const double ws = wave_sum(static_cast<double>(t));
     if (lane == 0) sh.rd[wid] = ws;
   }
-  int nsurv = 0;
+  MLXF_S1_STAMP(mlxf_s1_stamps, 6);
+  unsigned int msk = 0u;  // the thread's survivors (elements at or above t_64)
+  int pos0 = 0;           // ... their first slot
+  unsigned int t64 = 0u, t32 = 0u, t16 = 0u, t8 = 0u, t4 = 0u, t2 = 0u, t1 = 0u;
   if (md.need_list) {
-    // survivors: every element at or above theta, in slots from a block scan of
-    // the per-thread counts (its barrier also publishes sh.ri and sh.rd).  The
-    // float compare keeps -0 with +0, which (value desc, index asc) order ties.
-    unsigned int th = sh.rth[0];
-#pragma unroll
-    for (int w2 = 1; w2 < WAVES; ++w2) th = min(th, sh.rth[w2]);
-    const float thf = th <= KEY_NEG_INF ? -INFINITY : key2f(th);
+    // the slice's 64 largest thread maxima, descending, in every wave (two
+    // independent merges, then one)
+    static_assert(WAVES == 4, "four wave lists");
+    unsigned int mk = sh.klst[lane], mk2 = sh.klst[128 + lane];
+    wave_merge_keys(mk, sh.klst[64 + lane]);
+    wave_merge_keys(mk2, sh.klst[192 + lane]);
+    wave_merge_keys(mk, mk2);
+    t64 = rdl(mk, 63);
+    t32 = rdl(mk, 31);
+    t16 = rdl(mk, 15);
+    t8 = rdl(mk, 7);
+    t4 = rdl(mk, 3);
+    t2 = rdl(mk, 1);
+    t1 = rdl(mk, 0);
+    MLXF_S1_STAMP(mlxf_s1_stamps, 7);
+    // survivors: every element at or above t_64.  The float compare keeps -0
+    // with +0, which (value desc, index asc) order ties.
+    const float thf = t64 <= KEY_NEG_INF ? -INFINITY : key2f(t64);
     // entries past the row end read as -inf: they need the bounds check only
     // when theta is -inf
     const bool nochk = end - beg == a.L || thf > -INFINITY;
-    int mine = 0;
+    static_assert(EPT <= 32, "one mask bit per element");
     if (nochk) {
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) mine += v[e] >= thf ? 1 : 0;
+      for (int e = 0; e < EPT; ++e) msk |= (v[e] >= thf ? 1u : 0u) << e;
     } else {
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && v[e] >= thf) ? 1 : 0;
+      for (int e = 0; e < EPT; ++e) msk |= (((MLXF_IDX(e) < end) & (v[e] >= thf)) ? 1u : 0u) << e;
     }
-    int pos = block_excl_scan_dpp<int>(mine, sh.rsc, &nsurv);
-    if (nsurv <= SURV) {
-      if (mine) {
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) {
-          const int i = MLXF_IDX(e);
-          if ((nochk || i < end) && v[e] >= thf) {
-            sh.surv[pos].v = v[e];
-            sh.surv[pos].i = i;
-            ++pos;
-          }
-        }
-      }
-    } else {
-      // (heavy ties at theta) the exact 64th best thread maximum instead, which
-      // at most 64 * EPT elements reach: bitonic sort of each wave's 64 and a
-      // tree merge; with fewer than 64 threads holding elements it is the
-      // sentinel and every element survives
-      float lv = -INFINITY;
-      int li = INT_MAX;
-#pragma unroll
-      for (int e = EPT - 1; e >= 0; --e)
-        if (v[e] == tmax && MLXF_IDX(e) < end) li = MLXF_IDX(e);
-      if (li != INT_MAX) lv = tmax;
-      wave_sort(lv, li);
-      tree_merge(lv, li, sh.lists, WAVES);
-      if (tid == LIST - 1) {
-        sh.thv = lv;
-        sh.thi = li;
-      }
-      __syncthreads();
-      const float tv = sh.thv;
-      const int ti = sh.thi;
-      mine = 0;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) mine += (MLXF_IDX(e) < end && !better(tv, ti, v[e], MLXF_IDX(e))) ? 1 : 0;
-      pos = block_excl_scan_dpp<int>(mine, sh.rsc, &nsurv);
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const int i = MLXF_IDX(e);
-        if (i < end && !better(tv, ti, v[e], i)) {
-          sh.surv[pos].v = v[e];
-          sh.surv[pos].i = i;
-          ++pos;
-        }
-      }
+    const int mine = __builtin_popcount(msk);
+    MLXF_S1_STAMP(mlxf_s1_stamps, 8);
+    // slots: a DPP scan within the wave and one LDS atomic per wave for its
+    // base, no barrier.  (The waves' order varies from run to run, and with it
+    // the order of the slots; every reader orders candidates by value and
+    // index.)
+    const int incl = wave_incl_scan_dpp(mine);
+    int wbase = 0;
+    if (lane == 63) wbase = __hip_atomic_fetch_add(&sh.ncnt, incl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    pos0 = __builtin_amdgcn_readlane(wbase, 63) + incl - mine;
+    MLXF_S1_STAMP(mlxf_s1_stamps, 9);
+    // unsorted, straight into the slice's slots, one pass per candidate of
+    // the thread (usually none or one); a slice found to hold more than SCAP
+    // rewrites its slots below
+    unsigned long long* dst = a.list + (static_cast<size_t>(r) * S + s) * SCAP;
+    unsigned int m = msk;
+    int pos = pos0;
+    while (m) {
+      const int e = __builtin_ctz(m);
+      m &= m - 1u;
+      const int off = (e / VEC) * CHUNK + tid * VEC + (e % VEC);
+      if (pos < SCAP) dst[pos] = pack_ent(sh.stg[off], beg + off);
+      ++pos;
     }
   }
+  MLXF_S1_STAMP(mlxf_s1_stamps, 3);
   __syncthreads();
+  MLXF_S1_STAMP(mlxf_s1_stamps, 4);
   int zarg = sh.ri[0];
 #pragma unroll
   for (int w2 = 1; w2 < WAVES; ++w2) zarg = min(zarg, sh.ri[w2]);
@@ -621,9 +692,59 @@ __device__ __forceinline__ void scan1_slice(const Args& a, int r, int s, S1Lds& 
               ? static_cast<unsigned int>(SL_FAST)
               : 0u;
   }
-  if (md.need_list) {
-    // the survivors sorted: 64-entry chunks sorted by the waves and merged
-    unsigned long long* dst = a.list + (static_cast<size_t>(r) * S + s) * LIST;
+  // more than SCAP survivors (heavy ties at t_64): the slice hands on its
+  // best 64, sorted, in place of the slots written above
+  int nsurv = md.need_list ? sh.ncnt : 0;
+  const bool heavy = nsurv > SCAP;
+  if (heavy) {
+    if (nsurv <= SURV) {
+      // the survivors into LDS, at the slots counted above
+      int pos = pos0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        if ((msk >> e) & 1u) {
+          sh.surv[pos].v = v[e];
+          sh.surv[pos].i = MLXF_IDX(e);
+          ++pos;
+        }
+      }
+    } else {
+      // the exact 64th best thread maximum instead, which at most 64 * EPT
+      // elements reach: bitonic sort of each wave's 64 and a tree merge; with
+      // fewer than 64 threads holding elements it is the sentinel and every
+      // element survives
+      float lv = -INFINITY;
+      int li = INT_MAX;
+#pragma unroll
+      for (int e = EPT - 1; e >= 0; --e)
+        if (v[e] == tmax && MLXF_IDX(e) < end) li = MLXF_IDX(e);
+      if (li != INT_MAX) lv = tmax;
+      wave_sort(lv, li);
+      tree_merge(lv, li, sh.lists, WAVES);
+      if (tid == LIST - 1) {
+        sh.thv = lv;
+        sh.thi = li;
+      }
+      __syncthreads();
+      const float tv = sh.thv;
+      const int ti = sh.thi;
+      int mine2 = 0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) mine2 += (MLXF_IDX(e) < end && !better(tv, ti, v[e], MLXF_IDX(e))) ? 1 : 0;
+      int pos = block_excl_scan_dpp<int>(mine2, sh.rsc, &nsurv);
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int i = MLXF_IDX(e);
+        if (i < end && !better(tv, ti, v[e], i)) {
+          sh.surv[pos].v = v[e];
+          sh.surv[pos].i = i;
+          ++pos;
+        }
+      }
+    }
+    __syncthreads();
+    // 64-entry chunks sorted by the waves and merged
+    unsigned long long* dst = a.list + (static_cast<size_t>(r) * S + s) * SCAP;
     const int nch = (nsurv + LIST - 1) / LIST;
     float sv = -INFINITY;
     int si = INT_MAX;
@@ -643,11 +764,27 @@ __device__ __forceinline__ void scan1_slice(const Args& a, int r, int s, S1Lds& 
   }
 #undef MLXF_IDX
   if (tid == 0) {
-    unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + s) * 4;
+    unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + s) * REC;
     rp[0] = pack2(__float_as_uint(zmax), static_cast<unsigned int>(zarg));
     rp[1] = pack2(__float_as_uint(zmin), sfl);
     rp[2] = static_cast<unsigned long long>(__double_as_longlong(lse_s));
+    if (md.need_list) {
+      rp[3] = pack2(t64, t32);
+      rp[4] = pack2(t16, t8);
+      rp[5] = pack2(t4, static_cast<unsigned int>(heavy ? LIST : nsurv));
+      rp[6] = pack2(t2, t1);
+    }
   }
+  MLXF_S1_STAMP(mlxf_s1_stamps, 5);
+}
+
+// Slice s of row r (whole workgroup of THREADS threads).  Also called slice
+// after slice by the fallback kernel of the row-histogram path.
+template <int DT, int EPT, bool VECOK>
+__device__ __forceinline__ void scan1_slice(const Args& a, int r, int s, S1Lds& sh) {
+  SliceRaw<DT, EPT> raw;
+  scan1_load<DT, EPT, VECOK>(a, r, s, raw);
+  scan1_body<DT, EPT, VECOK>(a, r, s, raw, sh);
 }
 
 template <int DT, int EPT, bool VECOK>
@@ -667,10 +804,11 @@ __global__ __launch_bounds__(THREADS) void k_scan1(Args a) {
 // from the merged best-64 lists; a plan for every other sampling row.
 
 struct D1Lds {
-  unsigned long long lst[MAX_S * LIST];  // (the per-slice lists; dead once merged)
-  unsigned long long sv[MAX_S * LIST];   // list entries at or above theta
-  int ncnt[MAX_S];                       // ... per slice
-  unsigned int thk[WAVES];
+  unsigned long long sv[CBUF];  // the row's candidates at or above theta, as order keys
+  alignas(16) unsigned int thr[7 * MAX_S];  // [j][s]: t_64, t_32, t_16, t_8, t_4, t_2, t_1 of each slice
+  int sn[MAX_S];                // per slice: candidates handed on
+  int ncnt;                     // candidates gathered
+  unsigned int thw[WAVES];      // each wave's best theta
   TopEnt lists[WAVES * LIST];
   TopEnt mlist[LIST];
   float szmax[MAX_S];
@@ -681,6 +819,8 @@ struct D1Lds {
   int zarg;
   double lse;
   int sel[4];
+  unsigned long long kl_tu;  // two-wave top-k: the draw target
+  int kl_nk;                 // ... entries kept (negated when their weights are all 0)
 };
 
 // Top-k <= 63 from the row's merged best-64 list, by one wave.  Returns false
@@ -737,6 +877,33 @@ __device__ __forceinline__ bool klist_resolve(const Mode& md, float Mp, const To
   const double cum = wave_incl_scan_dpp(kw);
   const int cand = wave_min((ki != INT_MAX && (Wf == 0.0 || (kw > 0.0 && cum > static_cast<double>(Tu)))) ? ki : INT_MAX);
   *id_out = cand == INT_MAX ? rdl(si, 0) : cand;
+  return true;
+}
+
+// The part of klist_resolve both waves of the two-wave form compute: the list's
+// top-k entries in (z' desc, index asc) order (sv, si; (-inf, INT_MAX) past
+// them) and their fixed-point masses.  False as for klist_resolve.
+template <int DT>
+__device__ __forceinline__ bool klist_prep(const Mode& md, float Mp, const TopEnt* ml, float& sv, int& si,
+                                           float& wv, double& w) {
+  const int lane = threadIdx.x & 63;
+  const float lv = ml[lane].v;
+  const int li = ml[lane].i;
+  const bool real = li != INT_MAX;
+  const float zp = real ? zdiv<DT>(lv, md.Tr, md.y, false) : -INFINITY;
+  const float tau = rdl(zp, md.kk - 1);
+  const int last_i = rdl(li, LIST - 1);
+  const float last_zp = rdl(zp, LIST - 1);
+  if (last_i != INT_MAX && !(last_zp < tau)) return false;
+  const bool in_k = real && zp >= tau;
+  sv = in_k ? zp : -INFINITY;
+  si = in_k ? li : INT_MAX;
+  const float nsv = __shfl_down(sv, 1, 64);
+  const int nsi = __shfl_down(si, 1, 64);
+  if (__ballot(lane < 63 && sv == nsv && si > nsi)) wave_sort(sv, si);
+  const float nc = -(Mp * LOG2E);
+  wv = si != INT_MAX ? wfun(sv, Mp, nc, !__builtin_isfinite(Mp)) : 0.0f;
+  w = static_cast<double>(q40(wv));
   return true;
 }
 
@@ -843,7 +1010,7 @@ __device__ __forceinline__ void slice_stage(const Args& a, int r, int s, const P
   const int beg = s * a.L;
   const int end = min(a.V, beg + a.L);
   constexpr int NIT = EPT / VEC;
-  const unsigned int sfl = static_cast<unsigned int>(a.rec[(static_cast<size_t>(r) * a.S + s) * 4 + 1] >> 32);
+  const unsigned int sfl = static_cast<unsigned int>(a.rec[(static_cast<size_t>(r) * a.S + s) * REC + 1] >> 32);
   const bool fast = !md.tslow && (sfl & SL_FAST);
   const float Mp = pl.Mp;
   const float nc = -(Mp * LOG2E);
@@ -978,7 +1145,7 @@ __device__ __forceinline__ int walk(const Args& a, int r, int s, float Mp, unsig
   const void* row = row_ptr<DT>(a, r);
   const int b0 = s * a.L, e0 = min(a.V, b0 + a.L);
   const int my0 = b0 + tid * EPT;
-  const unsigned int sfl = static_cast<unsigned int>(a.rec[(static_cast<size_t>(r) * a.S + s) * 4 + 1] >> 32);
+  const unsigned int sfl = static_cast<unsigned int>(a.rec[(static_cast<size_t>(r) * a.S + s) * REC + 1] >> 32);
   const bool fast = !md.tslow && (sfl & SL_FAST);
   const float nc = -(Mp * LOG2E);
   const bool minf = !__builtin_isfinite(Mp);
@@ -1679,7 +1846,7 @@ __device__ __forceinline__ void serial_finish(const Args& a, int r, RLds& sh) {
     float bm = -INFINITY;
     int bi = 0;
     for (int s2 = 0; s2 < a.S; ++s2) {
-      const unsigned long long w0 = a.rec[(static_cast<size_t>(r) * a.S + s2) * 4];
+      const unsigned long long w0 = a.rec[(static_cast<size_t>(r) * a.S + s2) * REC];
       const float m = __uint_as_float(static_cast<unsigned int>(w0));
       if (m > bm) {
         bm = m;
@@ -1726,39 +1893,55 @@ union D1Shared {
 template <int DT, int EPT, bool VECOK>
 __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1Shared& shu) {
   D1Lds& sh = shu.d;
+  [[maybe_unused]] const int stamp_id = r;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int S = a.S;
-  // the slices' lists are requested before the row's parameters say whether
-  // they are needed: one memory round trip for everything this kernel reads
-  unsigned long long lw[MAX_S * LIST / THREADS];
-  {
-    const unsigned long long* src = a.list + static_cast<size_t>(r) * S * LIST;
+  // candidate slots: wave w takes slices w, w + 4, w + 8, ... (lane l their
+  // slots l and l + 64).  Those of the first 32 slices are requested before
+  // the row's parameters say whether they are needed: one memory round trip
+  // for the records, the parameters and (up to 32 slices) every candidate.
+  constexpr int SPW = 8;  // slices per wave and round
+  const unsigned long long* src = a.list + static_cast<size_t>(r) * S * SCAP;
+  unsigned long long cw[2 * SPW];
+  auto load_round = [&](int base) {
 #pragma unroll
-    for (int k = 0; k < MAX_S * LIST / THREADS; ++k) {
-      const int i = tid + k * THREADS;
-      lw[k] = i < S * LIST ? src[i] : 0ull;
+    for (int m = 0; m < SPW; ++m) {
+      const int s2 = base + wid + WAVES * m;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) cw[2 * m + h] = s2 < S ? src[s2 * SCAP + h * 64 + lane] : 0ull;
     }
-  }
+  };
+  load_round(0);
   const Mode md = decode<DT>(a, r);
-  if (tid < S) {
-    const unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + tid) * 4;
-    const unsigned long long w0 = rp[0], w1 = rp[1], w2 = rp[2];
-    sh.szmax[tid] = __uint_as_float(static_cast<unsigned int>(w0));
-    sh.szarg[tid] = static_cast<int>(w0 >> 32);
-    sh.szmin[tid] = __uint_as_float(static_cast<unsigned int>(w1));
-    sh.slse[tid] = __longlong_as_double(static_cast<long long>(w2));
-  }
-  if (md.need_list) {
+  MLXF_S1_STAMP(mlxf_d1_stamps, 0);
+  const int SP = (S + 3) & ~3;  // row stride of the threshold table (zero padded)
+  if (tid < SP) {
+    // (all seven words in one request: those of the list are not written for
+    // rows without one, and are then unused)
+    const bool real = tid < S;
+    const unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + (real ? tid : 0)) * REC;
+    const unsigned long long w0 = rp[0], w1 = rp[1], w2 = rp[2], w3 = rp[3], w4 = rp[4], w5 = rp[5], w6 = rp[6];
+    if (real) {
+      sh.szmax[tid] = __uint_as_float(static_cast<unsigned int>(w0));
+      sh.szarg[tid] = static_cast<int>(w0 >> 32);
+      sh.szmin[tid] = __uint_as_float(static_cast<unsigned int>(w1));
+      sh.slse[tid] = __longlong_as_double(static_cast<long long>(w2));
+      sh.sn[tid] = static_cast<int>(w5 >> 32);
+    }
+    if (md.need_list) {
+      const unsigned int t[7] = {static_cast<unsigned int>(w3), static_cast<unsigned int>(w3 >> 32),
+                                 static_cast<unsigned int>(w4), static_cast<unsigned int>(w4 >> 32),
+                                 static_cast<unsigned int>(w5), static_cast<unsigned int>(w6),
+                                 static_cast<unsigned int>(w6 >> 32)};
 #pragma unroll
-    for (int k = 0; k < MAX_S * LIST / THREADS; ++k) {
-      const int i = tid + k * THREADS;
-      if (i < S * LIST) sh.lst[i] = lw[k];
+      for (int j = 0; j < 7; ++j) sh.thr[j * SP + tid] = real ? t[j] : 0u;
     }
   }
+  if (tid == 0) sh.ncnt = 0;
   __syncthreads();
+  MLXF_S1_STAMP(mlxf_d1_stamps, 1);
   // the row's max, lowest argmax, minimum and log-sum-exp from the slice
-  // records, by one wave (the last: it has no survivor chunk to sort when they
-  // fill fewer than WAVES chunks, so the work overlaps the sort)
+  // records, by one wave (the last, when it has nothing else to do)
   auto row_stats = [&]() {
     const float zm = lane < S ? sh.szmax[lane] : -INFINITY;
     const int za = lane < S ? sh.szarg[lane] : INT_MAX;
@@ -1776,100 +1959,163 @@ __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1
     }
   };
   if (md.need_list) {
-    // theta, a value the row's 64th best reaches: slice t's j-th entry e_t has
-    // j entries of the slice at or above it, so a value c that 64 / j of the
-    // e_t reach is reached by 64 entries of the row.  Wave w takes j = 64 >> w
-    // (64, 32, 16, 8) and finds the (64 / j)-th largest e_t by a bisection over
-    // keys, rounded down to their top 16 bits (ballot and popcount); theta is
-    // the largest of the four.  An entry of the row's best 64 is in its slice's
-    // list, so the entries at or above theta hold the row's best 64.  (With
-    // slices alike, the 8th entries give a theta near the row's 64th best; the
-    // 64th entries alone would let most of every list through.)
-    {
-      const int j = LIST >> wid;
-      const unsigned int kt =
-          lane < S ? f2key(__uint_as_float(static_cast<unsigned int>(sh.lst[lane * LIST + j - 1]))) : 0u;
-      unsigned int c = 0u;
+    // theta, a key the row's 64th best reaches.  Slice s has at least j
+    // elements at or above t_j(s), hence at least
+    //   n_s(c) = 32 [t_64 >= c] + 16 [t_32 >= c] + 8 [t_16 >= c] + 4 [t_8 >= c]
+    //          + 2 [t_4 >= c] + [t_2 >= c] + [t_1 >= c]
+    // at or above c (the t_j decrease with j); theta is the largest of the 7S
+    // keys t_j(s) with sum_s n_s(theta) >= 64, one thread per key.  An entry
+    // of the row's best 64 is among its slice's candidates, so the candidates
+    // at or above theta hold the row's best 64.
+    auto okey = [](unsigned long long ent) {  // the value part of order_key
+      const float v = __uint_as_float(static_cast<unsigned int>(ent));
+      return f2key(v == 0.0f ? 0.0f : v);
+    };
+    unsigned int best = 0u;
+    for (int q = tid; q < 7 * SP; q += THREADS) {
+      const unsigned int c = sh.thr[q];
+      int cnt[7] = {0, 0, 0, 0, 0, 0, 0};
+      for (int s4 = 0; s4 < SP / 4; ++s4) {  // the seven levels' reads in flight together
+        uint4 t4[7];
 #pragma unroll
-      for (int b = 31; b >= 16; --b) {
-        const unsigned int t = c | (1u << b);
-        if (__builtin_popcountll(__builtin_amdgcn_ballot_w64(kt >= t)) >= (1 << wid)) c = t;
+        for (int j = 0; j < 7; ++j) t4[j] = reinterpret_cast<const uint4*>(&sh.thr[j * SP])[s4];
+#pragma unroll
+        for (int j = 0; j < 7; ++j)
+          cnt[j] += (t4[j].x >= c ? 1 : 0) + (t4[j].y >= c ? 1 : 0) + (t4[j].z >= c ? 1 : 0) + (t4[j].w >= c ? 1 : 0);
       }
-      if (lane == 0) sh.thk[wid] = c;
+      const int F = 32 * cnt[0] + 16 * cnt[1] + 8 * cnt[2] + 4 * cnt[3] + 2 * cnt[4] + cnt[5] + cnt[6];
+      if (F >= 64) best = max(best, c);
+    }
+    best = wave_max(best);
+    if (lane == 0) sh.thw[wid] = best;
+    if (wid == WAVES - 1) row_stats();
+    __syncthreads();
+    // (a key k of -0 passes the candidates of +0 and -0 alike: okey gives both +0's key)
+    const unsigned int thk = max(max(sh.thw[0], sh.thw[1]), max(sh.thw[2], sh.thw[3]));
+    MLXF_S1_STAMP(mlxf_d1_stamps, 2);
+    // the candidates at or above theta, as order keys, gathered into sv: per
+    // wave and round the slices' ballots, then one LDS atomic for the wave's
+    // places (the order of the waves varies from run to run; every reader
+    // orders by key)
+    auto lane_below = [&](unsigned long long b) {
+      return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(b >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(b), 0u)));
+    };
+    for (int base = 0; base < S; base += WAVES * SPW) {
+      if (base > 0) load_round(base);
+      unsigned long long bal[2 * SPW];
+      int tot = 0;
+#pragma unroll
+      for (int m = 0; m < SPW; ++m) {
+        const int s2 = base + wid + WAVES * m;
+        const int n2 = s2 < S ? sh.sn[s2] : 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const bool ok = (lane + 64 * h < n2) & (okey(cw[2 * m + h]) >= thk);
+          bal[2 * m + h] = __builtin_amdgcn_ballot_w64(ok);
+          tot += static_cast<int>(__builtin_popcountll(bal[2 * m + h]));
+        }
+      }
+      int wb = 0;
+      if (lane == 0 && tot) wb = __hip_atomic_fetch_add(&sh.ncnt, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      wb = __builtin_amdgcn_readlane(wb, 0);
+#pragma unroll
+      for (int q = 0; q < 2 * SPW; ++q) {
+        const int p = wb + lane_below(bal[q]);
+        if (((bal[q] >> lane) & 1ull) && p < CBUF) sh.sv[p] = order_key(cw[q]);
+        wb += static_cast<int>(__builtin_popcountll(bal[q]));
+      }
     }
     __syncthreads();
-    unsigned int ck = sh.thk[0];
+    const int nsv = sh.ncnt;
+    MLXF_S1_STAMP(mlxf_d1_stamps, 3);
+    MLXF_S1_VAL(mlxf_d1_stamps, 15, nsv);
+    if (nsv <= THREADS) {
+      // (the usual case) each candidate's place in the order is the number of
+      // candidates with a larger key, counted over the list in LDS (read two
+      // at a time, the same address in every lane) by P neighbouring lanes, a
+      // share each; the best 64 go straight to their places
+      int lp2 = 0;
+      while (lp2 < 3 && (nsv << (lp2 + 1)) <= THREADS) ++lp2;
+      const int P = 1 << lp2;
+      const int c = tid >> lp2, part = tid & (P - 1);
+      const int npair = nsv >> 1, per = (npair + P - 1) >> lp2;
+      const unsigned long long mk = c < nsv ? sh.sv[c] : ~0ull;
+      const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(sh.sv);
+      int c4[4] = {0, 0, 0, 0};  // independent counts: no chain through one register
+      int j = part * per;
+      const int jend = min(npair, j + per);
+      for (; j + 8 <= jend; j += 8) {  // eight reads in flight
+        ulonglong2 q[8];
 #pragma unroll
-    for (int w2 = 1; w2 < WAVES; ++w2) ck = max(ck, sh.thk[w2]);
-    const float th = ck <= KEY_NEG_INF ? -INFINITY : key2f(ck);
-    int nsv = 0;
-    if (th > -INFINITY) {
-      // the entries at or above theta are a prefix of each (sorted) list: its
-      // length by a ballot, the prefixes' places by a scan over the slices
-      constexpr int SPW = MAX_S / WAVES;  // slices per wave
-      unsigned long long w[SPW];
-      int cnt[SPW];
+        for (int u = 0; u < 8; ++u) q[u] = p2[j + u];
 #pragma unroll
-      for (int q = 0; q < SPW; ++q) {
-        const int t = wid + q * WAVES;
-        w[q] = 0ull;
-        cnt[q] = 0;
-        if (t < S) {
-          w[q] = sh.lst[t * LIST + lane];
-          cnt[q] = __builtin_popcountll(
-              __builtin_amdgcn_ballot_w64(__uint_as_float(static_cast<unsigned int>(w[q])) >= th));
-          if (lane == 0) sh.ncnt[t] = cnt[q];
+        for (int u = 0; u < 8; ++u) {
+          c4[u & 3] += q[u].x > mk ? 1 : 0;
+          c4[(u + 2) & 3] += q[u].y > mk ? 1 : 0;
         }
       }
-      __syncthreads();
-      const int incl = wave_incl_scan_dpp(lane < S ? sh.ncnt[lane] : 0);
-      nsv = __builtin_amdgcn_readlane(incl, S - 1);
-#pragma unroll
-      for (int q = 0; q < SPW; ++q) {
-        const int t = wid + q * WAVES;
-        if (t < S) {
-          const int off = __builtin_amdgcn_readlane(incl, t) - cnt[q];
-          if (lane < cnt[q]) sh.sv[off + lane] = w[q];
-        }
+      for (; j < jend; ++j) {
+        const ulonglong2 q = p2[j];
+        c4[0] += q.x > mk ? 1 : 0;
+        c4[1] += q.y > mk ? 1 : 0;
       }
-    }
-    __syncthreads();
-    float lv = -INFINITY;
-    int li = INT_MAX;
-    if (th > -INFINITY && nsv <= THREADS) {
-      // the survivors (in any order) sorted: 64-entry chunks by the waves, merged
-      const int nch = (nsv + LIST - 1) / LIST;
-      if (wid < nch) {
-        const int c = wid * LIST + lane;
-        float cv = -INFINITY;
-        int ci = INT_MAX;
-        if (c < nsv) {
-          const unsigned long long w = sh.sv[c];
-          cv = __uint_as_float(static_cast<unsigned int>(w));
-          ci = static_cast<int>(w >> 32);
-        }
-        wave_sort(cv, ci);
-        lv = cv;
-        li = ci;
+      if ((nsv & 1) && part == 0) c4[2] += sh.sv[nsv - 1] > mk ? 1 : 0;
+      int rk = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+      if (P > 1) rk += xshf<1>(rk);  // the P shares (whole wave active)
+      if (P > 2) rk += xshf<2>(rk);
+      if (P > 4) rk += xshf<4>(rk);
+      if (c < nsv && part == 0 && rk < LIST) {
+        sh.mlist[rk].v = order_key_v(mk);
+        sh.mlist[rk].i = order_key_i(mk);
       }
-      if (wid == WAVES - 1) row_stats();  // idle here when nch < WAVES
-      if (nch > 1) tree_merge(lv, li, sh.lists, nch);
+      if (tid >= nsv && tid < LIST) {
+        sh.mlist[tid].v = -INFINITY;
+        sh.mlist[tid].i = INT_MAX;
+      }
     } else {
-      for (int t = wid; t < S; t += WAVES) {
-        const unsigned long long w = sh.lst[t * LIST + lane];
-        wave_list_merge(lv, li, __uint_as_float(static_cast<unsigned int>(w)), static_cast<int>(w >> 32));
+      // (many candidates) 64-entry chunks sorted by the waves and merged:
+      // from LDS when they fit, else every slot from memory
+      float lv = -INFINITY;
+      int li = INT_MAX;
+      if (nsv <= CBUF) {
+        const int nch = (nsv + LIST - 1) / LIST;
+        for (int ch = wid; ch < nch; ch += WAVES) {
+          const int c = ch * LIST + lane;
+          float cv = -INFINITY;
+          int ci = INT_MAX;
+          if (c < nsv) {
+            const unsigned long long k = sh.sv[c];
+            cv = order_key_v(k);
+            ci = order_key_i(k);
+          }
+          wave_sort(cv, ci);
+          wave_list_merge(lv, li, cv, ci);
+        }
+      } else {
+        const int nch = S * SCAP / LIST;
+        for (int ch = wid; ch < nch; ch += WAVES) {
+          const int i = ch * LIST + lane;
+          const unsigned long long w = src[i];
+          const float v = __uint_as_float(static_cast<unsigned int>(w));
+          const bool ok = (i & (SCAP - 1)) < sh.sn[i >> SCAP_LOG2] && okey(w) >= thk;
+          float cv = ok ? v : -INFINITY;
+          int ci = ok ? static_cast<int>(w >> 32) : INT_MAX;
+          wave_sort(cv, ci);
+          wave_list_merge(lv, li, cv, ci);
+        }
       }
-      if (wid == WAVES - 1) row_stats();
-      tree_merge(lv, li, sh.lists, S < WAVES ? S : WAVES);
-    }
-    if (wid == 0) {
-      sh.mlist[lane].v = lv;
-      sh.mlist[lane].i = li;
+      tree_merge(lv, li, sh.lists, WAVES);
+      if (wid == 0) {
+        sh.mlist[lane].v = lv;
+        sh.mlist[lane].i = li;
+      }
     }
   } else if (wid == WAVES - 1) {
     row_stats();
   }
   __syncthreads();
+  MLXF_S1_STAMP(mlxf_d1_stamps, 4);
   const double lse = sh.lse;
   if (a.K_max > 0 && tid < a.K_max) {  // top_logprobs: the first K of the best 64
     const size_t o = static_cast<size_t>(r) * a.K_max + tid;
@@ -1909,17 +2155,65 @@ __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1
     return;
   }
   if (md.kind == KIND_KLIST) {
-    if (wid == 0) {
-      int id = -1;
-      const bool ok = klist_resolve<DT>(md, Mp, sh.mlist, &id);
-      if (lane == 0) {
-        sh.sel[0] = ok ? 1 : 0;
-        sh.sel[1] = id;
+    // klist_resolve on two waves: wave 0 makes the cut (the kept entries are
+    // a prefix of the (z' desc, index asc) order: top-k, then top-p while the
+    // mass before an entry is < p W_k, then min_p, non-increasing weights),
+    // while wave 1 sorts the list by index for the draw, each entry carrying
+    // its place in that order (in the low 6 bits of 64 w, exact in a double)
+    if (wid < 2) {
+      float sv, wv;
+      int si;
+      double w;
+      const bool ok = klist_prep<DT>(md, Mp, sh.mlist, sv, si, wv, w);
+      if (wid == 0) {
+        if (ok) {
+          const double incl = wave_incl_scan_dpp(w);
+          const double Wk = rdl(incl, 63);
+          bool keep = si != INT_MAX;
+          if (md.topp) keep = keep && (incl - w) < ceil(static_cast<double>(md.pr) * Wk);
+          if (md.mr > 0.0f) {
+            const float nc = -(Mp * LOG2E);
+            keep = keep && wv >= minp_thr(md.mr, Mp, nc, !__builtin_isfinite(Mp));
+          }
+          const double Wf = wave_sum(keep ? w : 0.0);
+          unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * Wf);
+          if (Wf == 0.0)
+            Tu = 0;
+          else if (static_cast<double>(Tu) >= Wf)
+            Tu = static_cast<unsigned long long>(Wf) - 1;
+          const int nk = static_cast<int>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(keep)));
+          if (lane == 0) {
+            sh.kl_tu = Tu;
+            sh.kl_nk = Wf == 0.0 ? -nk : nk;  // (negative: every kept weight is 0)
+            sh.sel[1] = si;                   // (the draw's answer when nothing is kept)
+          }
+        }
+        if (lane == 0) sh.sel[0] = ok ? 1 : 0;
+        __syncthreads();
+      } else {
+        int ki = si;
+        double kwp = ok ? w * 64.0 + static_cast<double>(lane) : 0.0;
+        if (ok) wave_sort_idx(ki, kwp);
+        __syncthreads();
+        if (ok) {
+          const int nkr = sh.kl_nk, nk = nkr < 0 ? -nkr : nkr;
+          const unsigned long long kq = static_cast<unsigned long long>(kwp);
+          const bool kept = ki != INT_MAX && static_cast<int>(kq & 63u) < nk;
+          const double kw = kept ? static_cast<double>(kq >> 6) : 0.0;
+          const double cum = wave_incl_scan_dpp(kw);
+          const bool hit = kept && (nkr < 0 || (kw > 0.0 && cum > static_cast<double>(sh.kl_tu)));
+          const int cand = wave_min(hit ? ki : INT_MAX);
+          if (lane == 0 && cand != INT_MAX) sh.sel[1] = cand;
+        }
       }
+    } else {
+      __syncthreads();
     }
     __syncthreads();
+    MLXF_S1_STAMP(mlxf_d1_stamps, 5);
     if (sh.sel[0]) {
       if (tid == 0) write_out<DT>(a, r, sh.sel[1], lse, md.want_lp);
+      MLXF_S1_STAMP(mlxf_d1_stamps, 6);
       return;
     }
   }
