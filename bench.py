@@ -37,7 +37,7 @@ ROTATE_BYTES = 512 << 20
 # (separate passes), each scaled by what the counter reads for a plain device
 # copy of known size (--copy-calibration): profiles/k_scan1_C3_hbm_traffic.md.
 # A counter run cannot share the timed process, so the figure is carried here.
-MEASURED_TRAFFIC_BYTES = {3: 20081881}
+MEASURED_TRAFFIC_BYTES = {3: 20069987}
 COPY_CALIBRATION_BYTES = 256 << 20
 
 
@@ -104,7 +104,8 @@ class Step:
 
 def time_first_pass(step, torch, warmup, steps):
     """Average duration of the step's dominant kernel (k_scan1, the one HBM read
-    of the logits) alone, from hipEvents on the stream the library launches on."""
+    of the logits) alone: a hipEvent pair around each launch, on the stream the
+    library launches on (the library uses torch's current stream), averaged."""
     def one():
         err = ctypes.c_void_p()
         rc = step.lib.mlxf_sampler_first_pass(step._logits(), step.code, step.wl.B, step.wl.V,
@@ -115,13 +116,14 @@ def time_first_pass(step, torch, warmup, steps):
     for _ in range(warmup):
         one()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record()
         one()
-    e1.record()
+        e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
 
 
 def time_steps(step, torch, warmup, steps):
