@@ -102,10 +102,55 @@ class Step:
             _lib.check(rc, err)
 
 
+class MaskedStep(Step):
+    """A grammar-constrained decode step (src/runtime/worker.cpp:142-179, 455-459):
+    mlxf_apply_mask turns the bf16 rows and a bit mask (one bit per token, half
+    of the tokens allowed, seeded) into fp32 rows, which mlxf_sample_staged then
+    samples as fp32 logits."""
+
+    def __init__(self, wl, torch, lib, frac=0.5):
+        import numpy as np
+        super().__init__(wl, torch, lib)
+        dev = torch.device("cuda:0")
+        rng = np.random.default_rng(0xB175)
+        allowed = rng.random((wl.B, wl.V)) < frac
+        nw = (wl.V + 31) // 32
+        packed = np.zeros((wl.B, nw * 32), np.uint8)
+        packed[:, :wl.V] = allowed
+        words = np.packbits(packed.reshape(wl.B, nw, 4, 8)[:, :, :, ::-1], axis=-1).reshape(wl.B, nw, 4)
+        bits = (words[:, :, 0].astype(np.uint32) | (words[:, :, 1].astype(np.uint32) << 8)
+                | (words[:, :, 2].astype(np.uint32) << 16) | (words[:, :, 3].astype(np.uint32) << 24))
+        self.bits = torch.from_numpy(bits.view(np.int32)).to(dev)
+        self.nw = nw
+        self.masked = torch.empty((wl.B, wl.V), dtype=torch.float32, device=dev)
+        from mlxforge_amd import _lib
+        self.ws_bytes_f32 = _lib.workspace_size(wl.B, wl.V, self.K, 0)
+        self.ws32 = torch.zeros(self.ws_bytes_f32, dtype=torch.uint8, device=dev)
+        self.stages32 = _lib.refine_stages(wl.B, wl.V, 0, wl.T, wl.k, wl.p)
+        self.mask_only = False
+
+    def run(self):
+        err = ctypes.c_void_p()
+        P = ctypes.c_void_p
+        rc = self.lib.mlxf_apply_mask(self._logits(), self.code, self.wl.B, self.wl.V, self.wl.V,
+                                      P(self.bits.data_ptr()), self.nw, P(self.masked.data_ptr()),
+                                      self.wl.V, self.stream, ctypes.byref(err))
+        if rc == 0 and not self.mask_only:
+            tail = list(self.args_tail)
+            tail[-3], tail[-2] = P(self.ws32.data_ptr()), self.ws_bytes_f32
+            rc = self.lib.mlxf_sample_staged(P(self.masked.data_ptr()), 0, self.wl.B, self.wl.V, self.wl.V,
+                                             *tail[:-1], self.stages32, tail[-1], ctypes.byref(err))
+        if rc:
+            from mlxforge_amd import _lib
+            _lib.check(rc, err)
+
+
 def time_first_pass(step, torch, warmup, steps):
     """Average duration of the step's dominant kernel (k_scan1, the one HBM read
-    of the logits) alone: a hipEvent pair around each launch, on the stream the
-    library launches on (the library uses torch's current stream), averaged."""
+    of the logits) alone, from hipEvents around K back-to-back launches on the
+    stream the library launches on (torch's current stream).  (An event pair
+    around each launch adds the events' own cost to every launch: 11.8 us
+    against the 9.7 us kernel-trace median on C3.)"""
     def one():
         err = ctypes.c_void_p()
         rc = step.lib.mlxf_sampler_first_pass(step._logits(), step.code, step.wl.B, step.wl.V,
@@ -116,14 +161,13 @@ def time_first_pass(step, torch, warmup, steps):
     for _ in range(warmup):
         one()
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
-    for e0, e1 in ev:
-        e0.record()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
         one()
-        e1.record()
+    e1.record()
     torch.cuda.synchronize()
-    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
+    return e0.elapsed_time(e1) / steps
 
 
 def time_steps(step, torch, warmup, steps):
@@ -316,6 +360,19 @@ def main():
                                 "achieved_GBps_step": round(w2.algorithmic_bytes() / (m2 * 1e-3) / 1e9, 1),
                                 "hbm_frac": round(w2.algorithmic_bytes() / (m2 * 1e-3) / 1e9
                                                   / HBM_PEAK_GBPS, 4)}
+        log("[bench] masked C2 step")
+        ms_m = MaskedStep(workloads.make(2), torch, lib)
+        m_step = time_steps(ms_m, torch, min(args.warmup, 10), min(args.steps, 100))
+        ms_m.mask_only = True
+        m_mask = time_steps(ms_m, torch, min(args.warmup, 10), min(args.steps, 100))
+        w2 = ms_m.wl
+        extra["C2_masked"] = {"workload": w2.name + " with a grammar bit mask (half the tokens allowed): "
+                                          "mlxf_apply_mask to fp32 rows, then sampled as fp32",
+                              "us_per_step": round(m_step * 1e3, 2), "us_mask_kernel": round(m_mask * 1e3, 2),
+                              "refine_stages": ms_m.stages32,
+                              "mask_GBps": round((w2.B * w2.V * (2 + 4) + w2.B * ms_m.nw * 4) / (m_mask * 1e-3) / 1e9, 1)}
+        del ms_m
+        torch.cuda.empty_cache()
         out["other_configs"] = extra
     out["parity_excluded"] = parity
     print(json.dumps(out), flush=True)

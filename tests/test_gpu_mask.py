@@ -44,3 +44,32 @@ def test_mask_matches_oracle_and_samples(dtype, V):
     for r in range(B):
         if allowed[r].any():
             assert allowed[r, ids[r]], (r, ids[r])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_mask_strided_and_unaligned_rows(dtype):
+    """Padded rows (row, bit-mask and output strides beyond V) and row starts
+    that are not 16-byte aligned take the element-wise loads and stores."""
+    rng = np.random.default_rng(7 + len(dtype))
+    B, V = 5, 10007
+    nw = (V + 31) // 32
+    z = (rng.standard_normal((B, V + 3)) * 3).astype(np.float32)
+    host = z if dtype == "f32" else workloads.to_bf16_bits(z)
+    vals = workloads.bf16_bits_to_f32(host) if dtype == "bf16" else host.astype(np.float32)
+    allowed = rng.random((B, V)) < np.array([0.3, 0.0, 1.0, 0.001, 0.7])[:, None]
+    packed = orc.pack_bits(allowed).view(np.int32)
+    bits = torch.zeros((B, nw + 5), dtype=torch.int32, device="cuda")
+    bits[:, :nw] = torch.from_numpy(packed).cuda()
+    bits[:, nw:] = -1  # words past the row's own must not count
+    for off in (0, 1):  # off = 1: rows start one element in (not 16-byte aligned)
+        print(f"[mask strided] dtype={dtype} offset={off}", flush=True)
+        dev = gu.to_device(host, dtype)[:, off:off + V]
+        out_full = torch.full((B, V + 9), 7.0, dtype=torch.float32, device="cuda")
+        out = out_full[:, 1:1 + V] if off else out_full[:, :V]
+        sampler.apply_mask(dev, bits, V=V, out=out)
+        torch.cuda.synchronize()
+        exp = np.stack([orc.apply_mask(vals[r, off:off + V], allowed[r]) for r in range(B)])
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), exp.view(np.uint32))
+        full = out_full.cpu().numpy()
+        lo = 1 if off else 0
+        assert (full[:, :lo] == 7.0).all() and (full[:, lo + V:] == 7.0).all()  # nothing written outside
