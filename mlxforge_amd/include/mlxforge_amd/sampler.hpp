@@ -102,6 +102,24 @@ struct DeviceBuf {
     if (p) (void)hipFree(p);
   }
 };
+// Page-locked host staging (hipHostMalloc), so the one upload and the one
+// readback of a step are true asynchronous copies.
+struct PinnedBuf {
+  unsigned char* p = nullptr;
+  size_t n = 0;
+  void reserve(size_t want) {
+    if (want <= n) return;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    n = 0;
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&p), want, hipHostMallocDefault), "hipHostMalloc");
+    n = want;
+  }
+  ~PinnedBuf() {
+    if (p) (void)hipHostFree(p);
+  }
+};
+inline size_t align64(size_t x) { return (x + 63) & ~static_cast<size_t>(63); }
 }  // namespace detail
 
 // Batched sampler on one HIP stream.  Reuses its device buffers across calls;
@@ -234,6 +252,10 @@ class Sampler {
                         "hipMemcpyAsync");
   }
 
+  // One step: the six per-row parameter arrays go up in one copy from a
+  // packed pinned buffer, and ids, logprobs and the top-K block come back in
+  // one copy into another (the reference's worker reads its results back
+  // once per step, src/runtime/worker.cpp:488-514).
   SampleResult run(const DeviceLogits& logits, const float* T, const int32_t* k, const float* p,
                    const float* mp, const int32_t* tlp, const float* u, int K_max) {
     const int B = logits.B, V = logits.V;
@@ -242,55 +264,69 @@ class Sampler {
     size_t ws = 0;
     detail::check(mlxf_sampler_workspace_size(B, V, K_max, logits.dtype, &ws, &err), err);
     ensure_workspace(ws);
-    upload(T_, T, B);
-    upload(k_, k, B);
-    upload(p_, p, B);
-    upload(mp_, mp, B);
-    upload(tlp_, tlp, B);
-    upload(u_, u, B);
-    ids_.reserve(B > 0 ? B : 1);
-    lp_.reserve(B > 0 ? B : 1);
-    const size_t BK = static_cast<size_t>(B) * (K_max > 0 ? K_max : 1);
-    top_ids_.reserve(BK);
-    top_lp_.reserve(BK);
-    // the parameters are on the host here, so only the refine stages some row
-    // can need are launched
-    const int stages = mlxf_sampler_refine_stages(B, V, logits.dtype, T, k, p);
-    err = nullptr;
-    detail::check(mlxf_sample_ex(logits.data, logits.dtype, B, V, stride, T_.p, k_.p, p_.p, mp_.p,
-                                 tlp_.p, u_.p, ids_.p, lp_.p, K_max ? top_ids_.p : nullptr,
-                                 K_max ? top_lp_.p : nullptr, K_max, ws_.p, ws_bytes_, stages, stream_,
-                                 &err),
-                  err);
     SampleResult res;
     res.K = K_max;
     res.tokens.resize(B);
     res.logprobs.resize(B);
-    res.top_tokens.resize(static_cast<size_t>(B) * K_max);
-    res.top_logprobs.resize(static_cast<size_t>(B) * K_max);
-    if (B) {
-      detail::hip_check(hipMemcpyAsync(res.tokens.data(), ids_.p, B * sizeof(int32_t),
-                                       hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
-      detail::hip_check(hipMemcpyAsync(res.logprobs.data(), lp_.p, B * sizeof(float),
-                                       hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
-      if (K_max) {
-        detail::hip_check(hipMemcpyAsync(res.top_tokens.data(), top_ids_.p,
-                                         res.top_tokens.size() * sizeof(int32_t),
-                                         hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
-        detail::hip_check(hipMemcpyAsync(res.top_logprobs.data(), top_lp_.p,
-                                         res.top_logprobs.size() * sizeof(float),
-                                         hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
-      }
-    }
+    const size_t BK = static_cast<size_t>(B) * K_max;
+    res.top_tokens.resize(BK);
+    res.top_logprobs.resize(BK);
+    if (B == 0) return res;
+    // parameters: T, k, p, min_p, top_logprobs, u (4 bytes each per row)
+    const size_t col = detail::align64(static_cast<size_t>(B) * 4);
+    const size_t in_bytes = 6 * col;
+    in_h_.reserve(in_bytes);
+    in_d_.reserve(in_bytes);
+    unsigned char* h = in_h_.p;
+    std::copy(T, T + B, reinterpret_cast<float*>(h + 0 * col));
+    std::copy(k, k + B, reinterpret_cast<int32_t*>(h + 1 * col));
+    std::copy(p, p + B, reinterpret_cast<float*>(h + 2 * col));
+    std::copy(mp, mp + B, reinterpret_cast<float*>(h + 3 * col));
+    std::copy(tlp, tlp + B, reinterpret_cast<int32_t*>(h + 4 * col));
+    std::copy(u, u + B, reinterpret_cast<float*>(h + 5 * col));
+    detail::hip_check(hipMemcpyAsync(in_d_.p, h, in_bytes, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+    const unsigned char* d = in_d_.p;
+    // results: ids, logprobs, then the (B, K) top ids and logprobs
+    const size_t tcol = detail::align64(BK * 4);
+    const size_t out_bytes = 2 * col + 2 * tcol;
+    out_h_.reserve(out_bytes);
+    out_d_.reserve(out_bytes);
+    unsigned char* o = out_d_.p;
+    // the parameters are on the host here, so only the refine stages some row
+    // can need are launched
+    const int stages = mlxf_sampler_refine_stages(B, V, logits.dtype, T, k, p);
+    err = nullptr;
+    detail::check(
+        mlxf_sample_ex(logits.data, logits.dtype, B, V, stride, reinterpret_cast<const float*>(d + 0 * col),
+                       reinterpret_cast<const int32_t*>(d + 1 * col), reinterpret_cast<const float*>(d + 2 * col),
+                       reinterpret_cast<const float*>(d + 3 * col), reinterpret_cast<const int32_t*>(d + 4 * col),
+                       reinterpret_cast<const float*>(d + 5 * col), reinterpret_cast<int32_t*>(o),
+                       reinterpret_cast<float*>(o + col), K_max ? reinterpret_cast<int32_t*>(o + 2 * col) : nullptr,
+                       K_max ? reinterpret_cast<float*>(o + 2 * col + tcol) : nullptr, K_max, ws_.p, ws_bytes_,
+                       stages, stream_, &err),
+        err);
+    detail::hip_check(hipMemcpyAsync(out_h_.p, o, out_bytes, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
     detail::hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    const unsigned char* q = out_h_.p;
+    std::copy(reinterpret_cast<const int32_t*>(q), reinterpret_cast<const int32_t*>(q) + B, res.tokens.begin());
+    std::copy(reinterpret_cast<const float*>(q + col), reinterpret_cast<const float*>(q + col) + B,
+              res.logprobs.begin());
+    if (K_max) {
+      std::copy(reinterpret_cast<const int32_t*>(q + 2 * col), reinterpret_cast<const int32_t*>(q + 2 * col) + BK,
+                res.top_tokens.begin());
+      std::copy(reinterpret_cast<const float*>(q + 2 * col + tcol),
+                reinterpret_cast<const float*>(q + 2 * col + tcol) + BK, res.top_logprobs.begin());
+    }
     return res;
   }
 
   hipStream_t stream_;
   detail::DeviceBuf<unsigned char> ws_;
   size_t ws_bytes_ = 0;
-  detail::DeviceBuf<float> T_, p_, mp_, u_, lp_, top_lp_, rep_, fq_, ps_;
-  detail::DeviceBuf<int32_t> k_, tlp_, ids_, top_ids_, hist_, hlen_;
+  detail::DeviceBuf<unsigned char> in_d_, out_d_;  // packed parameters / results of a step
+  detail::PinnedBuf in_h_, out_h_;                  // ... their host staging
+  detail::DeviceBuf<float> rep_, fq_, ps_;
+  detail::DeviceBuf<int32_t> ids_, hist_, hlen_;
   detail::DeviceBuf<unsigned char> pen_ws_;
   size_t pen_ws_bytes_ = 0;
 };
