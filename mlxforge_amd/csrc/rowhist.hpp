@@ -25,8 +25,10 @@
 // Rows the bins cannot decide exactly -- the maximum in a merged bin (a
 // logit >= 256, +inf, a positive NaN, or a row of values all within 2^-28 of
 // zero or below -256), a cutoff that falls in or next to a merged bin, or a
-// merged bin whose elements' weights differ -- are flagged, and k_rowfb runs
-// the per-slice path for them.
+// merged bin whose elements' weights differ -- fall back to the per-slice
+// path in the same workgroup: its first four waves run the first pass over
+// the row's slices and the deciding step (every refine level), the other
+// twelve end.
 //
 // Memory per row: one read of the row (V * 2 bytes) in pass 1, a quarter row
 // in the draw.  No MFMA: nothing here is a dense contraction.
@@ -37,7 +39,6 @@ namespace mlxf {
 struct RhArgs {
   int ipc;                   // pass-1 iterations per chunk (chunk length ipc * 8192 logits)
   int nfull;                 // iterations wholly inside the row
-  unsigned int* rowflag;     // [B] 1 = the fallback kernel finishes the row
 };
 
 // One bf16 call on the row-histogram path (defined in sampler_bf16.hip).
@@ -377,9 +378,31 @@ __device__ __forceinline__ unsigned long long walk_sum(const unsigned short* row
 
 }  // namespace rh
 
+// The fallback, out of line: its register demand (the deciding step's) stays
+// out of the histogram path's register allocation; the LDS pointer keeps its
+// address space, so its accesses stay LDS instructions.
+// The call's arguments are read from the kernel's argument segment (a copy
+// would be a stack frame for every wave).
+template <int DT, int EPT>
+__device__ __noinline__ void row_fallback(__attribute__((address_space(4))) const Args* ka, int r,
+                                          __attribute__((address_space(3))) unsigned char* lds3) {
+  const Args& a = *(const Args*)ka;
+  FbShared& fsh = *reinterpret_cast<FbShared*>((unsigned char*)lds3);
+  for (int s = 0; s < a.S; ++s) {
+    scan1_slice<DT, EPT, true>(a, r, s, fsh.s1);
+    __syncthreads();
+  }
+  // the slice records and lists this workgroup wrote are complete; drop stale
+  // L1 lines before reading them back
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  decide1_row<DT, EPT, true>(a, r, 0, fsh.d1);
+}
+
 constexpr int RH_DEPTH = 6;  // pass-1 iterations in flight per thread (96 KB per workgroup)
 
-template <int DT>
+template <int DT, int EPT>
 __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
   using namespace rh;
   __shared__ __align__(16) unsigned char lds[LDS_BYTES];
@@ -821,20 +844,25 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
     }
   }
   MLXF_RH_STAMP(10);
-  if (tid == 0) {
-    x.rowflag[r] = fb ? 1u : 0u;
-    if (!fb) write_out<DT>(a, r, id, lse, md.want_lp);
+  if (!fb) {
+    if (tid == 0) write_out<DT>(a, r, id, lse, md.want_lp);
+    return;
   }
+  // ---- the fallback (fb is the same in every thread): the per-slice path
+  // over this row in waves 0..3, on the LDS the histograms leave.  The other
+  // waves end here; a barrier waits for the waves that have not ended.
+  __syncthreads();
+  if (tid >= THREADS) return;
+  // (a is the kernel's first argument: offset 0 of the argument segment)
+  row_fallback<DT, EPT>((__attribute__((address_space(4))) const Args*)__builtin_amdgcn_kernarg_segment_ptr(), r,
+                        (__attribute__((address_space(3))) unsigned char*)lds);
 }
 
-// One call on the row-histogram path: k_row16 over every row, then the
-// per-slice path (first pass and deciding step in one workgroup) for the rows
-// it flagged.
+// One call on the row-histogram path: one launch, k_row16 over every row.
 template <int DT, int EPT>
 hipError_t launch_row16(const Args& a, const RhArgs& x, hipStream_t st) {
-  hipLaunchKernelGGL((k_row16<DT>), dim3(static_cast<unsigned int>(a.B)), dim3(rh::NT), 0, st, a, x);
-  hipLaunchKernelGGL((k_rowfb<DT, EPT, true>), dim3(static_cast<unsigned int>(a.B < 64 ? a.B : 64)), dim3(THREADS), 0, st, a,
-                     static_cast<const unsigned int*>(x.rowflag));
+  static_assert(sizeof(FbShared) <= rh::LDS_BYTES, "the fallback's LDS must fit in the histograms'");
+  hipLaunchKernelGGL((k_row16<DT, EPT>), dim3(static_cast<unsigned int>(a.B)), dim3(rh::NT), 0, st, a, x);
   return hipGetLastError();
 }
 

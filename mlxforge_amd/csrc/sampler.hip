@@ -24,7 +24,7 @@ __global__ void k_zero(unsigned int* p, size_t n) {
 struct Layout {
   int S, L, EPT;
   size_t off_ncand, off_actcnt, off_actlist, off_rec, off_list, off_rowst, off_hcnt, off_hmass, off_above,
-      off_dsum, off_cand, off_rowflag, total;
+      off_dsum, off_cand, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -87,8 +87,6 @@ Layout make_layout(int B, int V, int K_max) {
   o = align256(o + sizeof(unsigned long long) * BS);
   l.off_cand = o;
   o = align256(o + sizeof(unsigned long long) * nb * CAP);
-  l.off_rowflag = o;
-  o = align256(o + sizeof(unsigned int) * nb);
   l.total = o;
   return l;
 }
@@ -258,7 +256,6 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
       RhArgs x;
       x.ipc = (V + ROW_CHUNK_LOGITS - 1) / ROW_CHUNK_LOGITS;
       x.nfull = V / ROW_ITER_LOGITS;
-      x.rowflag = reinterpret_cast<unsigned int*>(ws + l.off_rowflag);
       e = launch_row16_bf16(a, l.EPT, x, st);
     } else if (dtype == MLXF_DTYPE_F32)
       e = launch_f32(a, l.EPT, vecok, nst, st);

@@ -2271,42 +2271,12 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide1(Args a, int nstage) {
   decide1_row<DT, EPT, VECOK>(a, static_cast<int>(blockIdx.x), nstage, shu);
 }
 
-// Fallback of the row-histogram path: rows it flagged (rowflag[r] != 0) run
-// the first pass over their slices and the deciding step here, one
-// workgroup per row, finishing every refine level in this workgroup.
+// LDS of the row-histogram path's fallback (the per-slice path over one row,
+// first pass and deciding step in one workgroup, every refine level there).
 union FbShared {
   S1Lds s1;
   D1Shared d1;
 };
-
-// Fallback rows are rare: a small grid strides over the rows, so a call with
-// none costs one short launch.
-template <int DT, int EPT, bool VECOK>
-__global__ __launch_bounds__(THREADS, 1) void k_rowfb(Args a, const unsigned int* rowflag) {
-  __shared__ FbShared sh;
-  // a workgroup with no flagged row leaves before any of the slice path's
-  // set-up (its code is large; the common call flags nothing)
-  unsigned int any = 0u;
-  for (int r = static_cast<int>(blockIdx.x); r < a.B; r += static_cast<int>(gridDim.x)) any |= rowflag[r];
-  if (any == 0u) return;
-  for (int r = static_cast<int>(blockIdx.x); r < a.B; r += static_cast<int>(gridDim.x)) {
-    if (rowflag[r] == 0u) continue;
-    for (int s = 0; s < a.S; ++s) {
-      scan1_slice<DT, EPT, VECOK>(a, r, s, sh.s1);
-      __syncthreads();
-    }
-    // this workgroup's slice records and lists are complete; drop stale L1
-    // lines before reading them back
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    decide1_row<DT, EPT, VECOK>(a, r, 0, sh.d1);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
-}
-
-
 
 // ================================================================ host side ==
 
