@@ -39,6 +39,11 @@ namespace mlxf {
 struct RhArgs {
   int ipc;                   // pass-1 iterations per chunk (chunk length ipc * 8192 logits)
   int nfull;                 // iterations wholly inside the row
+  // split calls (few rows): one workgroup per chunk counts it into
+  // hsplit[r][c][bin]; crec[r][c] = (largest bin offset + 65536) | lowest
+  // index holding it << 32 (the index only for greedy rows)
+  unsigned int* hsplit;
+  unsigned long long* crec;
 };
 
 // One bf16 call on the row-histogram path (defined in sampler_bf16.hip).
@@ -49,8 +54,11 @@ hipError_t launch_row16_bf16(const Args& a, int ept, const RhArgs& x, hipStream_
 #ifdef MLXF_RH_STAMPS
 #define MLXF_RH_STAMP(i) \
   if (threadIdx.x == 0) mlxf_rh_stamps[blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime()
+#define MLXF_RC_STAMP(i) \
+  if (threadIdx.x == 0) mlxf_rh_stamps[8192 + blockIdx.x * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
 #else
 #define MLXF_RH_STAMP(i)
+#define MLXF_RC_STAMP(i)
 #endif
 
 namespace {
@@ -232,18 +240,30 @@ __device__ __forceinline__ void count_iter_c(unsigned char* lds, const uint4& q,
     count_iter<PAGE1, PAGE1_ADD, static_cast<unsigned>(CHB)>(lds, q, it, best, bestit);
 }
 
-// The iteration the row ends in (ITER * it < V < ITER * (it + 1)): elements
-// past the end count in the trash slot and not towards the maximum.
-__device__ __forceinline__ void count_tail(unsigned char* lds, const unsigned short* row, int V, int it, int c,
-                                           int& best, int& bestit) {
+// This thread's word of the iteration the row ends in (ITER * it < V <
+// ITER * (it + 1)): a vector load when its 8 elements are all in the row,
+// element by element for the one word holding the row end, zeros past it.
+__device__ __forceinline__ uint4 tail_word(const unsigned short* row, int V, int it) {
   const int p0 = it * ITER + static_cast<int>(threadIdx.x) * 8;
-  unsigned int w[4];
+  if (p0 + 8 <= V) return reinterpret_cast<const uint4*>(row)[static_cast<size_t>(it) * NT + threadIdx.x];
+  unsigned int w[4] = {0u, 0u, 0u, 0u};
+  if (p0 < V) {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const unsigned int lo = p0 + 2 * k < V ? row[p0 + 2 * k] : 0u;
-    const unsigned int hi = p0 + 2 * k + 1 < V ? row[p0 + 2 * k + 1] : 0u;
-    w[k] = lo | (hi << 16);
+    for (int k = 0; k < 4; ++k) {
+      const unsigned int lo = p0 + 2 * k < V ? row[p0 + 2 * k] : 0u;
+      const unsigned int hi = p0 + 2 * k + 1 < V ? row[p0 + 2 * k + 1] : 0u;
+      w[k] = lo | (hi << 16);
+    }
   }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Counts the tail word q (from tail_word): elements past the end count in the
+// trash slot and not towards the maximum.
+__device__ __forceinline__ void count_tail(unsigned char* lds, const uint4& q, int V, int it, int c, int& best,
+                                           int& bestit) {
+  const int p0 = it * ITER + static_cast<int>(threadIdx.x) * 8;
+  const unsigned int w[4] = {q.x, q.y, q.z, q.w};
   constexpr unsigned int XT = static_cast<unsigned>(B_TRASH - (NWIN + 1));
   int mf = -32768;
 #pragma unroll
@@ -276,6 +296,9 @@ __device__ __forceinline__ void count_row(unsigned char* lds, const unsigned sho
                                           int& best, int& bestit) {
   const int tid = threadIdx.x;
   const uint4* rv = reinterpret_cast<const uint4*>(row);
+  const bool has_tail = nfull * ITER < V;
+  uint4 tq = make_uint4(0u, 0u, 0u, 0u);
+  if (has_tail) tq = tail_word(row, V, nfull);  // requested first: its latency hides behind the row
   uint4 buf[D];
 #pragma unroll
   for (int j = 0; j < D; ++j)
@@ -297,10 +320,60 @@ __device__ __forceinline__ void count_row(unsigned char* lds, const unsigned sho
       }
     }
   }
-  if (nfull * ITER < V) {
+  if (has_tail) {
     const int c = (nfull >= ipc) + (nfull >= 2 * ipc) + (nfull >= 3 * ipc);
-    count_tail(lds, row, V, nfull, c, best, bestit);
+    count_tail(lds, tq, V, nfull, c, best, bestit);
   }
+}
+
+// Pass 1 over one chunk (iterations [it0, it1), plus the row's last partial
+// iteration when has_tail) into the histogram at the start of lds; the same
+// register ring as count_row.
+template <int D>
+__device__ __forceinline__ void count_chunk(unsigned char* lds, const unsigned short* row, int V, int it0, int it1,
+                                            bool has_tail, int& best, int& bestit) {
+  const int tid = threadIdx.x;
+  const uint4* rv = reinterpret_cast<const uint4*>(row);
+  uint4 tq = make_uint4(0u, 0u, 0u, 0u);
+  if (has_tail) tq = tail_word(row, V, it1);
+  uint4 buf[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j)
+    if (it0 + j < it1) buf[j] = rv[static_cast<size_t>(it0 + j) * NT + tid];
+  {
+    uint4* h4 = reinterpret_cast<uint4*>(lds);
+    for (int i = tid; i < CHW / 4; i += NT) h4[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  __syncthreads();
+  for (int it = it0; it < it1; it += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int i = it + j;
+      if (i < it1) {
+        const uint4 q = buf[j];
+        if (i + D < it1) buf[j] = rv[static_cast<size_t>(i + D) * NT + tid];
+        count_iter<0u, 0u, 0u>(lds, q, i, best, bestit);
+      }
+    }
+  }
+  if (has_tail) count_tail(lds, tq, V, it1, 0, best, bestit);
+}
+
+// Lowest index in this thread's 8 elements of iteration it whose bin is b
+// (INT_MAX if none).
+__device__ __forceinline__ int first_at(const unsigned short* row, int V, int it, int b) {
+  int myarg = INT_MAX;
+  const int p0 = it * ITER + static_cast<int>(threadIdx.x) * 8;
+  for (int j = 0; j < 8 && myarg == INT_MAX; j += 2) {
+    const unsigned int lo = p0 + j < V ? row[p0 + j] : 0u;
+    const unsigned int hi = p0 + j + 1 < V ? row[p0 + j + 1] : 0u;
+    const unsigned int b2 = bins2(lo | (hi << 16));
+    if (p0 + j < V && static_cast<int>(b2 & 0xffffu) == b)
+      myarg = p0 + j;
+    else if (p0 + j + 1 < V && static_cast<int>(b2 >> 16) == b)
+      myarg = p0 + j + 1;
+  }
+  return myarg;
 }
 
 __device__ __forceinline__ unsigned int hcount(const unsigned int* hist, int c, int b) {
@@ -402,7 +475,54 @@ __device__ __noinline__ void row_fallback(__attribute__((address_space(4))) cons
 
 constexpr int RH_DEPTH = 6;  // pass-1 iterations in flight per thread (96 KB per workgroup)
 
-template <int DT, int EPT>
+// Split calls, first kernel: workgroup (r, c) counts chunk c of row r into
+// hsplit[r][c] and records the chunk's largest bin (and, for a greedy row, the
+// lowest index holding it) in crec[r][c].  Workgroup ids are laid out so that
+// a row's four chunks and its deciding workgroup (k_row16, id r) share an XCD
+// (id mod 8 = r mod 8).
+template <int DT>
+__global__ __launch_bounds__(rh::NT, 1) void k_cnt16(Args a, RhArgs x) {
+  using namespace rh;
+  __shared__ __align__(16) unsigned char lds[CHB];
+  __shared__ int red[NWV];
+  const int tid = threadIdx.x;
+  const int id = static_cast<int>(blockIdx.x);
+  const int grp = id / (8 * NCH), rem = id - grp * (8 * NCH);
+  const int c = rem >> 3, r = grp * 8 + (rem & 7);
+  if (r >= a.B) return;
+  const int V = a.V;
+  const Mode md = decode<DT>(a, r);
+  const unsigned short* row = static_cast<const unsigned short*>(row_ptr<DT>(a, r));
+  // chunk c: iterations [c * ipc, (c + 1) * ipc) of the nfull whole ones, and
+  // the partial last iteration (index nfull) when it falls in this chunk
+  const int it0 = min(c * x.ipc, x.nfull), it1 = min((c + 1) * x.ipc, x.nfull);
+  const bool has_tail = x.nfull * ITER < V && x.nfull >= c * x.ipc && x.nfull < (c + 1) * x.ipc;
+  int best = -(NWIN + 1) - 1;
+  int bestit = -1;
+  MLXF_RC_STAMP(0);
+  count_chunk<RH_DEPTH>(lds, row, V, it0, it1, has_tail, best, bestit);
+  __syncthreads();
+  MLXF_RC_STAMP(1);
+  const int cmax = bmax_i(best, red);  // bin offset; -(NWIN + 2) for an empty chunk
+  int cid = INT_MAX;
+  if (!md.sampling) {
+    const int myarg = best == cmax && bestit >= 0 ? first_at(row, V, bestit, cmax + NWIN + 1) : INT_MAX;
+    cid = bmin_i(myarg, red);
+  }
+  MLXF_RC_STAMP(2);
+  uint4* dst = reinterpret_cast<uint4*>(x.hsplit + (static_cast<size_t>(r) * NCH + c) * CHW);
+  const uint4* src = reinterpret_cast<const uint4*>(lds);
+  for (int i = tid; i < CHW / 4; i += NT) dst[i] = src[i];
+  MLXF_RC_STAMP(3);
+  if (tid == 0)
+    x.crec[r * NCH + c] = static_cast<unsigned long long>(static_cast<unsigned>(cmax + 65536)) |
+                          (static_cast<unsigned long long>(static_cast<unsigned>(cid)) << 32);
+}
+
+// SPLIT: the row's chunk histograms come from k_cnt16 (loaded into the LDS
+// layout pass 1 builds), the row maximum and a greedy row's index from its
+// chunk records; otherwise pass 1 counts the whole row here.
+template <int DT, int EPT, bool SPLIT>
 __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
   using namespace rh;
   __shared__ __align__(16) unsigned char lds[LDS_BYTES];
@@ -415,35 +535,61 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
   const unsigned short* row = static_cast<const unsigned short*>(row_ptr<DT>(a, r));
 
   MLXF_RH_STAMP(0);
-  // ---- pass 1: every element counted once
-  int best = -(NWIN + 1) - 1;  // (bin offset; below every bin)
-  int bestit = -1;
-  count_row<RH_DEPTH>(lds, row, V, x.ipc, x.nfull, best, bestit);
-  __syncthreads();
-  MLXF_RH_STAMP(1);
-
-  // ---- the row maximum (its bin); its lowest index only for greedy rows
-  const int bmax = bmax_i(best, &sc.ir[0][0]) + NWIN + 1;
-  bool fb = bmax == B_POSHUGE || bmax == B_TINY || bmax == B_NEGHUGE;
-  const float M = bin_value(bmax);
+  int bmax;
   int id = -1;
-  if (!md.sampling) {
-    int myarg = INT_MAX;
-    if (best + NWIN + 1 == bmax && bestit >= 0) {
-      const int p0 = bestit * ITER + tid * 8;
-      for (int j = 0; j < 8 && myarg == INT_MAX; j += 2) {
-        const unsigned int lo = p0 + j < V ? row[p0 + j] : 0u;
-        const unsigned int hi = p0 + j + 1 < V ? row[p0 + j + 1] : 0u;
-        const unsigned int b2 = bins2(lo | (hi << 16));
-        if (p0 + j < V && static_cast<int>(b2 & 0xffffu) == bmax)
-          myarg = p0 + j;
-        else if (p0 + j + 1 < V && static_cast<int>(b2 >> 16) == bmax)
-          myarg = p0 + j + 1;
-      }
+  bool fb;
+  if constexpr (SPLIT) {
+    static_assert(HIST_BYTES % 16 == 0, "chunk histograms as 16-byte words");
+    constexpr int NW = static_cast<int>(HIST_BYTES / 16);
+    // straight from global memory into LDS (global_load_lds_dwordx4: lane l
+    // of a wave writes 16 bytes at the wave's LDS base + 16 l), no registers
+    const uint4* src = reinterpret_cast<const uint4*>(x.hsplit + static_cast<size_t>(r) * NCH * CHW);
+    constexpr int NK = (NW + NT - 1) / NT;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      const int i = k * NT + tid;
+      if (i < NW)
+        __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src + i),
+                                         (__attribute__((address_space(3))) void*)(lds + 16 * (k * NT + (tid & ~63))), 16, 0, 0);
     }
-    id = bmin_i(myarg, &sc.ir[0][0]);
-    fb = fb || id == INT_MAX;
+    unsigned long long cr[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) cr[c] = x.crec[r * NCH + c];
+    __builtin_amdgcn_s_waitcnt(0);
+    // the largest bin over the chunks; the first chunk holding it has the
+    // row's lowest index of it
+    int cm = -65536;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) cm = max(cm, static_cast<int>(static_cast<unsigned>(cr[c])) - 65536);
+    bmax = cm + NWIN + 1;
+    fb = bmax == B_POSHUGE || bmax == B_TINY || bmax == B_NEGHUGE;
+    if (!md.sampling) {
+      id = INT_MAX;
+#pragma unroll
+      for (int c = NCH - 1; c >= 0; --c)
+        if (static_cast<int>(static_cast<unsigned>(cr[c])) - 65536 == cm) id = static_cast<int>(cr[c] >> 32);
+      fb = fb || id == INT_MAX;
+    }
+    __syncthreads();
+    MLXF_RH_STAMP(1);
+  } else {
+    // ---- pass 1: every element counted once
+    int best = -(NWIN + 1) - 1;  // (bin offset; below every bin)
+    int bestit = -1;
+    count_row<RH_DEPTH>(lds, row, V, x.ipc, x.nfull, best, bestit);
+    __syncthreads();
+    MLXF_RH_STAMP(1);
+
+    // ---- the row maximum (its bin); its lowest index only for greedy rows
+    bmax = bmax_i(best, &sc.ir[0][0]) + NWIN + 1;
+    fb = bmax == B_POSHUGE || bmax == B_TINY || bmax == B_NEGHUGE;
+    if (!md.sampling) {
+      const int myarg = best + NWIN + 1 == bmax && bestit >= 0 ? first_at(row, V, bestit, bmax) : INT_MAX;
+      id = bmin_i(myarg, &sc.ir[0][0]);
+      fb = fb || id == INT_MAX;
+    }
   }
+  const float M = bin_value(bmax);
 
   // the thread's bins (descending from the top) and their counts
   int cnt[BPT];
@@ -858,11 +1004,18 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
                         (__attribute__((address_space(3))) unsigned char*)lds);
 }
 
-// One call on the row-histogram path: one launch, k_row16 over every row.
+// One call on the row-histogram path: k_row16 over every row; with few rows
+// (x.hsplit set) the chunks are first counted in parallel by k_cnt16.
 template <int DT, int EPT>
 hipError_t launch_row16(const Args& a, const RhArgs& x, hipStream_t st) {
   static_assert(sizeof(FbShared) <= rh::LDS_BYTES, "the fallback's LDS must fit in the histograms'");
-  hipLaunchKernelGGL((k_row16<DT, EPT>), dim3(static_cast<unsigned int>(a.B)), dim3(rh::NT), 0, st, a, x);
+  if (x.hsplit) {
+    const unsigned int groups = static_cast<unsigned int>((a.B + 7) / 8);
+    hipLaunchKernelGGL((k_cnt16<DT>), dim3(groups * 8u * rh::NCH), dim3(rh::NT), 0, st, a, x);
+    hipLaunchKernelGGL((k_row16<DT, EPT, true>), dim3(static_cast<unsigned int>(a.B)), dim3(rh::NT), 0, st, a, x);
+  } else {
+    hipLaunchKernelGGL((k_row16<DT, EPT, false>), dim3(static_cast<unsigned int>(a.B)), dim3(rh::NT), 0, st, a, x);
+  }
   return hipGetLastError();
 }
 

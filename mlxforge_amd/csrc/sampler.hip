@@ -24,8 +24,23 @@ __global__ void k_zero(unsigned int* p, size_t n) {
 struct Layout {
   int S, L, EPT;
   size_t off_ncand, off_actcnt, off_actlist, off_rec, off_list, off_rowst, off_hcnt, off_hmass, off_above,
-      off_dsum, off_cand, total;
+      off_dsum, off_cand, off_hsplit, off_crec, total;
 };
+
+// bf16 rows with no top_logprobs take the row-histogram path (rowhist.hpp):
+// one workgroup per row counts the row into exact per-value histograms and
+// decides everything from them.  It serves every stage count alike (it has
+// no refine stages), but not the first-pass-only timing call (nst < 0).  With
+// at most ROW_SPLIT_MAX_B rows (four chunk workgroups per row still fit the
+// 256 CUs at once) the chunks are counted by their own workgroups first.
+constexpr int ROW_ITER_LOGITS = 1024 * 8;              // logits per pass-1 iteration
+constexpr int ROW_CHUNK_LOGITS = 4 * ROW_ITER_LOGITS;  // logits per chunk iteration count
+constexpr int ROW_MIN_V = 32768;
+constexpr int ROW_SPLIT_MAX_B = 64;
+bool use_row_path(int dtype, int V, int K_max, bool vecok, int nst) {
+  return dtype == MLXF_DTYPE_BF16 && K_max == 0 && vecok && nst >= 0 && V >= ROW_MIN_V;
+}
+bool row_split(int dtype, int B, int V) { return dtype == MLXF_DTYPE_BF16 && V >= ROW_MIN_V && B <= ROW_SPLIT_MAX_B; }
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
@@ -40,7 +55,7 @@ constexpr size_t CTR_BYTES_MAX = ROWS_MAX * sizeof(unsigned int) + 256;
 // EPT: the largest of {32, 16, 8} that still gives at least one workgroup per
 // CU (256) with at most MAX_S slices per row; otherwise the smallest EPT with
 // S <= MAX_S.
-Layout make_layout(int B, int V, int K_max) {
+Layout make_layout(int B, int V, int K_max, int dtype) {
   (void)K_max;
   Layout l;
   int ept = 0;
@@ -87,6 +102,12 @@ Layout make_layout(int B, int V, int K_max) {
   o = align256(o + sizeof(unsigned long long) * BS);
   l.off_cand = o;
   o = align256(o + sizeof(unsigned long long) * nb * CAP);
+  // the row-histogram path's split chunk histograms and chunk records
+  const size_t nsplit = row_split(dtype, B, V) ? nb : 0;
+  l.off_hsplit = o;
+  o = align256(o + rh::HIST_BYTES * nsplit);
+  l.off_crec = o;
+  o = align256(o + sizeof(unsigned long long) * rh::NCH * nsplit);
   l.total = o;
   return l;
 }
@@ -163,16 +184,6 @@ int host_refine_stages(int B, int V, int dtype, const float* T, const int32_t* k
   return need;
 }
 
-// bf16 rows with no top_logprobs take the row-histogram path (rowhist.hpp):
-// one workgroup per row counts the row into exact per-value histograms and
-// decides everything from them.  It serves every stage count alike (it has
-// no refine stages), but not the first-pass-only timing call (nst < 0).
-constexpr int ROW_ITER_LOGITS = 1024 * 8;              // logits per pass-1 iteration
-constexpr int ROW_CHUNK_LOGITS = 4 * ROW_ITER_LOGITS;  // logits per chunk iteration count
-constexpr int ROW_MIN_V = 32768;
-bool use_row_path(int dtype, int V, int K_max, bool vecok, int nst) {
-  return dtype == MLXF_DTYPE_BF16 && K_max == 0 && vecok && nst >= 0 && V >= ROW_MIN_V;
-}
 
 int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
                const float* d_temperature, const int32_t* d_top_k, const float* d_top_p, const float* d_min_p,
@@ -199,7 +210,7 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
       set_err(err, "mlxf: K_max > 0 needs d_out_top_ids and d_out_top_logprobs");
       return MLXF_EINVAL;
     }
-    const Layout l = make_layout(B, V, K_max);
+    const Layout l = make_layout(B, V, K_max, dtype);
     if (!d_workspace || workspace_bytes < l.total) {
       set_err(err, "mlxf: workspace is NULL or smaller than mlxf_sampler_workspace_size()");
       return MLXF_EWORKSPACE;
@@ -256,6 +267,9 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
       RhArgs x;
       x.ipc = (V + ROW_CHUNK_LOGITS - 1) / ROW_CHUNK_LOGITS;
       x.nfull = V / ROW_ITER_LOGITS;
+      const bool split = row_split(dtype, B, V);
+      x.hsplit = split ? reinterpret_cast<unsigned int*>(ws + l.off_hsplit) : nullptr;
+      x.crec = split ? reinterpret_cast<unsigned long long*>(ws + l.off_crec) : nullptr;
       e = launch_row16_bf16(a, l.EPT, x, st);
     } else if (dtype == MLXF_DTYPE_F32)
       e = launch_f32(a, l.EPT, vecok, nst, st);
@@ -334,7 +348,7 @@ int mlxf_sampler_workspace_size(int B, int V, int K_max, int dtype, size_t* byte
       set_err(err, "mlxf: bytes must not be NULL");
       return MLXF_EINVAL;
     }
-    *bytes = make_layout(B, V, K_max).total;
+    *bytes = make_layout(B, V, K_max, dtype).total;
     return MLXF_OK;
   } catch (...) {
     set_err(err, "mlxf: unexpected exception");
@@ -414,7 +428,7 @@ int mlxf_sample_noalloc(const void* d_logits, int dtype, int B, int V, int64_t r
     }
     int rc = check_shape(B, V, K_max, dtype, err);
     if (rc) return rc;
-    const size_t need = make_layout(B, V, K_max).total;
+    const size_t need = make_layout(B, V, K_max, dtype).total;
     if (need > MLXF_NOALLOC_SCRATCH_BYTES) {
       set_err(err, "mlxf: mlxf_sample_noalloc: this shape needs " + std::to_string(need) +
                        " bytes of scratch, more than its fixed " +

@@ -71,10 +71,13 @@ def _check(host, T, k, p, mp, tlp, u, label, V=None, dev=None):
     return rep
 
 
-@pytest.mark.parametrize("V", [32768, 32769, 50001, 151936, 262144])
-def test_row_kinds(V):
-    rng = np.random.default_rng(900 + V % 97)
-    B = 16
+@pytest.mark.parametrize("V,B", [(32768, 16), (32769, 16), (50001, 16), (151936, 16), (262144, 16),
+                                 (40000, 1), (65536 + 8192 * 3 + 5, 9), (151936, 80)])
+def test_row_kinds(V, B):
+    """B <= 64: split call (the chunks counted by their own workgroups, XCD
+    groups of 8 rows, a partial last group for B = 1 and 9); B = 80: one
+    workgroup per row."""
+    rng = np.random.default_rng(900 + V % 97 + B)
     z = np.empty((B, V), np.float32)
     for r in range(B):
         shape = r % 4
@@ -109,8 +112,12 @@ def test_heavy_ties_and_flat_rows():
         _check(_bits(z), T, k, p, mp, tlp, uu, "heavy ties")
 
 
-def test_fallback_rows():
-    """Rows the bins cannot decide: the fallback kernel finishes them."""
+@pytest.mark.parametrize("reps", [1, 6])
+def test_fallback_rows(reps):
+    """Rows the bins cannot decide: the per-slice fallback in the same
+    workgroup finishes them.  reps=1 (12 rows) takes the split call (chunk
+    workgroups, then one deciding workgroup per row), reps=6 (72 rows) the
+    one-workgroup-per-row call."""
     rng = np.random.default_rng(77)
     B, V = 12, 40000
     z = (rng.standard_normal((B, V)) * 2).astype(np.float32)
@@ -132,7 +139,10 @@ def test_fallback_rows():
     mp = np.array([0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.1, 0.0, 0.0, 0.5, 0.0], np.float32)
     tlp = np.zeros(B, np.int32)
     u = rng.random(B).astype(np.float32)
-    _check(bits, T, k, p, mp, tlp, u, "fallback rows")
+    if reps > 1:
+        bits, T, k, p, mp, tlp = (np.concatenate([v] * reps) for v in (bits, T, k, p, mp, tlp))
+        u = rng.random(B * reps).astype(np.float32)
+    _check(np.ascontiguousarray(bits), T, k, p, mp, tlp, u, f"fallback rows x{reps}")
 
 
 def test_padded_rows_and_benchmark_configs():
