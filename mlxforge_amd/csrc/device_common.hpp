@@ -392,6 +392,50 @@ __device__ __forceinline__ unsigned long long wave_incl_scan_dpp(unsigned long l
   return x;
 }
 
+// Inclusive scan within each row of 16 lanes (row_shr steps only; lanes
+// without a source add 0).  Whole wave active.
+__device__ __forceinline__ int row_incl_scan16(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);  // row_shr:8
+  return x;
+}
+__device__ __forceinline__ unsigned long long row_incl_scan16(unsigned long long x) {
+  x += dpp_u64<0x111, 0xf, true>(x);
+  x += dpp_u64<0x112, 0xf, true>(x);
+  x += dpp_u64<0x114, 0xf, true>(x);
+  x += dpp_u64<0x118, 0xf, true>(x);
+  return x;
+}
+
+// Butterfly sum / max / min within each row of 16 lanes: every lane of a row
+// ends with its row's result.  Whole wave active.
+template <typename T>
+__device__ __forceinline__ T row_sum16(T x) {
+  x += xshf<8>(x);
+  x += xshf<4>(x);
+  x += xshf<2>(x);
+  x += xshf<1>(x);
+  return x;
+}
+template <typename T>
+__device__ __forceinline__ T row_max16(T x) {
+  x = max(x, xshf<8>(x));
+  x = max(x, xshf<4>(x));
+  x = max(x, xshf<2>(x));
+  x = max(x, xshf<1>(x));
+  return x;
+}
+template <typename T>
+__device__ __forceinline__ T row_min16(T x) {
+  x = min(x, xshf<8>(x));
+  x = min(x, xshf<4>(x));
+  x = min(x, xshf<2>(x));
+  x = min(x, xshf<1>(x));
+  return x;
+}
+
 // Exclusive block scan of an integer (int or 64-bit) for an lds array that no
 // thread of the block has read since the last barrier: one barrier; *total is
 // the block sum.  lds: WAVES entries.

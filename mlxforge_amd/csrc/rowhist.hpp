@@ -54,10 +54,13 @@ hipError_t launch_row16_bf16(const Args& a, int ept, const RhArgs& x, hipStream_
 #ifdef MLXF_RH_STAMPS
 #define MLXF_RH_STAMP(i) \
   if (threadIdx.x == 0) mlxf_rh_stamps[blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime()
+#define MLXF_RH_WSTAMP(i) \
+  if ((threadIdx.x & 63) == 0) mlxf_rh_stamps[16384 + (blockIdx.x * 16 + (threadIdx.x >> 6)) * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
 #define MLXF_RC_STAMP(i) \
   if (threadIdx.x == 0) mlxf_rh_stamps[8192 + blockIdx.x * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
 #else
 #define MLXF_RH_STAMP(i)
+#define MLXF_RH_WSTAMP(i)
 #define MLXF_RC_STAMP(i)
 #endif
 
@@ -90,11 +93,14 @@ constexpr size_t HIST_BYTES = static_cast<size_t>(NCH) * CHB;
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
+constexpr int SPARSE = 512;  // largest sparse draw list (elements at or above the cutoff in the chunk)
 struct Scratch {
   unsigned long long u64r[NWV][NCH];
   double dr[NWV];
-  int ir[NWV][2];
   unsigned int ur[NWV][NCH];
+  unsigned int un[NWV][NCH];
+  unsigned int lst[SPARSE];
+  int ir[NWV][2];
   unsigned long long sel64[8];
   int sel[16];
 };
@@ -139,7 +145,11 @@ __device__ __forceinline__ float bin_value(int b) {
 // order from the top, BPT per thread; negative = none.
 __device__ __forceinline__ int own_bin(int tid, int j) { return NBIN - 1 - (tid * BPT + j); }
 
-// ---- block primitives for NT threads (16 waves)
+// ---- block primitives for NT threads (16 waves).  The 16 per-wave values
+// are combined by lanes 0..15 of every wave (one LDS read each and a 4-step
+// row reduction), not by a loop in every thread: at 16 waves on 4 SIMDs each
+// VALU instruction of a thread costs 16 cycles of a SIMD.
+static_assert(NWV == 16, "the wave combine is one row of 16 lanes");
 template <typename T>
 __device__ __forceinline__ T bsum(T x, T* red) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -147,10 +157,7 @@ __device__ __forceinline__ T bsum(T x, T* red) {
   __syncthreads();
   if (lane == 0) red[wid] = x;
   __syncthreads();
-  T t = red[0];
-#pragma unroll
-  for (int w = 1; w < NWV; ++w) t += red[w];
-  return t;
+  return rdl(row_sum16(lane < NWV ? red[lane & (NWV - 1)] : T(0)), 0);
 }
 __device__ __forceinline__ int bmin_i(int x, int* red) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -158,10 +165,7 @@ __device__ __forceinline__ int bmin_i(int x, int* red) {
   __syncthreads();
   if (lane == 0) red[wid] = x;
   __syncthreads();
-  int t = red[0];
-#pragma unroll
-  for (int w = 1; w < NWV; ++w) t = min(t, red[w]);
-  return t;
+  return rdl(row_min16(red[lane & (NWV - 1)]), 0);
 }
 __device__ __forceinline__ int bmax_i(int x, int* red) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -169,10 +173,7 @@ __device__ __forceinline__ int bmax_i(int x, int* red) {
   __syncthreads();
   if (lane == 0) red[wid] = x;
   __syncthreads();
-  int t = red[0];
-#pragma unroll
-  for (int w = 1; w < NWV; ++w) t = max(t, red[w]);
-  return t;
+  return rdl(row_max16(red[lane & (NWV - 1)]), 0);
 }
 // Exclusive scan over threads in index order; *total = the block sum.
 template <typename T>
@@ -182,15 +183,10 @@ __device__ __forceinline__ T bscan(T x, T* red, T* total) {
   __syncthreads();
   if (lane == 63) red[wid] = inc;
   __syncthreads();
-  T off = 0, tot = 0;
-#pragma unroll
-  for (int w = 0; w < NWV; ++w) {
-    const T t = red[w];
-    off += w < wid ? t : T(0);
-    tot += t;
-  }
-  *total = tot;
-  return inc - x + off;
+  const T ws = row_incl_scan16(lane < NWV ? red[lane & (NWV - 1)] : T(0));
+  *total = rdl(ws, NWV - 1);
+  const T before = rdl(ws, wid > 0 ? wid - 1 : 0);
+  return inc - x + (wid > 0 ? before : T(0));
 }
 
 // ---- pass 1: one word (two values, as bin offsets x2) into chunk histogram
@@ -258,11 +254,14 @@ __device__ __forceinline__ uint4 tail_word(const unsigned short* row, int V, int
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// Counts the tail word q (from tail_word): elements past the end count in the
+// Counts the tail word q (from tail_word).  A thread wholly past the end
+// counts nothing (all its elements in one counter would serialise the wave's
+// atomics); past-the-end elements of the word holding the end count in the
 // trash slot and not towards the maximum.
 __device__ __forceinline__ void count_tail(unsigned char* lds, const uint4& q, int V, int it, int c, int& best,
                                            int& bestit) {
   const int p0 = it * ITER + static_cast<int>(threadIdx.x) * 8;
+  if (p0 >= V) return;
   const unsigned int w[4] = {q.x, q.y, q.z, q.w};
   constexpr unsigned int XT = static_cast<unsigned>(B_TRASH - (NWIN + 1));
   int mf = -32768;
@@ -282,7 +281,7 @@ __device__ __forceinline__ void count_tail(unsigned char* lds, const uint4& q, i
     else
       count_word<PAGE1, PAGE1_ADD, static_cast<unsigned>(CHB)>(lds, x2);
   }
-  if (mf > best && p0 < V) {
+  if (mf > best) {
     best = mf;
     bestit = it;
   }
@@ -590,6 +589,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
     }
   }
   const float M = bin_value(bmax);
+  MLXF_RH_WSTAMP(0);
 
   // the thread's bins (descending from the top) and their counts
   int cnt[BPT];
@@ -601,62 +601,85 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
                     : 0;
   }
 
-  // ---- log-sum-exp of the unscaled row from the counts
-  double lse = static_cast<double>(NAN);
-  if (md.need_lse && !fb) {
-    double part = 0.0;
+  // ---- per-bin work, branch-free over the thread's bins: the log-sum-exp of
+  // the unscaled row, and for a sampling row the weight of each bin (0 for an
+  // empty one; a bin's fixed-point mass is q40 of it)
+  const int wid = tid >> 6;
+  const bool do_lse = md.need_lse && !fb;
+  const bool do_w = md.sampling && !fb;
+  float Mp = 0.0f, nc = 0.0f;
+  if (do_w) {
+    Mp = zdiv<DT>(M, md.Tr, md.y, false);
+    nc = -(Mp * LOG2E);
+  }
+  // every window value is in the fast division's range (2^-96 <= |z| < 2^100)
+  const bool fast = !md.tslow;
+  // z' of a bin: -inf for the low bin (its mass is zero, checked below), 0
+  // for the tiny bin (its elements' weights are equal, checked below)
+  auto zp_of = [&](int b) -> float {
+    if (b <= B_NEGHUGE || b >= B_POSHUGE) return -INFINITY;
+    return b == B_TINY ? 0.0f : zdiv<DT>(bin_value(b), md.Tr, md.y, fast);
+  };
+  MLXF_RH_WSTAMP(1);
+  // (the thread's 11 terms summed in fp32, relative error below 2^-20, then
+  // the block sum in fp64)
+  double part = 0.0;
+  if (do_lse) {
+    float pf = 0.0f;
 #pragma unroll
     for (int j = 0; j < BPT; ++j) {
       const int b = own_bin(tid, j);
-      if (cnt[j] > 0 && b > B_NEGHUGE) part += static_cast<double>(cnt[j]) * static_cast<double>(wexp(bin_value(b), M));
+      const float e = static_cast<float>(cnt[j]) * wexp(bin_value(b), M);
+      pf += (cnt[j] > 0 && b > B_NEGHUGE) ? e : 0.0f;
     }
-    lse = static_cast<double>(M) + log(bsum(part, sc.dr));
+    part = static_cast<double>(pf);
   }
-  MLXF_RH_STAMP(2);
-
-  if (md.sampling && !fb) {
-    const float Mp = zdiv<DT>(M, md.Tr, md.y, false);
-    const float nc = -(Mp * LOG2E);
-    // every window value is in the fast division's range (2^-96 <= |z| < 2^100)
-    const bool fast = !md.tslow;
-    // z' of a bin: -inf for the low bin (its mass is zero, checked below), 0
-    // for the tiny bin (its elements' weights are equal, checked below)
-    auto zp_of = [&](int b) -> float {
-      if (b <= B_NEGHUGE || b >= B_POSHUGE) return -INFINITY;
-      return b == B_TINY ? 0.0f : zdiv<DT>(bin_value(b), md.Tr, md.y, fast);
-    };
-    // the weight of each of the thread's bins, 0 for an empty one (a bin's
-    // fixed-point mass is q40 of it)
-    float w[BPT];
-    unsigned long long q[BPT];
+  float w[BPT];
+  unsigned long long q[BPT];
+  if (do_w) {
 #pragma unroll
     for (int j = 0; j < BPT; ++j) {
       const float z = cnt[j] > 0 ? zp_of(own_bin(tid, j)) : -INFINITY;
       w[j] = z == -INFINITY ? 0.0f : wfun(z, Mp, nc, false);
       q[j] = q40(w[j]);
     }
-    if (tid == 0) {
-      bool bad = !__builtin_isfinite(Mp);
-      if (!bad && hcount(hist, 0, B_TINY) + hcount(hist, 1, B_TINY) + hcount(hist, 2, B_TINY) +
-                          hcount(hist, 3, B_TINY) > 0u) {
-        // |z'| of a tiny value is below 2^-28 / T (rounded up by the bf16
-        // rounding); the weight's log2 offset nc must absorb it
-        const float zb = 0x1p-28f / md.Tr * 1.0078125f;
-        const int e = nc == 0.0f ? -1000 : ilogbf(nc);
-        bad = !(zb * LOG2E * 1.0001f < ldexpf(1.0f, e - 24));
-      }
-      if (!bad && hcount(hist, 0, B_NEGHUGE) + hcount(hist, 1, B_NEGHUGE) + hcount(hist, 2, B_NEGHUGE) +
-                          hcount(hist, 3, B_NEGHUGE) > 0u) {
-        // the largest value of the low bin, -256, must carry no mass
-        bad = q40(wfun(zdiv<DT>(-256.0f, md.Tr, md.y, false), Mp, nc, false)) != 0ull;
-      }
-      sc.sel[0] = bad ? 1 : 0;
-      sc.sel[3] = -1;
-      sc.sel[4] = -1;
-      sc.sel[5] = 0;
-      sc.sel[6] = INT_MAX;
+  }
+  MLXF_RH_WSTAMP(2);
+  // one barrier publishes the per-wave log-sum-exp partials and thread 0's
+  // checks of the merged bins
+  if (do_lse) {
+    part = wave_sum(part);
+    if (lane == 0) sc.dr[wid] = part;
+  }
+  if (do_w && tid == 0) {
+    bool bad = !__builtin_isfinite(Mp);
+    if (!bad && hcount(hist, 0, B_TINY) + hcount(hist, 1, B_TINY) + hcount(hist, 2, B_TINY) +
+                        hcount(hist, 3, B_TINY) > 0u) {
+      // |z'| of a tiny value is below 2^-28 / T (rounded up by the bf16
+      // rounding); the weight's log2 offset nc must absorb it
+      const float zb = 0x1p-28f / md.Tr * 1.0078125f;
+      const int e = nc == 0.0f ? -1000 : ilogbf(nc);
+      bad = !(zb * LOG2E * 1.0001f < ldexpf(1.0f, e - 24));
     }
-    __syncthreads();
+    if (!bad && hcount(hist, 0, B_NEGHUGE) + hcount(hist, 1, B_NEGHUGE) + hcount(hist, 2, B_NEGHUGE) +
+                        hcount(hist, 3, B_NEGHUGE) > 0u) {
+      // the largest value of the low bin, -256, must carry no mass
+      bad = q40(wfun(zdiv<DT>(-256.0f, md.Tr, md.y, false), Mp, nc, false)) != 0ull;
+    }
+    sc.sel[0] = bad ? 1 : 0;
+    sc.sel[3] = -1;
+    sc.sel[4] = -1;
+    sc.sel[5] = 0;
+    sc.sel[6] = INT_MAX;
+  }
+  MLXF_RH_WSTAMP(3);
+  __syncthreads();
+  MLXF_RH_WSTAMP(4);
+  double lse = static_cast<double>(NAN);
+  if (do_lse) lse = static_cast<double>(M) + log(rdl(row_sum16(lane < NWV ? sc.dr[lane & (NWV - 1)] : 0.0), 0));
+  MLXF_RH_STAMP(2);
+
+  if (do_w) {
     fb = sc.sel[0] != 0;
     MLXF_RH_STAMP(3);
 
@@ -693,7 +716,6 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         c += static_cast<int>(hcount(hist, 0, b) + hcount(hist, 1, b) + hcount(hist, 2, b) + hcount(hist, 3, b));
       return wave_sum(c);
     };
-    const int wid = tid >> 6;
 
     // the kept set so far, as published by wave 0 in sc: kb (sel[10]), the
     // partial group glo, ghi, t (sel[11..13]) and its mass (sel64[3])
@@ -740,6 +762,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
     // bin, empty bins below it changing nothing); both from one pass over the
     // bins
     if (!fb && (md.topp || md.mr > 0.0f)) {
+      MLXF_RH_STAMP(11);
       const float thr = md.mr > 0.0f ? minp_thr(md.mr, Mp, nc, false) : 0.0f;
       if (md.mr > 0.0f) {
         int lo = INT_MAX;
@@ -756,7 +779,8 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         };
         unsigned long long msum = 0ull;
 #pragma unroll
-        for (int j = 0; j < BPT; ++j) msum += mass(j);
+        for (int j = 0; j < BPT; ++j)
+          if (cnt[j] > 0) msum += mass(j);
         unsigned long long Wk;
         const unsigned long long run = bscan(msum, &sc.u64r[0][0], &Wk);
         PW = static_cast<unsigned long long>(ceil(static_cast<double>(md.pr) * static_cast<double>(Wk)));
@@ -775,6 +799,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         }
       }
       __syncthreads();
+      MLXF_RH_STAMP(12);
       if (wid == 0) {
         int kb = klo, glo = 0, ghi = -1;
         unsigned int t = 0u;
@@ -817,6 +842,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
           sc.sel64[3] = wt;
         }
       }
+      MLXF_RH_STAMP(13);
       __syncthreads();
       fb = sc.sel[0] != 0;
       kp.kb = sc.sel[10];
@@ -833,38 +859,50 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
     if (!fb) {
       // ---- per-chunk kept masses and the chunk holding u * W
       const int need_lo = kp.t > 0u ? kp.glo : kp.kb;
+      // per chunk: kept mass kc, partial-group elements gc, and elements of
+      // the wholly kept bins nk
       unsigned long long kc[NCH];
-      unsigned int gc[NCH];
+      unsigned int gc[NCH], nk[NCH];
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         kc[c] = 0ull;
         gc[c] = 0u;
+        nk[c] = 0u;
       }
-      if (own_bin(tid, 0) >= need_lo) {
+      // a wave whose highest bin is below every kept one adds nothing
+      if (own_bin(wid * 64, 0) >= need_lo) {
+        if (own_bin(tid, 0) >= need_lo) {
 #pragma unroll
-        for (int j = 0; j < BPT; ++j) {
-          const int b = own_bin(tid, j);
-          if (b < 0 || cnt[j] == 0) continue;
-          if (b >= kp.kb) {
-            const unsigned long long qq = q[j];
+          for (int j = 0; j < BPT; ++j) {
+            const int b = own_bin(tid, j);
+            if (b < 0 || cnt[j] == 0) continue;
+            if (b >= kp.kb) {
+              const unsigned long long qq = q[j];
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) kc[c] += static_cast<unsigned long long>(hcount(hist, c, b)) * qq;
-          } else if (kp.t > 0u && b >= kp.glo && b <= kp.ghi) {
+              for (int c = 0; c < NCH; ++c) {
+                const unsigned int h = hcount(hist, c, b);
+                kc[c] += static_cast<unsigned long long>(h) * qq;
+                nk[c] += h;
+              }
+            } else if (kp.t > 0u && b >= kp.glo && b <= kp.ghi) {
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) gc[c] += hcount(hist, c, b);
+              for (int c = 0; c < NCH; ++c) gc[c] += hcount(hist, c, b);
+            }
           }
         }
-      }
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        kc[c] = wave_sum(kc[c]);
-        gc[c] = static_cast<unsigned int>(wave_sum(static_cast<int>(gc[c])));
+        for (int c = 0; c < NCH; ++c) {
+          kc[c] = wave_sum(kc[c]);
+          gc[c] = static_cast<unsigned int>(wave_sum(static_cast<int>(gc[c])));
+          nk[c] = static_cast<unsigned int>(wave_sum(static_cast<int>(nk[c])));
+        }
       }
       if (lane == 0) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
           sc.u64r[wid][c] = kc[c];
           sc.ur[wid][c] = gc[c];
+          sc.un[wid][c] = nk[c];
         }
       }
       __syncthreads();
@@ -872,12 +910,13 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         // lane c < NCH: chunk c's kept mass; the first t ties in index order
         // are spread over the chunks in order
         unsigned long long K = 0ull;
-        int G = 0;
+        int G = 0, N = 0;
         if (lane < NCH) {
 #pragma unroll
           for (int w2 = 0; w2 < NWV; ++w2) {
             K += sc.u64r[w2][lane];
             G += static_cast<int>(sc.ur[w2][lane]);
+            N += static_cast<int>(sc.un[w2][lane]);
           }
         }
         const int before = wave_incl_scan_dpp(G) - G;
@@ -893,10 +932,17 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
           Tu = W - 1ull;
         const unsigned long long hit = __ballot(lane < NCH && K > 0ull && cumi > Tu);
         const int cs = hit ? __ffsll(static_cast<long long>(hit)) - 1 : -1;
+        // (lane reads with the whole wave active: a value computed only in
+        // the lane-0 branch would not exist in lane cs)
+        const int csr = cs >= 0 ? cs : 0;
+        const int tks = static_cast<int>(rdl(tk, csr));
+        const int ngs = rdl(N + G, csr);  // chunk cs's elements at or above need_lo
+        const unsigned long long rems = Tu - (rdl(cumi, csr) - rdl(K, csr));
         if (lane == 0) {
           sc.sel[1] = cs;
-          sc.sel[2] = cs >= 0 ? static_cast<int>(rdl(tk, cs)) : 0;
-          sc.sel64[0] = cs >= 0 ? Tu - (rdl(cumi, cs) - rdl(K, cs)) : 0ull;
+          sc.sel[2] = cs >= 0 ? tks : 0;
+          sc.sel[14] = cs >= 0 ? ngs : 0;
+          sc.sel64[0] = cs >= 0 ? rems : 0ull;
         }
       }
       __syncthreads();
@@ -919,6 +965,71 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
           for (int k = 0; k < WG; ++k)
             if (k < EPTW / 8) wq[k] = rv[k];
         }
+        if (sc.sel[14] <= SPARSE && EPTW <= 64) {
+          // ---- sparse draw: the chunk's few elements at or above need_lo,
+          // listed in index order (each thread's qualifying elements at its
+          // exclusive-scan offset), then walked by wave 0
+          unsigned long long mk = 0ull;  // bit e: element c0 + e qualifies
+          if (whole) {
+#pragma unroll
+            for (int k = 0; k < WG; ++k) {
+              if (k < EPTW / 8) {
+                const unsigned int w4[4] = {wq[k].x, wq[k].y, wq[k].z, wq[k].w};
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                  const unsigned int b2 = bins2(w4[h]);
+                  mk |= static_cast<unsigned long long>(static_cast<int>(b2 & 0xffffu) >= need_lo) << (8 * k + 2 * h);
+                  mk |= static_cast<unsigned long long>(static_cast<int>(b2 >> 16) >= need_lo) << (8 * k + 2 * h + 1);
+                }
+              }
+            }
+          } else {
+            for (int e = 0; e < EPTW; ++e) {
+              const int p = c0 + e;
+              if (p < V && static_cast<int>(bins2(row[p]) & 0xffffu) >= need_lo) mk |= 1ull << e;
+            }
+          }
+          int ntot;
+          int o = bscan(static_cast<int>(__builtin_popcountll(mk)), &sc.ir[0][0], &ntot);
+          while (mk) {
+            const int e = __ffsll(static_cast<long long>(mk)) - 1;
+            mk &= mk - 1ull;
+            if (o < SPARSE) sc.lst[o] = static_cast<unsigned int>(c0 + e);
+            ++o;
+          }
+          __syncthreads();
+          if (wid == 0) {
+            // (ntot equals the histograms' count; the guard only keeps the
+            // list reads in bounds)
+            const int n = min(ntot, SPARSE);
+            unsigned long long carry = 0ull;
+            unsigned int tie_rank = 0u;
+            int found = -1;
+            for (int i0 = 0; i0 < n && found < 0; i0 += 64) {
+              const bool valid = i0 + lane < n;
+              const int p = valid ? static_cast<int>(sc.lst[i0 + lane]) : 0;
+              const int b = valid ? static_cast<int>(bins2(row[p]) & 0xffffu) : B_TRASH;
+              unsigned long long mm = 0ull;
+              if (valid && b >= kp.kb) mm = q40(wfun(zp_of(b), Mp, nc, false));
+              if (kp.t > 0u) {
+                const bool tie = valid && b >= kp.glo && b <= kp.ghi;
+                const unsigned long long tb = __ballot(tie);
+                const unsigned int rk = tie_rank + __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(tb >> 32),
+                                                                            __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(tb), 0u));
+                if (tie && rk < tkc) mm = kp.wt;
+                tie_rank += static_cast<unsigned int>(__builtin_popcountll(tb));
+              }
+              const unsigned long long c = carry + wave_incl_scan_dpp(mm);
+              const int pk = wave_min((mm > 0ull && c > rem) ? p : INT_MAX);
+              if (pk != INT_MAX) found = pk;
+              carry = rdl(c, 63);
+            }
+            if (lane == 0) sc.sel[9] = ntot == sc.sel[14] ? found : -1;
+          }
+          __syncthreads();
+          id = sc.sel[9];
+          fb = id < 0;
+        } else {
         // the weight table over the dead histograms: each wholly kept bin's
         // mass at byte 8 * bin, 0 for every other bin
         unsigned long long* tab = reinterpret_cast<unsigned long long*>(lds);
@@ -930,10 +1041,12 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         }
         if (tid == 0) tab[B_TRASH] = 0ull;
         __syncthreads();
+        MLXF_RH_WSTAMP(5);
         const unsigned long long km0 = kp.t > 0u ? walk_sum<true, WG>(row, V, c0, EPTW, tab, kp, wq, whole)
                                                  : walk_sum<false, WG>(row, V, c0, EPTW, tab, kp, wq, whole);
         unsigned long long km = km0 & 0x00ffffffffffffffull;  // (mass; tie count in the top byte, see walk_sum)
         const int gt = static_cast<int>(km0 >> 56);
+        MLXF_RH_WSTAMP(6);
         MLXF_RH_STAMP(8);
         int gex = 0;
         if (kp.t > 0u) {
@@ -953,6 +1066,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
           sc.sel64[1] = rem - kex;
         }
         __syncthreads();
+        MLXF_RH_WSTAMP(7);
         MLXF_RH_STAMP(9);
         const int holder = sc.sel[7];
         if (holder >= 0 && tid < 64) {
@@ -986,6 +1100,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         __syncthreads();
         id = holder >= 0 ? sc.sel[9] : -1;
         fb = id < 0;
+        }
       }
     }
   }

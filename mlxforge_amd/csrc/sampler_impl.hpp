@@ -1425,9 +1425,14 @@ __device__ __forceinline__ unsigned long long cmass(int n, PRED pred, float Mp, 
 // one tie's mass (wt), at least 1, at most g.
 __device__ __forceinline__ unsigned int ties_kept(unsigned long long need, unsigned long long wt, unsigned int g) {
   unsigned long long t = g;
-  if (wt > 0) {
-    const unsigned long long nd = (need + wt - 1) / wt;
-    t = nd < t ? nd : t;
+  // ceil(need / wt) when it is at most g: a double quotient (within one of
+  // the integer one, the quotient being below 2^32) corrected by exact
+  // products, in place of a 64-bit integer division
+  if (wt > 0 && __umul64hi(g, wt) == 0ull && need < static_cast<unsigned long long>(g) * wt) {
+    unsigned long long nd = static_cast<unsigned long long>(ceil(static_cast<double>(need) / static_cast<double>(wt)));
+    if (nd > 0 && (nd - 1) * wt >= need) --nd;
+    if (nd * wt < need) ++nd;
+    t = nd;
   }
   if (t == 0) t = 1;
   return static_cast<unsigned int>(t);
