@@ -716,6 +716,88 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         c += static_cast<int>(hcount(hist, 0, b) + hcount(hist, 1, b) + hcount(hist, 2, b) + hcount(hist, 3, b));
       return wave_sum(c);
     };
+    // (wave 0, whole wave) the chunk holding the draw, from lane c < NCH's
+    // chunk c kept mass K, partial-group elements G and kept-bin elements N:
+    // sel[1] = the chunk, sel[2] = its kept ties, sel[14] = its elements at
+    // or above the cutoff, sel64[0] = the draw's offset into its kept mass
+    auto chunk_pick = [&](unsigned long long K, int G, int N, const Kept& k) {
+      // the first t ties in index order are spread over the chunks in order
+      const int before = wave_incl_scan_dpp(G) - G;
+      const unsigned int want = k.t > static_cast<unsigned>(before) ? k.t - static_cast<unsigned>(before) : 0u;
+      const unsigned int tk = want < static_cast<unsigned>(G) ? want : static_cast<unsigned>(G);
+      K += static_cast<unsigned long long>(tk) * k.wt;
+      const unsigned long long cumi = wave_incl_scan_dpp(K);
+      const unsigned long long W = rdl(cumi, 63);
+      unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(W));
+      if (W == 0ull)
+        Tu = 0ull;
+      else if (Tu >= W)
+        Tu = W - 1ull;
+      const unsigned long long hit = __ballot(lane < NCH && K > 0ull && cumi > Tu);
+      const int cs = hit ? __ffsll(static_cast<long long>(hit)) - 1 : -1;
+      // (lane reads with the whole wave active: a value computed only in
+      // the lane-0 branch would not exist in lane cs)
+      const int csr = cs >= 0 ? cs : 0;
+      const int tks = static_cast<int>(rdl(tk, csr));
+      const int ngs = rdl(N + G, csr);
+      const unsigned long long rems = Tu - (rdl(cumi, csr) - rdl(K, csr));
+      if (lane == 0) {
+        sc.sel[1] = cs;
+        sc.sel[2] = cs >= 0 ? tks : 0;
+        sc.sel[14] = cs >= 0 ? ngs : 0;
+        sc.sel64[0] = cs >= 0 ? rems : 0ull;
+      }
+    };
+    // (wave 0, whole wave) chunk_pick for a kept range [need, bmax] of at most
+    // 4 x 64 bins, lane i taking bins bmax - i - 64 j (weights recomputed, a
+    // bin with no elements skipped): no other wave takes part.  False (nothing
+    // done) for a wider range.
+    auto narrow_chunks = [&](const Kept& k) -> bool {
+      const int need = k.t > 0u ? k.glo : k.kb;
+      const int nr = (bmax - need + 64) >> 6;  // rounds of 64 bins
+      if (nr > 4) return false;
+      unsigned long long kc[NCH];
+      int gc[NCH], nk[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        kc[c] = 0ull;
+        gc[c] = 0;
+        nk[c] = 0;
+      }
+      for (int j = 0; j < nr; ++j) {
+        const int b = bmax - lane - 64 * j;
+        const bool in = b >= need;
+        unsigned int h[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) h[c] = in ? hcount(hist, c, b) : 0u;
+        if ((h[0] | h[1] | h[2] | h[3]) != 0u) {
+          if (b >= k.kb) {
+            const unsigned long long qq = q40(wfun(zp_of(b), Mp, nc, false));
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+              kc[c] += static_cast<unsigned long long>(h[c]) * qq;
+              nk[c] += static_cast<int>(h[c]);
+            }
+          } else {
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) gc[c] += static_cast<int>(h[c]);
+          }
+        }
+      }
+      unsigned long long K = 0ull;
+      int G = 0, N = 0;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const unsigned long long kcs = wave_sum(kc[c]);
+        const int gcs = wave_sum(gc[c]);
+        const int nks = wave_sum(nk[c]);
+        K = lane == c ? kcs : K;
+        G = lane == c ? gcs : G;
+        N = lane == c ? nks : N;
+      }
+      chunk_pick(K, G, N, k);
+      return true;
+    };
 
     // the kept set so far, as published by wave 0 in sc: kb (sel[10]), the
     // partial group glo, ghi, t (sel[11..13]) and its mass (sel64[3])
@@ -745,9 +827,22 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         const int bk = sc.sel[3];
         int glo = 0, ghi = 0;
         if (bk >= 0) group_of(bk, &glo, &ghi);
+        const bool bad = bk < 0 || near_merged(glo, ghi);
+        bool done = false;
+        if (!bad && !(md.topp || md.mr > 0.0f)) {
+          // the kept set is final: every bin >= glo
+          Kept k2;
+          k2.kb = glo;
+          k2.glo = 0;
+          k2.ghi = -1;
+          k2.t = 0u;
+          k2.wt = 0ull;
+          done = narrow_chunks(k2);
+        }
         if (lane == 0) {
           sc.sel[10] = glo;
-          sc.sel[0] = (bk < 0 || near_merged(glo, ghi)) ? 1 : 0;
+          sc.sel[0] = bad ? 1 : 0;
+          sc.sel[5] = done ? 1 : 0;
         }
       }
       __syncthreads();
@@ -833,8 +928,19 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
             t = 0u;
           }
         }
+        bool done = false;
+        if (!bad) {
+          Kept k2;
+          k2.kb = kb;
+          k2.glo = t > 0u ? glo : 0;
+          k2.ghi = t > 0u ? ghi : -1;
+          k2.t = t;
+          k2.wt = t > 0u ? wt : 0ull;
+          done = narrow_chunks(k2);
+        }
         if (lane == 0) {
           sc.sel[0] = bad ? 1 : 0;
+          sc.sel[5] = done ? 1 : 0;
           sc.sel[10] = kb;
           sc.sel[11] = glo;
           sc.sel[12] = ghi;
@@ -860,89 +966,66 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
       // ---- per-chunk kept masses and the chunk holding u * W
       const int need_lo = kp.t > 0u ? kp.glo : kp.kb;
       // per chunk: kept mass kc, partial-group elements gc, and elements of
-      // the wholly kept bins nk
-      unsigned long long kc[NCH];
-      unsigned int gc[NCH], nk[NCH];
+      // the wholly kept bins nk (unless wave 0 has picked the chunk already)
+      if (sc.sel[5] == 0) {
+        unsigned long long kc[NCH];
+        unsigned int gc[NCH], nk[NCH];
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        kc[c] = 0ull;
-        gc[c] = 0u;
-        nk[c] = 0u;
-      }
-      // a wave whose highest bin is below every kept one adds nothing
-      if (own_bin(wid * 64, 0) >= need_lo) {
-        if (own_bin(tid, 0) >= need_lo) {
+        for (int c = 0; c < NCH; ++c) {
+          kc[c] = 0ull;
+          gc[c] = 0u;
+          nk[c] = 0u;
+        }
+        // a wave whose highest bin is below every kept one adds nothing
+        if (own_bin(wid * 64, 0) >= need_lo) {
+          if (own_bin(tid, 0) >= need_lo) {
 #pragma unroll
-          for (int j = 0; j < BPT; ++j) {
-            const int b = own_bin(tid, j);
-            if (b < 0 || cnt[j] == 0) continue;
-            if (b >= kp.kb) {
-              const unsigned long long qq = q[j];
+            for (int j = 0; j < BPT; ++j) {
+              const int b = own_bin(tid, j);
+              if (b < 0 || cnt[j] == 0) continue;
+              if (b >= kp.kb) {
+                const unsigned long long qq = q[j];
 #pragma unroll
-              for (int c = 0; c < NCH; ++c) {
-                const unsigned int h = hcount(hist, c, b);
-                kc[c] += static_cast<unsigned long long>(h) * qq;
-                nk[c] += h;
+                for (int c = 0; c < NCH; ++c) {
+                  const unsigned int h = hcount(hist, c, b);
+                  kc[c] += static_cast<unsigned long long>(h) * qq;
+                  nk[c] += h;
+                }
+              } else if (kp.t > 0u && b >= kp.glo && b <= kp.ghi) {
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) gc[c] += hcount(hist, c, b);
               }
-            } else if (kp.t > 0u && b >= kp.glo && b <= kp.ghi) {
-#pragma unroll
-              for (int c = 0; c < NCH; ++c) gc[c] += hcount(hist, c, b);
             }
           }
-        }
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          kc[c] = wave_sum(kc[c]);
-          gc[c] = static_cast<unsigned int>(wave_sum(static_cast<int>(gc[c])));
-          nk[c] = static_cast<unsigned int>(wave_sum(static_cast<int>(nk[c])));
-        }
-      }
-      if (lane == 0) {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          sc.u64r[wid][c] = kc[c];
-          sc.ur[wid][c] = gc[c];
-          sc.un[wid][c] = nk[c];
-        }
-      }
-      __syncthreads();
-      if (wid == 0) {
-        // lane c < NCH: chunk c's kept mass; the first t ties in index order
-        // are spread over the chunks in order
-        unsigned long long K = 0ull;
-        int G = 0, N = 0;
-        if (lane < NCH) {
-#pragma unroll
-          for (int w2 = 0; w2 < NWV; ++w2) {
-            K += sc.u64r[w2][lane];
-            G += static_cast<int>(sc.ur[w2][lane]);
-            N += static_cast<int>(sc.un[w2][lane]);
+          for (int c = 0; c < NCH; ++c) {
+            kc[c] = wave_sum(kc[c]);
+            gc[c] = static_cast<unsigned int>(wave_sum(static_cast<int>(gc[c])));
+            nk[c] = static_cast<unsigned int>(wave_sum(static_cast<int>(nk[c])));
           }
         }
-        const int before = wave_incl_scan_dpp(G) - G;
-        const unsigned int want = kp.t > static_cast<unsigned>(before) ? kp.t - static_cast<unsigned>(before) : 0u;
-        const unsigned int tk = want < static_cast<unsigned>(G) ? want : static_cast<unsigned>(G);
-        K += static_cast<unsigned long long>(tk) * kp.wt;
-        const unsigned long long cumi = wave_incl_scan_dpp(K);
-        const unsigned long long W = rdl(cumi, 63);
-        unsigned long long Tu = static_cast<unsigned long long>(static_cast<double>(md.u) * static_cast<double>(W));
-        if (W == 0ull)
-          Tu = 0ull;
-        else if (Tu >= W)
-          Tu = W - 1ull;
-        const unsigned long long hit = __ballot(lane < NCH && K > 0ull && cumi > Tu);
-        const int cs = hit ? __ffsll(static_cast<long long>(hit)) - 1 : -1;
-        // (lane reads with the whole wave active: a value computed only in
-        // the lane-0 branch would not exist in lane cs)
-        const int csr = cs >= 0 ? cs : 0;
-        const int tks = static_cast<int>(rdl(tk, csr));
-        const int ngs = rdl(N + G, csr);  // chunk cs's elements at or above need_lo
-        const unsigned long long rems = Tu - (rdl(cumi, csr) - rdl(K, csr));
         if (lane == 0) {
-          sc.sel[1] = cs;
-          sc.sel[2] = cs >= 0 ? tks : 0;
-          sc.sel[14] = cs >= 0 ? ngs : 0;
-          sc.sel64[0] = cs >= 0 ? rems : 0ull;
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) {
+            sc.u64r[wid][c] = kc[c];
+            sc.ur[wid][c] = gc[c];
+            sc.un[wid][c] = nk[c];
+          }
+        }
+        __syncthreads();
+        if (wid == 0) {
+          // lane c < NCH: chunk c's sums over the waves
+          unsigned long long K = 0ull;
+          int G = 0, N = 0;
+          if (lane < NCH) {
+#pragma unroll
+            for (int w2 = 0; w2 < NWV; ++w2) {
+              K += sc.u64r[w2][lane];
+              G += static_cast<int>(sc.ur[w2][lane]);
+              N += static_cast<int>(sc.un[w2][lane]);
+            }
+          }
+          chunk_pick(K, G, N, kp);
         }
       }
       __syncthreads();
