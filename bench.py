@@ -9,8 +9,8 @@ Timing: hipEvents (torch.cuda.Event on the stream the library launches on)
 around K back-to-back steps after W warm-up steps; the input is rotated over
 enough copies to exceed 512 MB so neither L2 nor the 256 MB MALL holds it when
 a step starts ("cold" HBM).  A step launches the stage count the host-side
-parameters call for (mlxf_sampler_refine_stages); the generic three-stage path
-(plain mlxf_sample) is timed too.  The roofline figure is for the step's
+parameters call for (mlxf_sampler_refine_stages); the generic call (plain
+mlxf_sample, two refine stages) and all three stages are timed too.  The roofline figure is for the step's
 dominant kernel, k_scan1 (the one HBM read of the logits), timed alone through
 mlxf_sampler_first_pass.  cpu_baseline times the CPU restatement of the
 reference sampler (oracle/, "port") on the same workload with a bounded number
@@ -299,17 +299,21 @@ def main():
         st = Step(wl, torch, lib)
         parity[f"C{cfg}"] = parity_report(st, torch)
         ms = time_steps(st, torch, warmup, steps)
-        st.stages, stages = 3, st.stages
+        # the generic call (mlxf_sample: two refine stages, for a caller without
+        # the parameters on the host) and all three stages
+        st.stages, stages = 2, st.stages
+        ms_gen = time_steps(st, torch, warmup, steps)
+        st.stages = 3
         ms_all = time_steps(st, torch, warmup, steps)
         ms_k1 = time_first_pass(st, torch, warmup, steps)
         st_hot = Step(wl, torch, lib, rotate=False)
         ms_hot = time_steps(st_hot, torch, warmup, steps)
         del st, st_hot
         torch.cuda.empty_cache()
-        return wl, ms, ms_hot, ms_all, stages, ms_k1
+        return wl, ms, ms_hot, ms_all, stages, ms_k1, ms_gen
 
     log(f"[bench] config C{args.config}: warmup {args.warmup}, steps {args.steps}")
-    wl, ms, ms_hot, ms_all, stages, ms_k1 = measure(args.config, args.steps, args.warmup)
+    wl, ms, ms_hot, ms_all, stages, ms_k1, ms_gen = measure(args.config, args.steps, args.warmup)
     alg = wl.algorithmic_bytes()
     # the dominant kernel, k_scan1, makes the step's one read of the logits; its
     # algorithmic bytes are the step's (logits read once, ids / logprobs / top-K
@@ -333,6 +337,7 @@ def main():
         "us_per_step": round(ms * 1e3, 2),
         "us_per_step_hot": round(ms_hot * 1e3, 2),
         "refine_stages": stages,
+        "us_per_step_generic": round(ms_gen * 1e3, 2),
         "us_per_step_all_stages": round(ms_all * 1e3, 2),
         "achieved_GBps_step": round(alg / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "kernel": "k_scan1", "achieved": round(achieved, 1),
@@ -351,10 +356,11 @@ def main():
             if cfg == args.config:
                 continue
             log(f"[bench] extra config C{cfg}")
-            w2, m2, mh2, ma2, st2, mk2 = measure(cfg, min(args.steps, 100), min(args.warmup, 10))
+            w2, m2, mh2, ma2, st2, mk2, mg2 = measure(cfg, min(args.steps, 100), min(args.warmup, 10))
             extra[f"C{cfg}"] = {"workload": w2.name, "us_per_step": round(m2 * 1e3, 2),
                                 "us_per_step_hot": round(mh2 * 1e3, 2),
-                                "refine_stages": st2, "us_per_step_all_stages": round(ma2 * 1e3, 2),
+                                "refine_stages": st2, "us_per_step_generic": round(mg2 * 1e3, 2),
+                                "us_per_step_all_stages": round(ma2 * 1e3, 2),
                                 "k_scan1_us": round(mk2 * 1e3, 2),
                                 "rows_per_s": round(w2.B / (m2 * 1e-3), 1),
                                 "achieved_GBps_step": round(w2.algorithmic_bytes() / (m2 * 1e-3) / 1e9, 1),

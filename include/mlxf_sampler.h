@@ -110,13 +110,15 @@ int mlxf_sample(const void* d_logits, int dtype, int B, int V, int64_t row_strid
                 int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err);
 
 /* mlxf_sample with the number of refine stages to launch (0..3) given by the
- * caller.  mlxf_sample launches all three, which any mix of parameters needs;
- * a caller that knows its rows' parameters on the host (as Worker::sample_rows
- * does, src/runtime/worker.cpp:453-473) passes
- * mlxf_sampler_refine_stages(...) instead and skips launches no row can use.
- * Results are identical for every count >= that value: rows still open after
- * the last stage launched are finished by its deciding kernel.  No reference
- * counterpart (the reference builds one MLX graph per row). */
+ * caller.  mlxf_sample launches two, the most mlxf_sampler_refine_stages ever
+ * asks for (a third measured slower on every configuration: the rows it would
+ * serve finish sooner in the second stage's deciding kernel); a caller that
+ * knows its rows' parameters on the host (as Worker::sample_rows does,
+ * src/runtime/worker.cpp:453-473) passes mlxf_sampler_refine_stages(...)
+ * instead and skips launches no row can use.  Results are identical for every
+ * count: rows still open after the last stage launched are finished by its
+ * deciding kernel.  No reference counterpart (the reference builds one MLX
+ * graph per row). */
 int mlxf_sample_staged(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
                        const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
                        const int32_t* d_top_logprobs, const float* d_uniforms, int32_t* d_out_ids,

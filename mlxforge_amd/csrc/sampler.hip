@@ -382,7 +382,7 @@ int mlxf_sample(const void* d_logits, int dtype, int B, int V, int64_t row_strid
                 int K_max, void* d_workspace, size_t workspace_bytes, void* stream, char** err) {
   return run_sample(d_logits, dtype, B, V, row_stride, d_temperature, d_top_k, d_top_p, nullptr,
                     d_top_logprobs, d_uniforms, d_out_ids, d_out_logprobs, d_out_top_ids,
-                    d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, mlxf::NSTAGE, err);
+                    d_out_top_logprobs, K_max, d_workspace, workspace_bytes, stream, mlxf::HINT_STAGES, err);
 }
 
 int mlxf_sample_staged(const void* d_logits, int dtype, int B, int V, int64_t row_stride,

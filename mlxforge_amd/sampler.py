@@ -109,7 +109,7 @@ def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
     host sequences, which are copied); None disables the knob (temperature
     None = all greedy; min_p None = off).  refine_stages: refine stages to launch (0..3); by
     default derived from the parameters when they are all known on the host
-    (mlxf_sampler_refine_stages: 0, 1 or 2), else 3 (mlxf_sample's count).
+    (mlxf_sampler_refine_stages: 0, 1 or 2), else 2 (mlxf_sample's count).
     """
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be a [B, V] view with unit stride along V")
@@ -122,7 +122,7 @@ def sample_rows(logits: torch.Tensor, temperature=None, top_k=None, top_p=None,
     if refine_stages is None:
         hv = [_host_view(x, B) for x in (temperature, top_k, top_p)]
         if any(h is None for h in hv):
-            refine_stages = 3
+            refine_stages = 2
         else:
             hv = [None if isinstance(h, str) else h for h in hv]
             refine_stages = _lib.refine_stages(B, V, code, *hv)

@@ -40,7 +40,7 @@ def to_device(host: np.ndarray, dtype: str, device="cuda:0") -> torch.Tensor:
 
 def gpu_sample(logits_dev, T=None, k=None, p=None, tlp=None, u=None, K_max=0, V=None,
                stages=None, min_p=None):
-    """stages: refine stages to launch (None: all three, the generic path)."""
+    """stages: refine stages to launch (None: all three)."""
     dev = logits_dev.device
     f = lambda a, t: None if a is None else torch.as_tensor(np.asarray(a), dtype=t).to(dev)
     res = sampler.sample_rows(logits_dev, temperature=f(T, torch.float32), top_k=f(k, torch.int32),
