@@ -240,6 +240,39 @@ int mlxf_apply_mask(const void* d_logits, int dtype, int B, int V, int64_t row_s
                     const uint32_t* d_allowed_bits, int64_t bits_stride, float* d_out,
                     int64_t out_stride, void* stream, char** err);
 
+/* The reference's filter helpers (src/sample/sampler.h:63-69; graph ops that
+ * return the logits with every removed entry set to -inf), on a [B, V] matrix:
+ *   mlxf_apply_top_k  Sampler::apply_top_k (src/sample/sampler.cpp:63-68): keep
+ *                     the entries at or above the k-th largest, counting
+ *                     multiplicity (ties there are kept, so more than k can
+ *                     remain); k clamped to V (:159-161); k <= 0 keeps all.
+ *   mlxf_apply_top_p  Sampler::apply_top_p (:70-85): keep the smallest prefix
+ *                     in (value desc, index asc) order whose prior mass is
+ *                     below p; p outside (0, 1) keeps all.
+ *   mlxf_apply_min_p  Sampler::apply_min_p (:87-93): keep the entries whose
+ *                     probability reaches min_p times the largest; min_p
+ *                     outside (0, 1] keeps all.
+ *   mlxf_filter_logits  all three after the temperature division, per row,
+ *                     as Sampler::sample applies them (:158-163): writes z' =
+ *                     round_dtype(z / T) (T <= 0, non-finite or NULL: no
+ *                     division) with the removed entries at -inf.  NULL
+ *                     arrays: that filter off.
+ * The kept sets are the sampling call's, with its masses and tie rules
+ * (D2, D3); NaN logits read as -inf.  d_out has the logits' dtype; it may be
+ * d_logits itself (in place, out_stride == row_stride) but must not overlap it
+ * otherwise.  No workspace: the output rows serve as scratch.  One workgroup
+ * per row that reads its row about a dozen times: a helper, not the decode
+ * step's path. */
+int mlxf_filter_logits(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
+                       const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                       const float* d_min_p, void* d_out, int64_t out_stride, void* stream, char** err);
+int mlxf_apply_top_k(const void* d_logits, int dtype, int B, int V, int64_t row_stride, int k,
+                     void* d_out, int64_t out_stride, void* stream, char** err);
+int mlxf_apply_top_p(const void* d_logits, int dtype, int B, int V, int64_t row_stride, float p,
+                     void* d_out, int64_t out_stride, void* stream, char** err);
+int mlxf_apply_min_p(const void* d_logits, int dtype, int B, int V, int64_t row_stride, float min_p,
+                     void* d_out, int64_t out_stride, void* stream, char** err);
+
 /* argmax over each row, lowest index on ties: Sampler::greedy
  * (src/sample/sampler.h:61, src/sample/sampler.cpp:59-61). */
 int mlxf_greedy(const void* d_logits, int dtype, int B, int V, int64_t row_stride,

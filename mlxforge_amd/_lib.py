@@ -33,6 +33,10 @@ SYMBOLS = (
     "mlxf_string_free",
     "mlxf_sampler_workspace_init",
     "mlxf_sample_noalloc",
+    "mlxf_filter_logits",
+    "mlxf_apply_top_k",
+    "mlxf_apply_top_p",
+    "mlxf_apply_min_p",
 )
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
@@ -79,6 +83,14 @@ def load() -> ctypes.CDLL:
     L.mlxf_sampler_refine_stages.restype = I
     L.mlxf_greedy.argtypes = [P, I, I, I, I64, P, P, SZ, P, PP]
     L.mlxf_greedy.restype = I
+    L.mlxf_filter_logits.argtypes = [P, I, I, I, I64, P, P, P, P, P, I64, P, PP]
+    L.mlxf_filter_logits.restype = I
+    L.mlxf_apply_top_k.argtypes = [P, I, I, I, I64, I, P, I64, P, PP]
+    L.mlxf_apply_top_k.restype = I
+    L.mlxf_apply_top_p.argtypes = [P, I, I, I, I64, ctypes.c_float, P, I64, P, PP]
+    L.mlxf_apply_top_p.restype = I
+    L.mlxf_apply_min_p.argtypes = [P, I, I, I, I64, ctypes.c_float, P, I64, P, PP]
+    L.mlxf_apply_min_p.restype = I
     L.mlxf_sample_noalloc.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, P, I, I, P, PP]
     L.mlxf_sample_noalloc.restype = I
     L.mlxf_sampler_workspace_init.argtypes = [P, SZ, P, PP]

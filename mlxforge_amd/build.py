@@ -2,8 +2,8 @@
 
 Produces ``mlxforge_amd/libmlxf_sampler.so`` in-tree from
 ``mlxforge_amd/csrc/sampler.hip`` (host side), ``sampler_{f32,bf16,f16}.hip``
-(one logits dtype's kernels each), ``penalties.hip``, ``uniforms.hip`` and
-``mask.hip``, compiled in parallel
+(one logits dtype's kernels each), ``penalties.hip``, ``uniforms.hip``,
+``mask.hip`` and ``filter.hip``, compiled in parallel
 with hipcc, and the C++
 known-answer test
 driver ``mlxforge_amd/sampler_kat`` (tests/cpp/sampler_kat.cpp) that exercises
@@ -28,7 +28,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 SRCS = [os.path.join(CSRC, f) for f in ("sampler.hip", "sampler_f32.hip", "sampler_bf16.hip", "sampler_f16.hip",
-                                         "penalties.hip", "uniforms.hip", "mask.hip")]
+                                         "penalties.hip", "uniforms.hip", "mask.hip", "filter.hip")]
 LIB = os.path.join(HERE, "libmlxf_sampler.so")
 KAT_SRC = os.path.join(ROOT, "tests", "cpp", "sampler_kat.cpp")
 KAT_BIN = os.path.join(HERE, "sampler_kat")

@@ -213,6 +213,29 @@ class Sampler {
                   err);
   }
 
+  // Sampler::apply_top_k / apply_top_p / apply_min_p (src/sample/sampler.h:63-69):
+  // the logits with every removed entry set to -inf, written to d_out (the
+  // logits' dtype, row stride out_stride, 0: V; d_out may be logits.data for
+  // in place).  Asynchronous on the sampler's stream.
+  void apply_top_k(const DeviceLogits& logits, int k, void* d_out, int64_t out_stride = 0) {
+    char* err = nullptr;
+    detail::check(mlxf_apply_top_k(logits.data, logits.dtype, logits.B, logits.V, stride_of(logits), k, d_out,
+                                   out_stride ? out_stride : logits.V, stream_, &err),
+                  err);
+  }
+  void apply_top_p(const DeviceLogits& logits, float p, void* d_out, int64_t out_stride = 0) {
+    char* err = nullptr;
+    detail::check(mlxf_apply_top_p(logits.data, logits.dtype, logits.B, logits.V, stride_of(logits), p, d_out,
+                                   out_stride ? out_stride : logits.V, stream_, &err),
+                  err);
+  }
+  void apply_min_p(const DeviceLogits& logits, float min_p, void* d_out, int64_t out_stride = 0) {
+    char* err = nullptr;
+    detail::check(mlxf_apply_min_p(logits.data, logits.dtype, logits.B, logits.V, stride_of(logits), min_p, d_out,
+                                   out_stride ? out_stride : logits.V, stream_, &err),
+                  err);
+  }
+
   // Sampler::greedy (src/sample/sampler.h:61): argmax, lowest index on ties.
   std::vector<int32_t> greedy(const DeviceLogits& logits) {
     const int B = logits.B, V = logits.V;
@@ -236,6 +259,7 @@ class Sampler {
   }
 
  private:
+  static int64_t stride_of(const DeviceLogits& l) { return l.row_stride ? l.row_stride : l.V; }
   void ensure_workspace(size_t bytes) {
     if (bytes <= ws_bytes_) return;
     ws_.reserve(bytes);

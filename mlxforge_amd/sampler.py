@@ -249,6 +249,75 @@ def apply_mask(logits: torch.Tensor, allowed_bits: torch.Tensor, V: int | None =
     return out
 
 
+def _filter_out(logits: torch.Tensor, V, out):
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be a [B, V] view with unit stride along V")
+    if logits.dtype not in _DTYPES:
+        raise ValueError(f"unsupported logits dtype {logits.dtype}")
+    B = logits.shape[0]
+    V = logits.shape[1] if V is None else V
+    if out is None:
+        out = torch.empty((B, V), dtype=logits.dtype, device=logits.device)
+    elif out.dtype != logits.dtype or out.dim() != 2 or out.stride(1) != 1:
+        raise ValueError("out must be a [B, V] view of the logits' dtype with unit stride along V")
+    stream = ctypes.c_void_p(torch.cuda.current_stream(logits.device).cuda_stream)
+    return B, V, out, stream
+
+
+def filter_logits(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p=None,
+                  V: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """z' = logits / temperature (rounded to the logits dtype) with the
+    entries that top-k, top-p and min_p remove set to -inf, per row, as
+    Sampler::sample filters before its draw (src/sample/sampler.cpp:158-163).
+    Per-row parameters as in sample_rows; None = that step off.  out may be
+    logits itself (in place)."""
+    B, V, out, stream = _filter_out(logits, V, out)
+    dev = logits.device
+    T = _param(temperature, B, torch.float32, dev)
+    k = _param(top_k, B, torch.int32, dev)
+    p = _param(top_p, B, torch.float32, dev)
+    mp = _param(min_p, B, torch.float32, dev)
+    err = ctypes.c_void_p()
+    rc = _lib.load().mlxf_filter_logits(_ptr(logits), _DTYPES[logits.dtype], B, V, logits.stride(0), _ptr(T),
+                                        _ptr(k), _ptr(p), _ptr(mp), _ptr(out), out.stride(0), stream,
+                                        ctypes.byref(err))
+    _lib.check(rc, err)
+    return out
+
+
+def apply_top_k(logits: torch.Tensor, k: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Sampler::apply_top_k (src/sample/sampler.cpp:63-68): entries below the
+    k-th largest (counting multiplicity) set to -inf."""
+    B, V, out, stream = _filter_out(logits, None, out)
+    err = ctypes.c_void_p()
+    rc = _lib.load().mlxf_apply_top_k(_ptr(logits), _DTYPES[logits.dtype], B, V, logits.stride(0), int(k),
+                                      _ptr(out), out.stride(0), stream, ctypes.byref(err))
+    _lib.check(rc, err)
+    return out
+
+
+def apply_top_p(logits: torch.Tensor, p: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Sampler::apply_top_p (src/sample/sampler.cpp:70-85): entries past the
+    smallest (value desc, index asc) prefix whose mass reaches p set to -inf."""
+    B, V, out, stream = _filter_out(logits, None, out)
+    err = ctypes.c_void_p()
+    rc = _lib.load().mlxf_apply_top_p(_ptr(logits), _DTYPES[logits.dtype], B, V, logits.stride(0), float(p),
+                                      _ptr(out), out.stride(0), stream, ctypes.byref(err))
+    _lib.check(rc, err)
+    return out
+
+
+def apply_min_p(logits: torch.Tensor, min_p: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Sampler::apply_min_p (src/sample/sampler.cpp:87-93): entries whose
+    probability is below min_p times the largest set to -inf."""
+    B, V, out, stream = _filter_out(logits, None, out)
+    err = ctypes.c_void_p()
+    rc = _lib.load().mlxf_apply_min_p(_ptr(logits), _DTYPES[logits.dtype], B, V, logits.stride(0),
+                                      float(min_p), _ptr(out), out.stride(0), stream, ctypes.byref(err))
+    _lib.check(rc, err)
+    return out
+
+
 def greedy(logits: torch.Tensor, workspace: Workspace | None = None) -> torch.Tensor:
     """argmax per row, lowest index on ties (src/sample/sampler.cpp:59-61)."""
     if logits.dim() != 2 or logits.stride(1) != 1:
@@ -289,3 +358,15 @@ class Sampler:
     @staticmethod
     def greedy(logits: torch.Tensor) -> torch.Tensor:
         return greedy(logits)
+
+    @staticmethod
+    def apply_top_k(logits: torch.Tensor, k: int) -> torch.Tensor:
+        return apply_top_k(logits, k)
+
+    @staticmethod
+    def apply_top_p(logits: torch.Tensor, p: float) -> torch.Tensor:
+        return apply_top_p(logits, p)
+
+    @staticmethod
+    def apply_min_p(logits: torch.Tensor, min_p: float) -> torch.Tensor:
+        return apply_min_p(logits, min_p)

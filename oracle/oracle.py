@@ -183,13 +183,14 @@ def check_rows(ids, ref: dict, logits: np.ndarray, dtype: int, T=None, k=None, p
                 excluded_admissible=int(adm_ok), bad=bad)
 
 
-def filter_row(z, T=0.0, k=0, p=1.0, min_p=0.0, dtype: int = F32) -> np.ndarray:
-    """z' after temperature / top-k / top-p / min-p (dropped entries are -inf)."""
+def filter_row(z, T=0.0, k=0, p=1.0, min_p=0.0, dtype: int = F32, with_flags: bool = False):
+    """z' after temperature / top-k / top-p / min-p (dropped entries are -inf);
+    with_flags: (z', ambiguity flags of the top-p and min_p cutoffs)."""
     z = np.ascontiguousarray(np.asarray(z, np.float32))
     out = np.zeros_like(z)
     rc = lib().orc_filter_row(_ptr(z), z.size, dtype, T, k, p, min_p, _ptr(out))
-    assert rc == 0
-    return out
+    assert rc >= 0
+    return (out, rc) if with_flags else out
 
 
 def apply_penalties(z, hist, rep=1.0, freq=0.0, pres=0.0, dtype: int = F32) -> np.ndarray:

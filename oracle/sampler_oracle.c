@@ -716,18 +716,26 @@ int orc_sample(const void* logits, int dtype, int B, int V, long row_stride, con
                        top_lp, K_max, flags, margins, nthreads);
 }
 
-/* Filter stage only (for the reference's filter known-answer tests):
- * writes z' after temperature / top-k / top-p / min-p into out (V floats). */
+/* Filter stage only (for the reference's filter known-answer tests and the
+ * filter entry points): writes z' after temperature / top-k / top-p / min-p
+ * into out (V floats).  Returns the ambiguity flags of the top-p and min_p
+ * cutoffs (ORC_FLAG_TOPP_AMBIG, ORC_FLAG_MINP_AMBIG; see the exclusion rule
+ * above), or -1 for bad arguments. */
 int orc_filter_row(const float* zin, int V, int dtype, float T, int k, float p, float min_p,
                    float* out) {
   if (!zin || !out || V <= 0) return -1;
   const float Tr = round_dtype(T, dtype);
+  /* the sampling call's sentinels: a temperature that is not a positive finite
+   * value of the dtype divides nothing; min_p outside (0, 1] is off and inside
+   * is rounded to the dtype (D9) */
+  const int div = isfinite(T) && T > 0.0f && Tr > 0.0f;
   for (int i = 0; i < V; ++i) {
     float z = isnan(zin[i]) ? -INFINITY : zin[i];
-    out[i] = T > 0.0f ? round_dtype(z / Tr, dtype) : z;
+    out[i] = div ? round_dtype(z / Tr, dtype) : z;
   }
+  int flags = 0;
   if (k > 0) orc_apply_top_k(out, V, k);
-  if (p > 0.0f && p < 1.0f) orc_apply_top_p(out, V, round_dtype(p, dtype), NULL);
-  if (min_p > 0.0f) orc_apply_min_p(out, V, min_p);
-  return 0;
+  if (p > 0.0f && p < 1.0f) flags |= orc_apply_top_p(out, V, round_dtype(p, dtype), NULL);
+  if (min_p > 0.0f && min_p <= 1.0f) flags |= apply_min_p_m(out, V, round_dtype(min_p, dtype), NULL);
+  return flags;
 }
