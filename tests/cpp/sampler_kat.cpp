@@ -7,9 +7,10 @@
 // boundary:
 //   * the MLX PRNG key becomes one caller-supplied uniform per row, so
 //     "same seed reproduces" is "same uniforms reproduce";
-//   * apply_top_k / apply_top_p are not separate entry points: their kept sets
-//     are observed through the draw (a uniform sweep only ever returns kept
-//     ids, and reaches every one of them).
+//   * the kept sets of top-k / top-p / min_p are checked twice: through the
+//     draw (a uniform sweep only ever returns kept ids, and reaches every one
+//     of them) and directly, through the filter entry points apply_top_k /
+//     apply_top_p / apply_min_p, on the reference's own cases.
 // The reference's min_p and penalty cases (sampler_test.cpp:76-124) run through
 // the wrapper's min_p parameter and apply_penalties; penalties left in the
 // parameters of a sampling call must be refused.  The C ABI's seeded uniforms
@@ -212,6 +213,31 @@ void case_min_p(Sampler& s) {  // :76-87
   KAT_CHECK((kept == std::set<int>{0, 1}));
 }
 
+// The filter entry points (sampler_test.cpp:54-87 call Sampler::apply_top_k /
+// apply_top_p / apply_min_p directly): finite entries after the filter.
+std::vector<bool> finite_after(Sampler& s, const std::vector<float>& z, int which, float arg) {
+  Logits lg({z});
+  float* out = nullptr;
+  if (hipMalloc(reinterpret_cast<void**>(&out), z.size() * sizeof(float)) != hipSuccess) std::exit(2);
+  if (which == 0) s.apply_top_k(lg.view(), static_cast<int>(arg), out);
+  if (which == 1) s.apply_top_p(lg.view(), arg, out);
+  if (which == 2) s.apply_min_p(lg.view(), arg, out);
+  std::vector<float> h(z.size());
+  (void)hipMemcpy(h.data(), out, z.size() * sizeof(float), hipMemcpyDeviceToHost);
+  (void)hipFree(out);
+  std::vector<bool> f(z.size());
+  for (size_t i = 0; i < z.size(); ++i) f[i] = std::isfinite(h[i]) && h[i] == z[i];
+  return f;
+}
+
+void case_filter_entry_points(Sampler& s) {  // :54-87
+  KAT_CHECK((finite_after(s, {5.0f, 1.0f, 4.0f, 2.0f, 3.0f}, 0, 2.0f) ==
+             std::vector<bool>{true, false, true, false, false}));
+  const std::vector<float> lg = log_of({0.5f, 0.3f, 0.15f, 0.05f});
+  KAT_CHECK((finite_after(s, lg, 1, 0.7f) == std::vector<bool>{true, true, false, false}));
+  KAT_CHECK((finite_after(s, lg, 2, 0.4f) == std::vector<bool>{true, true, false, false}));
+}
+
 void case_penalties_refused(Sampler& s) {  // :89-124 need apply_penalties first
   Logits lg({{2.0f, 1.0f, 0.5f}});
   for (int which = 0; which < 3; ++which) {
@@ -374,6 +400,7 @@ int main() {
       {"a full top-k recovers a normalised distribution", case_full_top_k_normalised},
       {"top_logprobs come from the pre-temperature logits", case_top_logprobs_pre_temperature},
       {"min-p keeps tokens with prob >= min_p * max_prob", case_min_p},
+      {"apply_top_k / apply_top_p / apply_min_p on the reference's cases", case_filter_entry_points},
       {"penalties left in the parameters are refused", case_penalties_refused},
       {"repetition penalty pushes a seen token below an unseen one", case_repetition_penalty},
       {"frequency penalty scales with count, presence is flat", case_frequency_presence},
