@@ -46,8 +46,12 @@ extern "C" {
 #define MLXF_EHIP (-3)       /* a HIP runtime call or kernel launch failed */
 
 /* Largest top_logprobs column count supported per call.  The reference's HTTP
- * layer admits top_logprobs in [0, 20] (src/server/openai.cpp:150-152). */
-#define MLXF_MAX_TOP_LOGPROBS 64
+ * layer admits top_logprobs in [0, 20] (src/server/openai.cpp:150-152), its
+ * sampler any K = min(top_logprobs, V) (src/sample/sampler.cpp:52).  Up to 64
+ * columns come out of the sampling kernels' best-64 lists; a call with K_max
+ * above 64 adds one kernel that selects and sorts every row's K (one
+ * workgroup per row, K sorted in LDS). */
+#define MLXF_MAX_TOP_LOGPROBS 4096
 /* Largest vocabulary accepted: at most 64 slices of 8192 logits per row. */
 #define MLXF_MAX_VOCAB 524288
 

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(HERE, "libmlxf_sampler.so")
 
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 OK, EINVAL, EWORKSPACE, EHIP = 0, -1, -2, -3
-MAX_TOP_LOGPROBS = 64
+MAX_TOP_LOGPROBS = 4096
 MAX_VOCAB = 524288
 
 # Every function include/*.h declares.

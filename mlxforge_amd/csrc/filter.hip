@@ -96,9 +96,9 @@ __device__ __forceinline__ T fsum(T x, T* red) {
 // mass when MASS) of candidates with key > c is below `target` and with key
 // >= c reaches it.  Returns c; *above = the measure above c, *cnt = the
 // number of candidates with key c.
-template <int DT, bool MASS, typename In, typename Mass>
-__device__ unsigned int radix_select(const void* orow, int V, unsigned long long target, In in, Mass massf,
-                                     FLds& sh, unsigned long long* above, unsigned int* cnt) {
+template <bool MASS, typename Load, typename In, typename Mass>
+__device__ unsigned int radix_select(int V, unsigned long long target, Load load, In in, Mass massf, FLds& sh,
+                                     unsigned long long* above, unsigned int* cnt) {
   const int tid = threadIdx.x;
   unsigned int prefix = 0u, mask = 0u;
   unsigned long long rem = target, abv = 0ull;
@@ -116,7 +116,7 @@ __device__ unsigned int radix_select(const void* orow, int V, unsigned long long
     }
     __syncthreads();
     for (int i = tid; i < V; i += FT) {
-      const float zp = raw1<DT>(orow, i);
+      const float zp = load(i);
       const unsigned int key = okey(zp);
       if ((key & mask) == prefix && in(zp, key)) {
         const unsigned int d = (key >> shift) & 255u;
@@ -200,6 +200,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f) {
   const bool minf = Mp == INFINITY;
   const float nc = minf ? 0.0f : -(Mp * LOG2E);
   auto massf = [&](float zp) -> unsigned long long { return q40(wfun(zp + 0.0f, Mp, nc, minf)); };
+  auto zload = [&](int i) { return raw1<DT>(orow, i); };
 
   // ---- top-k: the k'-th largest key counting multiplicity; every element at
   // or above it is kept (src/sample/sampler.cpp:63-68)
@@ -207,8 +208,8 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f) {
   if (kk > 0 && kk < V) {
     unsigned long long ab;
     unsigned int c;
-    tk = radix_select<DT, false>(orow, V, static_cast<unsigned long long>(kk),
-                                 [](float, unsigned int) { return true; }, massf, sh, &ab, &c);
+    tk = radix_select<false>(V, static_cast<unsigned long long>(kk), zload,
+                             [](float, unsigned int) { return true; }, massf, sh, &ab, &c);
   }
 
   // ---- top-p over the top-k survivors (src/sample/sampler.cpp:70-85): keep
@@ -227,8 +228,8 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f) {
     if (PW < 1ull) PW = 1ull;
     unsigned long long above;
     unsigned int g;
-    ck = radix_select<DT, true>(orow, V, PW, [tk](float, unsigned int key) { return key >= tk; }, massf, sh, &above,
-                                &g);
+    ck = radix_select<true>(V, PW, zload, [tk](float, unsigned int key) { return key >= tk; }, massf, sh, &above,
+                            &g);
     const unsigned long long wt = massf(key2f(ck));
     const unsigned int t = ties_kept(PW > above ? PW - above : 0ull, wt, g);
     tkeep = t >= g ? 0xffffffffu : t;
@@ -262,6 +263,117 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f) {
     }
     if (mr > 0.0f) keep = keep && wfun(zp + 0.0f, Mp, nc, minf) >= thr;
     if (!keep && zp != -INFINITY) st1<DT>(orow, i, -INFINITY);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// top_logprobs wider than the sampling kernels' best-64 lists (64 < K <= 4096):
+// top_k_logprobs (src/sample/sampler.cpp:30-38; K = min(top_logprobs, V) at
+// :52) as a call of its own after the sampling kernels.  One 1024-thread
+// workgroup per row: the log-sum-exp of the unscaled row (fp64 partials), the
+// K-th largest logit by a radix selection, the K entries (every logit above
+// it, then the tied ones in index order) gathered into LDS and sorted by
+// (logit desc, index asc) with a bitonic network, then written as (id, logit
+// - LSE); columns past the row's K get id -1 and -inf.
+
+constexpr int TOPK_WIDE_MAX = 4096;
+
+struct TkLds {
+  FLds f;
+  unsigned long long ent[TOPK_WIDE_MAX];  // (key << 32) | ~index: one unsigned order, larger first
+  unsigned int n;
+  double dr[FW];
+};
+
+template <int DT>
+__global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long long row_stride, int V, const int* tlp,
+                                                     int K_max, int* top_ids, float* top_lp) {
+  __shared__ TkLds sh;
+  const int tid = threadIdx.x;
+  const int r = static_cast<int>(blockIdx.x);
+  const void* row = static_cast<const char*>(logits) + static_cast<size_t>(r) * row_stride * elem_size<DT>();
+  int* oid = top_ids + static_cast<size_t>(r) * K_max;
+  float* olp = top_lp + static_cast<size_t>(r) * K_max;
+  const int t = tlp ? tlp[r] : -1;
+  const int K = t > 0 ? min(min(t, K_max), V) : 0;
+  for (int j = K + tid; j < K_max; j += FT) {
+    oid[j] = -1;
+    olp[j] = -INFINITY;
+  }
+  if (K == 0) return;
+  auto load = [&](int i) { return ld1<DT>(row, i); };  // NaN reads as -inf
+
+  // ---- log-sum-exp of the unscaled row
+  float mx = -INFINITY;
+  for (int i = tid; i < V; i += FT) mx = fmaxf(mx, load(i));
+  float M;
+  {
+    const float w = wave_max(mx);
+    if ((tid & 63) == 0) sh.f.fr[tid >> 6] = w;
+    __syncthreads();
+    M = rdl(row_max16(sh.f.fr[tid & (FW - 1)]), 0);
+  }
+  double part = 0.0;
+  for (int i = tid; i < V; i += FT) part += wexp_d(load(i), M);
+  const double lse = static_cast<double>(M) + log(fsum(part, sh.dr));
+
+  // ---- the K-th largest logit (counting multiplicity) and the entries
+  unsigned long long above;
+  unsigned int g;
+  const unsigned int tau = radix_select<false>(V, static_cast<unsigned long long>(K), load,
+                                               [](float, unsigned int) { return true; },
+                                               [](float) { return 0ull; }, sh.f, &above, &g);
+  const unsigned int need_eq = static_cast<unsigned int>(K) - static_cast<unsigned int>(above);
+  // contiguous ranges (index order for the tied entries)
+  const int E = (V + FT - 1) / FT;
+  const int i0 = min(tid * E, V), i1 = min(i0 + E, V);
+  int mine = 0;
+  for (int i = i0; i < i1; ++i) mine += okey(load(i)) == tau ? 1 : 0;
+  int tot;
+  unsigned int rank = static_cast<unsigned int>(rh::bscan(mine, sh.f.ir, &tot));
+  if (tid == 0) sh.n = 0u;
+  __syncthreads();
+  for (int i = i0; i < i1; ++i) {
+    const unsigned int key = okey(load(i));
+    bool take = key > tau;
+    if (key == tau) {
+      take = rank < need_eq;
+      ++rank;
+    }
+    if (take) {
+      const unsigned int slot = __hip_atomic_fetch_add(&sh.n, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (slot < static_cast<unsigned int>(TOPK_WIDE_MAX))
+        sh.ent[slot] = (static_cast<unsigned long long>(key) << 32) | (0xffffffffu - static_cast<unsigned int>(i));
+    }
+  }
+  __syncthreads();
+  // ---- bitonic sort, descending, over the next power of two (padding: 0)
+  int np = 1;
+  while (np < K) np <<= 1;
+  for (int j = K + tid; j < np; j += FT) sh.ent[j] = 0ull;
+  __syncthreads();
+  for (int k = 2; k <= np; k <<= 1) {
+    for (int jj = k >> 1; jj > 0; jj >>= 1) {
+      for (int i = tid; i < np; i += FT) {
+        const int ixj = i ^ jj;
+        if (ixj > i) {
+          const unsigned long long a = sh.ent[i], b = sh.ent[ixj];
+          const bool desc = (i & k) == 0;
+          if (desc ? (a < b) : (a > b)) {
+            sh.ent[i] = b;
+            sh.ent[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // ---- write (id, logit - LSE)
+  for (int j = tid; j < K; j += FT) {
+    const unsigned long long e = sh.ent[j];
+    const int id = static_cast<int>(0xffffffffu - static_cast<unsigned int>(e));
+    oid[j] = id;
+    olp[j] = static_cast<float>(static_cast<double>(load(id)) - lse);
   }
 }
 
@@ -337,6 +449,22 @@ FArgs scalars(float T, int k, float p, float mp) {
 }
 
 }  // namespace
+
+hipError_t launch_topk_wide(const void* logits, int dtype, int B, int V, long long row_stride, const int* tlp,
+                            int K_max, int* top_ids, float* top_lp, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned int>(B)), block(FT);
+  if (dtype == MLXF_DTYPE_F32)
+    hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_F32>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
+                       top_lp);
+  else if (dtype == MLXF_DTYPE_BF16)
+    hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_BF16>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
+                       top_lp);
+  else
+    hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_F16>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
+                       top_lp);
+  return hipGetLastError();
+}
+
 }  // namespace mlxf
 
 extern "C" int mlxf_filter_logits(const void* d_logits, int dtype, int B, int V, int64_t row_stride,

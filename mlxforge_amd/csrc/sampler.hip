@@ -227,12 +227,16 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
     const bool vecok = (reinterpret_cast<uintptr_t>(d_logits) % 16 == 0) &&
                        ((static_cast<size_t>(row_stride) * esz) % 16 == 0);
     char* ws = static_cast<char*>(d_workspace);
+    // top_logprobs wider than the sampling kernels' lists: the sampling
+    // kernels run without them, then one kernel writes every row's columns
+    const bool wide = K_max > TOPK_LIST;
+    const int K_main = wide ? 0 : K_max;
     Args a;
     a.logits = d_logits;
     a.row_stride = row_stride;
     a.B = B;
     a.V = V;
-    a.K_max = K_max;
+    a.K_max = K_main;
     a.S = l.S;
     a.L = l.L;
     a.T = d_temperature;
@@ -263,7 +267,7 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
     if (!d_temperature && nst > 0) nst = 0;  // every row greedy
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e;
-    if (use_row_path(dtype, V, K_max, vecok, nst)) {
+    if (use_row_path(dtype, V, K_main, vecok, nst)) {
       RhArgs x;
       x.ipc = (V + ROW_CHUNK_LOGITS - 1) / ROW_CHUNK_LOGITS;
       x.nfull = V / ROW_ITER_LOGITS;
@@ -277,6 +281,9 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
       e = launch_bf16(a, l.EPT, vecok, nst, st);
     else
       e = launch_f16(a, l.EPT, vecok, nst, st);
+    if (e == hipSuccess && wide)
+      e = launch_topk_wide(d_logits, dtype, B, V, row_stride, d_top_logprobs, K_max, d_out_top_ids,
+                           d_out_top_logprobs, st);
     if (e != hipSuccess) {
       set_err(err, std::string("mlxf: kernel launch failed: ") + hipGetErrorString(e));
       return MLXF_EHIP;

@@ -127,6 +127,13 @@ hipError_t launch_f32(const Args& a, int ept, bool vecok, int nst, hipStream_t s
 hipError_t launch_bf16(const Args& a, int ept, bool vecok, int nst, hipStream_t st);
 hipError_t launch_f16(const Args& a, int ept, bool vecok, int nst, hipStream_t st);
 
+// top_logprobs wider than the sampling kernels' lists (TOPK_LIST < K_max;
+// defined in filter.hip): every row's top-K (id, logprob), columns past the
+// row's K as (-1, -inf).
+constexpr int TOPK_LIST = 64;
+hipError_t launch_topk_wide(const void* logits, int dtype, int B, int V, long long row_stride, const int* tlp,
+                            int K_max, int* top_ids, float* top_lp, hipStream_t st);
+
 namespace {
 
 

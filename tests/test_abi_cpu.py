@@ -45,7 +45,8 @@ def test_workspace_size_is_positive_and_monotone():
 
 
 @pytest.mark.parametrize("args", [
-    (-1, 10, 0, 0), (1, 0, 0, 0), (1, 10, 65, 0), (1, 10, 0, 7), (1, _lib.MAX_VOCAB + 1, 0, 0)])
+    (-1, 10, 0, 0), (1, 0, 0, 0), (1, 10, _lib.MAX_TOP_LOGPROBS + 1, 0), (1, 10, 0, 7),
+    (1, _lib.MAX_VOCAB + 1, 0, 0)])
 def test_workspace_size_rejects_bad_shapes(args):
     with pytest.raises(_lib.SamplerError) as ei:
         _lib.workspace_size(*args)
