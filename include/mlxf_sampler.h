@@ -262,7 +262,8 @@ int mlxf_apply_mask(const void* d_logits, int dtype, int B, int V, int64_t row_s
  *                     division) with the removed entries at -inf.  NULL
  *                     arrays: that filter off.
  * The kept sets are the sampling call's, with its masses and tie rules
- * (D2, D3); NaN logits read as -inf.  d_out has the logits' dtype; it may be
+ * (top-p order is value desc, index asc; the mass is summed in fixed point,
+ * so it does not depend on the summation order); NaN logits read as -inf.  d_out has the logits' dtype; it may be
  * d_logits itself (in place, out_stride == row_stride) but must not overlap it
  * otherwise.  No workspace: the output rows serve as scratch.  One workgroup
  * per row that reads its row about a dozen times: a helper, not the decode
