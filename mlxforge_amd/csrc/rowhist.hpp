@@ -55,7 +55,7 @@ hipError_t launch_row16_bf16(const Args& a, int ept, const RhArgs& x, hipStream_
 #define MLXF_RH_STAMP(i) \
   if (threadIdx.x == 0) mlxf_rh_stamps[blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime()
 #define MLXF_RH_WSTAMP(i) \
-  if ((threadIdx.x & 63) == 0) mlxf_rh_stamps[16384 + (blockIdx.x * 16 + (threadIdx.x >> 6)) * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
+  if ((threadIdx.x & 63) == 0) mlxf_rh_stamps[16384 + (blockIdx.x * 16 + (threadIdx.x >> 6)) * 16 + (i)] = __builtin_amdgcn_s_memrealtime()
 #define MLXF_RC_STAMP(i) \
   if (threadIdx.x == 0) mlxf_rh_stamps[8192 + blockIdx.x * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
 #else
@@ -78,7 +78,9 @@ constexpr int B_POSHUGE = 2 * NWIN + 2;  // z >= 256, +inf, positive NaN
 constexpr int B_TRASH = NBIN;        // elements past the row end
 constexpr int CHW = NBIN + 1;        // counters per chunk histogram
 constexpr int CHB = CHW * 4;         // bytes per chunk histogram (36880)
-constexpr int NCH = 4;               // chunks per row
+constexpr int NCH = 4;               // chunk histograms per row
+constexpr int NSUB_MAX = 8;          // chunks the walk picks from: the halves of the four (packed
+                                     // counters) when one workgroup counts the row, else the four
 constexpr int ITER = NT * 8;         // elements one pass-1 iteration covers
 constexpr int BPT = 11;              // bins per thread in the deciding step (11 * 1024 >= NBIN;
                                      // an odd stride keeps a wave's LDS accesses on distinct banks)
@@ -95,10 +97,9 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int SPARSE = 512;  // largest sparse draw list (elements at or above the cutoff in the chunk)
 struct Scratch {
-  unsigned long long u64r[NWV][NCH];
+  unsigned long long u64r[NWV][NSUB_MAX];
   double dr[NWV];
-  unsigned int ur[NWV][NCH];
-  unsigned int un[NWV][NCH];
+  unsigned long long ugn[NWV][NSUB_MAX];
   unsigned int lst[SPARSE];
   int ir[NWV][2];
   unsigned long long sel64[8];
@@ -190,9 +191,10 @@ __device__ __forceinline__ T bscan(T x, T* red, T* total) {
 }
 
 // ---- pass 1: one word (two values, as bin offsets x2) into chunk histogram
-// (PAGE, ADD, IMM)
+// (PAGE, ADD, IMM); inc is 1, or 65536 for the second half of a chunk with
+// packed counters
 template <unsigned PAGE, unsigned ADD, unsigned IMM>
-__device__ __forceinline__ void count_word(unsigned char* lds, unsigned int x2) {
+__device__ __forceinline__ void count_word(unsigned char* lds, unsigned int x2, unsigned int inc) {
   constexpr unsigned short K = static_cast<unsigned short>(4u * (NWIN + 1) + ADD);
   const u16x2 o = __builtin_bit_cast(u16x2, x2) * (u16x2){4, 4} + (u16x2){K, K};
   const unsigned int o2 = __builtin_bit_cast(unsigned int, o);
@@ -200,21 +202,22 @@ __device__ __forceinline__ void count_word(unsigned char* lds, unsigned int x2) 
   // permute (one operation, and IMM stays in the instruction's offset field)
   const unsigned int a0 = PAGE ? __builtin_amdgcn_perm(PAGE, o2, 0x07060100u) : (o2 & 0xffffu);
   const unsigned int a1 = PAGE ? __builtin_amdgcn_alignbit(PAGE >> 16, o2, 16) : (o2 >> 16);
-  atomicAdd(reinterpret_cast<unsigned int*>(lds + IMM + a0), 1u);
-  atomicAdd(reinterpret_cast<unsigned int*>(lds + IMM + a1), 1u);
+  atomicAdd(reinterpret_cast<unsigned int*>(lds + IMM + a0), inc);
+  atomicAdd(reinterpret_cast<unsigned int*>(lds + IMM + a1), inc);
 }
 
 // One iteration (8 values) into a chunk histogram; best / bestit track the
 // largest bin offset and the first iteration holding it.
 template <unsigned PAGE, unsigned ADD, unsigned IMM>
-__device__ __forceinline__ void count_iter(unsigned char* lds, const uint4& q, int it, int& best, int& bestit) {
+__device__ __forceinline__ void count_iter(unsigned char* lds, const uint4& q, int it, unsigned int inc, int& best,
+                                           int& bestit) {
   const unsigned int w[4] = {q.x, q.y, q.z, q.w};
   unsigned int m = 0x80008000u;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const unsigned int x2 = binx2(w[k]);
     m = pkmax_i16(m, x2);
-    count_word<PAGE, ADD, IMM>(lds, x2);
+    count_word<PAGE, ADD, IMM>(lds, x2, inc);
   }
   const int mf = max(static_cast<int>(static_cast<short>(m & 0xffffu)), static_cast<int>(static_cast<short>(m >> 16)));
   if (mf > best) {
@@ -224,16 +227,16 @@ __device__ __forceinline__ void count_iter(unsigned char* lds, const uint4& q, i
 }
 
 // One iteration into the histogram of chunk c (wave-uniform).
-__device__ __forceinline__ void count_iter_c(unsigned char* lds, const uint4& q, int it, int c, int& best,
-                                             int& bestit) {
+__device__ __forceinline__ void count_iter_c(unsigned char* lds, const uint4& q, int it, int c, unsigned int inc,
+                                             int& best, int& bestit) {
   if (c == 0)
-    count_iter<0u, 0u, 0u>(lds, q, it, best, bestit);
+    count_iter<0u, 0u, 0u>(lds, q, it, inc, best, bestit);
   else if (c == 1)
-    count_iter<0u, 0u, static_cast<unsigned>(CHB)>(lds, q, it, best, bestit);
+    count_iter<0u, 0u, static_cast<unsigned>(CHB)>(lds, q, it, inc, best, bestit);
   else if (c == 2)
-    count_iter<PAGE1, PAGE1_ADD, 0u>(lds, q, it, best, bestit);
+    count_iter<PAGE1, PAGE1_ADD, 0u>(lds, q, it, inc, best, bestit);
   else
-    count_iter<PAGE1, PAGE1_ADD, static_cast<unsigned>(CHB)>(lds, q, it, best, bestit);
+    count_iter<PAGE1, PAGE1_ADD, static_cast<unsigned>(CHB)>(lds, q, it, inc, best, bestit);
 }
 
 // This thread's word of the iteration the row ends in (ITER * it < V <
@@ -258,8 +261,8 @@ __device__ __forceinline__ uint4 tail_word(const unsigned short* row, int V, int
 // counts nothing (all its elements in one counter would serialise the wave's
 // atomics); past-the-end elements of the word holding the end count in the
 // trash slot and not towards the maximum.
-__device__ __forceinline__ void count_tail(unsigned char* lds, const uint4& q, int V, int it, int c, int& best,
-                                           int& bestit) {
+__device__ __forceinline__ void count_tail(unsigned char* lds, const uint4& q, int V, int it, int c,
+                                           unsigned int inc, int& best, int& bestit) {
   const int p0 = it * ITER + static_cast<int>(threadIdx.x) * 8;
   if (p0 >= V) return;
   const unsigned int w[4] = {q.x, q.y, q.z, q.w};
@@ -273,13 +276,13 @@ __device__ __forceinline__ void count_tail(unsigned char* lds, const uint4& q, i
     if (vhi) mf = max(mf, static_cast<int>(static_cast<short>(x2 >> 16)));
     x2 = (vlo ? (x2 & 0xffffu) : XT) | (vhi ? (x2 & 0xffff0000u) : (XT << 16));
     if (c == 0)
-      count_word<0u, 0u, 0u>(lds, x2);
+      count_word<0u, 0u, 0u>(lds, x2, inc);
     else if (c == 1)
-      count_word<0u, 0u, static_cast<unsigned>(CHB)>(lds, x2);
+      count_word<0u, 0u, static_cast<unsigned>(CHB)>(lds, x2, inc);
     else if (c == 2)
-      count_word<PAGE1, PAGE1_ADD, 0u>(lds, x2);
+      count_word<PAGE1, PAGE1_ADD, 0u>(lds, x2, inc);
     else
-      count_word<PAGE1, PAGE1_ADD, static_cast<unsigned>(CHB)>(lds, x2);
+      count_word<PAGE1, PAGE1_ADD, static_cast<unsigned>(CHB)>(lds, x2, inc);
   }
   if (mf > best) {
     best = mf;
@@ -289,8 +292,9 @@ __device__ __forceinline__ void count_tail(unsigned char* lds, const uint4& q, i
 
 // Pass 1 over the whole row: D iterations' loads in flight (a register ring;
 // the first D are issued before the histograms are cleared, so the clear
-// overlaps them), chunk c = it / ipc.
-template <int D>
+// overlaps them), chunk c = it / ipc; with packed counters (PK, ipc even) the
+// second half of a chunk's iterations counts in the high 16 bits.
+template <int D, bool PK>
 __device__ __forceinline__ void count_row(unsigned char* lds, const unsigned short* row, int V, int ipc, int nfull,
                                           int& best, int& bestit) {
   const int tid = threadIdx.x;
@@ -315,13 +319,15 @@ __device__ __forceinline__ void count_row(unsigned char* lds, const unsigned sho
         const uint4 q = buf[j];
         if (i + D < nfull) buf[j] = rv[static_cast<size_t>(i + D) * NT + tid];
         const int c = (i >= ipc) + (i >= 2 * ipc) + (i >= 3 * ipc);
-        count_iter_c(lds, q, i, c, best, bestit);
+        const unsigned int inc = PK && i - c * ipc >= (ipc >> 1) ? 0x10000u : 1u;
+        count_iter_c(lds, q, i, c, inc, best, bestit);
       }
     }
   }
   if (has_tail) {
     const int c = (nfull >= ipc) + (nfull >= 2 * ipc) + (nfull >= 3 * ipc);
-    count_tail(lds, tq, V, nfull, c, best, bestit);
+    const unsigned int inc = PK && nfull - c * ipc >= (ipc >> 1) ? 0x10000u : 1u;
+    count_tail(lds, tq, V, nfull, c, inc, best, bestit);
   }
 }
 
@@ -351,11 +357,11 @@ __device__ __forceinline__ void count_chunk(unsigned char* lds, const unsigned s
       if (i < it1) {
         const uint4 q = buf[j];
         if (i + D < it1) buf[j] = rv[static_cast<size_t>(i + D) * NT + tid];
-        count_iter<0u, 0u, 0u>(lds, q, i, best, bestit);
+        count_iter<0u, 0u, 0u>(lds, q, i, 1u, best, bestit);
       }
     }
   }
-  if (has_tail) count_tail(lds, tq, V, it1, 0, best, bestit);
+  if (has_tail) count_tail(lds, tq, V, it1, 0, 1u, best, bestit);
 }
 
 // Lowest index in this thread's 8 elements of iteration it whose bin is b
@@ -375,8 +381,63 @@ __device__ __forceinline__ int first_at(const unsigned short* row, int V, int it
   return myarg;
 }
 
-__device__ __forceinline__ unsigned int hcount(const unsigned int* hist, int c, int b) {
-  return hist[c * CHW + b];
+// Counts with packed counters (PK): the word of chunk c holds the count of its
+// first half (the walk's chunk 2c) in the low 16 bits and of its second half
+// (chunk 2c + 1) in the high 16 bits.  hsub: walk chunk c's count of bin b;
+// htot: the row's count of bin b.
+template <bool PK>
+__device__ __forceinline__ unsigned int hsub(const unsigned int* hist, int c, int b) {
+  if constexpr (PK) {
+    const unsigned int w = hist[(c >> 1) * CHW + b];
+    return (c & 1) ? (w >> 16) : (w & 0xffffu);
+  } else {
+    return hist[c * CHW + b];
+  }
+}
+template <bool PK>
+__device__ __forceinline__ unsigned int htot(const unsigned int* hist, int b) {
+  const unsigned int w0 = hist[b], w1 = hist[CHW + b], w2 = hist[2 * CHW + b], w3 = hist[3 * CHW + b];
+  if constexpr (PK)
+    return ((w0 & 0xffffu) + (w0 >> 16)) + ((w1 & 0xffffu) + (w1 >> 16)) + ((w2 & 0xffffu) + (w2 >> 16)) +
+           ((w3 & 0xffffu) + (w3 >> 16));
+  else
+    return (w0 + w1) + (w2 + w3);
+}
+
+// Wave reduce-scatter of N per-lane values (N = 4 or 8): lane l receives the
+// wave's sum of v[l / (64 / N)].  Each step halves the values a lane holds,
+// swapping the other half with the lane 32, 16 (and 8) places away; the
+// remaining lanes of a group then sum by exchanges (whole wave active).
+// Lane src's value (ds_bpermute; whole wave active).
+__device__ __forceinline__ unsigned long long shfl_u64(unsigned long long v, int src) {
+  const int lo = __shfl(static_cast<int>(v), src, 64), hi = __shfl(static_cast<int>(v >> 32), src, 64);
+  return (static_cast<unsigned long long>(static_cast<unsigned int>(hi)) << 32) | static_cast<unsigned int>(lo);
+}
+template <int M, typename T>
+__device__ __forceinline__ T rs_step(T a, T b) {
+  const bool up = (threadIdx.x & M) != 0;
+  return (up ? b : a) + xshf<M>(up ? a : b);
+}
+template <int N, typename T>
+__device__ __forceinline__ T wave_rs(const T (&v)[N]) {
+  static_assert(N == 4 || N == 8, "four or eight values");
+  T a[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) a[i] = rs_step<32>(v[i], v[N / 2 + i]);
+  T b[N / 4];
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) b[i] = rs_step<16>(a[i], a[N / 4 + i]);
+  T c;
+  if constexpr (N == 8) {
+    c = rs_step<8>(b[0], b[1]);
+  } else {
+    c = b[0];
+    c += xshf<8>(c);
+  }
+  c += xshf<4>(c);
+  c += xshf<2>(c);
+  c += xshf<1>(c);
+  return c;
 }
 
 // The row's kept set after top-k, top-p and min_p, on the bins: every bin
@@ -524,6 +585,10 @@ __global__ __launch_bounds__(rh::NT, 1) void k_cnt16(Args a, RhArgs x) {
 template <int DT, int EPT, bool SPLIT>
 __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
   using namespace rh;
+  // counting here, the counters are packed and the walk picks one of eight
+  // half chunks; with split counting, one of the four chunks
+  constexpr bool PK = !SPLIT;
+  constexpr int NSUB = PK ? 2 * NCH : NCH;
   __shared__ __align__(16) unsigned char lds[LDS_BYTES];
   unsigned int* hist = reinterpret_cast<unsigned int*>(lds);
   Scratch& sc = *reinterpret_cast<Scratch*>(lds + HIST_BYTES);
@@ -575,7 +640,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
     // ---- pass 1: every element counted once
     int best = -(NWIN + 1) - 1;  // (bin offset; below every bin)
     int bestit = -1;
-    count_row<RH_DEPTH>(lds, row, V, x.ipc, x.nfull, best, bestit);
+    count_row<RH_DEPTH, PK>(lds, row, V, x.ipc, x.nfull, best, bestit);
     __syncthreads();
     MLXF_RH_STAMP(1);
 
@@ -596,9 +661,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
 #pragma unroll
   for (int j = 0; j < BPT; ++j) {
     const int b = own_bin(tid, j);
-    cnt[j] = b >= 0 ? static_cast<int>(hcount(hist, 0, b) + hcount(hist, 1, b) + hcount(hist, 2, b) +
-                                        hcount(hist, 3, b))
-                    : 0;
+    cnt[j] = b >= 0 ? static_cast<int>(htot<PK>(hist, b)) : 0;
   }
 
   // ---- per-bin work, branch-free over the thread's bins: the log-sum-exp of
@@ -653,16 +716,14 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
   }
   if (do_w && tid == 0) {
     bool bad = !__builtin_isfinite(Mp);
-    if (!bad && hcount(hist, 0, B_TINY) + hcount(hist, 1, B_TINY) + hcount(hist, 2, B_TINY) +
-                        hcount(hist, 3, B_TINY) > 0u) {
+    if (!bad && htot<PK>(hist, B_TINY) > 0u) {
       // |z'| of a tiny value is below 2^-28 / T (rounded up by the bf16
       // rounding); the weight's log2 offset nc must absorb it
       const float zb = 0x1p-28f / md.Tr * 1.0078125f;
       const int e = nc == 0.0f ? -1000 : ilogbf(nc);
       bad = !(zb * LOG2E * 1.0001f < ldexpf(1.0f, e - 24));
     }
-    if (!bad && hcount(hist, 0, B_NEGHUGE) + hcount(hist, 1, B_NEGHUGE) + hcount(hist, 2, B_NEGHUGE) +
-                        hcount(hist, 3, B_NEGHUGE) > 0u) {
+    if (!bad && htot<PK>(hist, B_NEGHUGE) > 0u) {
       // the largest value of the low bin, -256, must carry no mass
       bad = q40(wfun(zdiv<DT>(-256.0f, md.Tr, md.y, false), Mp, nc, false)) != 0ull;
     }
@@ -713,10 +774,10 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
     auto count_range = [&](int lo, int hi) -> int {
       int c = 0;
       for (int b = lo + lane; b <= hi; b += 64)
-        c += static_cast<int>(hcount(hist, 0, b) + hcount(hist, 1, b) + hcount(hist, 2, b) + hcount(hist, 3, b));
+        c += static_cast<int>(htot<PK>(hist, b));
       return wave_sum(c);
     };
-    // (wave 0, whole wave) the chunk holding the draw, from lane c < NCH's
+    // (wave 0, whole wave) the chunk holding the draw, from lane c < NSUB's
     // chunk c kept mass K, partial-group elements G and kept-bin elements N:
     // sel[1] = the chunk, sel[2] = its kept ties, sel[14] = its elements at
     // or above the cutoff, sel64[0] = the draw's offset into its kept mass
@@ -733,7 +794,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         Tu = 0ull;
       else if (Tu >= W)
         Tu = W - 1ull;
-      const unsigned long long hit = __ballot(lane < NCH && K > 0ull && cumi > Tu);
+      const unsigned long long hit = __ballot(lane < NSUB && K > 0ull && cumi > Tu);
       const int cs = hit ? __ffsll(static_cast<long long>(hit)) - 1 : -1;
       // (lane reads with the whole wave active: a value computed only in
       // the lane-0 branch would not exist in lane cs)
@@ -756,45 +817,44 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
       const int need = k.t > 0u ? k.glo : k.kb;
       const int nr = (bmax - need + 64) >> 6;  // rounds of 64 bins
       if (nr > 4) return false;
-      unsigned long long kc[NCH];
-      int gc[NCH], nk[NCH];
+      // per chunk: kept mass, and (packed) kept-bin elements << 32 | partial-group elements
+      unsigned long long kc[NSUB], gn[NSUB];
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
+      for (int c = 0; c < NSUB; ++c) {
         kc[c] = 0ull;
-        gc[c] = 0;
-        nk[c] = 0;
+        gn[c] = 0ull;
       }
       for (int j = 0; j < nr; ++j) {
         const int b = bmax - lane - 64 * j;
         const bool in = b >= need;
-        unsigned int h[NCH];
+        unsigned int h[NSUB];
+        unsigned int any = 0u;
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) h[c] = in ? hcount(hist, c, b) : 0u;
-        if ((h[0] | h[1] | h[2] | h[3]) != 0u) {
+        for (int c = 0; c < NSUB; ++c) {
+          h[c] = in ? hsub<PK>(hist, c, b) : 0u;
+          any |= h[c];
+        }
+        if (any != 0u) {
           if (b >= k.kb) {
             const unsigned long long qq = q40(wfun(zp_of(b), Mp, nc, false));
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) {
+            for (int c = 0; c < NSUB; ++c) {
               kc[c] += static_cast<unsigned long long>(h[c]) * qq;
-              nk[c] += static_cast<int>(h[c]);
+              gn[c] += static_cast<unsigned long long>(h[c]) << 32;
             }
           } else {
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) gc[c] += static_cast<int>(h[c]);
+            for (int c = 0; c < NSUB; ++c) gn[c] += h[c];
           }
         }
       }
-      unsigned long long K = 0ull;
-      int G = 0, N = 0;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        const unsigned long long kcs = wave_sum(kc[c]);
-        const int gcs = wave_sum(gc[c]);
-        const int nks = wave_sum(nk[c]);
-        K = lane == c ? kcs : K;
-        G = lane == c ? gcs : G;
-        N = lane == c ? nks : N;
-      }
+      // lane c < NSUB: chunk c's sums (held by lane c * 64 / NSUB after the
+      // reduce-scatter)
+      const unsigned long long kcs = wave_rs<NSUB>(kc), gns = wave_rs<NSUB>(gn);
+      const int src = (lane < NSUB ? lane : 0) * (64 / NSUB);
+      const unsigned long long K0 = shfl_u64(kcs, src), GN0 = shfl_u64(gns, src);
+      const unsigned long long K = lane < NSUB ? K0 : 0ull, GN = lane < NSUB ? GN0 : 0ull;
+      const int G = static_cast<int>(static_cast<unsigned int>(GN)), N = static_cast<int>(GN >> 32);
       chunk_pick(K, G, N, k);
       return true;
     };
@@ -967,65 +1027,73 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
       const int need_lo = kp.t > 0u ? kp.glo : kp.kb;
       // per chunk: kept mass kc, partial-group elements gc, and elements of
       // the wholly kept bins nk (unless wave 0 has picked the chunk already)
+      MLXF_RH_WSTAMP(12);
       if (sc.sel[5] == 0) {
-        unsigned long long kc[NCH];
-        unsigned int gc[NCH], nk[NCH];
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          kc[c] = 0ull;
-          gc[c] = 0u;
-          nk[c] = 0u;
-        }
-        // a wave whose highest bin is below every kept one adds nothing
+        // Per chunk, over the thread's own bins: kept mass kc (as h * low 32
+        // bits of the mass in 64 bits plus h * high bits in 32: h < 2^16 and
+        // a mass < 2^41), kept-bin elements nk and partial-group elements gc.
+        // A wave whose highest bin is below every kept one adds nothing.
+        unsigned long long kcs = 0ull, gns = 0ull;
         if (own_bin(wid * 64, 0) >= need_lo) {
+          unsigned long long kl[NSUB];
+          unsigned int kh[NSUB], nk[NSUB], gc[NSUB];
+#pragma unroll
+          for (int c = 0; c < NSUB; ++c) {
+            kl[c] = 0ull;
+            kh[c] = 0u;
+            nk[c] = 0u;
+            gc[c] = 0u;
+          }
           if (own_bin(tid, 0) >= need_lo) {
 #pragma unroll
             for (int j = 0; j < BPT; ++j) {
               const int b = own_bin(tid, j);
               if (b < 0 || cnt[j] == 0) continue;
               if (b >= kp.kb) {
-                const unsigned long long qq = q[j];
+                const unsigned int qlo = static_cast<unsigned int>(q[j]), qhi = static_cast<unsigned int>(q[j] >> 32);
 #pragma unroll
-                for (int c = 0; c < NCH; ++c) {
-                  const unsigned int h = hcount(hist, c, b);
-                  kc[c] += static_cast<unsigned long long>(h) * qq;
+                for (int c = 0; c < NSUB; ++c) {
+                  const unsigned int h = hsub<PK>(hist, c, b);
+                  kl[c] += static_cast<unsigned long long>(h) * qlo;
+                  kh[c] += h * qhi;
                   nk[c] += h;
                 }
               } else if (kp.t > 0u && b >= kp.glo && b <= kp.ghi) {
 #pragma unroll
-                for (int c = 0; c < NCH; ++c) gc[c] += hcount(hist, c, b);
+                for (int c = 0; c < NSUB; ++c) gc[c] += hsub<PK>(hist, c, b);
               }
             }
           }
+          unsigned long long kc[NSUB], gn[NSUB];
 #pragma unroll
-          for (int c = 0; c < NCH; ++c) {
-            kc[c] = wave_sum(kc[c]);
-            gc[c] = static_cast<unsigned int>(wave_sum(static_cast<int>(gc[c])));
-            nk[c] = static_cast<unsigned int>(wave_sum(static_cast<int>(nk[c])));
+          for (int c = 0; c < NSUB; ++c) {
+            kc[c] = kl[c] + (static_cast<unsigned long long>(kh[c]) << 32);
+            gn[c] = (static_cast<unsigned long long>(nk[c]) << 32) | gc[c];
           }
+          // the wave's sums of chunk c in lanes c * 64 / NSUB ...
+          kcs = wave_rs<NSUB>(kc);
+          gns = wave_rs<NSUB>(gn);
         }
-        if (lane == 0) {
-#pragma unroll
-          for (int c = 0; c < NCH; ++c) {
-            sc.u64r[wid][c] = kc[c];
-            sc.ur[wid][c] = gc[c];
-            sc.un[wid][c] = nk[c];
-          }
+        MLXF_RH_WSTAMP(8);
+        if ((lane & (64 / NSUB - 1)) == 0) {
+          sc.u64r[wid][lane / (64 / NSUB)] = kcs;
+          sc.ugn[wid][lane / (64 / NSUB)] = gns;
         }
         __syncthreads();
+        MLXF_RH_WSTAMP(9);
         if (wid == 0) {
-          // lane c < NCH: chunk c's sums over the waves
-          unsigned long long K = 0ull;
-          int G = 0, N = 0;
-          if (lane < NCH) {
+          // ... and lane c < NSUB's over the waves
+          unsigned long long K = 0ull, GN = 0ull;
+          if (lane < NSUB) {
 #pragma unroll
             for (int w2 = 0; w2 < NWV; ++w2) {
               K += sc.u64r[w2][lane];
-              G += static_cast<int>(sc.ur[w2][lane]);
-              N += static_cast<int>(sc.un[w2][lane]);
+              GN += sc.ugn[w2][lane];
             }
           }
-          chunk_pick(K, G, N, kp);
+          MLXF_RH_WSTAMP(10);
+          chunk_pick(K, static_cast<int>(static_cast<unsigned int>(GN)), static_cast<int>(GN >> 32), kp);
+          MLXF_RH_WSTAMP(11);
         }
       }
       __syncthreads();
@@ -1035,8 +1103,11 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
       fb = cs < 0;
       MLXF_RH_STAMP(7);
       if (!fb) {
-        const int EPTW = x.ipc * 8;
-        const int c0 = cs * x.ipc * ITER + tid * EPTW;
+        // the walk's chunk: ips iterations' elements, EPTW consecutive ones
+        // per thread
+        const int ips = PK ? x.ipc >> 1 : x.ipc;
+        const int EPTW = ips * 8;
+        const int c0 = cs * ips * ITER + tid * EPTW;
         // the thread's first 16-byte words of the walk requested before the
         // weight table is built (the table needs the histograms to be dead)
         constexpr int WG = 8;
@@ -1048,6 +1119,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
           for (int k = 0; k < WG; ++k)
             if (k < EPTW / 8) wq[k] = rv[k];
         }
+        MLXF_RH_WSTAMP(13);
         if (sc.sel[14] <= SPARSE && EPTW <= 64) {
           // ---- sparse draw: the chunk's few elements at or above need_lo,
           // listed in index order (each thread's qualifying elements at its
@@ -1117,12 +1189,14 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         // mass at byte 8 * bin, 0 for every other bin
         unsigned long long* tab = reinterpret_cast<unsigned long long*>(lds);
         __syncthreads();
+        MLXF_RH_WSTAMP(14);
 #pragma unroll
         for (int j = 0; j < BPT; ++j) {
           const int b = own_bin(tid, j);
           if (b >= 0) tab[b] = (b >= kp.kb && cnt[j] > 0) ? q[j] : 0ull;
         }
         if (tid == 0) tab[B_TRASH] = 0ull;
+        MLXF_RH_WSTAMP(15);
         __syncthreads();
         MLXF_RH_WSTAMP(5);
         const unsigned long long km0 = kp.t > 0u ? walk_sum<true, WG>(row, V, c0, EPTW, tab, kp, wq, whole)
@@ -1154,7 +1228,7 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         const int holder = sc.sel[7];
         if (holder >= 0 && tid < 64) {
           // wave 0 walks the holder's elements, one per lane per round
-          const int hbase = cs * x.ipc * ITER + holder * EPTW;
+          const int hbase = cs * ips * ITER + holder * EPTW;
           const unsigned long long hrem = sc.sel64[1];
           unsigned int tie_rank = static_cast<unsigned int>(sc.sel[8]);
           unsigned long long carry = 0ull;

@@ -33,14 +33,20 @@ struct Layout {
 // no refine stages), but not the first-pass-only timing call (nst < 0).  With
 // at most ROW_SPLIT_MAX_B rows (four chunk workgroups per row still fit the
 // 256 CUs at once) the chunks are counted by their own workgroups first.
+// With more rows each workgroup counts its row with 16-bit counters for the
+// two halves of each chunk, so no half may hold more than 65535 logits: an
+// even number of iterations per chunk, at most 7 per half (V <= 458752; larger
+// vocabularies with that many rows take the per-slice path).
 constexpr int ROW_ITER_LOGITS = 1024 * 8;              // logits per pass-1 iteration
 constexpr int ROW_CHUNK_LOGITS = 4 * ROW_ITER_LOGITS;  // logits per chunk iteration count
 constexpr int ROW_MIN_V = 32768;
 constexpr int ROW_SPLIT_MAX_B = 64;
-bool use_row_path(int dtype, int V, int K_max, bool vecok, int nst) {
-  return dtype == MLXF_DTYPE_BF16 && K_max == 0 && vecok && nst >= 0 && V >= ROW_MIN_V;
-}
+constexpr int ROW_PACK_MAX_V = 4 * 2 * 7 * ROW_ITER_LOGITS;
 bool row_split(int dtype, int B, int V) { return dtype == MLXF_DTYPE_BF16 && V >= ROW_MIN_V && B <= ROW_SPLIT_MAX_B; }
+bool use_row_path(int dtype, int B, int V, int K_max, bool vecok, int nst) {
+  return dtype == MLXF_DTYPE_BF16 && K_max == 0 && vecok && nst >= 0 && V >= ROW_MIN_V &&
+         (row_split(dtype, B, V) || V <= ROW_PACK_MAX_V);
+}
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
@@ -267,11 +273,12 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
     if (!d_temperature && nst > 0) nst = 0;  // every row greedy
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e;
-    if (use_row_path(dtype, V, K_main, vecok, nst)) {
+    if (use_row_path(dtype, B, V, K_main, vecok, nst)) {
       RhArgs x;
-      x.ipc = (V + ROW_CHUNK_LOGITS - 1) / ROW_CHUNK_LOGITS;
-      x.nfull = V / ROW_ITER_LOGITS;
       const bool split = row_split(dtype, B, V);
+      x.ipc = split ? (V + ROW_CHUNK_LOGITS - 1) / ROW_CHUNK_LOGITS
+                    : 2 * ((V + 2 * ROW_CHUNK_LOGITS - 1) / (2 * ROW_CHUNK_LOGITS));
+      x.nfull = V / ROW_ITER_LOGITS;
       x.hsplit = split ? reinterpret_cast<unsigned int*>(ws + l.off_hsplit) : nullptr;
       x.crec = split ? reinterpret_cast<unsigned long long*>(ws + l.off_crec) : nullptr;
       e = launch_row16_bf16(a, l.EPT, x, st);

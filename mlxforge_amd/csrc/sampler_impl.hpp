@@ -1983,11 +1983,11 @@ __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1
       const float v = __uint_as_float(static_cast<unsigned int>(ent));
       return f2key(v == 0.0f ? 0.0f : v);
     };
-    unsigned int best = 0u;
-    for (int q = tid; q < 7 * SP; q += THREADS) {
-      const unsigned int c = sh.thr[q];
+    // F(c) = sum_s n_s(c) over slices [s4b, s4e) x 4 (the seven levels' reads
+    // in flight together)
+    auto fcount = [&](unsigned int c, int s4b, int s4e) {
       int cnt[7] = {0, 0, 0, 0, 0, 0, 0};
-      for (int s4 = 0; s4 < SP / 4; ++s4) {  // the seven levels' reads in flight together
+      for (int s4 = s4b; s4 < s4e; ++s4) {
         uint4 t4[7];
 #pragma unroll
         for (int j = 0; j < 7; ++j) t4[j] = reinterpret_cast<const uint4*>(&sh.thr[j * SP])[s4];
@@ -1995,15 +1995,22 @@ __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1
         for (int j = 0; j < 7; ++j)
           cnt[j] += (t4[j].x >= c ? 1 : 0) + (t4[j].y >= c ? 1 : 0) + (t4[j].z >= c ? 1 : 0) + (t4[j].w >= c ? 1 : 0);
       }
-      const int F = 32 * cnt[0] + 16 * cnt[1] + 8 * cnt[2] + 4 * cnt[3] + 2 * cnt[4] + cnt[5] + cnt[6];
-      if (F >= 64) best = max(best, c);
+      return 32 * cnt[0] + 16 * cnt[1] + 8 * cnt[2] + 4 * cnt[3] + 2 * cnt[4] + cnt[5] + cnt[6];
+    };
+    unsigned int best = 0u;
+    for (int q = tid; q < 7 * SP; q += THREADS) {
+      const unsigned int c = sh.thr[q];
+      if (fcount(c, 0, SP / 4) >= 64) best = max(best, c);
     }
     best = wave_max(best);
     if (lane == 0) sh.thw[wid] = best;
     if (wid == WAVES - 1) row_stats();
     __syncthreads();
-    // (a key k of -0 passes the candidates of +0 and -0 alike: okey gives both +0's key)
+    // (a key k of -0 passes the candidates of +0 and -0 alike: okey gives both
+    // +0's key.  The float compare against thf is the same test: -0 == +0, and
+    // a theta at or below -inf's key passes every candidate.)
     const unsigned int thk = max(max(sh.thw[0], sh.thw[1]), max(sh.thw[2], sh.thw[3]));
+    const float thf = thk <= KEY_NEG_INF ? -INFINITY : key2f(thk);
     MLXF_S1_STAMP(mlxf_d1_stamps, 2);
     // the candidates at or above theta, as order keys, gathered into sv: per
     // wave and round the slices' ballots, then one LDS atomic for the wave's
@@ -2023,7 +2030,7 @@ __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1
         const int n2 = s2 < S ? sh.sn[s2] : 0;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const bool ok = (lane + 64 * h < n2) & (okey(cw[2 * m + h]) >= thk);
+          const bool ok = (lane + 64 * h < n2) & (__uint_as_float(static_cast<unsigned int>(cw[2 * m + h])) >= thf);
           bal[2 * m + h] = __builtin_amdgcn_ballot_w64(ok);
           tot += static_cast<int>(__builtin_popcountll(bal[2 * m + h]));
         }
@@ -2033,6 +2040,7 @@ __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1
       wb = __builtin_amdgcn_readlane(wb, 0);
 #pragma unroll
       for (int q = 0; q < 2 * SPW; ++q) {
+        if (bal[q] == 0ull) continue;  // (uniform: most slot groups hold no candidate)
         const int p = wb + lane_below(bal[q]);
         if (((bal[q] >> lane) & 1ull) && p < CBUF) sh.sv[p] = order_key(cw[q]);
         wb += static_cast<int>(__builtin_popcountll(bal[q]));

@@ -72,11 +72,15 @@ def _check(host, T, k, p, mp, tlp, u, label, V=None, dev=None):
 
 
 @pytest.mark.parametrize("V,B", [(32768, 16), (32769, 16), (50001, 16), (151936, 16), (262144, 16),
-                                 (40000, 1), (65536 + 8192 * 3 + 5, 9), (151936, 80)])
+                                 (40000, 1), (65536 + 8192 * 3 + 5, 9), (151936, 80), (32768, 72),
+                                 (32769, 72), (65536 + 8192 * 3 + 5, 70), (262144, 72), (458752, 65),
+                                 (458752 + 8, 65)])
 def test_row_kinds(V, B):
     """B <= 64: split call (the chunks counted by their own workgroups, XCD
-    groups of 8 rows, a partial last group for B = 1 and 9); B = 80: one
-    workgroup per row."""
+    groups of 8 rows, a partial last group for B = 1 and 9); B > 64: one
+    workgroup per row, 16-bit counters for the halves of each chunk (the walk
+    picks one of eight), up to V = 458752 (the largest whose half chunks hold
+    at most 65535 logits; one more takes the per-slice path)."""
     rng = np.random.default_rng(900 + V % 97 + B)
     z = np.empty((B, V), np.float32)
     for r in range(B):
@@ -94,11 +98,12 @@ def test_row_kinds(V, B):
     _check(_bits(z), T, k, p, mp, tlp, u, f"row kinds V={V}")
 
 
-def test_heavy_ties_and_flat_rows():
+@pytest.mark.parametrize("B", [16, 72])
+def test_heavy_ties_and_flat_rows(B):
     """Few distinct values: every cutoff lands in a tie group spread over the
-    four chunks."""
-    rng = np.random.default_rng(31)
-    B, V = 16, 120000
+    four chunks (B = 16) or the eight half chunks (B = 72)."""
+    rng = np.random.default_rng(31 + B)
+    V = 120000
     z = np.empty((B, V), np.float32)
     for r in range(B):
         if r % 3 == 0:
@@ -109,7 +114,7 @@ def test_heavy_ties_and_flat_rows():
             z[r] = rng.integers(0, 2, V).astype(np.float32) * 0.5
     T, k, p, mp, tlp, u = _params(rng, B)
     for uu in (u, np.full(B, 0.0, np.float32), np.full(B, 0.999999, np.float32)):
-        _check(_bits(z), T, k, p, mp, tlp, uu, "heavy ties")
+        _check(_bits(z), T, k, p, mp, tlp, uu, f"heavy ties B={B}")
 
 
 @pytest.mark.parametrize("reps", [1, 6])
