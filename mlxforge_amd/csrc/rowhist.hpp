@@ -190,6 +190,30 @@ __device__ __forceinline__ T bscan(T x, T* red, T* total) {
   return inc - x + (wid > 0 ? before : T(0));
 }
 
+// bscan of a 64-bit x and an int y at once (one pair of barriers): the
+// exclusive scans are returned in *ex, *ey, the block sums in *tx, *ty.
+__device__ __forceinline__ void bscan2(unsigned long long x, int y, unsigned long long* redx, int* redy,
+                                       unsigned long long* ex, int* ey, unsigned long long* tx, int* ty) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const unsigned long long ix = wave_incl_scan_dpp(x);
+  const int iy = wave_incl_scan_dpp(y);
+  __syncthreads();
+  if (lane == 63) {
+    redx[wid] = ix;
+    redy[wid] = iy;
+  }
+  __syncthreads();
+  const unsigned long long wx = row_incl_scan16(lane < NWV ? redx[lane & (NWV - 1)] : 0ull);
+  const int wy = row_incl_scan16(lane < NWV ? redy[lane & (NWV - 1)] : 0);
+  *tx = rdl(wx, NWV - 1);
+  *ty = rdl(wy, NWV - 1);
+  const int src = wid > 0 ? wid - 1 : 0;
+  const unsigned long long bx = rdl(wx, src);
+  const int by = rdl(wy, src);
+  *ex = ix - x + (wid > 0 ? bx : 0ull);
+  *ey = iy - y + (wid > 0 ? by : 0);
+}
+
 // ---- pass 1: one word (two values, as bin offsets x2) into chunk histogram
 // (PAGE, ADD, IMM); inc is 1, or 65536 for the second half of a chunk with
 // packed counters
@@ -1205,18 +1229,20 @@ __global__ __launch_bounds__(rh::NT, 1) void k_row16(Args a, RhArgs x) {
         const int gt = static_cast<int>(km0 >> 56);
         MLXF_RH_WSTAMP(6);
         MLXF_RH_STAMP(8);
-        int gex = 0;
+        // one scan of the wholly kept mass and the partial group's elements;
+        // the first tkc of those (index order) are kept, so the threads before
+        // this one keep min(gex, tkc) of them
+        if (tid == 0) sc.sel[7] = -1;
+        unsigned long long kex, ktot;
+        int gex, gtot;
+        bscan2(km, gt, &sc.u64r[0][0], &sc.ir[0][0], &kex, &gex, &ktot, &gtot);
         if (kp.t > 0u) {
-          int gtot;
-          gex = bscan(gt, &sc.ir[0][0], &gtot);
           const unsigned int kt = tkc > static_cast<unsigned>(gex)
                                       ? min(tkc - static_cast<unsigned>(gex), static_cast<unsigned>(gt))
                                       : 0u;
           km += static_cast<unsigned long long>(kt) * kp.wt;
+          kex += static_cast<unsigned long long>(min(static_cast<unsigned>(gex), tkc)) * kp.wt;
         }
-        if (tid == 0) sc.sel[7] = -1;
-        unsigned long long ktot;
-        const unsigned long long kex = bscan(km, &sc.u64r[0][0], &ktot);
         if (km > 0ull && kex <= rem && rem < kex + km) {
           sc.sel[7] = tid;
           sc.sel[8] = gex;
