@@ -461,6 +461,7 @@ struct alignas(16) S1Lds {
   int ri[WAVES];
   float ramin[WAVES];
   double rd[WAVES];
+  double rw[WAVES];
   int rsc[WAVES + 1];
   int ncnt;  // survivors counted so far
   float thv;
@@ -609,6 +610,21 @@ __device__ __forceinline__ void scan1_body(const Args& a, int r, int s, const Sl
     }
     const double ws = wave_sum(static_cast<double>(t));
     if (lane == 0) sh.rd[wid] = ws;
+  }
+  if (md.kind == KIND_TOPP && md.need_list) {
+    // top-p rows with a list: the slice's weights relative to its own
+    // largest z' (the weight function of the draw with the slice's offset
+    // ncs in place of the row's), from which the deciding kernel bounds the
+    // row's total mass.  (Entries past the row end read as -inf and weigh 0.)
+    const float mps = zdiv<DT>(zmax, md.Tr, md.y, true);
+    float t = 0.0f;
+    if (__builtin_isfinite(mps)) {
+      const float ncs = -(mps * LOG2E);
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) t += __builtin_amdgcn_exp2f(wlog2(zdiv<DT>(v[e], md.Tr, md.y, true), ncs));
+    }
+    const double ws = wave_sum(static_cast<double>(t));
+    if (lane == 0) sh.rw[wid] = ws;
   }
   MLXF_S1_STAMP(mlxf_s1_stamps, 6);
   unsigned int msk = 0u;  // the thread's survivors (elements at or above t_64)
@@ -781,6 +797,15 @@ __device__ __forceinline__ void scan1_body(const Args& a, int r, int s, const Sl
       rp[5] = pack2(t4, static_cast<unsigned int>(heavy ? LIST : nsurv));
       rp[6] = pack2(t2, t1);
     }
+    if (md.kind == KIND_TOPP && md.need_list) {
+      // the slice's weight sum; 0 for a slice of -inf only, NaN (no bound)
+      // when its max is +inf
+      double ws = sh.rw[0];
+#pragma unroll
+      for (int w2 = 1; w2 < WAVES; ++w2) ws += sh.rw[w2];
+      if (!__builtin_isfinite(zmax)) ws = zmax < 0.0f ? 0.0 : static_cast<double>(NAN);
+      rp[7] = static_cast<unsigned long long>(__double_as_longlong(ws));
+    }
   }
   MLXF_S1_STAMP(mlxf_s1_stamps, 5);
 }
@@ -822,9 +847,12 @@ struct D1Lds {
   int szarg[MAX_S];
   float szmin[MAX_S];
   double slse[MAX_S];
+  double swsum[MAX_S];  // top-p rows: each slice's weight sum relative to its own max
   float zmax, zmin;
   int zarg;
   double lse;
+  double wlo, whi;      // top-p rows: bounds on the row's total fixed-point mass
+  int wok;              // ... usable
   int sel[4];
   unsigned long long kl_tu;  // two-wave top-k: the draw target
   int kl_nk;                 // ... entries kept (negated when their weights are all 0)
@@ -912,6 +940,30 @@ __device__ __forceinline__ bool klist_prep(const Mode& md, float Mp, const TopEn
   wv = si != INT_MAX ? wfun(sv, Mp, nc, !__builtin_isfinite(Mp)) : 0.0f;
   w = static_cast<double>(q40(wv));
   return true;
+}
+
+// For a top-p row: every real entry of the row's best-64 list in (z' desc,
+// index asc) order (sv, si; (-inf, INT_MAX) past them), their weights and
+// fixed-point masses, and the z' and index of the list's last entry (every
+// element outside the list has z' at most that z').
+template <int DT>
+__device__ __forceinline__ void plist_prep(const Mode& md, float Mp, const TopEnt* ml, float& sv, int& si, float& wv,
+                                           double& w, float& last_zp, int& last_i) {
+  const int lane = threadIdx.x & 63;
+  const float lv = ml[lane].v;
+  const int li = ml[lane].i;
+  const bool real = li != INT_MAX;
+  const float zp = real ? zdiv<DT>(lv, md.Tr, md.y, false) : -INFINITY;
+  last_i = rdl(li, LIST - 1);
+  last_zp = rdl(zp, LIST - 1);
+  sv = zp;
+  si = real ? li : INT_MAX;
+  const float nsv = __shfl_down(sv, 1, 64);
+  const int nsi = __shfl_down(si, 1, 64);
+  if (__ballot(lane < 63 && sv == nsv && si > nsi)) wave_sort(sv, si);
+  const float nc = -(Mp * LOG2E);
+  wv = si != INT_MAX ? wfun(sv, Mp, nc, !__builtin_isfinite(Mp)) : 0.0f;
+  w = static_cast<double>(q40(wv));
 }
 
 // Put row r (its next phase in the high half) on the list of refine stage
@@ -1701,6 +1753,8 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
     id = draw<DT, EPT, VECOK>(a, r, md, Mp, pl.fkey, true, sh);
     done = true;
   } else if (ph == PH_GATHER) {
+    [[maybe_unused]] const int stamp_id = r;
+    MLXF_S1_STAMP(mlxf_d1_stamps, 8);
     // every candidate slot is requested at once, together with the count
     // (unused slots hold stale words that are never stored)
     unsigned long long cv[CAP / THREADS];
@@ -1724,6 +1778,8 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
       }
     }
     __syncthreads();
+    MLXF_S1_STAMP(mlxf_d1_stamps, 9);
+    MLXF_S1_VAL(mlxf_d1_stamps, 14, n);
     unsigned long long bef;
     unsigned int g;
     if (pl.flags & FL_GALL) {
@@ -1767,6 +1823,7 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
       auto all = [](unsigned long long) { return true; };
       unsigned long long pgt;
       const unsigned int tau = cselect<DT, true, true>(n, all, Mp, pl.target, false, sh, &pgt, &g);
+      MLXF_S1_STAMP(mlxf_d1_stamps, 10);
       const unsigned long long wt = q40(wfun(kval<DT>(tau), Mp, nc, minf));
       const unsigned int t = ties_kept(pl.target > pgt ? pl.target - pgt : 0ull, wt, g);
       unsigned int cut = 0xffffffffu;
@@ -1774,6 +1831,7 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
         auto eq = [tau](unsigned long long e) { return static_cast<unsigned int>(e) == tau; };
         cut = cselect<DT, false, false>(n, eq, Mp, t, false, sh, &bef, &g);
       }
+      MLXF_S1_STAMP(mlxf_d1_stamps, 11);
       const unsigned int tm = md.mr > 0.0f ? minp_key_block<DT>(md.mr, Mp, nc, minf, sh) : 0u;
       if (tm > tau) {
         plan_minp_drawsum<DT>(pl, tm, md.Tr, sh);
@@ -1796,7 +1854,9 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
           }
         }
         __syncthreads();
+        MLXF_S1_STAMP(mlxf_d1_stamps, 12);
         id = draw<DT, EPT, VECOK>(a, r, md, Mp, tau, false, sh);
+        MLXF_S1_STAMP(mlxf_d1_stamps, 13);
         done = true;
       }
     }
@@ -1882,7 +1942,10 @@ __global__ __launch_bounds__(THREADS, 1) void k_decide(Args a, int stage, int la
   const unsigned int e = a.actlist[static_cast<size_t>(stage) * a.B + bid];
   if (static_cast<unsigned int>(bid) >= n) return;
   const int r = static_cast<int>(e & 0xffffu);
+  [[maybe_unused]] const int stamp_id = r;
+  MLXF_S1_STAMP(mlxf_d1_stamps, 7);
   finish_stage<DT, EPT, VECOK>(a, r, e >> 16, a.rowst + static_cast<size_t>(r) * RS_WORDS, sh);
+  MLXF_S1_STAMP(mlxf_d1_stamps, 15);
   if (static_cast<unsigned int>(sh.sl.pw[RS_PHASE]) == PH_DONE) return;
   if (!last) {
     if (tid == 0) enlist(a, stage + 1, r, static_cast<unsigned int>(sh.sl.pw[RS_PHASE]));
@@ -1932,13 +1995,15 @@ __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1
     // rows without one, and are then unused)
     const bool real = tid < S;
     const unsigned long long* rp = a.rec + (static_cast<size_t>(r) * S + (real ? tid : 0)) * REC;
-    const unsigned long long w0 = rp[0], w1 = rp[1], w2 = rp[2], w3 = rp[3], w4 = rp[4], w5 = rp[5], w6 = rp[6];
+    const unsigned long long w0 = rp[0], w1 = rp[1], w2 = rp[2], w3 = rp[3], w4 = rp[4], w5 = rp[5], w6 = rp[6],
+                             w7 = rp[7];
     if (real) {
       sh.szmax[tid] = __uint_as_float(static_cast<unsigned int>(w0));
       sh.szarg[tid] = static_cast<int>(w0 >> 32);
       sh.szmin[tid] = __uint_as_float(static_cast<unsigned int>(w1));
       sh.slse[tid] = __longlong_as_double(static_cast<long long>(w2));
       sh.sn[tid] = static_cast<int>(w5 >> 32);
+      sh.swsum[tid] = __longlong_as_double(static_cast<long long>(w7));
     }
     if (md.need_list) {
       const unsigned int t[7] = {static_cast<unsigned int>(w3), static_cast<unsigned int>(w3 >> 32),
@@ -1968,6 +2033,40 @@ __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1
       sh.zarg = ra;
       sh.zmin = mn;
       sh.lse = md.need_lse ? static_cast<double>(rm) + log(part) : static_cast<double>(NAN);
+    }
+    if (md.kind == KIND_TOPP && md.need_list) {
+      // Bounds on W = sum floor(2^40 w_i), w_i = exp2(RN(z'_i log2 e + nc)),
+      // nc = -RN(Mp log2 e), from the slice sums of w'_i = exp2(RN(z'_i log2 e
+      // + ncs)) (ncs: the same with the slice's own max): z'_i log2 e + nc is
+      // (z'_i log2 e + ncs) + (nc - ncs) exactly, so for every element of
+      // weight >= 2^-41 (both arguments in [-41, 0]) the two roundings and the
+      // two exp2 evaluations (each within 2^-22) put w_i within 2^-17.9 of
+      // w'_i 2^(nc - ncs) relatively; an element below 2^-41 has floor 0 and
+      // adds under half a unit to the float sum; floor loses under one unit
+      // per element; the 32-term fp32 sums add at most 2^-19.  So W lies in
+      // [Wf (1 - 2^-15) - 2V - 64, Wf (1 + 2^-15) + V + 64] with margin.
+      // (No bound for an infinite, huge or tiny-temperature max.)
+      const float Mp = zdiv<DT>(rm, md.Tr, md.y, false);
+      const float nc = -(Mp * LOG2E);
+      bool bad = !__builtin_isfinite(Mp) || fabsf(Mp) > 0x1p20f || md.tslow != 0;
+      double wp = 0.0;
+      if (lane < S && !bad) {
+        const double ws = sh.swsum[lane];
+        const float ncs = -(zdiv<DT>(sh.szmax[lane], md.Tr, md.y, true) * LOG2E);
+        if (!(ws >= 0.0)) {
+          bad = true;
+        } else if (ws > 0.0) {
+          wp = ws * exp2(static_cast<double>(nc) - static_cast<double>(ncs));
+        }
+      }
+      const bool anybad = __ballot(bad) != 0ull;
+      const double wf = wave_sum(wp) * 0x1p40;
+      if (lane == 0) {
+        const double slack = static_cast<double>(a.V) + 64.0;
+        sh.wlo = wf * (1.0 - 0x1p-15) - 2.0 * slack;
+        sh.whi = wf * (1.0 + 0x1p-15) + slack;
+        sh.wok = (!anybad && __builtin_isfinite(wf)) ? 1 : 0;
+      }
     }
   };
   if (md.need_list) {
@@ -2174,7 +2273,15 @@ __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1
     if (tid == 0) write_out<DT>(a, r, 0, lse, md.want_lp);
     return;
   }
-  if (md.kind == KIND_KLIST) {
+  // A top-p row with a best-64 list (it wants top_logprobs) whose nucleus
+  // provably ends inside the list is finished from it like a top-k row: with W (the row's total mass)
+  // known only within [wlo, whi], the cut (keep while the mass before an entry
+  // is below ceil(p W)) is taken at both ends; when both keep the same K < 64
+  // entries and no element outside the list ties or passes the K-th z', that
+  // is the cut for the exact W.  Otherwise the row goes on to the refine
+  // stages.
+  const bool plist = md.kind == KIND_TOPP && md.need_list && sh.wok != 0;
+  if (md.kind == KIND_KLIST || plist) {
     // klist_resolve on two waves: wave 0 makes the cut (the kept entries are
     // a prefix of the (z' desc, index asc) order: top-k, then top-p while the
     // mass before an entry is < p W_k, then min_p, non-increasing weights),
@@ -2184,13 +2291,32 @@ __device__ __forceinline__ void decide1_row(const Args& a, int r, int nstage, D1
       float sv, wv;
       int si;
       double w;
-      const bool ok = klist_prep<DT>(md, Mp, sh.mlist, sv, si, wv, w);
+      bool ok;
+      float last_zp = 0.0f;
+      int last_i = INT_MAX;
+      if (plist) {
+        plist_prep<DT>(md, Mp, sh.mlist, sv, si, wv, w, last_zp, last_i);
+        ok = true;
+      } else {
+        ok = klist_prep<DT>(md, Mp, sh.mlist, sv, si, wv, w);
+      }
       if (wid == 0) {
         if (ok) {
           const double incl = wave_incl_scan_dpp(w);
           const double Wk = rdl(incl, 63);
           bool keep = si != INT_MAX;
-          if (md.topp) keep = keep && (incl - w) < ceil(static_cast<double>(md.pr) * Wk);
+          if (plist) {
+            const double pwl = fmax(ceil(static_cast<double>(md.pr) * sh.wlo), 1.0);
+            const double pwh = fmax(ceil(static_cast<double>(md.pr) * sh.whi), 1.0);
+            const bool kl = keep && (incl - w) < pwl, kh = keep && (incl - w) < pwh;
+            const int nl = static_cast<int>(__builtin_popcountll(__ballot(kl)));
+            const int nh = static_cast<int>(__builtin_popcountll(__ballot(kh)));
+            const float zk = rdl(sv, nh > 0 ? nh - 1 : 0);
+            ok = nl == nh && nh > 0 && nh < LIST && (last_i == INT_MAX || last_zp < zk);
+            keep = kl;
+          } else if (md.topp) {
+            keep = keep && (incl - w) < ceil(static_cast<double>(md.pr) * Wk);
+          }
           if (md.mr > 0.0f) {
             const float nc = -(Mp * LOG2E);
             keep = keep && wv >= minp_thr(md.mr, Mp, nc, !__builtin_isfinite(Mp));

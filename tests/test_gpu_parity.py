@@ -477,3 +477,59 @@ def test_mixed_rows_every_path(seed):
     gu.compare(g, o, dtype, tlp=tlp, label=f"mixed seed={seed}")
     gh = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=3, min_p=mp, stages=1)
     assert np.array_equal(gh["ids"], g["ids"])
+
+
+def _peaked_topp_case(rng, B, V, dtype):
+    """Top-p rows whose nucleus mostly lies in the best 64 (Zipf-like and
+    spiked rows), with some whose nucleus does not (flat rows), exact ties at
+    the top (values on a 0.5 grid), temperatures from 0.05 to 2, and min_p."""
+    z = np.empty((B, V), np.float32)
+    for r in range(B):
+        kind = r % 5
+        if kind == 0:
+            z[r] = rng.gumbel(size=V) * 2.5 - 1.1 * np.log(np.arange(1, V + 1))
+        elif kind == 1:
+            z[r] = rng.standard_normal(V) * 0.5
+            hot = rng.choice(V, size=min(V, 20), replace=False)
+            z[r, hot] += rng.uniform(4.0, 12.0, hot.size)
+        elif kind == 2:
+            z[r] = np.round(rng.standard_normal(V) * 2, 0) * 0.5 - 3.0
+            z[r, rng.choice(V, size=min(V, 40), replace=False)] = 4.0  # a tie group at the top
+        elif kind == 3:
+            z[r] = rng.standard_normal(V) * 0.2  # flat: the nucleus is far beyond the list
+        else:
+            z[r] = rng.gumbel(size=V) * 4.0
+    host = z if dtype == "f32" else (workloads.to_bf16_bits(z) if dtype == "bf16" else z.astype(np.float16))
+    T = rng.choice(np.array([0.05, 0.3, 0.7, 1.0, 1.6, 2.0], np.float32), B)
+    k = np.zeros(B, np.int32)
+    p = rng.choice(np.array([0.1, 0.5, 0.8, 0.9, 0.95, 0.99, 0.999], np.float32), B)
+    mp = rng.choice(np.array([0.0, 0.0, 0.0, 0.01, 0.2], np.float32), B)
+    u = rng.random(B).astype(np.float32)
+    return host, T, k, p, mp, u
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("V", [100, 5000, 151936])
+def test_topp_from_best_list(dtype, V):
+    """Top-p rows that want top_logprobs (so carry a best-64 list) are
+    finished in the first deciding kernel when the bounds on the row's total
+    mass put the nucleus inside the list; every other row takes the refine
+    stages.  Both must agree with the oracle, and every stage count (0: rows
+    the list cannot settle are finished serially) must give the same bits.
+    A third of the rows want no alternatives (no list: the stages)."""
+    rng = np.random.default_rng(2024 + V + len(dtype))
+    B = 20
+    host, T, k, p, mp, u = _peaked_topp_case(rng, B, V, dtype)
+    tlp = np.full(B, 3, np.int32)
+    tlp[::3] = 0
+    K_max = 3
+    dev = gu.to_device(host, dtype)
+    say(f"[parity] top-p from the best list dtype={dtype} V={V}")
+    ref = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=K_max, stages=3, min_p=mp)
+    o = gu.oracle_sample(host, dtype, T=T, k=k, p=p, tlp=tlp, u=u, K_max=K_max, min_p=mp)
+    rep = gu.compare(ref, o, dtype, tlp=tlp, label=f"topp list {dtype} V={V}")
+    say(f"[parity] {rep}")
+    for st in (0, 1, 2):
+        g = gu.gpu_sample(dev, T=T, k=k, p=p, tlp=tlp, u=u, K_max=K_max, stages=st, min_p=mp)
+        assert np.array_equal(g["ids"], ref["ids"]), (st, g["ids"], ref["ids"])
+        assert np.array_equal(g["lp"].view(np.uint32), ref["lp"].view(np.uint32))
