@@ -1561,6 +1561,15 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
   // thread t < S holds slice t's mass above the bracket so far, or its kept mass.
   const bool hist = ph == PH_COUNT || ph == PH_MASS;
   const bool mass = ph == PH_MASS;
+  // (a gathering row's candidate slots are requested here too, in the same
+  // memory round trip as its plan; unused slots hold stale words that are
+  // never stored)
+  unsigned long long cv[CAP / THREADS];
+  if (ph == PH_GATHER) {
+    const unsigned long long* src = a.cand + static_cast<size_t>(r) * CAP;
+#pragma unroll
+    for (int k = 0; k < CAP / THREADS; ++k) cv[k] = src[tid + k * THREADS];
+  }
   const size_t o0 = static_cast<size_t>(r) * S * NB;
   unsigned int Cc = 0;
   unsigned long long Mc = 0;
@@ -1755,14 +1764,6 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
   } else if (ph == PH_GATHER) {
     [[maybe_unused]] const int stamp_id = r;
     MLXF_S1_STAMP(mlxf_d1_stamps, 8);
-    // every candidate slot is requested at once, together with the count
-    // (unused slots hold stale words that are never stored)
-    unsigned long long cv[CAP / THREADS];
-    {
-      const unsigned long long* src = a.cand + static_cast<size_t>(r) * CAP;
-#pragma unroll
-      for (int k = 0; k < CAP / THREADS; ++k) cv[k] = src[tid + k * THREADS];
-    }
     if (tid == 0) {
       sh.ncand = ng < CAP ? ng : CAP;
       a.ncand[r] = 0u;
