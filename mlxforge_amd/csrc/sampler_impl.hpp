@@ -311,27 +311,43 @@ __device__ __forceinline__ unsigned int wave_search(unsigned int lo, unsigned in
   return lo;
 }
 
+// wave_search with a guess: one probe of the 64 keys around est (clamped to
+// [lo, hi]) settles it when pred turns true inside them and not at the first;
+// else the full search.  Whole wave.
+template <typename PRED>
+__device__ __forceinline__ unsigned int wave_search_near(unsigned int lo, unsigned int hi, unsigned int est, PRED pred) {
+  const unsigned int lane = threadIdx.x & 63;
+  const unsigned int k0 = est > lo + 32u ? est - 32u : lo;
+  const unsigned int k = k0 + lane < hi && k0 + lane >= k0 ? k0 + lane : hi;
+  const unsigned long long bal = __ballot(pred(k));
+  if (bal != 0ull && (bal & 1ull) == 0ull) return rdl(k, __ffsll(static_cast<long long>(bal)) - 1);
+  return wave_search(lo, hi, pred);
+}
+
 // Smallest z key whose z' reaches y (z' non-decreasing in z); 0xffffffff if
 // none.  Whole wave.
 template <int DT>
 __device__ __forceinline__ unsigned int gkey(float y, float Tr) {
   if (!(zdiv<DT>(INFINITY, Tr, 1.0f, false) >= y)) return 0xffffffffu;
-  return wave_search(KEY_NEG_INF, KEY_POS_INF,
-                     [&](unsigned int k) { return zdiv<DT>(key2f(k), Tr, 1.0f, false) >= y; });
-}
-
-// z-key bracket [zlo, zhi] of the elements whose z' key lies in [klo, khi].
-// Whole wave.
-template <int DT>
-__device__ __forceinline__ void zbracket(unsigned int klo, unsigned int khi, float Tr, unsigned int* zlo,
-                         unsigned int* zhi) {
-  *zlo = gkey<DT>(kval<DT>(klo), Tr);
-  if (khi >= key_hi<DT>()) {
-    *zhi = KEY_POS_INF;
-  } else {
-    const unsigned int g = gkey<DT>(kval<DT>(khi + 1u), Tr);
-    *zhi = g == 0u ? 0u : g - 1u;
+  auto pred = [&](unsigned int k) { return zdiv<DT>(key2f(k), Tr, 1.0f, false) >= y; };
+  // The answer lies within an ulp or two of m * Tr, m the rounding boundary
+  // below y (y itself for fp32): one probe of the 64 keys around it settles
+  // it when the predicate turns true inside them; else the full search.
+  float m = y;
+  if constexpr (DT != MLXF_DTYPE_F32) {
+    const unsigned int ky = zkey<DT>(y);
+    m = ky > key_lo<DT>() ? 0.5f * (y + kval<DT>(ky - 1u)) : y;
   }
+  const float est = m * Tr;
+  if (__builtin_isfinite(est)) {
+    const int lane = threadIdx.x & 63;
+    const unsigned int ke = f2key(est);
+    const unsigned int k0 = ke > KEY_NEG_INF + 32u ? ke - 32u : KEY_NEG_INF;
+    const unsigned int k = min(k0 + static_cast<unsigned int>(lane), KEY_POS_INF);
+    const unsigned long long bal = __ballot(pred(k));
+    if (bal != 0ull && (bal & 1ull) == 0ull) return rdl(k, __ffsll(static_cast<long long>(bal)) - 1);
+  }
+  return wave_search(KEY_NEG_INF, KEY_POS_INF, pred);
 }
 
 __device__ __forceinline__ unsigned long long pack_ent(float v, int i) {
@@ -1500,13 +1516,19 @@ __device__ __forceinline__ unsigned int ties_kept(unsigned long long need, unsig
 // Publish wave 0's bracket [klo, khi] -> z-key bracket to the workgroup.
 template <int DT>
 __device__ __forceinline__ void set_bracket(Plan& pl, unsigned int klo, unsigned int khi, float Tr, RLds& sh) {
-  if ((threadIdx.x >> 6) == 0) {
-    unsigned int zl, zh;
-    zbracket<DT>(klo, khi, Tr, &zl, &zh);
-    if (threadIdx.x == 0) {
-      sh.sel[6] = static_cast<int>(zl);
-      sh.sel[7] = static_cast<int>(zh);
+  // the z-key bracket [zlo, zhi] of the elements whose z' key lies in
+  // [klo, khi]: its two ends, one wave each
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wid == 0) {
+    const unsigned int zl = gkey<DT>(kval<DT>(klo), Tr);
+    if (lane == 0) sh.sel[6] = static_cast<int>(zl);
+  } else if (wid == 1) {
+    unsigned int zh = KEY_POS_INF;
+    if (khi < key_hi<DT>()) {
+      const unsigned int g = gkey<DT>(kval<DT>(khi + 1u), Tr);
+      zh = g == 0u ? 0u : g - 1u;
     }
+    if (lane == 0) sh.sel[7] = static_cast<int>(zh);
   }
   __syncthreads();
   pl.zlo = static_cast<unsigned int>(sh.sel[6]);
@@ -1588,6 +1610,8 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
       Mc += mc[j];
     }
   }
+  [[maybe_unused]] const int stamp_id = r;
+  if (mass) MLXF_S1_STAMP(mlxf_m_stamps, 0);
   unsigned long long pre = 0;
   if (tid < S) {
     if (mass) pre = a.above[static_cast<size_t>(r) * S + tid];
@@ -1624,6 +1648,7 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
       if (bal && lane == 0) atomicMin(&sh.sel[4], wid * 64 + __ffsll(static_cast<long long>(bal)) - 1);
     }
     __syncthreads();
+    if (mass) MLXF_S1_STAMP(mlxf_m_stamps, 1);
     const int bstar = sh.sel[4] < NB ? sh.sel[4] : NB - 1;
     const unsigned long long abv = bstar > 0 ? sh.sl.hm[bstar - 1] : 0ull;  // measure above the bin
     const unsigned int cabv = bstar > 0 ? sh.sl.hc[bstar - 1] : 0u;         // participants above it
@@ -1644,6 +1669,7 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
     }
     // key range [klo, khi] of the chosen bin: wave 0 the low edge, wave 1 the
     // high edge, wave 2 the first key with a positive mass
+    if (mass) MLXF_S1_STAMP(mlxf_m_stamps, 2);
     if (tid == 0) {
       sh.sel[6] = 0;
       sh.sel[7] = static_cast<int>(khi_all);
@@ -1652,11 +1678,19 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
     __syncthreads();
     if (pl.flags & FL_VGRID) {
       auto vb = [&](unsigned int k) { return vbin_x(wlog2(kval<DT>(k), nc), pl.R2); };
+      // (bin b's upper edge in z': vbin_x(x) <= b once x > -(b + 1) / R2, with
+      // x = z' log2 e + nc: the search's guess)
+      auto edge = [&](int b) {
+        const float ze = (-static_cast<float>(b + 1) / pl.R2 - nc) * (1.0f / LOG2E);
+        return __builtin_isfinite(ze) ? zkey<DT>(ze) : klo_all;
+      };
       if (wid == 0) {
-        const unsigned int klo = wave_search(klo_all, khi_all, [&](unsigned int k) { return vb(k) <= bstar; });
+        const unsigned int klo =
+            wave_search_near(klo_all, khi_all, edge(bstar), [&](unsigned int k) { return vb(k) <= bstar; });
         if (lane == 0) sh.sel[6] = static_cast<int>(klo);
       } else if (wid == 1 && bstar > 0) {
-        const unsigned int nx = wave_search(klo_all, khi_all, [&](unsigned int k) { return vb(k) <= bstar - 1; });
+        const unsigned int nx =
+            wave_search_near(klo_all, khi_all, edge(bstar - 1), [&](unsigned int k) { return vb(k) <= bstar - 1; });
         if (lane == 0) sh.sel[7] = static_cast<int>(nx > klo_all ? nx - 1u : klo_all);
       }
     } else if (tid == 0) {
@@ -1669,9 +1703,10 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
     if (mass && wid == 2) {
       // elements whose mass quantises to zero never count: the bracket starts
       // at the first key with a positive mass
-      const unsigned int kq = wave_search(klo_all, khi_all, [&](unsigned int k) {
-        return q40(wfun(kval<DT>(k), Mp, nc, minf)) > 0;
-      });
+      // (a mass is positive from weight 2^-40 up: x >= -40)
+      const float ze = (-40.0f - nc) * (1.0f / LOG2E);
+      const unsigned int kq = wave_search_near(klo_all, khi_all, __builtin_isfinite(ze) ? zkey<DT>(ze) : klo_all,
+                                               [&](unsigned int k) { return q40(wfun(kval<DT>(k), Mp, nc, minf)) > 0; });
       if (lane == 0) sh.sel[3] = static_cast<int>(kq);
     }
     __syncthreads();
@@ -1687,6 +1722,7 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
       }
     }
     __syncthreads();
+    if (mass) MLXF_S1_STAMP(mlxf_m_stamps, 3);
     const unsigned int klo = static_cast<unsigned int>(sh.sel[6]);
     const unsigned int khi = static_cast<unsigned int>(sh.sel[7]);
     __syncthreads();
@@ -1750,6 +1786,7 @@ __device__ __forceinline__ void finish_stage(const Args& a, int r, unsigned int 
         pl.phase = PH_GATHER;
         pl.target = rest;
         set_bracket<DT>(pl, klo, khi, md.Tr, sh);
+        MLXF_S1_STAMP(mlxf_m_stamps, 4);
       } else {
         set_digits(pl, klo, khi);
         pl.target = rest;
