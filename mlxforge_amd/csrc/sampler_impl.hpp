@@ -1250,23 +1250,27 @@ __device__ __forceinline__ int walk(const Args& a, int r, int s, float Mp, unsig
   if (!all_ties) {
     int nt = 0;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) nt += (my0 + e < e0 && zp[e] == tauf) ? 1 : 0;
+    for (int e = 0; e < EPT; ++e) nt += ((my0 + e < e0) & (zp[e] == tauf)) ? 1 : 0;
     int ttot;
     tex = block_excl_scan_dpp<int>(nt, sh.ri, &ttot);
   }
   unsigned long long qs = 0;
   int last = -1;
   {
+    // straight-line over the elements (bitwise tests, every weight computed
+    // and masked): a branch per test would run the elements one by one, each
+    // waiting for its exp
     unsigned int rk = static_cast<unsigned int>(tex);
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       const bool valid = my0 + e < e0;
-      const bool tie = valid && zp[e] == tauf;
-      const bool kept = valid && (zp[e] > tauf || (tie && rk < lim));
+      const bool tie = valid & (zp[e] == tauf);
+      const bool kept = valid & ((zp[e] > tauf) | (tie & (rk < lim)));
       rk += tie ? 1u : 0u;
-      const unsigned long long q = kept ? q40(wfun(zp[e], Mp, nc, minf)) : 0ull;
+      const unsigned long long qv = q40(wfun(zp[e], Mp, nc, minf));
+      const unsigned long long q = kept ? qv : 0ull;
       qs += q;
-      if (q > 0) last = my0 + e;
+      last = q > 0 ? my0 + e : last;
     }
   }
   if (tid == 0) sh.found = -1;
