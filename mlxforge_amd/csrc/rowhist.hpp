@@ -3,7 +3,8 @@
 // workgroup per row reads the row once and counts it into exact per-value
 // histograms in LDS, from which every selection of Sampler::sample
 // (src/sample/sampler.cpp:141-166) follows without touching the logits
-// again; only the draw re-reads one quarter of the row.
+// again; only the draw re-reads an eighth (a quarter with split counting) of
+// the row.
 //
 // Why it is exact: for bf16 logits, z' = round_bf16(z / T), the weight
 // w = exp2(fma(z', log2 e, -RN(max z' log2 e))) and its fixed-point mass
@@ -19,8 +20,12 @@
 // z' cannot be told apart by the weight function: the tiny bin when |z' log2 e|
 // stays below half an ulp of the weight's offset, the low bin when its weight
 // rounds to a zero mass.  The row is split into four contiguous chunks with a
-// histogram each (4 x 9220 32-bit counters, 144 KB of LDS), so per-chunk kept
-// masses locate the draw to one chunk, which the walk then reads.
+// histogram each (4 x 9220 32-bit counter words, 144 KB of LDS), so per-chunk
+// kept masses locate the draw to one chunk, which the walk then reads.  When
+// the workgroup counts its row itself, each word holds two 16-bit counters,
+// one for each half of its chunk, and the walk reads one of eight half chunks
+// (at most 65535 logits each: V <= 458752); with split counting (chunk
+// workgroups, few rows) the counters are 32-bit and the walk reads a chunk.
 //
 // Rows the bins cannot decide exactly -- the maximum in a merged bin (a
 // logit >= 256, +inf, a positive NaN, or a row of values all within 2^-28 of
@@ -30,14 +35,15 @@
 // the row's slices and the deciding step (every refine level), the other
 // twelve end.
 //
-// Memory per row: one read of the row (V * 2 bytes) in pass 1, a quarter row
-// in the draw.  No MFMA: nothing here is a dense contraction.
+// Memory per row: one read of the row (V * 2 bytes) in pass 1, a half chunk
+// (or a chunk) in the draw.  No MFMA: nothing here is a dense contraction.
 
 namespace mlxf {
 
 // Per-call constants of the row-histogram path.
 struct RhArgs {
-  int ipc;                   // pass-1 iterations per chunk (chunk length ipc * 8192 logits)
+  int ipc;                   // pass-1 iterations per chunk (chunk length ipc * 8192 logits;
+                             // even when the counters are packed)
   int nfull;                 // iterations wholly inside the row
   // split calls (few rows): one workgroup per chunk counts it into
   // hsplit[r][c][bin]; crec[r][c] = (largest bin offset + 65536) | lowest
