@@ -263,20 +263,28 @@ int mlxf_apply_mask(const void* d_logits, int dtype, int B, int V, int64_t row_s
  *                     arrays: that filter off.
  * The kept sets are the sampling call's, with its masses and tie rules
  * (top-p order is value desc, index asc; the mass is summed in fixed point,
- * so it does not depend on the summation order); NaN logits read as -inf.  d_out has the logits' dtype; it may be
- * d_logits itself (in place, out_stride == row_stride) but must not overlap it
- * otherwise.  No workspace: the output rows serve as scratch.  One workgroup
- * per row that reads its row about a dozen times: a helper, not the decode
- * step's path. */
+ * so it does not depend on the summation order); NaN logits read as -inf.
+ * d_out has the logits' dtype; it may be d_logits itself (in place,
+ * out_stride == row_stride) but must not overlap it otherwise.
+ *   d_workspace   >= mlxf_filter_workspace_size(B, V) bytes, 256-byte aligned;
+ *                 no initialisation needed (every call writes what it reads).
+ * Up to ten kernels on `stream` (fewer for the single-filter calls), each over
+ * every row with several workgroups per row; no allocation.  A helper, not
+ * the decode step's path. */
+int mlxf_filter_workspace_size(int B, int V, size_t* bytes, char** err);
 int mlxf_filter_logits(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
                        const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
-                       const float* d_min_p, void* d_out, int64_t out_stride, void* stream, char** err);
+                       const float* d_min_p, void* d_out, int64_t out_stride, void* d_workspace,
+                       size_t workspace_bytes, void* stream, char** err);
 int mlxf_apply_top_k(const void* d_logits, int dtype, int B, int V, int64_t row_stride, int k,
-                     void* d_out, int64_t out_stride, void* stream, char** err);
+                     void* d_out, int64_t out_stride, void* d_workspace, size_t workspace_bytes,
+                     void* stream, char** err);
 int mlxf_apply_top_p(const void* d_logits, int dtype, int B, int V, int64_t row_stride, float p,
-                     void* d_out, int64_t out_stride, void* stream, char** err);
+                     void* d_out, int64_t out_stride, void* d_workspace, size_t workspace_bytes,
+                     void* stream, char** err);
 int mlxf_apply_min_p(const void* d_logits, int dtype, int B, int V, int64_t row_stride, float min_p,
-                     void* d_out, int64_t out_stride, void* stream, char** err);
+                     void* d_out, int64_t out_stride, void* d_workspace, size_t workspace_bytes,
+                     void* stream, char** err);
 
 /* argmax over each row, lowest index on ties: Sampler::greedy
  * (src/sample/sampler.h:61, src/sample/sampler.cpp:59-61). */

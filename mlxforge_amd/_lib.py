@@ -33,6 +33,7 @@ SYMBOLS = (
     "mlxf_string_free",
     "mlxf_sampler_workspace_init",
     "mlxf_sample_noalloc",
+    "mlxf_filter_workspace_size",
     "mlxf_filter_logits",
     "mlxf_apply_top_k",
     "mlxf_apply_top_p",
@@ -83,13 +84,15 @@ def load() -> ctypes.CDLL:
     L.mlxf_sampler_refine_stages.restype = I
     L.mlxf_greedy.argtypes = [P, I, I, I, I64, P, P, SZ, P, PP]
     L.mlxf_greedy.restype = I
-    L.mlxf_filter_logits.argtypes = [P, I, I, I, I64, P, P, P, P, P, I64, P, PP]
+    L.mlxf_filter_workspace_size.argtypes = [I, I, ctypes.POINTER(SZ), PP]
+    L.mlxf_filter_workspace_size.restype = I
+    L.mlxf_filter_logits.argtypes = [P, I, I, I, I64, P, P, P, P, P, I64, P, SZ, P, PP]
     L.mlxf_filter_logits.restype = I
-    L.mlxf_apply_top_k.argtypes = [P, I, I, I, I64, I, P, I64, P, PP]
+    L.mlxf_apply_top_k.argtypes = [P, I, I, I, I64, I, P, I64, P, SZ, P, PP]
     L.mlxf_apply_top_k.restype = I
-    L.mlxf_apply_top_p.argtypes = [P, I, I, I, I64, ctypes.c_float, P, I64, P, PP]
+    L.mlxf_apply_top_p.argtypes = [P, I, I, I, I64, ctypes.c_float, P, I64, P, SZ, P, PP]
     L.mlxf_apply_top_p.restype = I
-    L.mlxf_apply_min_p.argtypes = [P, I, I, I, I64, ctypes.c_float, P, I64, P, PP]
+    L.mlxf_apply_min_p.argtypes = [P, I, I, I, I64, ctypes.c_float, P, I64, P, SZ, P, PP]
     L.mlxf_apply_min_p.restype = I
     L.mlxf_sample_noalloc.argtypes = [P, I, I, I, I64, P, P, P, P, P, P, P, P, P, P, I, I, P, PP]
     L.mlxf_sample_noalloc.restype = I
@@ -120,6 +123,14 @@ def workspace_size(B: int, V: int, K_max: int, dtype: int) -> int:
     n = ctypes.c_size_t(0)
     err = ctypes.c_void_p()
     rc = load().mlxf_sampler_workspace_size(B, V, K_max, dtype, ctypes.byref(n), ctypes.byref(err))
+    check(rc, err)
+    return n.value
+
+
+def filter_workspace_size(B: int, V: int) -> int:
+    n = ctypes.c_size_t(0)
+    err = ctypes.c_void_p()
+    rc = load().mlxf_filter_workspace_size(B, V, ctypes.byref(n), ctypes.byref(err))
     check(rc, err)
     return n.value
 

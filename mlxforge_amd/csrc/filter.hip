@@ -14,7 +14,15 @@
 // the nucleus cutoff are radix selections over 32-bit order keys (four 8-bit
 // digit levels, a histogram of counts or of masses in LDS per level), and the
 // last pass writes -inf over the removed entries.  The row is read about a
-// dozen times, which suits a helper the decode step never calls.
+// dozen times, which suits a helper the decode step never calls.  Two things
+// keep those passes near the rate at which one CU streams its row:
+//  - the radix histograms hold RC copies of each bin, lane l adding into copy
+//    l % RC: the first digit levels put most of a row into a few bins, and
+//    64 lanes adding into one LDS word are served one after another;
+//  - every pass reads the row in coalesced 64-element steps; where index
+//    order matters (the nucleus's partial tie group) wave w takes the
+//    contiguous segment [w S, (w + 1) S) and ranks its tied elements by a
+//    ballot, after one scan of the waves' tie counts.
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
@@ -28,6 +36,8 @@ namespace {
 
 constexpr int FT = 1024;      // threads per workgroup
 constexpr int FW = FT / 64;   // waves
+constexpr int RC = 32;        // copies of each radix bin (lanes l and l + 32 share one)
+constexpr int FU = 8;         // loads in flight per lane in a row pass
 
 struct FArgs {
   const void* logits;
@@ -45,8 +55,8 @@ struct FArgs {
 };
 
 struct FLds {
-  unsigned int hc[256];
-  unsigned long long hm[256];
+  unsigned int hc[256 * RC];        // bin d, copy c at d * RC + c
+  unsigned long long hm[256 * RC];
   unsigned long long u64r[FW];
   float fr[FW];
   int ir[FW];
@@ -81,6 +91,47 @@ __device__ __forceinline__ float raw1(const void* row, int i) {
 // comparisons do), so they share a key.
 __device__ __forceinline__ unsigned int okey(float zp) { return f2key(zp + 0.0f); }
 
+// fn(i, load(i)) for i = lo + tid, lo + tid + FT, ... < hi, with FU loads issued before
+// the first fn of each group: one workgroup streams its row, and a lane with
+// one load in flight at a time would wait out the memory latency per element.
+template <typename Load, typename Fn>
+__device__ __forceinline__ void row_pass(int lo, int hi, Load load, Fn fn) {
+  for (int b = lo + static_cast<int>(threadIdx.x); b < hi; b += FU * FT) {
+    float v[FU];
+#pragma unroll
+    for (int u = 0; u < FU; ++u) {
+      const int i = b + u * FT;
+      v[u] = i < hi ? load(i) : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < FU; ++u) {
+      const int i = b + u * FT;
+      if (i < hi) fn(i, v[u]);
+    }
+  }
+}
+
+// The same over wave w's contiguous segment [s0, s1) in index order, in
+// 64-element steps: fn(i, in, v) with every lane of the wave taking part (in
+// false, v -inf past the segment's end), so fn may take ballots.
+template <typename Load, typename Fn>
+__device__ __forceinline__ void seg_pass(int s0, int s1, Load load, Fn fn) {
+  const int lane = static_cast<int>(threadIdx.x) & 63;
+  for (int b = s0; b < s1; b += FU * 64) {
+    float v[FU];
+#pragma unroll
+    for (int u = 0; u < FU; ++u) {
+      const int i = b + u * 64 + lane;
+      v[u] = i < s1 ? load(i) : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < FU; ++u) {
+      const int i = b + u * 64 + lane;
+      fn(i, i < s1, v[u]);
+    }
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ T fsum(T x, T* red) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -103,11 +154,12 @@ __device__ unsigned int radix_select(int V, unsigned long long target, Load load
   unsigned int prefix = 0u, mask = 0u;
   unsigned long long rem = target, abv = 0ull;
   unsigned int c_at = 0u;
+  const unsigned int cpy = static_cast<unsigned int>(tid) & (RC - 1);
   for (int shift = 24; shift >= 0; shift -= 8) {
     __syncthreads();
-    if (tid < 256) {
-      sh.hc[tid] = 0u;
-      sh.hm[tid] = 0ull;
+    for (int j = tid; j < 256 * RC; j += FT) {
+      sh.hc[j] = 0u;
+      if (MASS) sh.hm[j] = 0ull;
     }
     if (tid == 0) {
       sh.sel[0] = 0u;
@@ -115,28 +167,38 @@ __device__ unsigned int radix_select(int V, unsigned long long target, Load load
       sh.sel64[0] = 0ull;
     }
     __syncthreads();
-    for (int i = tid; i < V; i += FT) {
-      const float zp = load(i);
+    row_pass(0, V, load, [&](int, float zp) {
       const unsigned int key = okey(zp);
       if ((key & mask) == prefix && in(zp, key)) {
-        const unsigned int d = (key >> shift) & 255u;
+        const unsigned int d = ((key >> shift) & 255u) * RC + cpy;
         __hip_atomic_fetch_add(&sh.hc[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         if (MASS) {
           const unsigned long long m = massf(zp);
           if (m) __hip_atomic_fetch_add(&sh.hm[d], m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
       }
-    }
+    });
     __syncthreads();
-    // digits in descending order: thread t < 256 takes digit 255 - t
+    // digits in descending order: thread t < 256 takes digit 255 - t and sums
+    // its copies (starting at copy d, so that a wave's reads spread over the
+    // banks)
     const unsigned int d = 255u - static_cast<unsigned int>(tid & 255);
-    const unsigned long long meas = tid < 256 ? (MASS ? sh.hm[d] : static_cast<unsigned long long>(sh.hc[d])) : 0ull;
+    unsigned int cnt_d = 0u;
+    unsigned long long meas = 0ull;
+    if (tid < 256) {
+      for (unsigned int c = 0; c < static_cast<unsigned int>(RC); ++c) {
+        const unsigned int j = d * RC + ((c + d) & (RC - 1));
+        cnt_d += sh.hc[j];
+        if (MASS) meas += sh.hm[j];
+      }
+      if (!MASS) meas = cnt_d;
+    }
     unsigned long long tot;
     const unsigned long long excl = rh::bscan(meas, sh.u64r, &tot);
     if (tid < 256 && excl < rem && rem <= excl + meas) {
       sh.sel[0] = d;
       sh.sel64[0] = excl;
-      sh.sel[1] = sh.hc[d];
+      sh.sel[1] = cnt_d;
     }
     __syncthreads();
     const unsigned int dd = sh.sel[0];
@@ -152,14 +214,195 @@ __device__ unsigned int radix_select(int V, unsigned long long target, Load load
   return prefix;
 }
 
+// Wave w's contiguous segment [*s0, *s1) of the range [lo, hi), in whole
+// 64-element steps (each step one coalesced load per lane).
+__device__ __forceinline__ void wave_segment(int lo, int hi, int* s0, int* s1) {
+  const int S = ((hi - lo + FT - 1) / FT) * 64;
+  *s0 = min(lo + (static_cast<int>(threadIdx.x) >> 6) * S, hi);
+  *s1 = min(*s0 + S, hi);
+}
+
+// The lanes below this one whose bit is set in a ballot.
+__device__ __forceinline__ unsigned int lanes_below(unsigned long long b) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(b >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(b), 0u));
+}
+
+// The number of elements whose value satisfies pred in the segments of the
+// waves below this one (red: FW words of LDS).
+template <typename Load, typename Pred>
+__device__ unsigned int ties_before(int s0, int s1, Load load, Pred pred, int* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  unsigned int mine = 0u;
+  seg_pass(s0, s1, load, [&](int, bool in, float v) {
+    mine += static_cast<unsigned int>(__popcll(__ballot(in && pred(v))));
+  });
+  __syncthreads();
+  if (lane == 0) red[wid] = static_cast<int>(mine);
+  __syncthreads();
+  unsigned int base = 0u;
+  for (int w = 0; w < wid; ++w) base += static_cast<unsigned int>(red[w]);
+  return base;
+}
+
+// ---- the filter calls: G workgroups per row, one kernel per phase.
+// Workgroup g of row r takes the slice [g L, (g + 1) L) of the row.  Every
+// phase recomputes z' from the input (the division is deterministic), so the
+// output is written only by the last phase and may be the input itself.  A
+// radix level's histogram is built per slice in LDS and written out whole
+// (every bin, zeros included); the next phase sums the G slice histograms of
+// its row (integer sums, so the order does not matter), picks the digit, and
+// builds the next level.  Workgroup 0 of a row stores the selection's state
+// after each level for the phases after it; states and histograms alternate
+// between two slots, so no phase reads a slot it writes.
+
+constexpr int FG_MAX = 16;   // workgroups per row at most
+
+// A radix selection's state after a level: the digits chosen so far (prefix
+// under mask), the target left below them, the measure above them, the count
+// of candidates with the chosen key (after the last level), the target.
+struct FSel {
+  unsigned int prefix, mask, cnt, pad;
+  unsigned long long rem, abv, tgt;
+};
+
+struct FRow {
+  FSel sk[2], sp[2];          // top-k and top-p states after level j at [j & 1]
+  float mxp[FG_MAX];          // slice maxima of z'
+  unsigned int tiec[FG_MAX];  // slice counts of the nucleus cutoff's key
+};
+
+enum FPhase { FP_MAX, FP_K1, FP_K2, FP_K3, FP_P0, FP_P1, FP_P2, FP_P3, FP_TIES, FP_FIN };
+
+struct FWs {
+  FRow* rows;               // [B]
+  unsigned int* hc;         // [B][2][G][256]
+  unsigned long long* hm;   // [B][2][G][256]
+  int G;
+};
+
+__host__ __device__ inline size_t fws_align(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+// Workgroups per row: the B G workgroups fill the CUs (one per CU, as each
+// holds its radix histograms in most of a CU's LDS) with slices of at least
+// 4096 elements.
+__host__ __device__ inline int filter_groups(int B, int V) {
+  int G = B > 0 ? (256 + B - 1) / B : 1;
+  const int gv = (V + 4095) / 4096;
+  G = G < gv ? G : gv;
+  return G < 1 ? 1 : (G > FG_MAX ? FG_MAX : G);
+}
+
+__host__ __device__ inline size_t filter_ws_bytes(int B, int V) {
+  const size_t G = static_cast<size_t>(filter_groups(B, V));
+  const size_t nb = static_cast<size_t>(B) * 2 * G * 256;
+  return fws_align(static_cast<size_t>(B) * sizeof(FRow)) + fws_align(nb * 4) + fws_align(nb * 8);
+}
+
+// Sum the G slice histograms of level slot `slot` for this row and choose the
+// digit at `shift`: the state s moves to the digit d whose measure (count, or
+// mass when MASS) brings the measure above it from below s.rem to at least
+// s.rem.  With FROM_TOTAL the target is first set from the candidates' whole
+// measure W: max(1, ceil(p W)) (the nucleus's first level).
+template <bool MASS, bool FROM_TOTAL>
+__device__ FSel select_level(FSel s, int shift, const unsigned int* hc, const unsigned long long* hm, int G,
+                             float pr, FLds& sh) {
+  const int tid = threadIdx.x;
+  const unsigned int d = 255u - static_cast<unsigned int>(tid & 255);
+  unsigned int cnt_d = 0u;
+  unsigned long long meas = 0ull;
+  if (tid < 256) {
+    for (int g = 0; g < G; ++g) {
+      cnt_d += hc[g * 256 + d];
+      if (MASS) meas += hm[g * 256 + d];
+    }
+    if (!MASS) meas = cnt_d;
+  }
+  __syncthreads();  // sh.sel may still be read by the caller's last use
+  if (tid == 0) {
+    sh.sel[0] = 0u;
+    sh.sel[1] = 0u;
+    sh.sel64[0] = 0ull;
+  }
+  unsigned long long tot;
+  const unsigned long long excl = rh::bscan(meas, sh.u64r, &tot);  // (barriers inside)
+  if (FROM_TOTAL) {
+    unsigned long long PW = static_cast<unsigned long long>(ceil(static_cast<double>(pr) * static_cast<double>(tot)));
+    if (PW < 1ull) PW = 1ull;
+    s.rem = PW;
+    s.tgt = PW;
+  }
+  if (tid < 256 && excl < s.rem && s.rem <= excl + meas) {
+    sh.sel[0] = d;
+    sh.sel64[0] = excl;
+    sh.sel[1] = cnt_d;
+  }
+  __syncthreads();
+  const unsigned int dd = sh.sel[0];
+  const unsigned long long ex = sh.sel64[0];
+  s.cnt = sh.sel[1];
+  s.rem -= ex;
+  s.abv += ex;
+  s.prefix |= dd << shift;
+  s.mask |= 255u << shift;
+  return s;
+}
+
+// This slice's histogram at `shift` of the candidates (key under s's prefix,
+// in(zp, key)) into level slot hc / hm (this workgroup's 256 bins).
+template <bool MASS, typename Load, typename In, typename Mass>
+__device__ void slice_hist(int lo, int hi, int shift, FSel s, Load load, In in, Mass massf, unsigned int* hc,
+                           unsigned long long* hm, FLds& sh) {
+  const int tid = threadIdx.x;
+  const unsigned int cpy = static_cast<unsigned int>(tid) & (RC - 1);
+  __syncthreads();
+  for (int j = tid; j < 256 * RC; j += FT) {
+    sh.hc[j] = 0u;
+    if (MASS) sh.hm[j] = 0ull;
+  }
+  __syncthreads();
+  const unsigned int prefix = s.prefix, mask = s.mask;
+  row_pass(lo, hi, load, [&](int, float zp) {
+    const unsigned int key = okey(zp);
+    if ((key & mask) == prefix && in(zp, key)) {
+      const unsigned int d = ((key >> shift) & 255u) * RC + cpy;
+      __hip_atomic_fetch_add(&sh.hc[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (MASS) {
+        const unsigned long long m = massf(zp);
+        if (m) __hip_atomic_fetch_add(&sh.hm[d], m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+  });
+  __syncthreads();
+  if (tid < 256) {
+    const unsigned int d = static_cast<unsigned int>(tid);
+    unsigned int c = 0u;
+    unsigned long long m = 0ull;
+    for (unsigned int k = 0; k < static_cast<unsigned int>(RC); ++k) {
+      const unsigned int j = d * RC + ((k + d) & (RC - 1));
+      c += sh.hc[j];
+      if (MASS) m += sh.hm[j];
+    }
+    hc[d] = c;
+    if (MASS) hm[d] = m;
+  }
+}
+
 template <int DT>
-__global__ __launch_bounds__(FT, 1) void k_filter(FArgs f) {
+__global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
   __shared__ FLds sh;
   const int tid = threadIdx.x;
-  const int r = static_cast<int>(blockIdx.x);
-  const int V = f.V;
+  const int r = static_cast<int>(blockIdx.x), g = static_cast<int>(blockIdx.y);
+  const int V = f.V, G = ws.G;
+  const int L = (((V + G - 1) / G) + 63) & ~63;
+  const int lo = min(g * L, V), hi = min(lo + L, V);
   const void* irow = static_cast<const char*>(f.logits) + static_cast<size_t>(r) * f.row_stride * elem_size<DT>();
   void* orow = static_cast<char*>(f.out) + static_cast<size_t>(r) * f.out_stride * elem_size<DT>();
+  FRow& row = ws.rows[r];
+  unsigned int* hc0 = ws.hc + static_cast<size_t>(r) * 2 * G * 256;
+  unsigned long long* hm0 = ws.hm + static_cast<size_t>(r) * 2 * G * 256;
+  auto hcs = [&](int slot) { return hc0 + static_cast<size_t>(slot) * G * 256; };
+  auto hms = [&](int slot) { return hm0 + static_cast<size_t>(slot) * G * 256; };
 
   // ---- the row's parameters (the sampling call's sentinels)
   const float T = f.T ? f.T[r] : f.Ts;
@@ -167,6 +410,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f) {
   const bool div = __builtin_isfinite(T) && T > 0.0f && Tr > 0.0f;
   const int k0 = f.k ? f.k[r] : f.ks;
   const int kk = k0 > 0 ? (k0 < V ? k0 : V) : 0;
+  const bool tk_on = kk > 0 && kk < V;
   // (a p that rounds to 1 in the dtype keeps every element: every prior mass
   // is below the whole mass.  With integer masses the elements of zero mass
   // would reach it, so the filter is off then.)
@@ -175,95 +419,154 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f) {
   const bool topp = p > 0.0f && p < 1.0f && pr < 1.0f;
   const float mp = f.minp ? f.minp[r] : f.mps;
   const float mr = (mp > 0.0f && mp <= 1.0f) ? round_dt<DT>(mp) : 0.0f;
-
-  // ---- pass 1: z' into the output row (NaN read as -inf), and the row max
-  float mx = -INFINITY;
-  for (int i = tid; i < V; i += FT) {
+  // z' (NaN read as -inf)
+  auto zload = [&](int i) {
     const float z = ld1<DT>(irow, i);
-    const float zp = div ? round_dt<DT>(z / Tr) : z;
-    st1<DT>(orow, i, zp);
-    mx = fmaxf(mx, zp);
-  }
-  float Mp;
-  {
+    return div ? round_dt<DT>(z / Tr) : z;
+  };
+  auto all = [](float, unsigned int) { return true; };
+  auto nomass = [](float) { return 0ull; };
+
+  if (ph == FP_MAX) {
+    // ---- the slice's max of z', and the top-k's first level
+    float mx = -INFINITY;
+    row_pass(lo, hi, zload, [&](int, float zp) { mx = fmaxf(mx, zp); });
     const float w = wave_max(mx);
     if ((tid & 63) == 0) sh.fr[tid >> 6] = w;
-    // the stores above are complete before the barrier, and stale L1 lines
-    // (the row itself when filtering in place) are dropped after it: the
-    // passes below read the output row back
-    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    Mp = rdl(row_max16(sh.fr[tid & (FW - 1)]), 0);
+    const float m = rdl(row_max16(sh.fr[tid & (FW - 1)]), 0);
+    if (tid == 0) row.mxp[g] = m;
+    if (tk_on) {
+      FSel s{};
+      slice_hist<false>(lo, hi, 24, s, zload, all, nomass, hcs(0) + g * 256, nullptr, sh);
+    }
+    return;
   }
-  if (Mp == -INFINITY || (kk == 0 && !topp && mr == 0.0f)) return;  // nothing is removed
+  if (ph >= FP_K1 && ph <= FP_K3) {
+    // ---- top-k level l = ph: choose digit l from slot (l - 1) & 1, build
+    // level l + 1 into slot l & 1 (src/sample/sampler.cpp:63-68)
+    if (!tk_on) return;
+    const int l = ph - FP_K1 + 1;
+    FSel s{};
+    s.rem = s.tgt = static_cast<unsigned long long>(kk);
+    if (l > 1) s = row.sk[(l - 1) & 1];
+    s = select_level<false, false>(s, 32 - 8 * l, hcs((l - 1) & 1), nullptr, G, 0.0f, sh);
+    if (g == 0 && tid == 0) row.sk[l & 1] = s;
+    slice_hist<false>(lo, hi, 24 - 8 * l, s, zload, all, nomass, hcs(l & 1) + g * 256, nullptr, sh);
+    return;
+  }
+
+  // ---- the row max (every phase from here sums the slices the same way)
+  float Mp = -INFINITY;
+  for (int q = 0; q < G; ++q) Mp = fmaxf(Mp, row.mxp[q]);
   const bool minf = Mp == INFINITY;
   const float nc = minf ? 0.0f : -(Mp * LOG2E);
   auto massf = [&](float zp) -> unsigned long long { return q40(wfun(zp + 0.0f, Mp, nc, minf)); };
-  auto zload = [&](int i) { return raw1<DT>(orow, i); };
+  const bool live = Mp != -INFINITY;  // a row of -inf (or NaN) keeps everything
+  const bool tp_on = topp && live;
 
-  // ---- top-k: the k'-th largest key counting multiplicity; every element at
-  // or above it is kept (src/sample/sampler.cpp:63-68)
-  unsigned int tk = 0u;
-  if (kk > 0 && kk < V) {
-    unsigned long long ab;
-    unsigned int c;
-    tk = radix_select<false>(V, static_cast<unsigned long long>(kk), zload,
-                             [](float, unsigned int) { return true; }, massf, sh, &ab, &c);
-  }
-
-  // ---- top-p over the top-k survivors (src/sample/sampler.cpp:70-85): keep
-  // while the mass before an element, in (z' desc, index asc) order, is below
-  // ceil(p * W); the cutoff key's tie group keeps its first t in index order
-  unsigned int ck = 0u;          // keys above ck: kept; key ck: the first tkeep
-  unsigned int tkeep = 0xffffffffu;
-  if (topp) {
-    unsigned long long ms = 0ull;
-    for (int i = tid; i < V; i += FT) {
-      const float zp = raw1<DT>(orow, i);
-      if (okey(zp) >= tk) ms += massf(zp);
+  if (ph == FP_P0) {
+    // ---- top-k's last digit, then the nucleus's first level over the top-k
+    // survivors (src/sample/sampler.cpp:70-85)
+    unsigned int tk = 0u;
+    if (tk_on) {
+      const FSel s = select_level<false, false>(row.sk[1], 0, hcs(1), nullptr, G, 0.0f, sh);
+      if (g == 0 && tid == 0) row.sk[0] = s;
+      tk = s.prefix;
     }
-    const unsigned long long W = fsum(ms, sh.u64r);
-    unsigned long long PW = static_cast<unsigned long long>(ceil(static_cast<double>(pr) * static_cast<double>(W)));
-    if (PW < 1ull) PW = 1ull;
-    unsigned long long above;
-    unsigned int g;
-    ck = radix_select<true>(V, PW, zload, [tk](float, unsigned int key) { return key >= tk; }, massf, sh, &above,
-                            &g);
-    const unsigned long long wt = massf(key2f(ck));
-    const unsigned int t = ties_kept(PW > above ? PW - above : 0ull, wt, g);
-    tkeep = t >= g ? 0xffffffffu : t;
+    if (tp_on) {
+      FSel s{};
+      slice_hist<true>(lo, hi, 24, s, zload, [tk](float, unsigned int key) { return key >= tk; }, massf,
+                       hcs(0) + g * 256, hms(0) + g * 256, sh);
+    }
+    return;
   }
-  // ---- min_p after them (src/sample/sampler.cpp:87-93): the weights that
-  // reach min_p times the max's own weight
-  const float thr = mr > 0.0f ? minp_thr(mr, Mp, nc, minf) : 0.0f;
+  const unsigned int tk = tk_on ? row.sk[0].prefix : 0u;
+  auto above_tk = [tk](float, unsigned int key) { return key >= tk; };
+  if (ph >= FP_P1 && ph <= FP_P3) {
+    // ---- nucleus level l: keep while the mass before an element, in (z'
+    // desc, index asc) order, is below ceil(p W)
+    if (!tp_on) return;
+    const int l = ph - FP_P1 + 1;
+    FSel s;
+    if (l == 1) {
+      s = FSel{};
+      s = select_level<true, true>(s, 24, hcs(0), hms(0), G, pr, sh);
+    } else {
+      s = select_level<true, false>(row.sp[(l - 1) & 1], 32 - 8 * l, hcs((l - 1) & 1), hms((l - 1) & 1), G, pr, sh);
+    }
+    if (g == 0 && tid == 0) row.sp[l & 1] = s;
+    slice_hist<true>(lo, hi, 24 - 8 * l, s, zload, above_tk, massf, hcs(l & 1) + g * 256, hms(l & 1) + g * 256,
+                     sh);
+    return;
+  }
 
-  // ---- the last pass: -inf over every removed entry.  The partial tie group
-  // needs index order: thread t takes the contiguous range [t E, (t + 1) E)
-  const int E = (V + FT - 1) / FT;
-  const int i0 = min(tid * E, V), i1 = min(i0 + E, V);
+  // the nucleus cutoff: keys above ck kept, key ck keeps its first tkeep in
+  // index order (all of them: tkeep = ~0)
+  auto cutoff = [&](const FSel& s, unsigned int* ck, unsigned int* tkeep) {
+    *ck = s.prefix;
+    const unsigned long long wt = massf(key2f(s.prefix));
+    const unsigned int t = ties_kept(s.tgt > s.abv ? s.tgt - s.abv : 0ull, wt, s.cnt);
+    *tkeep = t >= s.cnt ? 0xffffffffu : t;
+  };
+  if (ph == FP_TIES) {
+    // ---- the nucleus's last digit, and this slice's count of the cutoff key
+    // when the cutoff's tie group is kept in part
+    if (!tp_on) return;
+    const FSel s = select_level<true, false>(row.sp[1], 0, hcs(1), hms(1), G, pr, sh);
+    if (g == 0 && tid == 0) row.sp[0] = s;
+    unsigned int ck, tkeep;
+    cutoff(s, &ck, &tkeep);
+    if (tkeep == 0xffffffffu) return;
+    unsigned int mine = 0u;
+    row_pass(lo, hi, zload, [&](int, float zp) { mine += okey(zp) == ck ? 1u : 0u; });
+    mine = wave_sum(mine);
+    if ((tid & 63) == 0) sh.ir[tid >> 6] = static_cast<int>(mine);
+    __syncthreads();
+    if (tid == 0) {
+      unsigned int tot = 0u;
+      for (int q = 0; q < FW; ++q) tot += static_cast<unsigned int>(sh.ir[q]);
+      row.tiec[g] = tot;
+    }
+    return;
+  }
+
+  // ---- FP_FIN: z', or -inf over every removed entry.  The partial tie
+  // group keeps its first tkeep in index order: a tied element's rank is the
+  // ties of the lower slices, of the lower waves' segments of this slice, and
+  // those before it in its own segment
+  unsigned int ck = 0u, tkeep = 0xffffffffu;
+  if (tp_on) cutoff(row.sp[0], &ck, &tkeep);
+  const bool filt = live && (tk_on || tp_on || mr > 0.0f);
+  // min_p after them (src/sample/sampler.cpp:87-93): the weights that reach
+  // min_p times the max's own weight
+  const float thr = filt && mr > 0.0f ? minp_thr(mr, Mp, nc, minf) : 0.0f;
+  const bool partial = tkeep != 0xffffffffu;
+  int s0, s1;
+  wave_segment(lo, hi, &s0, &s1);
   unsigned int rank = 0u;
-  if (tkeep != 0xffffffffu) {
-    int mine = 0;
-    for (int i = i0; i < i1; ++i) mine += okey(raw1<DT>(orow, i)) == ck ? 1 : 0;
-    int tot;
-    rank = static_cast<unsigned int>(rh::bscan(mine, sh.ir, &tot));
+  if (partial) {
+    for (int q = 0; q < g; ++q) rank += row.tiec[q];
+    rank += ties_before(s0, s1, zload, [&](float zp) { return okey(zp) == ck; }, sh.ir);
   }
-  for (int i = i0; i < i1; ++i) {
-    const float zp = raw1<DT>(orow, i);
-    const unsigned int key = okey(zp);
-    bool keep = key >= tk;
-    if (topp) {
-      if (key < ck) {
-        keep = false;
-      } else if (key == ck && tkeep != 0xffffffffu) {
-        keep = keep && rank < tkeep;
-        ++rank;
+  seg_pass(s0, s1, zload, [&](int i, bool in, float zp) {
+    bool keep = true;
+    if (filt) {
+      const unsigned int key = okey(zp);
+      keep = key >= tk;
+      if (tp_on) {
+        keep = keep && key >= ck;
+        if (partial) {
+          const bool tie = in && key == ck;
+          const unsigned long long tb = __ballot(tie);
+          if (tie) keep = keep && rank + lanes_below(tb) < tkeep;
+          rank += static_cast<unsigned int>(__popcll(tb));
+        }
       }
+      if (mr > 0.0f) keep = keep && wfun(zp + 0.0f, Mp, nc, minf) >= thr;
     }
-    if (mr > 0.0f) keep = keep && wfun(zp + 0.0f, Mp, nc, minf) >= thr;
-    if (!keep && zp != -INFINITY) st1<DT>(orow, i, -INFINITY);
-  }
+    if (in) st1<DT>(orow, i, keep ? zp : -INFINITY);
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -305,7 +608,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
 
   // ---- log-sum-exp of the unscaled row
   float mx = -INFINITY;
-  for (int i = tid; i < V; i += FT) mx = fmaxf(mx, load(i));
+  row_pass(0, V, load, [&](int, float z) { mx = fmaxf(mx, z); });
   float M;
   {
     const float w = wave_max(mx);
@@ -314,7 +617,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
     M = rdl(row_max16(sh.f.fr[tid & (FW - 1)]), 0);
   }
   double part = 0.0;
-  for (int i = tid; i < V; i += FT) part += wexp_d(load(i), M);
+  row_pass(0, V, load, [&](int, float z) { part += wexp_d(z, M); });
   const double lse = static_cast<double>(M) + log(fsum(part, sh.dr));
 
   // ---- the K-th largest logit (counting multiplicity) and the entries
@@ -324,28 +627,23 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
                                                [](float, unsigned int) { return true; },
                                                [](float) { return 0ull; }, sh.f, &above, &g);
   const unsigned int need_eq = static_cast<unsigned int>(K) - static_cast<unsigned int>(above);
-  // contiguous ranges (index order for the tied entries)
-  const int E = (V + FT - 1) / FT;
-  const int i0 = min(tid * E, V), i1 = min(i0 + E, V);
-  int mine = 0;
-  for (int i = i0; i < i1; ++i) mine += okey(load(i)) == tau ? 1 : 0;
-  int tot;
-  unsigned int rank = static_cast<unsigned int>(rh::bscan(mine, sh.f.ir, &tot));
+  // wave segments (index order for the tied entries)
+  int s0, s1;
+  wave_segment(0, V, &s0, &s1);
   if (tid == 0) sh.n = 0u;
-  __syncthreads();
-  for (int i = i0; i < i1; ++i) {
-    const unsigned int key = okey(load(i));
-    bool take = key > tau;
-    if (key == tau) {
-      take = rank < need_eq;
-      ++rank;
-    }
+  unsigned int rank = ties_before(s0, s1, load, [&](float z) { return okey(z) == tau; }, sh.f.ir);
+  seg_pass(s0, s1, load, [&](int i, bool in, float z) {
+    const unsigned int key = in ? okey(z) : 0u;
+    const bool tie = in && key == tau;
+    const unsigned long long tb = __ballot(tie);
+    const bool take = in && (key > tau || (tie && rank + lanes_below(tb) < need_eq));
+    rank += static_cast<unsigned int>(__popcll(tb));
     if (take) {
       const unsigned int slot = __hip_atomic_fetch_add(&sh.n, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       if (slot < static_cast<unsigned int>(TOPK_WIDE_MAX))
         sh.ent[slot] = (static_cast<unsigned long long>(key) << 32) | (0xffffffffu - static_cast<unsigned int>(i));
     }
-  }
+  });
   __syncthreads();
   // ---- bitonic sort, descending, over the next power of two (padding: 0)
   int np = 1;
@@ -384,8 +682,12 @@ void set_err(char** err, const std::string& msg) {
   *err = q;
 }
 
+// Which phases a call launches: every one for per-row parameters, only those
+// of the filters that are on for the single-filter calls.
+enum FUse { FU_ALL, FU_TOPK, FU_TOPP, FU_MINP };
+
 int launch_filter(const void* d_logits, int dtype, int B, int V, int64_t row_stride, void* d_out, int64_t out_stride,
-                  FArgs f, void* stream, char** err) {
+                  FArgs f, FUse use, void* d_ws, size_t ws_bytes, void* stream, char** err) {
   if (dtype != MLXF_DTYPE_F32 && dtype != MLXF_DTYPE_BF16 && dtype != MLXF_DTYPE_F16) {
     set_err(err, "mlxf: dtype must be MLXF_DTYPE_F32, MLXF_DTYPE_BF16 or MLXF_DTYPE_F16");
     return MLXF_EINVAL;
@@ -417,24 +719,56 @@ int launch_filter(const void* d_logits, int dtype, int B, int V, int64_t row_str
       return MLXF_EINVAL;
     }
   }
+  if (!d_ws || ws_bytes < filter_ws_bytes(B, V)) {
+    set_err(err, "mlxf: workspace is NULL or smaller than mlxf_filter_workspace_size()");
+    return MLXF_EWORKSPACE;
+  }
+  if (reinterpret_cast<uintptr_t>(d_ws) & 255u) {
+    set_err(err, "mlxf: workspace must be 256-byte aligned");
+    return MLXF_EINVAL;
+  }
   f.logits = d_logits;
   f.row_stride = row_stride;
   f.out = d_out;
   f.out_stride = out_stride;
   f.B = B;
   f.V = V;
+  FWs ws;
+  ws.G = filter_groups(B, V);
+  const size_t nb = static_cast<size_t>(B) * 2 * ws.G * 256;
+  char* base = static_cast<char*>(d_ws);
+  ws.rows = reinterpret_cast<FRow*>(base);
+  ws.hc = reinterpret_cast<unsigned int*>(base + fws_align(static_cast<size_t>(B) * sizeof(FRow)));
+  ws.hm = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws.hc) + fws_align(nb * 4));
+  int phases[10], np = 0;
+  phases[np++] = FP_MAX;
+  if (use == FU_ALL || use == FU_TOPK) {
+    phases[np++] = FP_K1;
+    phases[np++] = FP_K2;
+    phases[np++] = FP_K3;
+  }
+  if (use != FU_MINP) phases[np++] = FP_P0;
+  if (use == FU_ALL || use == FU_TOPP) {
+    phases[np++] = FP_P1;
+    phases[np++] = FP_P2;
+    phases[np++] = FP_P3;
+    phases[np++] = FP_TIES;
+  }
+  phases[np++] = FP_FIN;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned int>(B)), block(FT);
-  if (dtype == MLXF_DTYPE_F32)
-    hipLaunchKernelGGL(k_filter<MLXF_DTYPE_F32>, grid, block, 0, st, f);
-  else if (dtype == MLXF_DTYPE_BF16)
-    hipLaunchKernelGGL(k_filter<MLXF_DTYPE_BF16>, grid, block, 0, st, f);
-  else
-    hipLaunchKernelGGL(k_filter<MLXF_DTYPE_F16>, grid, block, 0, st, f);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    set_err(err, std::string("mlxf: kernel launch failed: ") + hipGetErrorString(e));
-    return MLXF_EHIP;
+  const dim3 grid(static_cast<unsigned int>(B), static_cast<unsigned int>(ws.G)), block(FT);
+  for (int q = 0; q < np; ++q) {
+    if (dtype == MLXF_DTYPE_F32)
+      hipLaunchKernelGGL(k_filter<MLXF_DTYPE_F32>, grid, block, 0, st, f, ws, phases[q]);
+    else if (dtype == MLXF_DTYPE_BF16)
+      hipLaunchKernelGGL(k_filter<MLXF_DTYPE_BF16>, grid, block, 0, st, f, ws, phases[q]);
+    else
+      hipLaunchKernelGGL(k_filter<MLXF_DTYPE_F16>, grid, block, 0, st, f, ws, phases[q]);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      set_err(err, std::string("mlxf: kernel launch failed: ") + hipGetErrorString(e));
+      return MLXF_EHIP;
+    }
   }
   return MLXF_OK;
 }
@@ -467,16 +801,27 @@ hipError_t launch_topk_wide(const void* logits, int dtype, int B, int V, long lo
 
 }  // namespace mlxf
 
+extern "C" int mlxf_filter_workspace_size(int B, int V, size_t* bytes, char** err) {
+  if (!bytes || B < 0 || V < 1 || V > MLXF_MAX_VOCAB) {
+    mlxf::set_err(err, "mlxf: bad arguments (bytes non-NULL, B >= 0, V in [1, MLXF_MAX_VOCAB])");
+    return MLXF_EINVAL;
+  }
+  *bytes = B == 0 ? 0 : mlxf::filter_ws_bytes(B, V);
+  return MLXF_OK;
+}
+
 extern "C" int mlxf_filter_logits(const void* d_logits, int dtype, int B, int V, int64_t row_stride,
                                   const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
-                                  const float* d_min_p, void* d_out, int64_t out_stride, void* stream, char** err) {
+                                  const float* d_min_p, void* d_out, int64_t out_stride, void* d_workspace,
+                                  size_t workspace_bytes, void* stream, char** err) {
   try {
     mlxf::FArgs f = mlxf::scalars(0.0f, 0, 1.0f, 0.0f);
     f.T = d_temperature;
     f.k = d_top_k;
     f.p = d_top_p;
     f.minp = d_min_p;
-    return mlxf::launch_filter(d_logits, dtype, B, V, row_stride, d_out, out_stride, f, stream, err);
+    return mlxf::launch_filter(d_logits, dtype, B, V, row_stride, d_out, out_stride, f, mlxf::FU_ALL, d_workspace,
+                               workspace_bytes, stream, err);
   } catch (...) {
     mlxf::set_err(err, "mlxf: unexpected exception");
     return MLXF_EINVAL;
@@ -484,19 +829,23 @@ extern "C" int mlxf_filter_logits(const void* d_logits, int dtype, int B, int V,
 }
 
 extern "C" int mlxf_apply_top_k(const void* d_logits, int dtype, int B, int V, int64_t row_stride, int k,
-                                void* d_out, int64_t out_stride, void* stream, char** err) {
+                                void* d_out, int64_t out_stride, void* d_workspace, size_t workspace_bytes,
+                                void* stream, char** err) {
   return mlxf::launch_filter(d_logits, dtype, B, V, row_stride, d_out, out_stride, mlxf::scalars(0.0f, k, 1.0f, 0.0f),
-                             stream, err);
+                             mlxf::FU_TOPK, d_workspace, workspace_bytes, stream, err);
 }
 
 extern "C" int mlxf_apply_top_p(const void* d_logits, int dtype, int B, int V, int64_t row_stride, float p,
-                                void* d_out, int64_t out_stride, void* stream, char** err) {
+                                void* d_out, int64_t out_stride, void* d_workspace, size_t workspace_bytes,
+                                void* stream, char** err) {
   return mlxf::launch_filter(d_logits, dtype, B, V, row_stride, d_out, out_stride, mlxf::scalars(0.0f, 0, p, 0.0f),
-                             stream, err);
+                             mlxf::FU_TOPP, d_workspace, workspace_bytes, stream, err);
 }
 
 extern "C" int mlxf_apply_min_p(const void* d_logits, int dtype, int B, int V, int64_t row_stride, float min_p,
-                                void* d_out, int64_t out_stride, void* stream, char** err) {
+                                void* d_out, int64_t out_stride, void* d_workspace, size_t workspace_bytes,
+                                void* stream, char** err) {
   return mlxf::launch_filter(d_logits, dtype, B, V, row_stride, d_out, out_stride,
-                             mlxf::scalars(0.0f, 0, 1.0f, min_p), stream, err);
+                             mlxf::scalars(0.0f, 0, 1.0f, min_p), mlxf::FU_MINP, d_workspace, workspace_bytes,
+                             stream, err);
 }

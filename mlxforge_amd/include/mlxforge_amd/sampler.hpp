@@ -219,20 +219,23 @@ class Sampler {
   // in place).  Asynchronous on the sampler's stream.
   void apply_top_k(const DeviceLogits& logits, int k, void* d_out, int64_t out_stride = 0) {
     char* err = nullptr;
+    ensure_filter_workspace(logits);
     detail::check(mlxf_apply_top_k(logits.data, logits.dtype, logits.B, logits.V, stride_of(logits), k, d_out,
-                                   out_stride ? out_stride : logits.V, stream_, &err),
+                                   out_stride ? out_stride : logits.V, flt_ws_.p, flt_ws_bytes_, stream_, &err),
                   err);
   }
   void apply_top_p(const DeviceLogits& logits, float p, void* d_out, int64_t out_stride = 0) {
     char* err = nullptr;
+    ensure_filter_workspace(logits);
     detail::check(mlxf_apply_top_p(logits.data, logits.dtype, logits.B, logits.V, stride_of(logits), p, d_out,
-                                   out_stride ? out_stride : logits.V, stream_, &err),
+                                   out_stride ? out_stride : logits.V, flt_ws_.p, flt_ws_bytes_, stream_, &err),
                   err);
   }
   void apply_min_p(const DeviceLogits& logits, float min_p, void* d_out, int64_t out_stride = 0) {
     char* err = nullptr;
+    ensure_filter_workspace(logits);
     detail::check(mlxf_apply_min_p(logits.data, logits.dtype, logits.B, logits.V, stride_of(logits), min_p, d_out,
-                                   out_stride ? out_stride : logits.V, stream_, &err),
+                                   out_stride ? out_stride : logits.V, flt_ws_.p, flt_ws_bytes_, stream_, &err),
                   err);
   }
 
@@ -260,6 +263,15 @@ class Sampler {
 
  private:
   static int64_t stride_of(const DeviceLogits& l) { return l.row_stride ? l.row_stride : l.V; }
+  void ensure_filter_workspace(const DeviceLogits& logits) {
+    size_t need = 0;
+    char* err = nullptr;
+    detail::check(mlxf_filter_workspace_size(logits.B, logits.V, &need, &err), err);
+    if (need > flt_ws_bytes_) {
+      flt_ws_.reserve(need);
+      flt_ws_bytes_ = need;
+    }
+  }
   void ensure_workspace(size_t bytes) {
     if (bytes <= ws_bytes_) return;
     ws_.reserve(bytes);
@@ -353,6 +365,8 @@ class Sampler {
   detail::DeviceBuf<int32_t> ids_, hist_, hlen_;
   detail::DeviceBuf<unsigned char> pen_ws_;
   size_t pen_ws_bytes_ = 0;
+  detail::DeviceBuf<unsigned char> flt_ws_;  // the filter calls' scratch
+  size_t flt_ws_bytes_ = 0;
 };
 
 }  // namespace mlxforge_amd

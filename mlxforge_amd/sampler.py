@@ -249,7 +249,25 @@ def apply_mask(logits: torch.Tensor, allowed_bits: torch.Tensor, V: int | None =
     return out
 
 
-def _filter_out(logits: torch.Tensor, V, out):
+class FilterWorkspace:
+    """Caller-owned scratch of the filter calls (no initialisation needed)."""
+
+    def __init__(self, device=None):
+        self.device = torch.device(device) if device is not None else torch.device("cuda")
+        self.buf = None
+
+    def get(self, B: int, V: int) -> torch.Tensor:
+        need = _lib.filter_workspace_size(B, V)
+        if self.buf is None or self.buf.numel() < need:
+            # torch's caching allocator returns >= 512-byte aligned blocks
+            self.buf = torch.empty(max(need, 256), dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+_default_filter_ws: dict = {}
+
+
+def _filter_out(logits: torch.Tensor, V, out, workspace=None):
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be a [B, V] view with unit stride along V")
     if logits.dtype not in _DTYPES:
@@ -260,18 +278,22 @@ def _filter_out(logits: torch.Tensor, V, out):
         out = torch.empty((B, V), dtype=logits.dtype, device=logits.device)
     elif out.dtype != logits.dtype or out.dim() != 2 or out.stride(1) != 1:
         raise ValueError("out must be a [B, V] view of the logits' dtype with unit stride along V")
+    if workspace is None:
+        workspace = _default_filter_ws.setdefault(logits.device, FilterWorkspace(logits.device))
+    ws = workspace.get(B, V)
     stream = ctypes.c_void_p(torch.cuda.current_stream(logits.device).cuda_stream)
-    return B, V, out, stream
+    return B, V, out, (_ptr(ws), ws.numel()), stream
 
 
 def filter_logits(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p=None,
-                  V: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                  V: int | None = None, out: torch.Tensor | None = None,
+                  workspace: FilterWorkspace | None = None) -> torch.Tensor:
     """z' = logits / temperature (rounded to the logits dtype) with the
     entries that top-k, top-p and min_p remove set to -inf, per row, as
     Sampler::sample filters before its draw (src/sample/sampler.cpp:158-163).
     Per-row parameters as in sample_rows; None = that step off.  out may be
     logits itself (in place)."""
-    B, V, out, stream = _filter_out(logits, V, out)
+    B, V, out, ws, stream = _filter_out(logits, V, out, workspace)
     dev = logits.device
     T = _param(temperature, B, torch.float32, dev)
     k = _param(top_k, B, torch.int32, dev)
@@ -279,41 +301,44 @@ def filter_logits(logits: torch.Tensor, temperature=None, top_k=None, top_p=None
     mp = _param(min_p, B, torch.float32, dev)
     err = ctypes.c_void_p()
     rc = _lib.load().mlxf_filter_logits(_ptr(logits), _DTYPES[logits.dtype], B, V, logits.stride(0), _ptr(T),
-                                        _ptr(k), _ptr(p), _ptr(mp), _ptr(out), out.stride(0), stream,
+                                        _ptr(k), _ptr(p), _ptr(mp), _ptr(out), out.stride(0), *ws, stream,
                                         ctypes.byref(err))
     _lib.check(rc, err)
     return out
 
 
-def apply_top_k(logits: torch.Tensor, k: int, out: torch.Tensor | None = None) -> torch.Tensor:
+def apply_top_k(logits: torch.Tensor, k: int, out: torch.Tensor | None = None,
+                workspace: FilterWorkspace | None = None) -> torch.Tensor:
     """Sampler::apply_top_k (src/sample/sampler.cpp:63-68): entries below the
     k-th largest (counting multiplicity) set to -inf."""
-    B, V, out, stream = _filter_out(logits, None, out)
+    B, V, out, ws, stream = _filter_out(logits, None, out, workspace)
     err = ctypes.c_void_p()
     rc = _lib.load().mlxf_apply_top_k(_ptr(logits), _DTYPES[logits.dtype], B, V, logits.stride(0), int(k),
-                                      _ptr(out), out.stride(0), stream, ctypes.byref(err))
+                                      _ptr(out), out.stride(0), *ws, stream, ctypes.byref(err))
     _lib.check(rc, err)
     return out
 
 
-def apply_top_p(logits: torch.Tensor, p: float, out: torch.Tensor | None = None) -> torch.Tensor:
+def apply_top_p(logits: torch.Tensor, p: float, out: torch.Tensor | None = None,
+                workspace: FilterWorkspace | None = None) -> torch.Tensor:
     """Sampler::apply_top_p (src/sample/sampler.cpp:70-85): entries past the
     smallest (value desc, index asc) prefix whose mass reaches p set to -inf."""
-    B, V, out, stream = _filter_out(logits, None, out)
+    B, V, out, ws, stream = _filter_out(logits, None, out, workspace)
     err = ctypes.c_void_p()
     rc = _lib.load().mlxf_apply_top_p(_ptr(logits), _DTYPES[logits.dtype], B, V, logits.stride(0), float(p),
-                                      _ptr(out), out.stride(0), stream, ctypes.byref(err))
+                                      _ptr(out), out.stride(0), *ws, stream, ctypes.byref(err))
     _lib.check(rc, err)
     return out
 
 
-def apply_min_p(logits: torch.Tensor, min_p: float, out: torch.Tensor | None = None) -> torch.Tensor:
+def apply_min_p(logits: torch.Tensor, min_p: float, out: torch.Tensor | None = None,
+                workspace: FilterWorkspace | None = None) -> torch.Tensor:
     """Sampler::apply_min_p (src/sample/sampler.cpp:87-93): entries whose
     probability is below min_p times the largest set to -inf."""
-    B, V, out, stream = _filter_out(logits, None, out)
+    B, V, out, ws, stream = _filter_out(logits, None, out, workspace)
     err = ctypes.c_void_p()
     rc = _lib.load().mlxf_apply_min_p(_ptr(logits), _DTYPES[logits.dtype], B, V, logits.stride(0),
-                                      float(min_p), _ptr(out), out.stride(0), stream, ctypes.byref(err))
+                                      float(min_p), _ptr(out), out.stride(0), *ws, stream, ctypes.byref(err))
     _lib.check(rc, err)
     return out
 

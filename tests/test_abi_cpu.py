@@ -153,6 +153,21 @@ def test_pre_sampling_entry_points_argument_errors_need_no_gpu():
                                   None, None) == 0  # no penalty array: nothing to do
     assert L.mlxf_apply_penalties(fake, 0, 2, 10, 10, fake, 0, None, fake, None, None, None, 0,
                                   None, None) == 0  # empty history
+    # filters: workspace size grows with B; a missing or small workspace and a
+    # misaligned one are refused before any GPU work
+    a, b = ctypes.c_size_t(), ctypes.c_size_t()
+    assert L.mlxf_filter_workspace_size(8, 151936, ctypes.byref(a), None) == 0
+    assert L.mlxf_filter_workspace_size(64, 151936, ctypes.byref(b), None) == 0
+    assert 0 < a.value <= b.value and a.value % 256 == 0
+    assert L.mlxf_filter_workspace_size(0, 10, ctypes.byref(a), None) == 0 and a.value == 0
+    assert L.mlxf_filter_workspace_size(4, 0, ctypes.byref(a), None) == _lib.EINVAL
+    out = ctypes.c_void_p(0x100000)
+    for ws, nbytes, code in ((None, 1 << 20, _lib.EWORKSPACE), (fake, 16, _lib.EWORKSPACE),
+                             (ctypes.c_void_p(0x1008), 1 << 24, _lib.EINVAL)):
+        err = ctypes.c_void_p()
+        assert L.mlxf_apply_top_k(fake, 0, 2, 10, 10, 3, out, 10, ws, nbytes, None, ctypes.byref(err)) == code
+        assert err.value
+        L.mlxf_string_free(err)
     # uniforms
     err = ctypes.c_void_p()
     assert L.mlxf_uniforms(-1, fake, None, 0, fake, None, ctypes.byref(err)) == _lib.EINVAL
