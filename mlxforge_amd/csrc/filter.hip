@@ -142,78 +142,6 @@ __device__ __forceinline__ T fsum(T x, T* red) {
   return rdl(row_sum16(lane < FW ? red[lane & (FW - 1)] : T(0)), 0);
 }
 
-// Radix selection over the order keys of the row's candidates (elements whose
-// key passes `in`): the key c such that the measure (count, or fixed-point
-// mass when MASS) of candidates with key > c is below `target` and with key
-// >= c reaches it.  Returns c; *above = the measure above c, *cnt = the
-// number of candidates with key c.
-template <bool MASS, typename Load, typename In, typename Mass>
-__device__ unsigned int radix_select(int V, unsigned long long target, Load load, In in, Mass massf, FLds& sh,
-                                     unsigned long long* above, unsigned int* cnt) {
-  const int tid = threadIdx.x;
-  unsigned int prefix = 0u, mask = 0u;
-  unsigned long long rem = target, abv = 0ull;
-  unsigned int c_at = 0u;
-  const unsigned int cpy = static_cast<unsigned int>(tid) & (RC - 1);
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    __syncthreads();
-    for (int j = tid; j < 256 * RC; j += FT) {
-      sh.hc[j] = 0u;
-      if (MASS) sh.hm[j] = 0ull;
-    }
-    if (tid == 0) {
-      sh.sel[0] = 0u;
-      sh.sel[1] = 0u;
-      sh.sel64[0] = 0ull;
-    }
-    __syncthreads();
-    row_pass(0, V, load, [&](int, float zp) {
-      const unsigned int key = okey(zp);
-      if ((key & mask) == prefix && in(zp, key)) {
-        const unsigned int d = ((key >> shift) & 255u) * RC + cpy;
-        __hip_atomic_fetch_add(&sh.hc[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (MASS) {
-          const unsigned long long m = massf(zp);
-          if (m) __hip_atomic_fetch_add(&sh.hm[d], m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-      }
-    });
-    __syncthreads();
-    // digits in descending order: thread t < 256 takes digit 255 - t and sums
-    // its copies (starting at copy d, so that a wave's reads spread over the
-    // banks)
-    const unsigned int d = 255u - static_cast<unsigned int>(tid & 255);
-    unsigned int cnt_d = 0u;
-    unsigned long long meas = 0ull;
-    if (tid < 256) {
-      for (unsigned int c = 0; c < static_cast<unsigned int>(RC); ++c) {
-        const unsigned int j = d * RC + ((c + d) & (RC - 1));
-        cnt_d += sh.hc[j];
-        if (MASS) meas += sh.hm[j];
-      }
-      if (!MASS) meas = cnt_d;
-    }
-    unsigned long long tot;
-    const unsigned long long excl = rh::bscan(meas, sh.u64r, &tot);
-    if (tid < 256 && excl < rem && rem <= excl + meas) {
-      sh.sel[0] = d;
-      sh.sel64[0] = excl;
-      sh.sel[1] = cnt_d;
-    }
-    __syncthreads();
-    const unsigned int dd = sh.sel[0];
-    const unsigned long long ex = sh.sel64[0];
-    c_at = sh.sel[1];
-    rem -= ex;
-    abv += ex;
-    prefix |= dd << shift;
-    mask |= 255u << shift;
-  }
-  *above = abv;
-  *cnt = c_at;
-  return prefix;
-}
-
 // Wave w's contiguous segment [*s0, *s1) of the range [lo, hi), in whole
 // 64-element steps (each step one coalesced load per lane).
 __device__ __forceinline__ void wave_segment(int lo, int hi, int* s0, int* s1) {
@@ -349,10 +277,15 @@ __device__ FSel select_level(FSel s, int shift, const unsigned int* hc, const un
 }
 
 // This slice's histogram at `shift` of the candidates (key under s's prefix,
-// in(zp, key)) into level slot hc / hm (this workgroup's 256 bins).
-template <bool MASS, typename Load, typename In, typename Mass>
+// in(zp, key)) into level slot hc / hm (this workgroup's 256 bins); extra(zp)
+// sees every element of the slice on the way.
+struct NoExtra {
+  __device__ void operator()(float) const {}
+};
+
+template <bool MASS, typename Load, typename In, typename Mass, typename Extra = NoExtra>
 __device__ void slice_hist(int lo, int hi, int shift, FSel s, Load load, In in, Mass massf, unsigned int* hc,
-                           unsigned long long* hm, FLds& sh) {
+                           unsigned long long* hm, FLds& sh, Extra extra = Extra{}) {
   const int tid = threadIdx.x;
   const unsigned int cpy = static_cast<unsigned int>(tid) & (RC - 1);
   __syncthreads();
@@ -363,6 +296,7 @@ __device__ void slice_hist(int lo, int hi, int shift, FSel s, Load load, In in, 
   __syncthreads();
   const unsigned int prefix = s.prefix, mask = s.mask;
   row_pass(lo, hi, load, [&](int, float zp) {
+    extra(zp);
     const unsigned int key = okey(zp);
     if ((key & mask) == prefix && in(zp, key)) {
       const unsigned int d = ((key >> shift) & 255u) * RC + cpy;
@@ -572,66 +506,178 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
 // ---------------------------------------------------------------------------
 // top_logprobs wider than the sampling kernels' best-64 lists (64 < K <= 4096):
 // top_k_logprobs (src/sample/sampler.cpp:30-38; K = min(top_logprobs, V) at
-// :52) as a call of its own after the sampling kernels.  One 1024-thread
-// workgroup per row: the log-sum-exp of the unscaled row (fp64 partials), the
-// K-th largest logit by a radix selection, the K entries (every logit above
-// it, then the tied ones in index order) gathered into LDS and sorted by
-// (logit desc, index asc) with a bitonic network, then written as (id, logit
-// - LSE); columns past the row's K get id -1 and -inf.
+// :52) as launches of their own after the sampling kernels, G workgroups per
+// row as in the filter calls: the slice maxima of the unscaled row with the
+// first radix level of the K-th largest logit; the slices' fp64 sums of
+// exp(z - M) with the second level; the third and fourth levels; the last
+// digit with the slices' counts of the K-th logit's tie group; the gather of
+// the K entries (every logit above the K-th, then the tied ones in index
+// order) into the row's list in the workspace; and one workgroup per row that
+// sorts the list by (logit desc, index asc) with a bitonic network in LDS and
+// writes (id, logit - LSE), columns past the row's K as id -1 and -inf.
 
 constexpr int TOPK_WIDE_MAX = 4096;
+
+enum WPhase { W_MAX, W_K1, W_K2, W_K3, W_TIES, W_GATHER, W_SORT };
+
+struct WRow {
+  FRow f;
+  double lsep[FG_MAX];        // slice sums of exp(z - M)
+  unsigned int n, pad[63];    // entries gathered so far
+};
+
+struct WWs {
+  WRow* rows;                 // [B]
+  unsigned int* hc;           // [B][2][G][256]
+  unsigned long long* list;   // [B][K_max]: (key << 32) | ~index
+  int G;
+};
 
 struct TkLds {
   FLds f;
   unsigned long long ent[TOPK_WIDE_MAX];  // (key << 32) | ~index: one unsigned order, larger first
-  unsigned int n;
+  unsigned int n, base;
   double dr[FW];
 };
 
+__host__ __device__ inline size_t wide_ws_bytes(int B, int V, int K_max) {
+  const size_t G = static_cast<size_t>(filter_groups(B, V));
+  const size_t nb = static_cast<size_t>(B) * 2 * G * 256;
+  return fws_align(static_cast<size_t>(B) * sizeof(WRow)) + fws_align(nb * 4) +
+         fws_align(static_cast<size_t>(B) * K_max * 8);
+}
+
 template <int DT>
 __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long long row_stride, int V, const int* tlp,
-                                                     int K_max, int* top_ids, float* top_lp) {
+                                                     int K_max, int* top_ids, float* top_lp, WWs ws, int ph) {
   __shared__ TkLds sh;
   const int tid = threadIdx.x;
-  const int r = static_cast<int>(blockIdx.x);
+  const int r = static_cast<int>(blockIdx.x), g = static_cast<int>(blockIdx.y);
+  const int G = ws.G;
+  const int L = (((V + G - 1) / G) + 63) & ~63;
+  const int lo = min(g * L, V), hi = min(lo + L, V);
   const void* row = static_cast<const char*>(logits) + static_cast<size_t>(r) * row_stride * elem_size<DT>();
-  int* oid = top_ids + static_cast<size_t>(r) * K_max;
-  float* olp = top_lp + static_cast<size_t>(r) * K_max;
+  WRow& wr = ws.rows[r];
+  FRow& fr = wr.f;
+  unsigned int* hc0 = ws.hc + static_cast<size_t>(r) * 2 * G * 256;
+  auto hcs = [&](int slot) { return hc0 + static_cast<size_t>(slot) * G * 256; };
+  unsigned long long* lst = ws.list + static_cast<size_t>(r) * K_max;
   const int t = tlp ? tlp[r] : -1;
   const int K = t > 0 ? min(min(t, K_max), V) : 0;
-  for (int j = K + tid; j < K_max; j += FT) {
-    oid[j] = -1;
-    olp[j] = -INFINITY;
+  auto load = [&](int i) { return ld1<DT>(row, i); };  // NaN reads as -inf
+  auto all = [](float, unsigned int) { return true; };
+  auto nomass = [](float) { return 0ull; };
+
+  if (ph == W_SORT) {
+    // ---- one workgroup per row: sort the K gathered entries, write them
+    int* oid = top_ids + static_cast<size_t>(r) * K_max;
+    float* olp = top_lp + static_cast<size_t>(r) * K_max;
+    for (int j = K + tid; j < K_max; j += FT) {
+      oid[j] = -1;
+      olp[j] = -INFINITY;
+    }
+    if (K == 0) return;
+    int np = 1;
+    while (np < K) np <<= 1;
+    for (int j = tid; j < np; j += FT) sh.ent[j] = j < K ? lst[j] : 0ull;  // padding sorts last
+    float M = -INFINITY;
+    double S = 0.0;
+    for (int q = 0; q < G; ++q) M = fmaxf(M, fr.mxp[q]);
+    for (int q = 0; q < G; ++q) S += wr.lsep[q];
+    const double lse = static_cast<double>(M) + log(S);
+    __syncthreads();
+    for (int k = 2; k <= np; k <<= 1) {
+      for (int jj = k >> 1; jj > 0; jj >>= 1) {
+        for (int i = tid; i < np; i += FT) {
+          const int ixj = i ^ jj;
+          if (ixj > i) {
+            const unsigned long long a = sh.ent[i], b = sh.ent[ixj];
+            const bool desc = (i & k) == 0;
+            if (desc ? (a < b) : (a > b)) {
+              sh.ent[i] = b;
+              sh.ent[ixj] = a;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int j = tid; j < K; j += FT) {
+      const unsigned long long e = sh.ent[j];
+      const int id = static_cast<int>(0xffffffffu - static_cast<unsigned int>(e));
+      oid[j] = id;
+      olp[j] = static_cast<float>(static_cast<double>(load(id)) - lse);
+    }
+    return;
   }
   if (K == 0) return;
-  auto load = [&](int i) { return ld1<DT>(row, i); };  // NaN reads as -inf
 
-  // ---- log-sum-exp of the unscaled row
-  float mx = -INFINITY;
-  row_pass(0, V, load, [&](int, float z) { mx = fmaxf(mx, z); });
-  float M;
-  {
+  if (ph == W_MAX) {
+    // ---- the slice max, and the first level of the K-th largest logit
+    float mx = -INFINITY;
+    row_pass(lo, hi, load, [&](int, float z) { mx = fmaxf(mx, z); });
     const float w = wave_max(mx);
     if ((tid & 63) == 0) sh.f.fr[tid >> 6] = w;
     __syncthreads();
-    M = rdl(row_max16(sh.f.fr[tid & (FW - 1)]), 0);
+    const float m = rdl(row_max16(sh.f.fr[tid & (FW - 1)]), 0);
+    if (tid == 0) {
+      fr.mxp[g] = m;
+      if (g == 0) wr.n = 0u;
+    }
+    FSel s{};
+    slice_hist<false>(lo, hi, 24, s, load, all, nomass, hcs(0) + g * 256, nullptr, sh.f);
+    return;
   }
-  double part = 0.0;
-  row_pass(0, V, load, [&](int, float z) { part += wexp_d(z, M); });
-  const double lse = static_cast<double>(M) + log(fsum(part, sh.dr));
+  if (ph >= W_K1 && ph <= W_K3) {
+    // ---- level l = ph: choose digit l from slot (l - 1) & 1, build level l +
+    // 1 into slot l & 1; the first also sums exp(z - M) over the slice
+    const int l = ph - W_K1 + 1;
+    FSel s{};
+    s.rem = s.tgt = static_cast<unsigned long long>(K);
+    if (l > 1) s = fr.sk[(l - 1) & 1];
+    s = select_level<false, false>(s, 32 - 8 * l, hcs((l - 1) & 1), nullptr, G, 0.0f, sh.f);
+    if (g == 0 && tid == 0) fr.sk[l & 1] = s;
+    if (l == 1) {
+      float M = -INFINITY;
+      for (int q = 0; q < G; ++q) M = fmaxf(M, fr.mxp[q]);
+      double part = 0.0;
+      slice_hist<false>(lo, hi, 16, s, load, all, nomass, hcs(1) + g * 256, nullptr, sh.f,
+                        [&](float z) { part += wexp_d(z, M); });
+      const double tot = fsum(part, sh.dr);
+      if (tid == 0) wr.lsep[g] = tot;
+    } else {
+      slice_hist<false>(lo, hi, 24 - 8 * l, s, load, all, nomass, hcs(l & 1) + g * 256, nullptr, sh.f);
+    }
+    return;
+  }
+  if (ph == W_TIES) {
+    // ---- the last digit: tau is the K-th largest key; this slice's count of it
+    const FSel s = select_level<false, false>(fr.sk[1], 0, hcs(1), nullptr, G, 0.0f, sh.f);
+    if (g == 0 && tid == 0) fr.sk[0] = s;
+    unsigned int mine = 0u;
+    row_pass(lo, hi, load, [&](int, float z) { mine += okey(z) == s.prefix ? 1u : 0u; });
+    mine = wave_sum(mine);
+    if ((tid & 63) == 0) sh.f.ir[tid >> 6] = static_cast<int>(mine);
+    __syncthreads();
+    if (tid == 0) {
+      unsigned int tot = 0u;
+      for (int q = 0; q < FW; ++q) tot += static_cast<unsigned int>(sh.f.ir[q]);
+      fr.tiec[g] = tot;
+    }
+    return;
+  }
 
-  // ---- the K-th largest logit (counting multiplicity) and the entries
-  unsigned long long above;
-  unsigned int g;
-  const unsigned int tau = radix_select<false>(V, static_cast<unsigned long long>(K), load,
-                                               [](float, unsigned int) { return true; },
-                                               [](float) { return 0ull; }, sh.f, &above, &g);
-  const unsigned int need_eq = static_cast<unsigned int>(K) - static_cast<unsigned int>(above);
-  // wave segments (index order for the tied entries)
+  // ---- W_GATHER: every entry above tau, and the first need_eq of tau's tie
+  // group in index order, into LDS, then one reservation of the row's list
+  const FSel s = fr.sk[0];
+  const unsigned int tau = s.prefix;
+  const unsigned int need_eq = static_cast<unsigned int>(K) - static_cast<unsigned int>(s.abv);
   int s0, s1;
-  wave_segment(0, V, &s0, &s1);
+  wave_segment(lo, hi, &s0, &s1);
   if (tid == 0) sh.n = 0u;
-  unsigned int rank = ties_before(s0, s1, load, [&](float z) { return okey(z) == tau; }, sh.f.ir);
+  unsigned int rank = 0u;
+  for (int q = 0; q < g; ++q) rank += fr.tiec[q];
+  rank += ties_before(s0, s1, load, [&](float z) { return okey(z) == tau; }, sh.f.ir);
   seg_pass(s0, s1, load, [&](int i, bool in, float z) {
     const unsigned int key = in ? okey(z) : 0u;
     const bool tie = in && key == tau;
@@ -645,34 +691,13 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
     }
   });
   __syncthreads();
-  // ---- bitonic sort, descending, over the next power of two (padding: 0)
-  int np = 1;
-  while (np < K) np <<= 1;
-  for (int j = K + tid; j < np; j += FT) sh.ent[j] = 0ull;
+  const unsigned int n = min(sh.n, static_cast<unsigned int>(TOPK_WIDE_MAX));
+  if (tid == 0)
+    sh.base = n ? __hip_atomic_fetch_add(&wr.n, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
   __syncthreads();
-  for (int k = 2; k <= np; k <<= 1) {
-    for (int jj = k >> 1; jj > 0; jj >>= 1) {
-      for (int i = tid; i < np; i += FT) {
-        const int ixj = i ^ jj;
-        if (ixj > i) {
-          const unsigned long long a = sh.ent[i], b = sh.ent[ixj];
-          const bool desc = (i & k) == 0;
-          if (desc ? (a < b) : (a > b)) {
-            sh.ent[i] = b;
-            sh.ent[ixj] = a;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-  // ---- write (id, logit - LSE)
-  for (int j = tid; j < K; j += FT) {
-    const unsigned long long e = sh.ent[j];
-    const int id = static_cast<int>(0xffffffffu - static_cast<unsigned int>(e));
-    oid[j] = id;
-    olp[j] = static_cast<float>(static_cast<double>(load(id)) - lse);
-  }
+  const unsigned int base = sh.base;
+  for (unsigned int j = tid; j < n; j += FT)
+    if (base + j < static_cast<unsigned int>(K)) lst[base + j] = sh.ent[j];
 }
 
 void set_err(char** err, const std::string& msg) {
@@ -784,19 +809,32 @@ FArgs scalars(float T, int k, float p, float mp) {
 
 }  // namespace
 
+size_t topk_wide_ws_bytes(int B, int V, int K_max) { return K_max > TOPK_LIST ? wide_ws_bytes(B, V, K_max) : 0; }
+
 hipError_t launch_topk_wide(const void* logits, int dtype, int B, int V, long long row_stride, const int* tlp,
-                            int K_max, int* top_ids, float* top_lp, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned int>(B)), block(FT);
-  if (dtype == MLXF_DTYPE_F32)
-    hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_F32>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
-                       top_lp);
-  else if (dtype == MLXF_DTYPE_BF16)
-    hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_BF16>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
-                       top_lp);
-  else
-    hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_F16>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
-                       top_lp);
-  return hipGetLastError();
+                            int K_max, int* top_ids, float* top_lp, void* d_ws, hipStream_t st) {
+  WWs ws;
+  ws.G = filter_groups(B, V);
+  const size_t nb = static_cast<size_t>(B) * 2 * ws.G * 256;
+  char* base = static_cast<char*>(d_ws);
+  ws.rows = reinterpret_cast<WRow*>(base);
+  ws.hc = reinterpret_cast<unsigned int*>(base + fws_align(static_cast<size_t>(B) * sizeof(WRow)));
+  ws.list = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws.hc) + fws_align(nb * 4));
+  for (int ph = W_MAX; ph <= W_SORT; ++ph) {
+    const dim3 grid(static_cast<unsigned int>(B), ph == W_SORT ? 1u : static_cast<unsigned int>(ws.G)), block(FT);
+    if (dtype == MLXF_DTYPE_F32)
+      hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_F32>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
+                         top_lp, ws, ph);
+    else if (dtype == MLXF_DTYPE_BF16)
+      hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_BF16>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
+                         top_lp, ws, ph);
+    else
+      hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_F16>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
+                         top_lp, ws, ph);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace mlxf

@@ -24,7 +24,7 @@ __global__ void k_zero(unsigned int* p, size_t n) {
 struct Layout {
   int S, L, EPT;
   size_t off_ncand, off_actcnt, off_actlist, off_rec, off_list, off_rowst, off_hcnt, off_hmass, off_above,
-      off_dsum, off_cand, off_hsplit, off_crec, total;
+      off_dsum, off_cand, off_hsplit, off_crec, off_wide, total;
 };
 
 // bf16 rows with no top_logprobs take the row-histogram path (rowhist.hpp):
@@ -62,7 +62,6 @@ constexpr size_t CTR_BYTES_MAX = ROWS_MAX * sizeof(unsigned int) + 256;
 // CU (256) with at most MAX_S slices per row; otherwise the smallest EPT with
 // S <= MAX_S.
 Layout make_layout(int B, int V, int K_max, int dtype) {
-  (void)K_max;
   Layout l;
   int ept = 0;
   for (int e : {32, 16, 8}) {
@@ -114,6 +113,9 @@ Layout make_layout(int B, int V, int K_max, int dtype) {
   o = align256(o + rh::HIST_BYTES * nsplit);
   l.off_crec = o;
   o = align256(o + sizeof(unsigned long long) * rh::NCH * nsplit);
+  // the wide top_logprobs kernels' states, slice histograms and lists
+  l.off_wide = o;
+  o = align256(o + topk_wide_ws_bytes(B, V, K_max));
   l.total = o;
   return l;
 }
@@ -234,7 +236,7 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
                        ((static_cast<size_t>(row_stride) * esz) % 16 == 0);
     char* ws = static_cast<char*>(d_workspace);
     // top_logprobs wider than the sampling kernels' lists: the sampling
-    // kernels run without them, then one kernel writes every row's columns
+    // kernels run without them, then the wide kernels write every row's columns
     const bool wide = K_max > TOPK_LIST;
     const int K_main = wide ? 0 : K_max;
     Args a;
@@ -290,7 +292,7 @@ int run_sample(const void* d_logits, int dtype, int B, int V, int64_t row_stride
       e = launch_f16(a, l.EPT, vecok, nst, st);
     if (e == hipSuccess && wide)
       e = launch_topk_wide(d_logits, dtype, B, V, row_stride, d_top_logprobs, K_max, d_out_top_ids,
-                           d_out_top_logprobs, st);
+                           d_out_top_logprobs, ws + l.off_wide, st);
     if (e != hipSuccess) {
       set_err(err, std::string("mlxf: kernel launch failed: ") + hipGetErrorString(e));
       return MLXF_EHIP;

@@ -129,10 +129,12 @@ hipError_t launch_f16(const Args& a, int ept, bool vecok, int nst, hipStream_t s
 
 // top_logprobs wider than the sampling kernels' lists (TOPK_LIST < K_max;
 // defined in filter.hip): every row's top-K (id, logprob), columns past the
-// row's K as (-1, -inf).
+// row's K as (-1, -inf), with topk_wide_ws_bytes(B, V, K_max) bytes of
+// workspace (256-byte aligned, no initialisation; 0 when K_max <= TOPK_LIST).
 constexpr int TOPK_LIST = 64;
+size_t topk_wide_ws_bytes(int B, int V, int K_max);
 hipError_t launch_topk_wide(const void* logits, int dtype, int B, int V, long long row_stride, const int* tlp,
-                            int K_max, int* top_ids, float* top_lp, hipStream_t st);
+                            int K_max, int* top_ids, float* top_lp, void* d_ws, hipStream_t st);
 
 namespace {
 
