@@ -37,7 +37,7 @@ namespace {
 constexpr int FT = 1024;      // threads per workgroup
 constexpr int FW = FT / 64;   // waves
 constexpr int RC = 32;        // copies of each radix bin (lanes l and l + 32 share one)
-constexpr int FU = 8;         // loads in flight per lane in a row pass
+constexpr int FU8 = 4;        // 8-element units in flight per lane in a row pass
 
 struct FArgs {
   const void* logits;
@@ -52,6 +52,8 @@ struct FArgs {
   const float* minp;
   float Ts, ps, mps;
   int ks;
+  bool vec;   // 16-byte loads: the logits' base and row stride allow them
+  bool ovec;  // 16-byte stores: the output's base and row stride allow them
 };
 
 struct FLds {
@@ -74,16 +76,30 @@ __device__ __forceinline__ void st1(void* row, int i, float v) {
     static_cast<__half*>(row)[i] = __float2half_rn(v);
   }
 }
-// The stored value, NaN kept as NaN (the first pass has already read NaN as
-// -inf and written that).
+// n (<= 8) consecutive values from i0 (i0 % 8 == 0), each representable in
+// the dtype: whole units in 16-byte stores where the row allows them.
 template <int DT>
-__device__ __forceinline__ float raw1(const void* row, int i) {
-  if constexpr (DT == MLXF_DTYPE_F32) {
-    return static_cast<const float*>(row)[i];
-  } else if constexpr (DT == MLXF_DTYPE_BF16) {
-    return __uint_as_float(static_cast<unsigned int>(static_cast<const unsigned short*>(row)[i]) << 16);
+__device__ __forceinline__ void st8(void* row, bool vec, int i0, const float* v, int n) {
+  if (vec && n == 8) {
+    uint4* p = reinterpret_cast<uint4*>(static_cast<char*>(row) + static_cast<size_t>(i0) * elem_size<DT>());
+    if constexpr (DT == MLXF_DTYPE_F32) {
+      p[0] = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+      p[1] = make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7]));
+    } else {
+      unsigned int h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (DT == MLXF_DTYPE_BF16)
+          h[e] = __float_as_uint(v[e]) >> 16;
+        else
+          h[e] = static_cast<unsigned int>(__half_as_ushort(__float2half_rn(v[e])));
+      }
+      p[0] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+    }
   } else {
-    return __half2float(static_cast<const __half*>(row)[i]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < n) st1<DT>(row, i0 + e, v[e]);
   }
 }
 
@@ -91,43 +107,91 @@ __device__ __forceinline__ float raw1(const void* row, int i) {
 // comparisons do), so they share a key.
 __device__ __forceinline__ unsigned int okey(float zp) { return f2key(zp + 0.0f); }
 
-// fn(i, load(i)) for i = lo + tid, lo + tid + FT, ... < hi, with FU loads issued before
-// the first fn of each group: one workgroup streams its row, and a lane with
-// one load in flight at a time would wait out the memory latency per element.
-template <typename Load, typename Fn>
-__device__ __forceinline__ void row_pass(int lo, int hi, Load load, Fn fn) {
-  for (int b = lo + static_cast<int>(threadIdx.x); b < hi; b += FU * FT) {
-    float v[FU];
+// A row as the passes read it: 8-element units of raw storage (two 16-byte
+// loads for fp32, one for the 16-bit types, where the row's base and stride
+// allow; element loads otherwise), each decoded value passed through xf.
+template <int DT, typename Xf>
+struct RowSrc {
+  const void* row;
+  bool vec;
+  Xf xf;
+  __device__ __forceinline__ void load(int i0, int end, Raw8<DT>& r) const {
+    if (vec)
+      load_raw<DT, true>(row, i0, end, r);
+    else
+      load_raw<DT, false>(row, i0, end, r);
+  }
+  __device__ __forceinline__ float at(int i) const {
+    Raw8<DT> r;
+    load_raw<DT, false>(row, i, i + 1, r);
+    float v[8];
+    decode8_nan<DT>(r, v);
+    return xf(v[0]);
+  }
+};
+template <int DT, typename Xf>
+__device__ __forceinline__ RowSrc<DT, Xf> row_src(const void* row, bool vec, Xf xf) {
+  return RowSrc<DT, Xf>{row, vec, xf};
+}
+
+// fn(i, value) for every i in [lo, hi) (lo % 8 == 0), lane t taking the units
+// t, t + FT, ...; FU8 units per lane are loaded before the first is used: one
+// CU streams a slice, and it needs many bytes in flight per lane to do it at
+// the memory's rate.
+template <int DT, typename Xf, typename Fn>
+__device__ __forceinline__ void row_pass(int lo, int hi, const RowSrc<DT, Xf>& src, Fn fn) {
+  const int nu = (hi - lo + 7) >> 3;
+  for (int j0 = static_cast<int>(threadIdx.x); j0 < nu; j0 += FU8 * FT) {
+    Raw8<DT> raw[FU8];
 #pragma unroll
-    for (int u = 0; u < FU; ++u) {
-      const int i = b + u * FT;
-      v[u] = i < hi ? load(i) : 0.0f;
+    for (int q = 0; q < FU8; ++q) {
+      const int j = j0 + q * FT;
+      if (j < nu) src.load(lo + 8 * j, hi, raw[q]);
     }
 #pragma unroll
-    for (int u = 0; u < FU; ++u) {
-      const int i = b + u * FT;
-      if (i < hi) fn(i, v[u]);
+    for (int q = 0; q < FU8; ++q) {
+      const int j = j0 + q * FT;
+      if (j < nu) {
+        float v[8];
+        decode8_nan<DT>(raw[q], v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = lo + 8 * j + e;
+          if (i < hi) fn(i, src.xf(v[e]));
+        }
+      }
     }
   }
 }
 
-// The same over wave w's contiguous segment [s0, s1) in index order, in
-// 64-element steps: fn(i, in, v) with every lane of the wave taking part (in
-// false, v -inf past the segment's end), so fn may take ballots.
-template <typename Load, typename Fn>
-__device__ __forceinline__ void seg_pass(int s0, int s1, Load load, Fn fn) {
+// Over wave w's contiguous segment [s0, s1) (s0 % 8 == 0) in index order,
+// 512 elements per step, 8 consecutive ones per lane: fn(i0, v, n) with the
+// lane's first index, its 8 values and how many of them are in the segment
+// (0 to 8).  Every lane of the wave takes part in every step, so fn may use
+// wave operations.
+template <int DT, typename Xf, typename Fn>
+__device__ __forceinline__ void seg_pass(int s0, int s1, const RowSrc<DT, Xf>& src, Fn fn) {
   const int lane = static_cast<int>(threadIdx.x) & 63;
-  for (int b = s0; b < s1; b += FU * 64) {
-    float v[FU];
+  for (int b = s0; b < s1; b += FU8 * 512) {
+    Raw8<DT> raw[FU8];
 #pragma unroll
-    for (int u = 0; u < FU; ++u) {
-      const int i = b + u * 64 + lane;
-      v[u] = i < s1 ? load(i) : -INFINITY;
+    for (int q = 0; q < FU8; ++q) {
+      const int i0 = b + q * 512 + 8 * lane;
+      if (i0 < s1) src.load(i0, s1, raw[q]);
     }
 #pragma unroll
-    for (int u = 0; u < FU; ++u) {
-      const int i = b + u * 64 + lane;
-      fn(i, i < s1, v[u]);
+    for (int q = 0; q < FU8; ++q) {
+      const int i0 = b + q * 512 + 8 * lane;
+      float v[8];
+      if (i0 < s1) {
+        decode8_nan<DT>(raw[q], v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = src.xf(v[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = -INFINITY;
+      }
+      fn(i0, v, min(max(s1 - i0, 0), 8));
     }
   }
 }
@@ -142,29 +206,34 @@ __device__ __forceinline__ T fsum(T x, T* red) {
   return rdl(row_sum16(lane < FW ? red[lane & (FW - 1)] : T(0)), 0);
 }
 
-// Wave w's contiguous segment [*s0, *s1) of the range [lo, hi), in whole
-// 64-element steps (each step one coalesced load per lane).
+// Wave w's contiguous segment [*s0, *s1) of the range [lo, hi) (lo % 8 == 0),
+// in whole 512-element steps.
 __device__ __forceinline__ void wave_segment(int lo, int hi, int* s0, int* s1) {
-  const int S = ((hi - lo + FT - 1) / FT) * 64;
+  const int S = ((hi - lo + FW * 512 - 1) / (FW * 512)) * 512;
   *s0 = min(lo + (static_cast<int>(threadIdx.x) >> 6) * S, hi);
   *s1 = min(*s0 + S, hi);
 }
 
-// The lanes below this one whose bit is set in a ballot.
-__device__ __forceinline__ unsigned int lanes_below(unsigned long long b) {
-  return __builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(b >> 32),
-                                   __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(b), 0u));
+// Index-order ranks inside one seg_pass step: each lane's count c of marked
+// elements among its 8; returns the marked elements of the lower lanes, and
+// the step's total in *tot.
+__device__ __forceinline__ unsigned int lanes_before(unsigned int c, unsigned int* tot) {
+  const int inc = wave_incl_scan_dpp(static_cast<int>(c));
+  *tot = static_cast<unsigned int>(rdl(inc, 63));
+  return static_cast<unsigned int>(inc) - c;
 }
 
 // The number of elements whose value satisfies pred in the segments of the
 // waves below this one (red: FW words of LDS).
-template <typename Load, typename Pred>
-__device__ unsigned int ties_before(int s0, int s1, Load load, Pred pred, int* red) {
+template <int DT, typename Xf, typename Pred>
+__device__ unsigned int ties_before(int s0, int s1, const RowSrc<DT, Xf>& src, Pred pred, int* red) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   unsigned int mine = 0u;
-  seg_pass(s0, s1, load, [&](int, bool in, float v) {
-    mine += static_cast<unsigned int>(__popcll(__ballot(in && pred(v))));
+  seg_pass(s0, s1, src, [&](int, const float* v, int n) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mine += (e < n && pred(v[e])) ? 1u : 0u;
   });
+  mine = wave_sum(mine);
   __syncthreads();
   if (lane == 0) red[wid] = static_cast<int>(mine);
   __syncthreads();
@@ -354,17 +423,17 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
   const float mp = f.minp ? f.minp[r] : f.mps;
   const float mr = (mp > 0.0f && mp <= 1.0f) ? round_dt<DT>(mp) : 0.0f;
   // z' (NaN read as -inf)
-  auto zload = [&](int i) {
-    const float z = ld1<DT>(irow, i);
+  const auto src = row_src<DT>(irow, f.vec, [=](float z) {
+    z = z != z ? -INFINITY : z;
     return div ? round_dt<DT>(z / Tr) : z;
-  };
+  });
   auto all = [](float, unsigned int) { return true; };
   auto nomass = [](float) { return 0ull; };
 
   if (ph == FP_MAX) {
     // ---- the slice's max of z', and the top-k's first level
     float mx = -INFINITY;
-    row_pass(lo, hi, zload, [&](int, float zp) { mx = fmaxf(mx, zp); });
+    row_pass(lo, hi, src, [&](int, float zp) { mx = fmaxf(mx, zp); });
     const float w = wave_max(mx);
     if ((tid & 63) == 0) sh.fr[tid >> 6] = w;
     __syncthreads();
@@ -372,7 +441,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     if (tid == 0) row.mxp[g] = m;
     if (tk_on) {
       FSel s{};
-      slice_hist<false>(lo, hi, 24, s, zload, all, nomass, hcs(0) + g * 256, nullptr, sh);
+      slice_hist<false>(lo, hi, 24, s, src, all, nomass, hcs(0) + g * 256, nullptr, sh);
     }
     return;
   }
@@ -386,7 +455,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     if (l > 1) s = row.sk[(l - 1) & 1];
     s = select_level<false, false>(s, 32 - 8 * l, hcs((l - 1) & 1), nullptr, G, 0.0f, sh);
     if (g == 0 && tid == 0) row.sk[l & 1] = s;
-    slice_hist<false>(lo, hi, 24 - 8 * l, s, zload, all, nomass, hcs(l & 1) + g * 256, nullptr, sh);
+    slice_hist<false>(lo, hi, 24 - 8 * l, s, src, all, nomass, hcs(l & 1) + g * 256, nullptr, sh);
     return;
   }
 
@@ -410,7 +479,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     }
     if (tp_on) {
       FSel s{};
-      slice_hist<true>(lo, hi, 24, s, zload, [tk](float, unsigned int key) { return key >= tk; }, massf,
+      slice_hist<true>(lo, hi, 24, s, src, [tk](float, unsigned int key) { return key >= tk; }, massf,
                        hcs(0) + g * 256, hms(0) + g * 256, sh);
     }
     return;
@@ -430,7 +499,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
       s = select_level<true, false>(row.sp[(l - 1) & 1], 32 - 8 * l, hcs((l - 1) & 1), hms((l - 1) & 1), G, pr, sh);
     }
     if (g == 0 && tid == 0) row.sp[l & 1] = s;
-    slice_hist<true>(lo, hi, 24 - 8 * l, s, zload, above_tk, massf, hcs(l & 1) + g * 256, hms(l & 1) + g * 256,
+    slice_hist<true>(lo, hi, 24 - 8 * l, s, src, above_tk, massf, hcs(l & 1) + g * 256, hms(l & 1) + g * 256,
                      sh);
     return;
   }
@@ -453,7 +522,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     cutoff(s, &ck, &tkeep);
     if (tkeep == 0xffffffffu) return;
     unsigned int mine = 0u;
-    row_pass(lo, hi, zload, [&](int, float zp) { mine += okey(zp) == ck ? 1u : 0u; });
+    row_pass(lo, hi, src, [&](int, float zp) { mine += okey(zp) == ck ? 1u : 0u; });
     mine = wave_sum(mine);
     if ((tid & 63) == 0) sh.ir[tid >> 6] = static_cast<int>(mine);
     __syncthreads();
@@ -481,25 +550,39 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
   unsigned int rank = 0u;
   if (partial) {
     for (int q = 0; q < g; ++q) rank += row.tiec[q];
-    rank += ties_before(s0, s1, zload, [&](float zp) { return okey(zp) == ck; }, sh.ir);
+    rank += ties_before(s0, s1, src, [&](float zp) { return okey(zp) == ck; }, sh.ir);
   }
-  seg_pass(s0, s1, zload, [&](int i, bool in, float zp) {
-    bool keep = true;
-    if (filt) {
-      const unsigned int key = okey(zp);
-      keep = key >= tk;
-      if (tp_on) {
-        keep = keep && key >= ck;
-        if (partial) {
-          const bool tie = in && key == ck;
-          const unsigned long long tb = __ballot(tie);
-          if (tie) keep = keep && rank + lanes_below(tb) < tkeep;
-          rank += static_cast<unsigned int>(__popcll(tb));
+  seg_pass(s0, s1, src, [&](int i0, const float* v, int n) {
+    bool keep[8];
+    unsigned int c = 0u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      keep[e] = true;
+      if (filt) {
+        const unsigned int key = okey(v[e]);
+        keep[e] = key >= tk && (!tp_on || key >= ck);
+        if (mr > 0.0f) keep[e] = keep[e] && wfun(v[e] + 0.0f, Mp, nc, minf) >= thr;
+        if (partial) c += (e < n && key == ck) ? 1u : 0u;
+      }
+    }
+    if (partial) {
+      // the tied elements in index order: the lower lanes' first, then this
+      // lane's own
+      unsigned int tot;
+      unsigned int my = rank + lanes_before(c, &tot);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (e < n && okey(v[e]) == ck) {
+          keep[e] = keep[e] && my < tkeep;
+          ++my;
         }
       }
-      if (mr > 0.0f) keep = keep && wfun(zp + 0.0f, Mp, nc, minf) >= thr;
+      rank += tot;
     }
-    if (in) st1<DT>(orow, i, keep ? zp : -INFINITY);
+    float w[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = keep[e] ? v[e] : -INFINITY;
+    st8<DT>(orow, f.ovec, i0, w, n);
   });
 }
 
@@ -549,7 +632,8 @@ __host__ __device__ inline size_t wide_ws_bytes(int B, int V, int K_max) {
 
 template <int DT>
 __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long long row_stride, int V, const int* tlp,
-                                                     int K_max, int* top_ids, float* top_lp, WWs ws, int ph) {
+                                                     int K_max, int* top_ids, float* top_lp, WWs ws, int ph,
+                                                     bool vec) {
   __shared__ TkLds sh;
   const int tid = threadIdx.x;
   const int r = static_cast<int>(blockIdx.x), g = static_cast<int>(blockIdx.y);
@@ -564,7 +648,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
   unsigned long long* lst = ws.list + static_cast<size_t>(r) * K_max;
   const int t = tlp ? tlp[r] : -1;
   const int K = t > 0 ? min(min(t, K_max), V) : 0;
-  auto load = [&](int i) { return ld1<DT>(row, i); };  // NaN reads as -inf
+  const auto src = row_src<DT>(row, vec, [](float z) { return z != z ? -INFINITY : z; });  // NaN reads as -inf
   auto all = [](float, unsigned int) { return true; };
   auto nomass = [](float) { return 0ull; };
 
@@ -606,7 +690,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
       const unsigned long long e = sh.ent[j];
       const int id = static_cast<int>(0xffffffffu - static_cast<unsigned int>(e));
       oid[j] = id;
-      olp[j] = static_cast<float>(static_cast<double>(load(id)) - lse);
+      olp[j] = static_cast<float>(static_cast<double>(src.at(id)) - lse);
     }
     return;
   }
@@ -615,7 +699,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
   if (ph == W_MAX) {
     // ---- the slice max, and the first level of the K-th largest logit
     float mx = -INFINITY;
-    row_pass(lo, hi, load, [&](int, float z) { mx = fmaxf(mx, z); });
+    row_pass(lo, hi, src, [&](int, float z) { mx = fmaxf(mx, z); });
     const float w = wave_max(mx);
     if ((tid & 63) == 0) sh.f.fr[tid >> 6] = w;
     __syncthreads();
@@ -625,7 +709,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
       if (g == 0) wr.n = 0u;
     }
     FSel s{};
-    slice_hist<false>(lo, hi, 24, s, load, all, nomass, hcs(0) + g * 256, nullptr, sh.f);
+    slice_hist<false>(lo, hi, 24, s, src, all, nomass, hcs(0) + g * 256, nullptr, sh.f);
     return;
   }
   if (ph >= W_K1 && ph <= W_K3) {
@@ -641,12 +725,12 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
       float M = -INFINITY;
       for (int q = 0; q < G; ++q) M = fmaxf(M, fr.mxp[q]);
       double part = 0.0;
-      slice_hist<false>(lo, hi, 16, s, load, all, nomass, hcs(1) + g * 256, nullptr, sh.f,
+      slice_hist<false>(lo, hi, 16, s, src, all, nomass, hcs(1) + g * 256, nullptr, sh.f,
                         [&](float z) { part += wexp_d(z, M); });
       const double tot = fsum(part, sh.dr);
       if (tid == 0) wr.lsep[g] = tot;
     } else {
-      slice_hist<false>(lo, hi, 24 - 8 * l, s, load, all, nomass, hcs(l & 1) + g * 256, nullptr, sh.f);
+      slice_hist<false>(lo, hi, 24 - 8 * l, s, src, all, nomass, hcs(l & 1) + g * 256, nullptr, sh.f);
     }
     return;
   }
@@ -655,7 +739,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
     const FSel s = select_level<false, false>(fr.sk[1], 0, hcs(1), nullptr, G, 0.0f, sh.f);
     if (g == 0 && tid == 0) fr.sk[0] = s;
     unsigned int mine = 0u;
-    row_pass(lo, hi, load, [&](int, float z) { mine += okey(z) == s.prefix ? 1u : 0u; });
+    row_pass(lo, hi, src, [&](int, float z) { mine += okey(z) == s.prefix ? 1u : 0u; });
     mine = wave_sum(mine);
     if ((tid & 63) == 0) sh.f.ir[tid >> 6] = static_cast<int>(mine);
     __syncthreads();
@@ -677,17 +761,30 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
   if (tid == 0) sh.n = 0u;
   unsigned int rank = 0u;
   for (int q = 0; q < g; ++q) rank += fr.tiec[q];
-  rank += ties_before(s0, s1, load, [&](float z) { return okey(z) == tau; }, sh.f.ir);
-  seg_pass(s0, s1, load, [&](int i, bool in, float z) {
-    const unsigned int key = in ? okey(z) : 0u;
-    const bool tie = in && key == tau;
-    const unsigned long long tb = __ballot(tie);
-    const bool take = in && (key > tau || (tie && rank + lanes_below(tb) < need_eq));
-    rank += static_cast<unsigned int>(__popcll(tb));
-    if (take) {
-      const unsigned int slot = __hip_atomic_fetch_add(&sh.n, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (slot < static_cast<unsigned int>(TOPK_WIDE_MAX))
-        sh.ent[slot] = (static_cast<unsigned long long>(key) << 32) | (0xffffffffu - static_cast<unsigned int>(i));
+  rank += ties_before(s0, s1, src, [&](float z) { return okey(z) == tau; }, sh.f.ir);
+  seg_pass(s0, s1, src, [&](int i0, const float* v, int n) {
+    unsigned int c = 0u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c += (e < n && okey(v[e]) == tau) ? 1u : 0u;
+    unsigned int tot;
+    unsigned int my = rank + lanes_before(c, &tot);
+    rank += tot;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (e >= n) continue;
+      const unsigned int key = okey(v[e]);
+      bool take = key > tau;
+      if (key == tau) {
+        take = my < need_eq;
+        ++my;
+      }
+      if (take) {
+        const unsigned int slot =
+            __hip_atomic_fetch_add(&sh.n, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int i = i0 + e;
+        if (slot < static_cast<unsigned int>(TOPK_WIDE_MAX))
+          sh.ent[slot] = (static_cast<unsigned long long>(key) << 32) | (0xffffffffu - static_cast<unsigned int>(i));
+      }
     }
   });
   __syncthreads();
@@ -754,6 +851,8 @@ int launch_filter(const void* d_logits, int dtype, int B, int V, int64_t row_str
   }
   f.logits = d_logits;
   f.row_stride = row_stride;
+  f.vec = reinterpret_cast<uintptr_t>(d_logits) % 16 == 0 && (static_cast<size_t>(row_stride) * esz) % 16 == 0;
+  f.ovec = reinterpret_cast<uintptr_t>(d_out) % 16 == 0 && (static_cast<size_t>(out_stride) * esz) % 16 == 0;
   f.out = d_out;
   f.out_stride = out_stride;
   f.B = B;
@@ -820,17 +919,19 @@ hipError_t launch_topk_wide(const void* logits, int dtype, int B, int V, long lo
   ws.rows = reinterpret_cast<WRow*>(base);
   ws.hc = reinterpret_cast<unsigned int*>(base + fws_align(static_cast<size_t>(B) * sizeof(WRow)));
   ws.list = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws.hc) + fws_align(nb * 4));
+  const size_t esz = dtype == MLXF_DTYPE_F32 ? 4 : 2;
+  const bool vec = reinterpret_cast<uintptr_t>(logits) % 16 == 0 && (static_cast<size_t>(row_stride) * esz) % 16 == 0;
   for (int ph = W_MAX; ph <= W_SORT; ++ph) {
     const dim3 grid(static_cast<unsigned int>(B), ph == W_SORT ? 1u : static_cast<unsigned int>(ws.G)), block(FT);
     if (dtype == MLXF_DTYPE_F32)
       hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_F32>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
-                         top_lp, ws, ph);
+                         top_lp, ws, ph, vec);
     else if (dtype == MLXF_DTYPE_BF16)
       hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_BF16>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
-                         top_lp, ws, ph);
+                         top_lp, ws, ph, vec);
     else
       hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_F16>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
-                         top_lp, ws, ph);
+                         top_lp, ws, ph, vec);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
