@@ -258,6 +258,52 @@ def parity_report(step, torch):
     return rep
 
 
+def helpers_line(steps, warmup):
+    """Microseconds per call of the calls around the decode step: the filter
+    helpers (apply_top_k / apply_top_p / apply_min_p / filter_logits) and the
+    sampling call with top_logprobs above the 64-entry lists, at B=64,
+    V=151936 on N(0, 4^2) logits (fp32 and bf16), timed with events on
+    torch's current stream."""
+    import torch
+    from mlxforge_amd import sampler
+    B, V = 64, 151936
+    g = torch.Generator(device="cuda").manual_seed(64)
+
+    def t(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(e0.elapsed_time(e1) * 1000 / steps, 1)
+
+    res = {}
+    for name, dt in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+        x = (torch.randn(B, V, device="cuda", generator=g) * 4).to(dt)
+        out = torch.empty_like(x)
+        T = torch.full((B,), 0.8, device="cuda")
+        k = torch.full((B,), 50, dtype=torch.int32, device="cuda")
+        p = torch.full((B,), 0.9, device="cuda")
+        mp = torch.full((B,), 0.05, device="cuda")
+        u = torch.rand(B, device="cuda", generator=g)
+        r = {"apply_top_k(50)": t(lambda: sampler.apply_top_k(x, 50, out=out)),
+             "apply_top_p(0.9)": t(lambda: sampler.apply_top_p(x, 0.9, out=out)),
+             "apply_min_p(0.05)": t(lambda: sampler.apply_min_p(x, 0.05, out=out)),
+             "filter_logits(T=0.8,k=50,p=0.9,min_p=0.05)": t(lambda: sampler.filter_logits(
+                 x, temperature=T, top_k=k, top_p=p, min_p=mp, out=out))}
+        for K in (20, 65, 256, 4096):
+            tl = torch.full((B,), K, dtype=torch.int32, device="cuda")
+            r[f"sample_rows(T=0.8,p=0.9,top_logprobs={K})"] = t(lambda: sampler.sample_rows(
+                x, temperature=T, top_p=p, top_logprobs=tl, uniforms=u, K_max=K, refine_stages=2))
+        res[name] = r
+    print(json.dumps({"helpers_us_per_call": res, "B": B, "V": V, "steps": steps, "warmup": warmup,
+                      "data": "synthetic N(0, 4^2) logits"}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -269,7 +315,12 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs' lines")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run five plain 256 MiB device copies (counter scale factors)")
+    ap.add_argument("--helpers", action="store_true",
+                    help="only time the filter calls and wide top_logprobs (B=64, V=151936; one JSON line)")
     args = ap.parse_args()
+    if args.helpers:
+        helpers_line(args.steps, args.warmup)
+        return
     if args.copy_calibration:
         import torch
         x = torch.ones(COPY_CALIBRATION_BYTES // 4, device="cuda")
