@@ -182,6 +182,37 @@ def test_in_place_padded_and_non_finite():
     assert _same(full[:, V:].cpu().numpy(), z[:, V:])
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("off", [0, 3])
+def test_in_place_several_workgroups_per_row(dtype, off):
+    """Rows split over several workgroups (G > 1), filtered in place, with the
+    view's base 16-byte aligned (off = 0: 16-byte loads and stores) or not
+    (off = 3: element loads and stores); the columns around the view keep
+    their values."""
+    rng = np.random.default_rng(900 + off + len(dtype))
+    B, V, pad = 8, 40000, 24
+    z = _rows(rng, B, V + pad, dtype)
+    host = _host(z, dtype)
+    full = gu.to_device(host, dtype)
+    view = full[:, off:off + V]
+    vals = _vals(host, dtype)[:, off:off + V]
+    T = rng.uniform(0.5, 1.2, B).astype(np.float32)
+    k = np.array([0, 40, 0, 5000, 0, 1, 0, 20000], np.int32)
+    p = np.array([0.9, 1.0, 0.5, 0.95, 0.3, 1.0, 0.99, 0.8], np.float32)
+    mp = np.array([0.0, 0.0, 0.02, 0.0, 0.0, 0.0, 0.001, 0.1], np.float32)
+    say(f"[filter] in place, G > 1, {dtype} off={off}")
+    d = lambda a, t: torch.as_tensor(a, dtype=t).cuda()
+    before = _out_vals(full, dtype)
+    out = sampler.filter_logits(view, temperature=d(T, torch.float32), top_k=d(k, torch.int32),
+                                top_p=d(p, torch.float32), min_p=d(mp, torch.float32), out=view)
+    assert out.data_ptr() == view.data_ptr()
+    after = _out_vals(full, dtype)
+    _compare(after[:, off:off + V], vals, dtype, f"in place off={off}",
+             per_row={"T": [float(x) for x in T], "k": [int(x) for x in k], "p": [float(x) for x in p],
+                      "min_p": [float(x) for x in mp]})
+    assert _same(after[:, :off], before[:, :off]) and _same(after[:, off + V:], before[:, off + V:])
+
+
 def test_overlap_refused():
     x = torch.zeros((4, 100), dtype=torch.float32, device="cuda")
     with pytest.raises(Exception):
