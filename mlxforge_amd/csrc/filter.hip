@@ -271,6 +271,19 @@ struct FRow {
 
 enum FPhase { FP_MAX, FP_K1, FP_K2, FP_K3, FP_P0, FP_P1, FP_P2, FP_P3, FP_TIES, FP_FIN };
 
+// Radix levels a dtype needs: the order key of a 16-bit value has its low
+// bits fixed (bf16: 16, f16: 13; zeros for a non-negative value, ones for a
+// negative one), so the digits above them decide it: bf16 2 levels, f16 3,
+// fp32 4.  complete_key fills the bits below the decided digits.
+__host__ __device__ constexpr int nlev(int dt) { return dt == MLXF_DTYPE_F32 ? 4 : (dt == MLXF_DTYPE_BF16 ? 2 : 3); }
+template <int DT>
+__device__ __forceinline__ unsigned int complete_key(unsigned int prefix) {
+  constexpr int NL = nlev(DT);
+  if constexpr (NL == 4) return prefix;
+  constexpr unsigned int low = (1u << (32 - 8 * NL)) - 1u;
+  return (prefix & 0x80000000u) ? prefix : (prefix | low);
+}
+
 struct FWs {
   FRow* rows;               // [B]
   unsigned int* hc;         // [B][2][G][256]
@@ -445,9 +458,10 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     }
     return;
   }
+  constexpr int NL = nlev(DT);
   if (ph >= FP_K1 && ph <= FP_K3) {
-    // ---- top-k level l = ph: choose digit l from slot (l - 1) & 1, build
-    // level l + 1 into slot l & 1 (src/sample/sampler.cpp:63-68)
+    // ---- top-k level l = ph (l < NL): choose digit l from slot (l - 1) & 1,
+    // build level l + 1 into slot l & 1 (src/sample/sampler.cpp:63-68)
     if (!tk_on) return;
     const int l = ph - FP_K1 + 1;
     FSel s{};
@@ -473,18 +487,20 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     // survivors (src/sample/sampler.cpp:70-85)
     unsigned int tk = 0u;
     if (tk_on) {
-      const FSel s = select_level<false, false>(row.sk[1], 0, hcs(1), nullptr, G, 0.0f, sh);
-      if (g == 0 && tid == 0) row.sk[0] = s;
+      FSel s = select_level<false, false>(row.sk[(NL - 1) & 1], 32 - 8 * NL, hcs((NL - 1) & 1), nullptr, G, 0.0f,
+                                          sh);
+      s.prefix = complete_key<DT>(s.prefix);
+      if (g == 0 && tid == 0) row.sk[NL & 1] = s;
       tk = s.prefix;
     }
     if (tp_on) {
       FSel s{};
       slice_hist<true>(lo, hi, 24, s, src, [tk](float, unsigned int key) { return key >= tk; }, massf,
-                       hcs(0) + g * 256, hms(0) + g * 256, sh);
+                       hcs(NL & 1) + g * 256, hms(NL & 1) + g * 256, sh);
     }
     return;
   }
-  const unsigned int tk = tk_on ? row.sk[0].prefix : 0u;
+  const unsigned int tk = tk_on ? row.sk[NL & 1].prefix : 0u;
   auto above_tk = [tk](float, unsigned int key) { return key >= tk; };
   if (ph >= FP_P1 && ph <= FP_P3) {
     // ---- nucleus level l: keep while the mass before an element, in (z'
@@ -494,12 +510,14 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     FSel s;
     if (l == 1) {
       s = FSel{};
-      s = select_level<true, true>(s, 24, hcs(0), hms(0), G, pr, sh);
+      s = select_level<true, true>(s, 24, hcs(NL & 1), hms(NL & 1), G, pr, sh);
     } else {
-      s = select_level<true, false>(row.sp[(l - 1) & 1], 32 - 8 * l, hcs((l - 1) & 1), hms((l - 1) & 1), G, pr, sh);
+      const int in = (NL + l - 1) & 1;
+      s = select_level<true, false>(row.sp[(l - 1) & 1], 32 - 8 * l, hcs(in), hms(in), G, pr, sh);
     }
     if (g == 0 && tid == 0) row.sp[l & 1] = s;
-    slice_hist<true>(lo, hi, 24 - 8 * l, s, src, above_tk, massf, hcs(l & 1) + g * 256, hms(l & 1) + g * 256,
+    const int outs = (NL + l) & 1;
+    slice_hist<true>(lo, hi, 24 - 8 * l, s, src, above_tk, massf, hcs(outs) + g * 256, hms(outs) + g * 256,
                      sh);
     return;
   }
@@ -516,8 +534,10 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     // ---- the nucleus's last digit, and this slice's count of the cutoff key
     // when the cutoff's tie group is kept in part
     if (!tp_on) return;
-    const FSel s = select_level<true, false>(row.sp[1], 0, hcs(1), hms(1), G, pr, sh);
-    if (g == 0 && tid == 0) row.sp[0] = s;
+    FSel s = select_level<true, false>(row.sp[(NL - 1) & 1], 32 - 8 * NL, hcs((2 * NL - 1) & 1),
+                                       hms((2 * NL - 1) & 1), G, pr, sh);
+    s.prefix = complete_key<DT>(s.prefix);
+    if (g == 0 && tid == 0) row.sp[NL & 1] = s;
     unsigned int ck, tkeep;
     cutoff(s, &ck, &tkeep);
     if (tkeep == 0xffffffffu) return;
@@ -539,7 +559,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
   // ties of the lower slices, of the lower waves' segments of this slice, and
   // those before it in its own segment
   unsigned int ck = 0u, tkeep = 0xffffffffu;
-  if (tp_on) cutoff(row.sp[0], &ck, &tkeep);
+  if (tp_on) cutoff(row.sp[NL & 1], &ck, &tkeep);
   const bool filt = live && (tk_on || tp_on || mr > 0.0f);
   // min_p after them (src/sample/sampler.cpp:87-93): the weights that reach
   // min_p times the max's own weight
@@ -712,6 +732,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
     slice_hist<false>(lo, hi, 24, s, src, all, nomass, hcs(0) + g * 256, nullptr, sh.f);
     return;
   }
+  constexpr int NL = nlev(DT);
   if (ph >= W_K1 && ph <= W_K3) {
     // ---- level l = ph: choose digit l from slot (l - 1) & 1, build level l +
     // 1 into slot l & 1; the first also sums exp(z - M) over the slice
@@ -736,8 +757,10 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
   }
   if (ph == W_TIES) {
     // ---- the last digit: tau is the K-th largest key; this slice's count of it
-    const FSel s = select_level<false, false>(fr.sk[1], 0, hcs(1), nullptr, G, 0.0f, sh.f);
-    if (g == 0 && tid == 0) fr.sk[0] = s;
+    FSel s = select_level<false, false>(fr.sk[(NL - 1) & 1], 32 - 8 * NL, hcs((NL - 1) & 1), nullptr, G, 0.0f,
+                                        sh.f);
+    s.prefix = complete_key<DT>(s.prefix);
+    if (g == 0 && tid == 0) fr.sk[NL & 1] = s;
     unsigned int mine = 0u;
     row_pass(lo, hi, src, [&](int, float z) { mine += okey(z) == s.prefix ? 1u : 0u; });
     mine = wave_sum(mine);
@@ -753,7 +776,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
 
   // ---- W_GATHER: every entry above tau, and the first need_eq of tau's tie
   // group in index order, into LDS, then one reservation of the row's list
-  const FSel s = fr.sk[0];
+  const FSel s = fr.sk[NL & 1];
   const unsigned int tau = s.prefix;
   const unsigned int need_eq = static_cast<unsigned int>(K) - static_cast<unsigned int>(s.abv);
   int s0, s1;
@@ -866,16 +889,12 @@ int launch_filter(const void* d_logits, int dtype, int B, int V, int64_t row_str
   ws.hm = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws.hc) + fws_align(nb * 4));
   int phases[10], np = 0;
   phases[np++] = FP_MAX;
-  if (use == FU_ALL || use == FU_TOPK) {
-    phases[np++] = FP_K1;
-    phases[np++] = FP_K2;
-    phases[np++] = FP_K3;
-  }
+  const int nl = nlev(dtype);
+  if (use == FU_ALL || use == FU_TOPK)
+    for (int l = 1; l < nl; ++l) phases[np++] = FP_K1 + l - 1;
   if (use != FU_MINP) phases[np++] = FP_P0;
   if (use == FU_ALL || use == FU_TOPP) {
-    phases[np++] = FP_P1;
-    phases[np++] = FP_P2;
-    phases[np++] = FP_P3;
+    for (int l = 1; l < nl; ++l) phases[np++] = FP_P1 + l - 1;
     phases[np++] = FP_TIES;
   }
   phases[np++] = FP_FIN;
@@ -921,7 +940,9 @@ hipError_t launch_topk_wide(const void* logits, int dtype, int B, int V, long lo
   ws.list = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws.hc) + fws_align(nb * 4));
   const size_t esz = dtype == MLXF_DTYPE_F32 ? 4 : 2;
   const bool vec = reinterpret_cast<uintptr_t>(logits) % 16 == 0 && (static_cast<size_t>(row_stride) * esz) % 16 == 0;
+  const int nl = nlev(dtype);
   for (int ph = W_MAX; ph <= W_SORT; ++ph) {
+    if (ph >= W_K1 && ph <= W_K3 && ph - W_K1 + 1 >= nl) continue;  // levels the dtype does not need
     const dim3 grid(static_cast<unsigned int>(B), ph == W_SORT ? 1u : static_cast<unsigned int>(ws.G)), block(FT);
     if (dtype == MLXF_DTYPE_F32)
       hipLaunchKernelGGL(k_topk_wide<MLXF_DTYPE_F32>, grid, block, 0, st, logits, row_stride, V, tlp, K_max, top_ids,
