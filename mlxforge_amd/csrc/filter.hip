@@ -9,20 +9,21 @@
 // max's own weight), so a filter followed by a plain draw keeps what the
 // sampling call keeps.
 //
-// One 1024-thread workgroup per row.  The first pass writes z' into the
-// output row, which then serves as the row's scratch: the top-k threshold and
-// the nucleus cutoff are radix selections over 32-bit order keys (four 8-bit
-// digit levels, a histogram of counts or of masses in LDS per level), and the
-// last pass writes -inf over the removed entries.  The row is read about a
-// dozen times, which suits a helper the decode step never calls.  Two things
-// keep those passes near the rate at which one CU streams its row:
+// Each row is split over G workgroups of 1024 threads and the work runs as a
+// sequence of launches, one per phase (see the filter section below): the
+// top-k threshold and the nucleus cutoff are radix selections over 32-bit
+// order keys (11-bit digits; two levels decide a 16-bit dtype's key, three an
+// fp32 one), each level a histogram of counts or of fixed-point masses built
+// per slice in LDS and summed over the slices through the workspace, and the
+// last phase writes z' or -inf.  Two things keep the passes near the rate the
+// memory allows:
 //  - the radix histograms hold RC copies of each bin, lane l adding into copy
-//    l % RC: the first digit levels put most of a row into a few bins, and
-//    64 lanes adding into one LDS word are served one after another;
-//  - every pass reads the row in coalesced 64-element steps; where index
-//    order matters (the nucleus's partial tie group) wave w takes the
-//    contiguous segment [w S, (w + 1) S) and ranks its tied elements by a
-//    ballot, after one scan of the waves' tie counts.
+//    l % RC: a row's first digits fall into a few bins, and lanes adding into
+//    one LDS word are served one after another;
+//  - every pass reads 8-element units with 16-byte loads, several per lane in
+//    flight; where index order matters (a partial tie group) wave w takes the
+//    contiguous segment [w S, (w + 1) S) of its slice and ranks its tied
+//    elements by a wave prefix sum, after one scan of the waves' tie counts.
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
@@ -36,7 +37,8 @@ namespace {
 
 constexpr int FT = 1024;      // threads per workgroup
 constexpr int FW = FT / 64;   // waves
-constexpr int RC = 32;        // copies of each radix bin (lanes l and l + 32 share one)
+constexpr int NBIN = 2048;    // bins of a radix level (11-bit digits)
+constexpr int RC = 4;         // copies of each radix bin (lane l adds into copy l % RC)
 constexpr int FU8 = 4;        // 8-element units in flight per lane in a row pass
 
 struct FArgs {
@@ -57,8 +59,8 @@ struct FArgs {
 };
 
 struct FLds {
-  unsigned int hc[256 * RC];        // bin d, copy c at d * RC + c
-  unsigned long long hm[256 * RC];
+  unsigned int hc[NBIN * RC];        // bin d, copy c at d * RC + c
+  unsigned long long hm[NBIN * RC];
   unsigned long long u64r[FW];
   float fr[FW];
   int ir[FW];
@@ -273,21 +275,20 @@ enum FPhase { FP_MAX, FP_K1, FP_K2, FP_K3, FP_P0, FP_P1, FP_P2, FP_P3, FP_TIES, 
 
 // Radix levels a dtype needs: the order key of a 16-bit value has its low
 // bits fixed (bf16: 16, f16: 13; zeros for a non-negative value, ones for a
-// negative one), so the digits above them decide it: bf16 2 levels, f16 3,
-// fp32 4.  complete_key fills the bits below the decided digits.
-__host__ __device__ constexpr int nlev(int dt) { return dt == MLXF_DTYPE_F32 ? 4 : (dt == MLXF_DTYPE_BF16 ? 2 : 3); }
+// negative one), so the two 11-bit digits decide it; fp32 takes all three
+// levels.  complete_key fills the bits below the decided digits.
+__host__ __device__ constexpr int nlev(int dt) { return dt == MLXF_DTYPE_F32 ? 3 : 2; }
 template <int DT>
 __device__ __forceinline__ unsigned int complete_key(unsigned int prefix) {
-  constexpr int NL = nlev(DT);
-  if constexpr (NL == 4) return prefix;
-  constexpr unsigned int low = (1u << (32 - 8 * NL)) - 1u;
+  if constexpr (nlev(DT) == 3) return prefix;
+  constexpr unsigned int low = 0x3ffu;  // below the second level's digit (bits 10-20)
   return (prefix & 0x80000000u) ? prefix : (prefix | low);
 }
 
 struct FWs {
   FRow* rows;               // [B]
-  unsigned int* hc;         // [B][2][G][256]
-  unsigned long long* hm;   // [B][2][G][256]
+  unsigned int* hc;         // [B][2][G][NBIN]
+  unsigned long long* hm;   // [B][2][G][NBIN]
   int G;
 };
 
@@ -305,28 +306,39 @@ __host__ __device__ inline int filter_groups(int B, int V) {
 
 __host__ __device__ inline size_t filter_ws_bytes(int B, int V) {
   const size_t G = static_cast<size_t>(filter_groups(B, V));
-  const size_t nb = static_cast<size_t>(B) * 2 * G * 256;
+  const size_t nb = static_cast<size_t>(B) * 2 * G * NBIN;
   return fws_align(static_cast<size_t>(B) * sizeof(FRow)) + fws_align(nb * 4) + fws_align(nb * 8);
 }
 
-// Sum the G slice histograms of level slot `slot` for this row and choose the
-// digit at `shift`: the state s moves to the digit d whose measure (count, or
-// mass when MASS) brings the measure above it from below s.rem to at least
-// s.rem.  With FROM_TOTAL the target is first set from the candidates' whole
-// measure W: max(1, ceil(p W)) (the nucleus's first level).
+// The radix levels over the 32-bit order key: 11-bit digits at bits 21-31
+// and 10-20, then a 10-bit one at bits 0-9.
+__host__ __device__ constexpr int lvl_shift(int l) { return l == 1 ? 21 : (l == 2 ? 10 : 0); }
+__host__ __device__ constexpr unsigned int lvl_mask(int l) { return l < 3 ? 0x7ffu : 0x3ffu; }
+
+// Sum the G slice histograms of level l for this row and choose its digit:
+// the state s moves to the digit d whose measure (count, or mass when MASS)
+// brings the measure above it from below s.rem to at least s.rem.  With
+// FROM_TOTAL the target is first set from the candidates' whole measure W:
+// max(1, ceil(p W)) (the nucleus's first level).  Thread t takes the digits
+// 2047 - 2t and 2046 - 2t (descending order).
 template <bool MASS, bool FROM_TOTAL>
-__device__ FSel select_level(FSel s, int shift, const unsigned int* hc, const unsigned long long* hm, int G,
-                             float pr, FLds& sh) {
+__device__ FSel select_level(FSel s, int l, const unsigned int* hc, const unsigned long long* hm, int G, float pr,
+                             FLds& sh) {
   const int tid = threadIdx.x;
-  const unsigned int d = 255u - static_cast<unsigned int>(tid & 255);
-  unsigned int cnt_d = 0u;
-  unsigned long long meas = 0ull;
-  if (tid < 256) {
-    for (int g = 0; g < G; ++g) {
-      cnt_d += hc[g * 256 + d];
-      if (MASS) meas += hm[g * 256 + d];
+  const unsigned int d1 = static_cast<unsigned int>(NBIN - 1 - 2 * tid), d0 = d1 - 1u;
+  unsigned int c1 = 0u, c0 = 0u;
+  unsigned long long m1 = 0ull, m0 = 0ull;
+  for (int g = 0; g < G; ++g) {
+    c1 += hc[g * NBIN + d1];
+    c0 += hc[g * NBIN + d0];
+    if (MASS) {
+      m1 += hm[g * NBIN + d1];
+      m0 += hm[g * NBIN + d0];
     }
-    if (!MASS) meas = cnt_d;
+  }
+  if (!MASS) {
+    m1 = c1;
+    m0 = c0;
   }
   __syncthreads();  // sh.sel may still be read by the caller's last use
   if (tid == 0) {
@@ -335,17 +347,21 @@ __device__ FSel select_level(FSel s, int shift, const unsigned int* hc, const un
     sh.sel64[0] = 0ull;
   }
   unsigned long long tot;
-  const unsigned long long excl = rh::bscan(meas, sh.u64r, &tot);  // (barriers inside)
+  const unsigned long long excl = rh::bscan(m1 + m0, sh.u64r, &tot);  // (barriers inside)
   if (FROM_TOTAL) {
     unsigned long long PW = static_cast<unsigned long long>(ceil(static_cast<double>(pr) * static_cast<double>(tot)));
     if (PW < 1ull) PW = 1ull;
     s.rem = PW;
     s.tgt = PW;
   }
-  if (tid < 256 && excl < s.rem && s.rem <= excl + meas) {
-    sh.sel[0] = d;
+  if (excl < s.rem && s.rem <= excl + m1) {
+    sh.sel[0] = d1;
     sh.sel64[0] = excl;
-    sh.sel[1] = cnt_d;
+    sh.sel[1] = c1;
+  } else if (excl + m1 < s.rem && s.rem <= excl + m1 + m0) {
+    sh.sel[0] = d0;
+    sh.sel64[0] = excl + m1;
+    sh.sel[1] = c0;
   }
   __syncthreads();
   const unsigned int dd = sh.sel[0];
@@ -353,35 +369,37 @@ __device__ FSel select_level(FSel s, int shift, const unsigned int* hc, const un
   s.cnt = sh.sel[1];
   s.rem -= ex;
   s.abv += ex;
-  s.prefix |= dd << shift;
-  s.mask |= 255u << shift;
+  s.prefix |= dd << lvl_shift(l);
+  s.mask |= lvl_mask(l) << lvl_shift(l);
   return s;
 }
 
-// This slice's histogram at `shift` of the candidates (key under s's prefix,
-// in(zp, key)) into level slot hc / hm (this workgroup's 256 bins); extra(zp)
-// sees every element of the slice on the way.
+// This slice's level-l histogram of the candidates (key under s's prefix,
+// in(zp, key)) into hc / hm (this workgroup's NBIN bins); extra(zp) sees every
+// element of the slice on the way.
 struct NoExtra {
   __device__ void operator()(float) const {}
 };
 
 template <bool MASS, typename Load, typename In, typename Mass, typename Extra = NoExtra>
-__device__ void slice_hist(int lo, int hi, int shift, FSel s, Load load, In in, Mass massf, unsigned int* hc,
+__device__ void slice_hist(int lo, int hi, int l, FSel s, Load load, In in, Mass massf, unsigned int* hc,
                            unsigned long long* hm, FLds& sh, Extra extra = Extra{}) {
   const int tid = threadIdx.x;
   const unsigned int cpy = static_cast<unsigned int>(tid) & (RC - 1);
   __syncthreads();
-  for (int j = tid; j < 256 * RC; j += FT) {
+  for (int j = tid; j < NBIN * RC; j += FT) {
     sh.hc[j] = 0u;
     if (MASS) sh.hm[j] = 0ull;
   }
   __syncthreads();
   const unsigned int prefix = s.prefix, mask = s.mask;
+  const int shift = lvl_shift(l);
+  const unsigned int dmask = lvl_mask(l);
   row_pass(lo, hi, load, [&](int, float zp) {
     extra(zp);
     const unsigned int key = okey(zp);
     if ((key & mask) == prefix && in(zp, key)) {
-      const unsigned int d = ((key >> shift) & 255u) * RC + cpy;
+      const unsigned int d = ((key >> shift) & dmask) * RC + cpy;
       __hip_atomic_fetch_add(&sh.hc[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       if (MASS) {
         const unsigned long long m = massf(zp);
@@ -390,14 +408,13 @@ __device__ void slice_hist(int lo, int hi, int shift, FSel s, Load load, In in, 
     }
   });
   __syncthreads();
-  if (tid < 256) {
-    const unsigned int d = static_cast<unsigned int>(tid);
+  for (int d = tid; d < NBIN; d += FT) {
     unsigned int c = 0u;
     unsigned long long m = 0ull;
-    for (unsigned int k = 0; k < static_cast<unsigned int>(RC); ++k) {
-      const unsigned int j = d * RC + ((k + d) & (RC - 1));
-      c += sh.hc[j];
-      if (MASS) m += sh.hm[j];
+#pragma unroll
+    for (int k = 0; k < RC; ++k) {
+      c += sh.hc[d * RC + k];
+      if (MASS) m += sh.hm[d * RC + k];
     }
     hc[d] = c;
     if (MASS) hm[d] = m;
@@ -415,10 +432,10 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
   const void* irow = static_cast<const char*>(f.logits) + static_cast<size_t>(r) * f.row_stride * elem_size<DT>();
   void* orow = static_cast<char*>(f.out) + static_cast<size_t>(r) * f.out_stride * elem_size<DT>();
   FRow& row = ws.rows[r];
-  unsigned int* hc0 = ws.hc + static_cast<size_t>(r) * 2 * G * 256;
-  unsigned long long* hm0 = ws.hm + static_cast<size_t>(r) * 2 * G * 256;
-  auto hcs = [&](int slot) { return hc0 + static_cast<size_t>(slot) * G * 256; };
-  auto hms = [&](int slot) { return hm0 + static_cast<size_t>(slot) * G * 256; };
+  unsigned int* hc0 = ws.hc + static_cast<size_t>(r) * 2 * G * NBIN;
+  unsigned long long* hm0 = ws.hm + static_cast<size_t>(r) * 2 * G * NBIN;
+  auto hcs = [&](int slot) { return hc0 + static_cast<size_t>(slot) * G * NBIN; };
+  auto hms = [&](int slot) { return hm0 + static_cast<size_t>(slot) * G * NBIN; };
 
   // ---- the row's parameters (the sampling call's sentinels)
   const float T = f.T ? f.T[r] : f.Ts;
@@ -454,7 +471,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     if (tid == 0) row.mxp[g] = m;
     if (tk_on) {
       FSel s{};
-      slice_hist<false>(lo, hi, 24, s, src, all, nomass, hcs(0) + g * 256, nullptr, sh);
+      slice_hist<false>(lo, hi, 1, s, src, all, nomass, hcs(0) + g * NBIN, nullptr, sh);
     }
     return;
   }
@@ -467,9 +484,9 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     FSel s{};
     s.rem = s.tgt = static_cast<unsigned long long>(kk);
     if (l > 1) s = row.sk[(l - 1) & 1];
-    s = select_level<false, false>(s, 32 - 8 * l, hcs((l - 1) & 1), nullptr, G, 0.0f, sh);
+    s = select_level<false, false>(s, l, hcs((l - 1) & 1), nullptr, G, 0.0f, sh);
     if (g == 0 && tid == 0) row.sk[l & 1] = s;
-    slice_hist<false>(lo, hi, 24 - 8 * l, s, src, all, nomass, hcs(l & 1) + g * 256, nullptr, sh);
+    slice_hist<false>(lo, hi, l + 1, s, src, all, nomass, hcs(l & 1) + g * NBIN, nullptr, sh);
     return;
   }
 
@@ -487,7 +504,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     // survivors (src/sample/sampler.cpp:70-85)
     unsigned int tk = 0u;
     if (tk_on) {
-      FSel s = select_level<false, false>(row.sk[(NL - 1) & 1], 32 - 8 * NL, hcs((NL - 1) & 1), nullptr, G, 0.0f,
+      FSel s = select_level<false, false>(row.sk[(NL - 1) & 1], NL, hcs((NL - 1) & 1), nullptr, G, 0.0f,
                                           sh);
       s.prefix = complete_key<DT>(s.prefix);
       if (g == 0 && tid == 0) row.sk[NL & 1] = s;
@@ -495,8 +512,8 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     }
     if (tp_on) {
       FSel s{};
-      slice_hist<true>(lo, hi, 24, s, src, [tk](float, unsigned int key) { return key >= tk; }, massf,
-                       hcs(NL & 1) + g * 256, hms(NL & 1) + g * 256, sh);
+      slice_hist<true>(lo, hi, 1, s, src, [tk](float, unsigned int key) { return key >= tk; }, massf,
+                       hcs(NL & 1) + g * NBIN, hms(NL & 1) + g * NBIN, sh);
     }
     return;
   }
@@ -510,14 +527,14 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     FSel s;
     if (l == 1) {
       s = FSel{};
-      s = select_level<true, true>(s, 24, hcs(NL & 1), hms(NL & 1), G, pr, sh);
+      s = select_level<true, true>(s, 1, hcs(NL & 1), hms(NL & 1), G, pr, sh);
     } else {
       const int in = (NL + l - 1) & 1;
-      s = select_level<true, false>(row.sp[(l - 1) & 1], 32 - 8 * l, hcs(in), hms(in), G, pr, sh);
+      s = select_level<true, false>(row.sp[(l - 1) & 1], l, hcs(in), hms(in), G, pr, sh);
     }
     if (g == 0 && tid == 0) row.sp[l & 1] = s;
     const int outs = (NL + l) & 1;
-    slice_hist<true>(lo, hi, 24 - 8 * l, s, src, above_tk, massf, hcs(outs) + g * 256, hms(outs) + g * 256,
+    slice_hist<true>(lo, hi, l + 1, s, src, above_tk, massf, hcs(outs) + g * NBIN, hms(outs) + g * NBIN,
                      sh);
     return;
   }
@@ -534,7 +551,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     // ---- the nucleus's last digit, and this slice's count of the cutoff key
     // when the cutoff's tie group is kept in part
     if (!tp_on) return;
-    FSel s = select_level<true, false>(row.sp[(NL - 1) & 1], 32 - 8 * NL, hcs((2 * NL - 1) & 1),
+    FSel s = select_level<true, false>(row.sp[(NL - 1) & 1], NL, hcs((2 * NL - 1) & 1),
                                        hms((2 * NL - 1) & 1), G, pr, sh);
     s.prefix = complete_key<DT>(s.prefix);
     if (g == 0 && tid == 0) row.sp[NL & 1] = s;
@@ -612,8 +629,8 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
 // :52) as launches of their own after the sampling kernels, G workgroups per
 // row as in the filter calls: the slice maxima of the unscaled row with the
 // first radix level of the K-th largest logit; the slices' fp64 sums of
-// exp(z - M) with the second level; the third and fourth levels; the last
-// digit with the slices' counts of the K-th logit's tie group; the gather of
+// exp(z - M) with the second level; the third level (fp32); the last digit
+// with the slices' counts of the K-th logit's tie group; the gather of
 // the K entries (every logit above the K-th, then the tied ones in index
 // order) into the row's list in the workspace; and one workgroup per row that
 // sorts the list by (logit desc, index asc) with a bitonic network in LDS and
@@ -631,7 +648,7 @@ struct WRow {
 
 struct WWs {
   WRow* rows;                 // [B]
-  unsigned int* hc;           // [B][2][G][256]
+  unsigned int* hc;           // [B][2][G][NBIN]
   unsigned long long* list;   // [B][K_max]: (key << 32) | ~index
   int G;
 };
@@ -645,7 +662,7 @@ struct TkLds {
 
 __host__ __device__ inline size_t wide_ws_bytes(int B, int V, int K_max) {
   const size_t G = static_cast<size_t>(filter_groups(B, V));
-  const size_t nb = static_cast<size_t>(B) * 2 * G * 256;
+  const size_t nb = static_cast<size_t>(B) * 2 * G * NBIN;
   return fws_align(static_cast<size_t>(B) * sizeof(WRow)) + fws_align(nb * 4) +
          fws_align(static_cast<size_t>(B) * K_max * 8);
 }
@@ -663,8 +680,8 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
   const void* row = static_cast<const char*>(logits) + static_cast<size_t>(r) * row_stride * elem_size<DT>();
   WRow& wr = ws.rows[r];
   FRow& fr = wr.f;
-  unsigned int* hc0 = ws.hc + static_cast<size_t>(r) * 2 * G * 256;
-  auto hcs = [&](int slot) { return hc0 + static_cast<size_t>(slot) * G * 256; };
+  unsigned int* hc0 = ws.hc + static_cast<size_t>(r) * 2 * G * NBIN;
+  auto hcs = [&](int slot) { return hc0 + static_cast<size_t>(slot) * G * NBIN; };
   unsigned long long* lst = ws.list + static_cast<size_t>(r) * K_max;
   const int t = tlp ? tlp[r] : -1;
   const int K = t > 0 ? min(min(t, K_max), V) : 0;
@@ -729,7 +746,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
       if (g == 0) wr.n = 0u;
     }
     FSel s{};
-    slice_hist<false>(lo, hi, 24, s, src, all, nomass, hcs(0) + g * 256, nullptr, sh.f);
+    slice_hist<false>(lo, hi, 1, s, src, all, nomass, hcs(0) + g * NBIN, nullptr, sh.f);
     return;
   }
   constexpr int NL = nlev(DT);
@@ -740,24 +757,24 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
     FSel s{};
     s.rem = s.tgt = static_cast<unsigned long long>(K);
     if (l > 1) s = fr.sk[(l - 1) & 1];
-    s = select_level<false, false>(s, 32 - 8 * l, hcs((l - 1) & 1), nullptr, G, 0.0f, sh.f);
+    s = select_level<false, false>(s, l, hcs((l - 1) & 1), nullptr, G, 0.0f, sh.f);
     if (g == 0 && tid == 0) fr.sk[l & 1] = s;
     if (l == 1) {
       float M = -INFINITY;
       for (int q = 0; q < G; ++q) M = fmaxf(M, fr.mxp[q]);
       double part = 0.0;
-      slice_hist<false>(lo, hi, 16, s, src, all, nomass, hcs(1) + g * 256, nullptr, sh.f,
+      slice_hist<false>(lo, hi, 2, s, src, all, nomass, hcs(1) + g * NBIN, nullptr, sh.f,
                         [&](float z) { part += wexp_d(z, M); });
       const double tot = fsum(part, sh.dr);
       if (tid == 0) wr.lsep[g] = tot;
     } else {
-      slice_hist<false>(lo, hi, 24 - 8 * l, s, src, all, nomass, hcs(l & 1) + g * 256, nullptr, sh.f);
+      slice_hist<false>(lo, hi, l + 1, s, src, all, nomass, hcs(l & 1) + g * NBIN, nullptr, sh.f);
     }
     return;
   }
   if (ph == W_TIES) {
     // ---- the last digit: tau is the K-th largest key; this slice's count of it
-    FSel s = select_level<false, false>(fr.sk[(NL - 1) & 1], 32 - 8 * NL, hcs((NL - 1) & 1), nullptr, G, 0.0f,
+    FSel s = select_level<false, false>(fr.sk[(NL - 1) & 1], NL, hcs((NL - 1) & 1), nullptr, G, 0.0f,
                                         sh.f);
     s.prefix = complete_key<DT>(s.prefix);
     if (g == 0 && tid == 0) fr.sk[NL & 1] = s;
@@ -882,7 +899,7 @@ int launch_filter(const void* d_logits, int dtype, int B, int V, int64_t row_str
   f.V = V;
   FWs ws;
   ws.G = filter_groups(B, V);
-  const size_t nb = static_cast<size_t>(B) * 2 * ws.G * 256;
+  const size_t nb = static_cast<size_t>(B) * 2 * ws.G * NBIN;
   char* base = static_cast<char*>(d_ws);
   ws.rows = reinterpret_cast<FRow*>(base);
   ws.hc = reinterpret_cast<unsigned int*>(base + fws_align(static_cast<size_t>(B) * sizeof(FRow)));
@@ -933,7 +950,7 @@ hipError_t launch_topk_wide(const void* logits, int dtype, int B, int V, long lo
                             int K_max, int* top_ids, float* top_lp, void* d_ws, hipStream_t st) {
   WWs ws;
   ws.G = filter_groups(B, V);
-  const size_t nb = static_cast<size_t>(B) * 2 * ws.G * 256;
+  const size_t nb = static_cast<size_t>(B) * 2 * ws.G * NBIN;
   char* base = static_cast<char*>(d_ws);
   ws.rows = reinterpret_cast<WRow*>(base);
   ws.hc = reinterpret_cast<unsigned int*>(base + fws_align(static_cast<size_t>(B) * sizeof(WRow)));
