@@ -23,7 +23,8 @@
 //  - every pass reads 8-element units with 16-byte loads, several per lane in
 //    flight; where index order matters (a partial tie group) wave w takes the
 //    contiguous segment [w S, (w + 1) S) of its slice and ranks its tied
-//    elements by a wave prefix sum, after one scan of the waves' tie counts.
+//    elements by a wave prefix sum, after the tie counts of the segments
+//    before it (counted by the phase before).
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
@@ -225,23 +226,28 @@ __device__ __forceinline__ unsigned int lanes_before(unsigned int c, unsigned in
   return static_cast<unsigned int>(inc) - c;
 }
 
-// The number of elements whose value satisfies pred in the segments of the
-// waves below this one (red: FW words of LDS).
+// Each wave's count of the elements of its segment whose value satisfies
+// pred, stored at cnt[g FW + w] for the next phases.
 template <int DT, typename Xf, typename Pred>
-__device__ unsigned int ties_before(int s0, int s1, const RowSrc<DT, Xf>& src, Pred pred, int* red) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+__device__ void seg_counts(int lo, int hi, int g, const RowSrc<DT, Xf>& src, Pred pred, unsigned int* cnt) {
+  int s0, s1;
+  wave_segment(lo, hi, &s0, &s1);
   unsigned int mine = 0u;
   seg_pass(s0, s1, src, [&](int, const float* v, int n) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) mine += (e < n && pred(v[e])) ? 1u : 0u;
   });
   mine = wave_sum(mine);
-  __syncthreads();
-  if (lane == 0) red[wid] = static_cast<int>(mine);
-  __syncthreads();
-  unsigned int base = 0u;
-  for (int w = 0; w < wid; ++w) base += static_cast<unsigned int>(red[w]);
-  return base;
+  if ((threadIdx.x & 63) == 0) cnt[g * FW + (threadIdx.x >> 6)] = mine;
+}
+
+// The sum of cnt[0 .. g FW + w): the counted elements of the wave segments
+// before this wave's, in index order (whole wave).
+__device__ __forceinline__ unsigned int segs_before(const unsigned int* cnt, int g) {
+  const int idx = g * FW + (static_cast<int>(threadIdx.x) >> 6), lane = threadIdx.x & 63;
+  unsigned int t = 0u;
+  for (int q = lane; q < idx; q += 64) t += cnt[q];
+  return wave_sum(t);
 }
 
 // ---- the filter calls: G workgroups per row, one kernel per phase.
@@ -268,7 +274,7 @@ struct FSel {
 struct FRow {
   FSel sk[2], sp[2];          // top-k and top-p states after level j at [j & 1]
   float mxp[FG_MAX];          // slice maxima of z'
-  unsigned int tiec[FG_MAX];  // slice counts of the nucleus cutoff's key
+  unsigned int tiec[FG_MAX * FW];  // per wave segment (slice g, wave w at g FW + w): counts of a cutoff's key
 };
 
 enum FPhase { FP_MAX, FP_K1, FP_K2, FP_K3, FP_P0, FP_P1, FP_P2, FP_P3, FP_TIES, FP_FIN };
@@ -548,8 +554,8 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     *tkeep = t >= s.cnt ? 0xffffffffu : t;
   };
   if (ph == FP_TIES) {
-    // ---- the nucleus's last digit, and this slice's count of the cutoff key
-    // when the cutoff's tie group is kept in part
+    // ---- the nucleus's last digit, and each wave segment's count of the
+    // cutoff key when the cutoff's tie group is kept in part
     if (!tp_on) return;
     FSel s = select_level<true, false>(row.sp[(NL - 1) & 1], NL, hcs((2 * NL - 1) & 1),
                                        hms((2 * NL - 1) & 1), G, pr, sh);
@@ -558,23 +564,14 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
     unsigned int ck, tkeep;
     cutoff(s, &ck, &tkeep);
     if (tkeep == 0xffffffffu) return;
-    unsigned int mine = 0u;
-    row_pass(lo, hi, src, [&](int, float zp) { mine += okey(zp) == ck ? 1u : 0u; });
-    mine = wave_sum(mine);
-    if ((tid & 63) == 0) sh.ir[tid >> 6] = static_cast<int>(mine);
-    __syncthreads();
-    if (tid == 0) {
-      unsigned int tot = 0u;
-      for (int q = 0; q < FW; ++q) tot += static_cast<unsigned int>(sh.ir[q]);
-      row.tiec[g] = tot;
-    }
+    seg_counts(lo, hi, g, src, [&](float zp) { return okey(zp) == ck; }, row.tiec);
     return;
   }
 
   // ---- FP_FIN: z', or -inf over every removed entry.  The partial tie
   // group keeps its first tkeep in index order: a tied element's rank is the
-  // ties of the lower slices, of the lower waves' segments of this slice, and
-  // those before it in its own segment
+  // ties of the wave segments before its own (lower slices, then lower waves;
+  // counted by FP_TIES), and those before it in its own segment
   unsigned int ck = 0u, tkeep = 0xffffffffu;
   if (tp_on) cutoff(row.sp[NL & 1], &ck, &tkeep);
   const bool filt = live && (tk_on || tp_on || mr > 0.0f);
@@ -585,10 +582,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
   int s0, s1;
   wave_segment(lo, hi, &s0, &s1);
   unsigned int rank = 0u;
-  if (partial) {
-    for (int q = 0; q < g; ++q) rank += row.tiec[q];
-    rank += ties_before(s0, s1, src, [&](float zp) { return okey(zp) == ck; }, sh.ir);
-  }
+  if (partial) rank = segs_before(row.tiec, g);
   seg_pass(s0, s1, src, [&](int i0, const float* v, int n) {
     bool keep[8];
     unsigned int c = 0u;
@@ -773,21 +767,13 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
     return;
   }
   if (ph == W_TIES) {
-    // ---- the last digit: tau is the K-th largest key; this slice's count of it
+    // ---- the last digit: tau is the K-th largest key; each wave segment's
+    // count of it
     FSel s = select_level<false, false>(fr.sk[(NL - 1) & 1], NL, hcs((NL - 1) & 1), nullptr, G, 0.0f,
                                         sh.f);
     s.prefix = complete_key<DT>(s.prefix);
     if (g == 0 && tid == 0) fr.sk[NL & 1] = s;
-    unsigned int mine = 0u;
-    row_pass(lo, hi, src, [&](int, float z) { mine += okey(z) == s.prefix ? 1u : 0u; });
-    mine = wave_sum(mine);
-    if ((tid & 63) == 0) sh.f.ir[tid >> 6] = static_cast<int>(mine);
-    __syncthreads();
-    if (tid == 0) {
-      unsigned int tot = 0u;
-      for (int q = 0; q < FW; ++q) tot += static_cast<unsigned int>(sh.f.ir[q]);
-      fr.tiec[g] = tot;
-    }
+    seg_counts(lo, hi, g, src, [&](float z) { return okey(z) == s.prefix; }, fr.tiec);
     return;
   }
 
@@ -799,9 +785,8 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
   int s0, s1;
   wave_segment(lo, hi, &s0, &s1);
   if (tid == 0) sh.n = 0u;
-  unsigned int rank = 0u;
-  for (int q = 0; q < g; ++q) rank += fr.tiec[q];
-  rank += ties_before(s0, s1, src, [&](float z) { return okey(z) == tau; }, sh.f.ir);
+  unsigned int rank = segs_before(fr.tiec, g);
+  __syncthreads();  // sh.n cleared before the first slot is taken
   seg_pass(s0, s1, src, [&](int i0, const float* v, int n) {
     unsigned int c = 0u;
 #pragma unroll
