@@ -622,8 +622,9 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
 // top_k_logprobs (src/sample/sampler.cpp:30-38; K = min(top_logprobs, V) at
 // :52) as launches of their own after the sampling kernels, G workgroups per
 // row as in the filter calls: the slice maxima of the unscaled row with the
-// first radix level of the K-th largest logit; the slices' fp64 sums of
-// exp(z - M) with the second level; the third level (fp32); the last digit
+// first radix level of the K-th largest logit; the slices' sums of exp(z - M)
+// (fp32 exponentials, as the sampling kernels take them, summed in fp64) with
+// the second level; the third level (fp32); the last digit
 // with the slices' counts of the K-th logit's tie group; the gather of
 // the K entries (every logit above the K-th, then the tied ones in index
 // order) into the row's list in the workspace; and one workgroup per row that
@@ -758,7 +759,7 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
       for (int q = 0; q < G; ++q) M = fmaxf(M, fr.mxp[q]);
       double part = 0.0;
       slice_hist<false>(lo, hi, 2, s, src, all, nomass, hcs(1) + g * NBIN, nullptr, sh.f,
-                        [&](float z) { part += wexp_d(z, M); });
+                        [&](float z) { part += static_cast<double>(wexp(z, M)); });
       const double tot = fsum(part, sh.dr);
       if (tid == 0) wr.lsep[g] = tot;
     } else {
