@@ -632,6 +632,7 @@ __global__ __launch_bounds__(FT, 1) void k_filter(FArgs f, FWs ws, int ph) {
 // writes (id, logit - LSE), columns past the row's K as id -1 and -inf.
 
 constexpr int TOPK_WIDE_MAX = 4096;
+static_assert(TOPK_WIDE_MAX / 2 <= 2 * FT, "the sort gives each thread at most two pairs");
 
 enum WPhase { W_MAX, W_K1, W_K2, W_K3, W_TIES, W_GATHER, W_SORT };
 
@@ -702,16 +703,30 @@ __global__ __launch_bounds__(FT, 1) void k_topk_wide(const void* logits, long lo
     for (int q = 0; q < G; ++q) S += wr.lsep[q];
     const double lse = static_cast<double>(M) + log(S);
     __syncthreads();
+    // each step's np / 2 compare-exchange pairs (i, i | jj), i without bit jj,
+    // at most two per thread; both pairs' loads are issued before either store
+    // (a step's pairs are disjoint), so a step costs one LDS round trip
+    const int npairs = np >> 1;
     for (int k = 2; k <= np; k <<= 1) {
       for (int jj = k >> 1; jj > 0; jj >>= 1) {
-        for (int i = tid; i < np; i += FT) {
-          const int ixj = i ^ jj;
-          if (ixj > i) {
-            const unsigned long long a = sh.ent[i], b = sh.ent[ixj];
-            const bool desc = (i & k) == 0;
-            if (desc ? (a < b) : (a > b)) {
-              sh.ent[i] = b;
-              sh.ent[ixj] = a;
+        unsigned long long a[2], b[2];
+        int ia[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int pr = tid + q * FT;
+          ia[q] = ((pr & ~(jj - 1)) << 1) | (pr & (jj - 1));
+          if (pr < npairs) {
+            a[q] = sh.ent[ia[q]];
+            b[q] = sh.ent[ia[q] | jj];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          if (tid + q * FT < npairs) {
+            const bool desc = (ia[q] & k) == 0;
+            if (desc ? (a[q] < b[q]) : (a[q] > b[q])) {
+              sh.ent[ia[q]] = b[q];
+              sh.ent[ia[q] | jj] = a[q];
             }
           }
         }
