@@ -64,9 +64,8 @@ struct FLds {
   unsigned long long hm[NBIN * RC];
   unsigned long long u64r[FW];
   float fr[FW];
-  int ir[FW];
-  unsigned int sel[4];
-  unsigned long long sel64[2];
+  unsigned int sel[2];          // the chosen digit and its count
+  unsigned long long sel64[1];  // the measure above it
 };
 
 template <int DT>
