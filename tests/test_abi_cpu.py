@@ -42,6 +42,12 @@ def test_workspace_size_is_positive_and_monotone():
     a = _lib.workspace_size(8, 151936, 0, _lib.DTYPE_BF16)
     b = _lib.workspace_size(64, 151936, 20, _lib.DTYPE_F32)
     assert 0 < a < b
+    # top_logprobs above the 64-entry lists: the wide kernels' states, slice
+    # histograms and per-row lists (K_max entries of 8 bytes) come on top
+    c64 = _lib.workspace_size(64, 151936, 64, _lib.DTYPE_F32)
+    c65 = _lib.workspace_size(64, 151936, 65, _lib.DTYPE_F32)
+    c4k = _lib.workspace_size(64, 151936, 4096, _lib.DTYPE_F32)
+    assert c64 < c65 < c4k and c4k - c65 >= 64 * (4096 - 65) * 8
 
 
 @pytest.mark.parametrize("args", [
