@@ -20,11 +20,11 @@
 //  - the radix histograms hold RC copies of each bin, lane l adding into copy
 //    l % RC: a row's first digits fall into a few bins, and lanes adding into
 //    one LDS word are served one after another;
-//  - every pass reads 8-element units with 16-byte loads, several per lane in
-//    flight; where index order matters (a partial tie group) wave w takes the
-//    contiguous segment [w S, (w + 1) S) of its slice and ranks its tied
-//    elements by a wave prefix sum, after the tie counts of the segments
-//    before it (counted by the phase before).
+//  - every pass reads 8-element units with 16-byte loads; where index order
+//    matters (a partial tie group) wave w takes the contiguous segment
+//    [w S, (w + 1) S) of its slice and ranks its tied elements by a wave
+//    prefix sum, after the tie counts of the segments before it (counted by
+//    the phase before).
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
@@ -40,7 +40,7 @@ constexpr int FT = 1024;      // threads per workgroup
 constexpr int FW = FT / 64;   // waves
 constexpr int NBIN = 2048;    // bins of a radix level (11-bit digits)
 constexpr int RC = 4;         // copies of each radix bin (lane l adds into copy l % RC)
-constexpr int FU8 = 4;        // 8-element units in flight per lane in a row pass
+constexpr int FU8 = 1;        // 8-element units per lane per loop step (2 and 4 measured slower)
 
 struct FArgs {
   const void* logits;
@@ -137,9 +137,9 @@ __device__ __forceinline__ RowSrc<DT, Xf> row_src(const void* row, bool vec, Xf 
 }
 
 // fn(i, value) for every i in [lo, hi) (lo % 8 == 0), lane t taking the units
-// t, t + FT, ...; FU8 units per lane are loaded before the first is used: one
-// CU streams a slice, and it needs many bytes in flight per lane to do it at
-// the memory's rate.
+// t, t + FT, ...; FU8 units per lane per step are loaded before the first is
+// used (one 16- or 32-byte unit measured fastest: the 16 waves of a CU keep
+// enough loads in flight).
 template <int DT, typename Xf, typename Fn>
 __device__ __forceinline__ void row_pass(int lo, int hi, const RowSrc<DT, Xf>& src, Fn fn) {
   const int nu = (hi - lo + 7) >> 3;
